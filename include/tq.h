@@ -1,0 +1,195 @@
+/*
+ * tq.h -- C ABI of the MI355X (gfx950) quantized-inference library libtq.so.
+ *
+ * This is the drop-in boundary for neo-theano's `theano-quantize` crate: the
+ * entry points below are what the theano-rocm FFI layer binds (an
+ * `extern "C"` block on the Rust side) to run the crate's quantize,
+ * dequantize and quantized-Linear work on the GPU.  Each declaration names
+ * the reference interface it replaces (paths relative to the reference
+ * repository root).
+ *
+ * Conventions (all entry points):
+ *  - every tensor pointer is caller-owned DEVICE memory, row-major, dense;
+ *  - `stream` is the last argument; work is enqueued asynchronously on it and
+ *    is stream-ordered.  NULL means the default stream;
+ *  - the library allocates nothing and keeps no mutable global state, so calls
+ *    on distinct streams are reentrant and thread-safe;
+ *  - integer sizes are int64_t; a size of zero is a valid no-op unless noted;
+ *  - the return value is a tq_status.  On failure nothing was enqueued and
+ *    tq_last_error() (thread-local) holds a message.  The statuses map onto
+ *    the reference's error types: TQ_EINVAL -> TheanoError::InvalidArgument /
+ *    ShapeMismatch (crates/theano-types/src/error.rs:7-56), TQ_EHIP ->
+ *    RocmError::KernelError / DriverError, TQ_ENOMEM -> RocmError::OutOfMemory
+ *    (crates/theano-rocm/src/error.rs:3-73).
+ *
+ * Numerics (the parity contract):
+ *  - codes use the reference rounding, round-half-away-from-zero of the exact
+ *    quotient x/scale (+ zero point), then clamp (quantize.rs:15); integer
+ *    codes, packed bytes, scales and int32 accumulators are bit-exact with the
+ *    reference CPU path; dequantized values are bit-exact (IEEE ==, the
+ *    reference's -0.0 codes become +0.0);
+ *  - a NaN input gives code 0 (Rust's `f64 as i8` of the reference's NaN code);
+ *  - float matmul outputs are f32 with f32 accumulation, within 1e-3 relative
+ *    / 1e-4 absolute of the reference's f64 result.
+ */
+#ifndef TQ_H
+#define TQ_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* tq_stream_t; /* hipStream_t */
+
+typedef enum {
+    TQ_OK = 0,
+    TQ_EINVAL = 1,  /* bad shape, pointer, alignment or argument */
+    TQ_EHIP = 2,    /* HIP runtime / launch failure */
+    TQ_ENOMEM = 3,  /* device allocation failure (host-side helpers only) */
+} tq_status;
+
+/* QuantDType: crates/theano-quantize/src/qconfig.rs:5-10 (same order) */
+typedef enum {
+    TQ_QINT8 = 0,
+    TQ_QUINT8 = 1,
+    TQ_QINT4 = 2,
+    TQ_QFP8 = 3, /* range +-448 only, as in the reference (no FP8 encoding) */
+} tq_qdtype;
+
+/* Library version (major*10000 + minor*100 + patch). */
+int tq_version(void);
+/* Human-readable name of a status. */
+const char* tq_status_string(int status);
+/* Message describing the last failure on the calling thread ("" if none). */
+const char* tq_last_error(void);
+
+/* QuantDType::{bits, is_signed, qmin, qmax}: qconfig.rs:12-41. Host-only. */
+int tq_qdtype_info(int qdtype, int* bits, int* is_signed, double* qmin, double* qmax);
+
+/* ------------------------------------------------------------------------
+ * Reference primitives on device data.
+ * Codes are returned as f32 values: every code the reference returns in its
+ * Vec<f64> (integral, within +-448, -0.0 and NaN included) is exactly
+ * representable in f32, so the f32 buffer holds the reference's codes
+ * bit-for-bit after widening.  Arithmetic is done in f64 on the GPU.
+ * ------------------------------------------------------------------------ */
+
+/* quantize_tensor (crates/theano-quantize/src/quantize.rs:8-19):
+ *   q[i] = clamp(round(x[i]/scale + zero_point), qmin, qmax) */
+int tq_quantize_tensor(const float* x, int64_t n, double scale, double zero_point,
+                       int qdtype, float* q, tq_stream_t stream);
+
+/* dequantize_tensor (quantize.rs:22-27): out[i] = f32((q[i] - zero_point) * scale) */
+int tq_dequantize_tensor(const float* q, int64_t n, double scale, double zero_point,
+                         float* out, tq_stream_t stream);
+
+/* fake_quantize (quantize.rs:51-55): out = f32(dequantize(quantize(x))) */
+int tq_fake_quantize(const float* x, int64_t n, double scale, double zero_point,
+                     int qdtype, float* out, tq_stream_t stream);
+
+/* quantize_per_tensor (quantize.rs:30-48): asymmetric scale/zero point from the
+ * data's min/max, then quantize_tensor.  scale_zp (device, 2 doubles) receives
+ * {scale, zero_point}.  workspace: device memory of TQ_PER_TENSOR_WORKSPACE
+ * bytes, 16-byte aligned, contents need not be initialised. */
+#define TQ_PER_TENSOR_WORKSPACE 64
+int tq_quantize_per_tensor(const float* x, int64_t n, int qdtype, float* q,
+                           double* scale_zp, void* workspace, tq_stream_t stream);
+
+/* MinMaxObserver::{reset, observe} (crates/theano-quantize/src/observer.rs:42-73).
+ * state (device, 2 floats) = {min, max}; reset sets {+inf, -inf}; observe
+ * folds min/max ignoring NaN.  compute_scale_zero_point is scalar host math
+ * (see tq_observer_scale_zp). */
+int tq_minmax_reset(float* state, int64_t channels, tq_stream_t stream);
+int tq_minmax_observe(const float* x, int64_t n, float* state, tq_stream_t stream);
+
+/* PerChannelMinMaxObserver::observe (observer.rs:110-121): values laid out
+ * [channels, n/channels] (a trailing remainder is ignored, as in the
+ * reference); state (device) = channels x {min, max}. */
+int tq_minmax_observe_per_channel(const float* x, int64_t n, int64_t channels,
+                                  float* state, tq_stream_t stream);
+
+/* compute_scale_zero_point for one {min,max} pair (observer.rs:51-66,93-106).
+ * Host-only scalar helper; initialized=0 gives (1, 0) as the reference does. */
+int tq_observer_scale_zp(double min_val, double max_val, int initialized, int qdtype,
+                         double* scale, double* zero_point);
+
+/* ------------------------------------------------------------------------
+ * Weight formats (build-defined compositions of the primitives above).
+ * ------------------------------------------------------------------------ */
+
+/* Symmetric per-row INT8 (per output channel for a [N, K] weight; per token
+ * for [M, K] activations):
+ *   s[r] = f32(max(absmax_r / 127, 1e-10)),  absmax from the observer's
+ *          min/max (observer.rs:110-121) and the 1e-10 floor of quantize.rs:39
+ *   q[r,k] = quantize_tensor(row r, f64(s[r]), 0, Int8)   (quantize.rs:8-19)
+ * W [rows, K] f32 -> q int8 [rows, K], s f32 [rows]. */
+int tq_quantize_i8_rowwise(const float* w, int64_t rows, int64_t k, int8_t* q, float* s,
+                           tq_stream_t stream);
+/* dequantize_tensor per row (quantize.rs:22-27): w_hat = f32(q * s[r]). */
+int tq_dequantize_i8_rowwise(const int8_t* q, const float* s, int64_t rows, int64_t k,
+                             float* w_hat, tq_stream_t stream);
+/* Both in one pass (fake_quantize per row, quantize.rs:51-55); q, s, w_hat as above. */
+int tq_fake_quantize_i8_rowwise(const float* w, int64_t rows, int64_t k, int8_t* q,
+                                float* s, float* w_hat, tq_stream_t stream);
+
+/* Symmetric INT4 with groups of 128 along K (K % 128 == 0):
+ *   s[r,g] = max(f16_rne(absmax_{r,g} / 7), 2^-24)   (f16 bits)
+ *   q      = quantize_tensor(group, f64(s), 0, Int4)  in [-8, 7]
+ *   packed[r, j] = (q[r,2j] & 0xF) | (q[r,2j+1] & 0xF) << 4   (low nibble = even k)
+ * W [rows, K] f32 -> packed u8 [rows, K/2], s f16 [rows, K/128]. */
+int tq_quantize_i4_g128(const float* w, int64_t rows, int64_t k, uint8_t* packed,
+                        uint16_t* s_f16, tq_stream_t stream);
+/* w_hat = f32(q * s) (exact). */
+int tq_dequantize_i4_g128(const uint8_t* packed, const uint16_t* s_f16, int64_t rows,
+                          int64_t k, float* w_hat, tq_stream_t stream);
+
+/* ------------------------------------------------------------------------
+ * Quantized Linear: y = x . dequant(W)^T (+ bias), the reference's
+ * Linear::forward (crates/theano-nn/src/linear.rs:111-121) over the
+ * dequantized weight that Linear::from_tensors receives (linear.rs:65-75).
+ * y is f32 [M, N]; bias (f32 [N]) may be NULL.
+ * ------------------------------------------------------------------------ */
+
+/* Decode-shaped GEMV, INT8 per-row weights, f32 activations x [M, K], M <= 16. */
+int tq_gemv_w8(const float* x, int64_t m, const int8_t* q, const float* s,
+               const float* bias, int64_t n, int64_t k, float* y, tq_stream_t stream);
+
+/* Decode-shaped GEMV, INT4 g128 weights, bf16 activations x [M, K] (bf16 bits),
+ * M <= 16, K % 128 == 0. */
+int tq_gemv_w4g128(const uint16_t* x_bf16, int64_t m, const uint8_t* packed,
+                   const uint16_t* s_f16, const float* bias, int64_t n, int64_t k,
+                   float* y, tq_stream_t stream);
+
+/* Prefill-shaped W8A8: activations already quantized per row (use
+ * tq_quantize_i8_rowwise on X).  acc[i,j] = sum_p qa[i,p]*qw[j,p] (int32,
+ * bit-exact); y = f32(acc) * sa[i] * sw[j] (+ bias[j]).  acc may be NULL.
+ * K % 64 == 0, N % 16 == 0 (tile constraints), any M. */
+int tq_gemm_w8a8(const int8_t* qa, const float* sa, const int8_t* qw, const float* sw,
+                 const float* bias, int64_t m, int64_t n, int64_t k, int32_t* acc,
+                 float* y, tq_stream_t stream);
+
+/* Prefill-shaped W4A16: x bf16 [M, K], INT4 g128 weights, f32 accumulation with
+ * the group scale applied to each 128-long partial sum; y f32 [M, N].
+ * K % 128 == 0, N % 16 == 0. */
+int tq_gemm_w4g128_bf16(const uint16_t* x_bf16, int64_t m, const uint8_t* packed,
+                        const uint16_t* s_f16, const float* bias, int64_t n, int64_t k,
+                        float* y, tq_stream_t stream);
+
+/* Quantized Llama-style FFN (build-defined composition of Linear, SiLU
+ * (crates/theano-nn/src/activation.rs:66-79) and Tensor::mul):
+ *   h = SiLU(x Wg^T) * (x Wu^T)  kept in f32 (h_workspace, f32 [M, F]);
+ *   y = h Wd^T                   f32 [M, D].
+ * x bf16 [M, D]; gate/up INT4 g128 [F, D]; down INT4 g128 [D, F];
+ * D % 128 == 0, F % 128 == 0. */
+int tq_mlp_w4g128(const uint16_t* x_bf16, int64_t m, int64_t d, int64_t f,
+                  const uint8_t* gate_packed, const uint16_t* gate_s,
+                  const uint8_t* up_packed, const uint16_t* up_s,
+                  const uint8_t* down_packed, const uint16_t* down_s,
+                  float* h_workspace, float* y, tq_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* TQ_H */

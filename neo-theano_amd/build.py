@@ -1,0 +1,107 @@
+"""Builds libtq.so (HIP kernels + C ABI, gfx950 only) and the C++ host layer.
+
+Run as ``python neo-theano_amd/build.py`` or through ``__graft_entry__.build()``.
+Everything is compiled in-tree so that the shared objects travel with the
+source tree; nothing is installed.
+"""
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+from concurrent.futures import ThreadPoolExecutor
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(PKG)
+CSRC = os.path.join(PKG, "csrc")
+HOST = os.path.join(PKG, "host")
+OBJ = os.path.join(PKG, "_build")
+LIB = os.path.join(PKG, "libtq.so")
+HOSTLIB = os.path.join(PKG, "libtheano_quantize_rocm.so")
+
+ARCH = "gfx950"
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+
+HIP_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-Wall",
+    "-Wno-unused-function",
+    # packed f32 VALU forms are kept out of the generated code on this fleet
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    f"-I{os.path.join(ROOT, 'include')}",
+]
+
+SOURCES = ["tq_api.hip", "tq_quant.hip", "tq_gemv.hip", "tq_gemm.hip", "tq_mlp.hip"]
+
+
+def _run(cmd):
+    r = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    # hipcc's host pass warns that it does not know the packed-fp32 feature
+    out = "\n".join(l for l in r.stdout.splitlines() if "packed-fp32-ops" not in l)
+    if r.returncode != 0:
+        raise RuntimeError(f"build failed: {' '.join(cmd)}\n{out}")
+    return out
+
+
+def build_lib(verbose=False, jobs=8):
+    os.makedirs(OBJ, exist_ok=True)
+    srcs = [s for s in SOURCES if os.path.exists(os.path.join(CSRC, s))]
+
+    def compile_one(src):
+        obj = os.path.join(OBJ, src.replace(".hip", ".o"))
+        out = _run([HIPCC, *HIP_FLAGS, "-c", os.path.join(CSRC, src), "-o", obj])
+        if verbose and out.strip():
+            print(out)
+        return obj
+
+    with ThreadPoolExecutor(max_workers=jobs) as ex:
+        objs = list(ex.map(compile_one, srcs))
+    tmp = LIB + ".tmp"
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs])
+    os.replace(tmp, LIB)
+    return LIB
+
+
+def build_host(verbose=False):
+    """C++ host layer (theano_quantize mirror) over libtq.so."""
+    src = os.path.join(HOST, "theano_quantize.cpp")
+    if not os.path.exists(src):
+        return None
+    tmp = HOSTLIB + ".tmp"
+    out = _run([HIPCC, "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall",
+                f"-I{os.path.join(ROOT, 'include')}", f"-I{HOST}", src, "-o", tmp,
+                f"-L{PKG}", "-ltq", "-Wl,-rpath,$ORIGIN"])
+    if verbose and out.strip():
+        print(out)
+    os.replace(tmp, HOSTLIB)
+    return HOSTLIB
+
+
+def build_oracle():
+    """The C oracle (test infrastructure) -- compiled, never linked into libtq."""
+    odir = os.path.join(ROOT, "oracle")
+    out = os.path.join(odir, "libtq_oracle.so")
+    tmp = out + ".tmp"
+    _run(["gcc", "-O3", "-ffp-contract=off", "-fno-fast-math", "-fPIC", "-shared", "-std=c11",
+          "-Wall", "-Werror", os.path.join(odir, "tq_oracle.c"), "-o", tmp, "-lm"])
+    os.replace(tmp, out)
+    return out
+
+
+def build_all(verbose=False):
+    if shutil.which(HIPCC) is None and not os.path.exists(HIPCC):
+        raise RuntimeError(f"hipcc not found at {HIPCC}")
+    libs = [build_oracle(), build_lib(verbose=verbose)]
+    h = build_host(verbose=verbose)
+    if h:
+        libs.append(h)
+    return libs
+
+
+if __name__ == "__main__":
+    for p in build_all(verbose="-v" in sys.argv):
+        print("built", p)

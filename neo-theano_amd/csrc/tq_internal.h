@@ -1,0 +1,106 @@
+// tq_internal.h -- shared host/device helpers of libtq.so (gfx950 only).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+
+#include <cstdarg>
+#include <cstdint>
+#include <cstdio>
+
+#include "../../include/tq.h"
+
+namespace tq {
+
+// Native clang vectors (HIP's float4 & co. are structs, which the
+// nontemporal and bit-cast builtins do not accept).
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+
+// ---------------------------------------------------------------- host side
+
+// Records a thread-local error message and returns `status`.
+int fail(int status, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+void clear_error();
+
+inline hipStream_t as_hip(tq_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
+
+// Checks the launch that was just enqueued.
+int check_launch(const char* what);
+
+inline bool aligned(const void* p, uintptr_t a) {
+    return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0;
+}
+
+// Compute-unit count of the current device (cached per device).
+int device_cu_count();
+
+#define TQ_REQUIRE(cond, ...)                                 \
+    do {                                                      \
+        if (!(cond)) return ::tq::fail(TQ_EINVAL, __VA_ARGS__); \
+    } while (0)
+
+// -------------------------------------------------------------- device side
+
+constexpr int kWave = 64;
+
+// Wave64 butterfly reductions (DPP / ds_swizzle via __shfl_xor).
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+    return v;
+}
+
+__device__ __forceinline__ float wave_min(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fminf(v, __shfl_xor(v, o, kWave));
+    return v;
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+    return v;
+}
+
+// Max over aligned groups of `width` lanes (width a power of two <= 64).
+template <int kWidth>
+__device__ __forceinline__ float group_max(float v) {
+#pragma unroll
+    for (int o = kWidth / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+    return v;
+}
+
+// round_half_away_from_zero(a / s) for a >= 0 (or +inf), s > 0 finite normal,
+// exact with respect to the real quotient (the reference rounds the f64
+// quotient, which lies on the same side of every half-integer as the exact
+// one).  `inv_s` is any approximation of 1/s good to a few ulp; `cap` is an
+// integer-valued float <= 2^22: quotients above it come back as cap or cap+1,
+// which every caller clamps.  NaN `a` is the caller's business.
+//
+// Why it is exact: n0 = floor(min(a*inv_s, cap) + 1/2) is within one of the
+// true n.  The residual r = fma(-n0, s, a) = a - n0*s is exact whenever
+// |a - n0*s| <= s (it is a multiple of ulp(s)/2 below 2^24 of them), so the
+// tests r >= s/2 and r < -s/2 against the exact half-way points are exact;
+// when |a - n0*s| > s the rounded r is still on the correct side.
+__device__ __forceinline__ float rhaz_div(float a, float s, float inv_s, float half_s,
+                                          float cap) {
+    const float t = fminf(a * inv_s, cap);
+    float n = floorf(t + 0.5f);
+    const float r = fmaf(-n, s, a);
+    n = (r >= half_s) ? n + 1.0f : n;
+    n = (r < -half_s) ? n - 1.0f : n;
+    return n;
+}
+
+// Signed code for x given |x|'s rounded quotient n: NaN -> 0, sign from x,
+// clamp to [qmin, qmax].
+__device__ __forceinline__ int signed_code(float x, float n, int qmin, int qmax) {
+    n = (x == x) ? n : 0.0f;
+    int c = static_cast<int>(n);  // n is integral, 0 <= n <= cap + 1
+    c = (x < 0.0f) ? -c : c;
+    return min(max(c, qmin), qmax);
+}
+
+}  // namespace tq

@@ -1,0 +1,592 @@
+// tq_quant.hip -- quantize / dequantize kernels for gfx950 and their C ABI.
+//
+// Reference semantics: crates/theano-quantize/src/quantize.rs:8-55 and
+// observer.rs:42-136 (f64, round half away from zero, clamp).  The hot
+// formats (per-row INT8, INT4 group-128) use an exact f32 rounding (rhaz_div)
+// instead of f64 division; the generic primitives compute in f64 directly.
+//
+// All kernels are HBM-bound streams: each lane moves 16-byte vectors, rows or
+// groups are reduced with wave64 butterflies, and codes are packed in
+// registers before one coalesced store.
+#include <cmath>
+
+#include "tq_internal.h"
+
+#pragma clang fp contract(off)
+
+namespace tq {
+namespace {
+
+constexpr int kBlock = 256;
+constexpr int kWavesPerBlock = kBlock / kWave;
+
+// Block-wide max of a per-thread value (NaN-free inputs), result in every thread.
+__device__ __forceinline__ float block_max(float v, float* red) {
+    v = wave_max(v);
+    const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
+    if (lane == 0) red[wid] = v;
+    __syncthreads();
+    float r = red[0];
+#pragma unroll
+    for (int i = 1; i < kWavesPerBlock; ++i) r = fmaxf(r, red[i]);
+    return r;
+}
+
+__device__ __forceinline__ float block_min(float v, float* red) {
+    v = wave_min(v);
+    const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
+    if (lane == 0) red[wid] = v;
+    __syncthreads();
+    float r = red[0];
+#pragma unroll
+    for (int i = 1; i < kWavesPerBlock; ++i) r = fminf(r, red[i]);
+    return r;
+}
+
+// Symmetric absmax from a NaN-ignoring fold of |x| started at -inf: a row with
+// no non-NaN value folds to -inf, which the observer form
+// max(|min|, |max|) with min=+inf, max=-inf turns into +inf.
+__device__ __forceinline__ float absmax_finish(float m) { return (m == -INFINITY) ? INFINITY : m; }
+
+// s = f32(max(absmax / 127, 1e-10)), division in f64 (correctly rounded).
+__device__ __forceinline__ float scale_i8(float absmax) {
+    return static_cast<float>(fmax(static_cast<double>(absmax) / 127.0, 1e-10));
+}
+
+// INT8 code of x for scale s (finite, > 0).
+__device__ __forceinline__ int code_i8(float x, float s, float inv_s, float half_s) {
+    const float n = rhaz_div(fabsf(x), s, inv_s, half_s, 256.0f);
+    return signed_code(x, n, -128, 127);
+}
+
+__device__ __forceinline__ uint32_t pack4_i8(int a, int b, int c, int d) {
+    return (uint32_t)(a & 0xFF) | ((uint32_t)(b & 0xFF) << 8) | ((uint32_t)(c & 0xFF) << 16) |
+           ((uint32_t)(d & 0xFF) << 24);
+}
+
+// ---- per-row INT8, register-cached row (K % 4 == 0, K <= 1024 * kItems) ----
+// One 256-thread block per row; each thread holds kItems f32x4 of the row.
+template <int kItems>
+__global__ __launch_bounds__(kBlock) void k_quant_i8_rows_vec(const float* __restrict__ w,
+                                                              int64_t k,
+                                                              int8_t* __restrict__ q,
+                                                              float* __restrict__ s,
+                                                              float* __restrict__ w_hat) {
+    __shared__ float red[kWavesPerBlock];
+    const int64_t row = blockIdx.x;
+    const int k4 = static_cast<int>(k >> 2);
+    const f32x4* src = reinterpret_cast<const f32x4*>(w + row * k);
+    f32x4 v[kItems];
+    float m = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < kItems; ++i) {
+        const int idx = threadIdx.x + i * kBlock;
+        if (idx < k4) {
+            v[i] = __builtin_nontemporal_load(src + idx);
+            m = fmaxf(m, fmaxf(fmaxf(fabsf(v[i].x), fabsf(v[i].y)), fmaxf(fabsf(v[i].z), fabsf(v[i].w))));
+        }
+    }
+    const float sc = scale_i8(absmax_finish(block_max(m, red)));
+    if (threadIdx.x == 0) s[row] = sc;
+    const bool finite = sc < INFINITY;  // row-uniform: an infinite scale gives all-zero codes
+    const float inv = 1.0f / sc, half = 0.5f * sc;
+    uint32_t* qd = reinterpret_cast<uint32_t*>(q + row * k);
+    f32x4* wd = reinterpret_cast<f32x4*>(w_hat + row * k);
+#pragma unroll
+    for (int i = 0; i < kItems; ++i) {
+        const int idx = threadIdx.x + i * kBlock;
+        if (idx < k4) {
+            int c0 = 0, c1 = 0, c2 = 0, c3 = 0;
+            if (finite) {
+                c0 = code_i8(v[i].x, sc, inv, half);
+                c1 = code_i8(v[i].y, sc, inv, half);
+                c2 = code_i8(v[i].z, sc, inv, half);
+                c3 = code_i8(v[i].w, sc, inv, half);
+            }
+            if (q) qd[idx] = pack4_i8(c0, c1, c2, c3);
+            if (w_hat) {
+                f32x4 o;
+                o.x = static_cast<float>(c0) * sc;
+                o.y = static_cast<float>(c1) * sc;
+                o.z = static_cast<float>(c2) * sc;
+                o.w = static_cast<float>(c3) * sc;
+                wd[idx] = o;
+            }
+        }
+    }
+}
+
+// ---- per-row INT8, any K / alignment: two passes over the row ----
+__global__ __launch_bounds__(kBlock) void k_quant_i8_rows_generic(const float* __restrict__ w,
+                                                                  int64_t k,
+                                                                  int8_t* __restrict__ q,
+                                                                  float* __restrict__ s,
+                                                                  float* __restrict__ w_hat) {
+    __shared__ float red[kWavesPerBlock];
+    const int64_t row = blockIdx.x;
+    const float* src = w + row * k;
+    float m = -INFINITY;
+    for (int64_t i = threadIdx.x; i < k; i += kBlock) m = fmaxf(m, fabsf(src[i]));
+    const float sc = scale_i8(absmax_finish(block_max(m, red)));
+    if (threadIdx.x == 0) s[row] = sc;
+    const bool finite = sc < INFINITY;
+    const float inv = 1.0f / sc, half = 0.5f * sc;
+    for (int64_t i = threadIdx.x; i < k; i += kBlock) {
+        const int c = finite ? code_i8(src[i], sc, inv, half) : 0;
+        if (q) q[row * k + i] = static_cast<int8_t>(c);
+        if (w_hat) w_hat[row * k + i] = static_cast<float>(c) * sc;
+    }
+}
+
+// ---- per-row INT8 dequant: w_hat = f32(q * s[row]) ----
+// Vector form: 16 codes per thread (K % 16 == 0, aligned).
+__global__ __launch_bounds__(kBlock) void k_dequant_i8_rows_vec(const int8_t* __restrict__ q,
+                                                                const float* __restrict__ s,
+                                                                int64_t k, int64_t n16,
+                                                                float* __restrict__ w_hat) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+    if (i >= n16) return;
+    const int64_t row = (i * 16) / k;
+    const float sc = s[row];
+    const i32x4 c = __builtin_nontemporal_load(reinterpret_cast<const i32x4*>(q) + i);
+    const int words[4] = {c.x, c.y, c.z, c.w};
+    f32x4* dst = reinterpret_cast<f32x4*>(w_hat) + i * 4;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int wv = words[j];
+        f32x4 o;
+        o.x = static_cast<float>(static_cast<int8_t>(wv & 0xFF)) * sc;
+        o.y = static_cast<float>(static_cast<int8_t>((wv >> 8) & 0xFF)) * sc;
+        o.z = static_cast<float>(static_cast<int8_t>((wv >> 16) & 0xFF)) * sc;
+        o.w = static_cast<float>(static_cast<int8_t>((wv >> 24) & 0xFF)) * sc;
+        dst[j] = o;
+    }
+}
+
+__global__ __launch_bounds__(kBlock) void k_dequant_i8_rows_generic(const int8_t* __restrict__ q,
+                                                                    const float* __restrict__ s,
+                                                                    int64_t k, int64_t total,
+                                                                    float* __restrict__ w_hat) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+    if (i >= total) return;
+    w_hat[i] = static_cast<float>(q[i]) * s[i / k];
+}
+
+// ---- INT4 group-128: 16 lanes per group, 8 consecutive elements per lane ----
+__device__ __forceinline__ uint16_t scale_i4_bits(float absmax) {
+    const float sf = static_cast<float>(static_cast<double>(absmax) / 7.0);
+    uint16_t h = __half_as_ushort(__float2half_rn(sf));
+    return h == 0 ? uint16_t(1) : h;  // floor at 2^-24, the smallest positive f16
+}
+
+__global__ __launch_bounds__(kBlock) void k_quant_i4_g128(const float* __restrict__ w,
+                                                          int64_t groups,
+                                                          uint8_t* __restrict__ packed,
+                                                          uint16_t* __restrict__ s16,
+                                                          float* __restrict__ w_hat) {
+    const int64_t slot = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+    const int64_t g = slot >> 4;
+    const bool valid = g < groups;
+    float x[8];
+    float m = -INFINITY;
+    if (valid) {
+        const f32x4* p = reinterpret_cast<const f32x4*>(w) + slot * 2;
+        const f32x4 a = __builtin_nontemporal_load(p);
+        const f32x4 b = __builtin_nontemporal_load(p + 1);
+        x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
+        x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) m = fmaxf(m, fabsf(x[i]));
+    }
+    m = group_max<16>(m);  // all 16 lanes of a group are valid or invalid together
+    if (!valid) return;
+    const uint16_t hb = scale_i4_bits(absmax_finish(m));
+    const float sc = __half2float(__ushort_as_half(hb));
+    if ((threadIdx.x & 15) == 0) s16[g] = hb;
+    int c[8];
+    if (sc < INFINITY) {
+        const float inv = 1.0f / sc, half = 0.5f * sc;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) c[i] = signed_code(x[i], rhaz_div(fabsf(x[i]), sc, inv, half, 32.0f), -8, 7);
+    } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) c[i] = 0;
+    }
+    if (packed) {
+        uint32_t word = 0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) word |= static_cast<uint32_t>(c[i] & 0xF) << (4 * i);
+        reinterpret_cast<uint32_t*>(packed)[slot] = word;
+    }
+    if (w_hat) {
+        f32x4* d = reinterpret_cast<f32x4*>(w_hat) + slot * 2;
+        d[0] = f32x4{c[0] * sc, c[1] * sc, c[2] * sc, c[3] * sc};
+        d[1] = f32x4{c[4] * sc, c[5] * sc, c[6] * sc, c[7] * sc};
+    }
+}
+
+// 8 codes (one packed dword) per thread.
+__global__ __launch_bounds__(kBlock) void k_dequant_i4_g128(const uint8_t* __restrict__ packed,
+                                                            const uint16_t* __restrict__ s16,
+                                                            int64_t slots,
+                                                            float* __restrict__ w_hat) {
+    const int64_t slot = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+    if (slot >= slots) return;
+    const float sc = __half2float(__ushort_as_half(s16[slot >> 4]));
+    const uint32_t word = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(packed) + slot);
+    float o[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int nib = static_cast<int>((word >> (4 * i)) & 0xF);
+        o[i] = static_cast<float>(nib >= 8 ? nib - 16 : nib) * sc;
+    }
+    f32x4* d = reinterpret_cast<f32x4*>(w_hat) + slot * 2;
+    d[0] = f32x4{o[0], o[1], o[2], o[3]};
+    d[1] = f32x4{o[4], o[5], o[6], o[7]};
+}
+
+// ---- generic reference primitives, f64 arithmetic ----
+// Rust f64::clamp: keeps NaN (comparisons with NaN are false).
+__device__ __forceinline__ double rust_clamp(double v, double lo, double hi) {
+    v = (v < lo) ? lo : v;
+    v = (v > hi) ? hi : v;
+    return v;
+}
+
+__global__ __launch_bounds__(kBlock) void k_quantize_tensor(const float* __restrict__ x, int64_t n,
+                                                            double scale, double zp, double qmin,
+                                                            double qmax, float* __restrict__ q) {
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlock;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; i < n; i += stride)
+        q[i] = static_cast<float>(rust_clamp(round(static_cast<double>(x[i]) / scale + zp), qmin, qmax));
+}
+
+__global__ __launch_bounds__(kBlock) void k_dequantize_tensor(const float* __restrict__ q, int64_t n,
+                                                              double scale, double zp,
+                                                              float* __restrict__ out) {
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlock;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; i < n; i += stride)
+        out[i] = static_cast<float>((static_cast<double>(q[i]) - zp) * scale);
+}
+
+__global__ __launch_bounds__(kBlock) void k_fake_quantize(const float* __restrict__ x, int64_t n,
+                                                          double scale, double zp, double qmin,
+                                                          double qmax, float* __restrict__ out) {
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlock;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; i < n; i += stride) {
+        const double c = rust_clamp(round(static_cast<double>(x[i]) / scale + zp), qmin, qmax);
+        out[i] = static_cast<float>((c - zp) * scale);
+    }
+}
+
+// Order-preserving int keys for non-NaN floats (atomic min/max on ints).
+__device__ __forceinline__ int float_key(float f) {
+    const int b = __float_as_int(f);
+    return b >= 0 ? b : b ^ 0x7FFFFFFF;
+}
+__device__ __forceinline__ float key_float(int k) { return __int_as_float(k >= 0 ? k : k ^ 0x7FFFFFFF); }
+
+// workspace layout for quantize_per_tensor: int keys {min, max}
+__global__ void k_per_tensor_init(int* ws) {
+    if (threadIdx.x == 0) {
+        ws[0] = float_key(INFINITY);
+        ws[1] = float_key(-INFINITY);
+    }
+}
+
+// NaN-ignoring min/max of x folded into int keys (one atomic pair per block).
+__global__ __launch_bounds__(kBlock) void k_minmax_keys(const float* __restrict__ x, int64_t n,
+                                                        int* ws) {
+    __shared__ float red[kWavesPerBlock];
+    float mn = INFINITY, mx = -INFINITY;
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlock;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; i < n; i += stride) {
+        const float v = x[i];
+        mn = fminf(mn, v);
+        mx = fmaxf(mx, v);
+    }
+    mn = block_min(mn, red);
+    __syncthreads();
+    mx = block_max(mx, red);
+    if (threadIdx.x == 0) {
+        atomicMin(ws, float_key(mn));
+        atomicMax(ws + 1, float_key(mx));
+    }
+}
+
+// quantize.rs:33-40: scale = max((max-min)/(qmax-qmin), 1e-10), zp = clamp(round(qmin - min/scale))
+__device__ __forceinline__ void per_tensor_params(const int* ws, double qmin, double qmax,
+                                                  double* scale, double* zp) {
+    const double mn = static_cast<double>(key_float(ws[0]));
+    const double mx = static_cast<double>(key_float(ws[1]));
+    const double s = fmax((mx - mn) / (qmax - qmin), 1e-10);
+    *scale = s;
+    *zp = rust_clamp(round(qmin - mn / s), qmin, qmax);
+}
+
+__global__ __launch_bounds__(kBlock) void k_per_tensor_quantize(const float* __restrict__ x,
+                                                                int64_t n, const int* ws,
+                                                                double qmin, double qmax,
+                                                                float* __restrict__ q,
+                                                                double* scale_zp) {
+    double s, zp;
+    per_tensor_params(ws, qmin, qmax, &s, &zp);
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+        scale_zp[0] = s;
+        scale_zp[1] = zp;
+    }
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlock;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; i < n; i += stride)
+        q[i] = static_cast<float>(rust_clamp(round(static_cast<double>(x[i]) / s + zp), qmin, qmax));
+}
+
+// ---- observers: state = channels x {min, max} floats ----
+__global__ void k_minmax_reset(float* state, int64_t channels) {
+    const int64_t c = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+    if (c < channels) {
+        state[2 * c] = INFINITY;
+        state[2 * c + 1] = -INFINITY;
+    }
+}
+
+// Folds the per-tensor min/max into state[0..1] with CAS loops (one per block).
+__device__ void atomic_fold_min(float* addr, float v) {
+    unsigned int* a = reinterpret_cast<unsigned int*>(addr);
+    unsigned int old = __atomic_load_n(a, __ATOMIC_RELAXED);
+    while (v < __uint_as_float(old)) {
+        const unsigned int prev = atomicCAS(a, old, __float_as_uint(v));
+        if (prev == old) break;
+        old = prev;
+    }
+}
+
+__device__ void atomic_fold_max(float* addr, float v) {
+    unsigned int* a = reinterpret_cast<unsigned int*>(addr);
+    unsigned int old = __atomic_load_n(a, __ATOMIC_RELAXED);
+    while (v > __uint_as_float(old)) {
+        const unsigned int prev = atomicCAS(a, old, __float_as_uint(v));
+        if (prev == old) break;
+        old = prev;
+    }
+}
+
+__global__ __launch_bounds__(kBlock) void k_minmax_observe(const float* __restrict__ x, int64_t n,
+                                                           float* state) {
+    __shared__ float red[kWavesPerBlock];
+    float mn = INFINITY, mx = -INFINITY;
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlock;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; i < n; i += stride) {
+        const float v = x[i];
+        mn = fminf(mn, v);
+        mx = fmaxf(mx, v);
+    }
+    mn = block_min(mn, red);
+    __syncthreads();
+    mx = block_max(mx, red);
+    if (threadIdx.x == 0) {
+        atomic_fold_min(state, mn);
+        atomic_fold_max(state + 1, mx);
+    }
+}
+
+// One block per channel; channel c covers x[c*per, (c+1)*per).
+__global__ __launch_bounds__(kBlock) void k_minmax_observe_per_channel(const float* __restrict__ x,
+                                                                       int64_t per, float* state) {
+    __shared__ float red[kWavesPerBlock];
+    const int64_t c = blockIdx.x;
+    const float* src = x + c * per;
+    float mn = INFINITY, mx = -INFINITY;
+    for (int64_t i = threadIdx.x; i < per; i += kBlock) {
+        const float v = src[i];
+        mn = fminf(mn, v);
+        mx = fmaxf(mx, v);
+    }
+    mn = block_min(mn, red);
+    __syncthreads();
+    mx = block_max(mx, red);
+    if (threadIdx.x == 0) {
+        state[2 * c] = fminf(state[2 * c], mn);
+        state[2 * c + 1] = fmaxf(state[2 * c + 1], mx);
+    }
+}
+
+int grid_for(int64_t n, int64_t per_block, int64_t cap) {
+    int64_t g = (n + per_block - 1) / per_block;
+    if (g > cap) g = cap;
+    return static_cast<int>(g < 1 ? 1 : g);
+}
+
+int qrange(int qdtype, double* qmin, double* qmax) {
+    return tq_qdtype_info(qdtype, nullptr, nullptr, qmin, qmax);
+}
+
+int launch_quant_i8_rows(const float* w, int64_t rows, int64_t k, int8_t* q, float* s,
+                         float* w_hat, hipStream_t st, const char* what) {
+    TQ_REQUIRE(rows >= 0 && k >= 0, "%s: negative shape [%lld, %lld]", what, (long long)rows,
+               (long long)k);
+    TQ_REQUIRE(rows < (int64_t(1) << 31), "%s: too many rows (%lld)", what, (long long)rows);
+    if (rows == 0) return TQ_OK;
+    TQ_REQUIRE(w && s, "%s: null pointer", what);
+    const bool vec = (k % 16 == 0) && k > 0 && k <= 16384 && aligned(w, 16) &&
+                     (!q || aligned(q, 4)) && (!w_hat || aligned(w_hat, 16));
+    const dim3 grid(static_cast<unsigned>(rows)), block(kBlock);
+    if (vec) {
+        const int64_t items = (k / 4 + kBlock - 1) / kBlock;
+        if (items <= 1) k_quant_i8_rows_vec<1><<<grid, block, 0, st>>>(w, k, q, s, w_hat);
+        else if (items <= 2) k_quant_i8_rows_vec<2><<<grid, block, 0, st>>>(w, k, q, s, w_hat);
+        else if (items <= 4) k_quant_i8_rows_vec<4><<<grid, block, 0, st>>>(w, k, q, s, w_hat);
+        else if (items <= 8) k_quant_i8_rows_vec<8><<<grid, block, 0, st>>>(w, k, q, s, w_hat);
+        else k_quant_i8_rows_vec<16><<<grid, block, 0, st>>>(w, k, q, s, w_hat);
+    } else {
+        k_quant_i8_rows_generic<<<grid, block, 0, st>>>(w, k, q, s, w_hat);
+    }
+    return check_launch(what);
+}
+
+}  // namespace
+}  // namespace tq
+
+using namespace tq;
+
+extern "C" {
+
+int tq_quantize_i8_rowwise(const float* w, int64_t rows, int64_t k, int8_t* q, float* s,
+                           tq_stream_t stream) {
+    if (rows > 0 && k > 0 && !q) return fail(TQ_EINVAL, "tq_quantize_i8_rowwise: null q");
+    return launch_quant_i8_rows(w, rows, k, q, s, nullptr, as_hip(stream), "tq_quantize_i8_rowwise");
+}
+
+int tq_fake_quantize_i8_rowwise(const float* w, int64_t rows, int64_t k, int8_t* q, float* s,
+                                float* w_hat, tq_stream_t stream) {
+    if (rows > 0 && k > 0 && (!q || !w_hat))
+        return fail(TQ_EINVAL, "tq_fake_quantize_i8_rowwise: null output");
+    return launch_quant_i8_rows(w, rows, k, q, s, w_hat, as_hip(stream), "tq_fake_quantize_i8_rowwise");
+}
+
+int tq_dequantize_i8_rowwise(const int8_t* q, const float* s, int64_t rows, int64_t k,
+                             float* w_hat, tq_stream_t stream) {
+    TQ_REQUIRE(rows >= 0 && k >= 0, "tq_dequantize_i8_rowwise: negative shape");
+    const int64_t total = rows * k;
+    if (total == 0) return TQ_OK;
+    TQ_REQUIRE(q && s && w_hat, "tq_dequantize_i8_rowwise: null pointer");
+    const hipStream_t st = as_hip(stream);
+    if (k % 16 == 0 && aligned(q, 16) && aligned(w_hat, 16)) {
+        const int64_t n16 = total / 16;
+        k_dequant_i8_rows_vec<<<grid_for(n16, kBlock, INT32_MAX), kBlock, 0, st>>>(q, s, k, n16, w_hat);
+    } else {
+        k_dequant_i8_rows_generic<<<grid_for(total, kBlock, INT32_MAX), kBlock, 0, st>>>(q, s, k, total, w_hat);
+    }
+    return check_launch("tq_dequantize_i8_rowwise");
+}
+
+int tq_quantize_i4_g128(const float* w, int64_t rows, int64_t k, uint8_t* packed,
+                        uint16_t* s_f16, tq_stream_t stream) {
+    TQ_REQUIRE(rows >= 0 && k >= 0, "tq_quantize_i4_g128: negative shape");
+    TQ_REQUIRE(k % 128 == 0, "tq_quantize_i4_g128: K=%lld is not a multiple of the group size 128",
+               (long long)k);
+    const int64_t groups = rows * (k / 128);
+    if (groups == 0) return TQ_OK;
+    TQ_REQUIRE(w && packed && s_f16, "tq_quantize_i4_g128: null pointer");
+    TQ_REQUIRE(aligned(w, 16) && aligned(packed, 4) && aligned(s_f16, 2),
+               "tq_quantize_i4_g128: misaligned pointer (W 16 B, packed 4 B, scales 2 B)");
+    k_quant_i4_g128<<<grid_for(groups * 16, kBlock, INT32_MAX), kBlock, 0, as_hip(stream)>>>(
+        w, groups, packed, s_f16, nullptr);
+    return check_launch("tq_quantize_i4_g128");
+}
+
+int tq_dequantize_i4_g128(const uint8_t* packed, const uint16_t* s_f16, int64_t rows, int64_t k,
+                          float* w_hat, tq_stream_t stream) {
+    TQ_REQUIRE(rows >= 0 && k >= 0, "tq_dequantize_i4_g128: negative shape");
+    TQ_REQUIRE(k % 128 == 0, "tq_dequantize_i4_g128: K=%lld is not a multiple of 128", (long long)k);
+    const int64_t slots = rows * (k / 8);
+    if (slots == 0) return TQ_OK;
+    TQ_REQUIRE(packed && s_f16 && w_hat, "tq_dequantize_i4_g128: null pointer");
+    TQ_REQUIRE(aligned(packed, 4) && aligned(w_hat, 16) && aligned(s_f16, 2),
+               "tq_dequantize_i4_g128: misaligned pointer (packed 4 B, W_hat 16 B)");
+    k_dequant_i4_g128<<<grid_for(slots, kBlock, INT32_MAX), kBlock, 0, as_hip(stream)>>>(
+        packed, s_f16, slots, w_hat);
+    return check_launch("tq_dequantize_i4_g128");
+}
+
+int tq_quantize_tensor(const float* x, int64_t n, double scale, double zero_point, int qdtype,
+                       float* q, tq_stream_t stream) {
+    double qmin, qmax;
+    const int st = qrange(qdtype, &qmin, &qmax);
+    if (st != TQ_OK) return st;
+    TQ_REQUIRE(n >= 0, "tq_quantize_tensor: negative size");
+    if (n == 0) return TQ_OK;
+    TQ_REQUIRE(x && q, "tq_quantize_tensor: null pointer");
+    k_quantize_tensor<<<grid_for(n, kBlock, 65536), kBlock, 0, as_hip(stream)>>>(x, n, scale, zero_point,
+                                                                                 qmin, qmax, q);
+    return check_launch("tq_quantize_tensor");
+}
+
+int tq_dequantize_tensor(const float* q, int64_t n, double scale, double zero_point, float* out,
+                         tq_stream_t stream) {
+    TQ_REQUIRE(n >= 0, "tq_dequantize_tensor: negative size");
+    if (n == 0) return TQ_OK;
+    TQ_REQUIRE(q && out, "tq_dequantize_tensor: null pointer");
+    k_dequantize_tensor<<<grid_for(n, kBlock, 65536), kBlock, 0, as_hip(stream)>>>(q, n, scale, zero_point,
+                                                                                   out);
+    return check_launch("tq_dequantize_tensor");
+}
+
+int tq_fake_quantize(const float* x, int64_t n, double scale, double zero_point, int qdtype,
+                     float* out, tq_stream_t stream) {
+    double qmin, qmax;
+    const int st = qrange(qdtype, &qmin, &qmax);
+    if (st != TQ_OK) return st;
+    TQ_REQUIRE(n >= 0, "tq_fake_quantize: negative size");
+    if (n == 0) return TQ_OK;
+    TQ_REQUIRE(x && out, "tq_fake_quantize: null pointer");
+    k_fake_quantize<<<grid_for(n, kBlock, 65536), kBlock, 0, as_hip(stream)>>>(x, n, scale, zero_point,
+                                                                               qmin, qmax, out);
+    return check_launch("tq_fake_quantize");
+}
+
+int tq_quantize_per_tensor(const float* x, int64_t n, int qdtype, float* q, double* scale_zp,
+                           void* workspace, tq_stream_t stream) {
+    double qmin, qmax;
+    const int st = qrange(qdtype, &qmin, &qmax);
+    if (st != TQ_OK) return st;
+    TQ_REQUIRE(n >= 0, "tq_quantize_per_tensor: negative size");
+    TQ_REQUIRE(scale_zp && workspace, "tq_quantize_per_tensor: null scale_zp/workspace");
+    TQ_REQUIRE(n == 0 || (x && q), "tq_quantize_per_tensor: null pointer");
+    TQ_REQUIRE(aligned(workspace, 16) && aligned(scale_zp, 8),
+               "tq_quantize_per_tensor: misaligned workspace/scale_zp");
+    const hipStream_t s = as_hip(stream);
+    int* ws = static_cast<int*>(workspace);
+    k_per_tensor_init<<<1, kWave, 0, s>>>(ws);
+    if (n > 0) k_minmax_keys<<<grid_for(n, kBlock * 8, 4096), kBlock, 0, s>>>(x, n, ws);
+    k_per_tensor_quantize<<<grid_for(n, kBlock, 65536), kBlock, 0, s>>>(x, n, ws, qmin, qmax, q,
+                                                                        scale_zp);
+    return check_launch("tq_quantize_per_tensor");
+}
+
+int tq_minmax_reset(float* state, int64_t channels, tq_stream_t stream) {
+    TQ_REQUIRE(state && channels > 0, "tq_minmax_reset: null state or channels <= 0");
+    k_minmax_reset<<<grid_for(channels, kBlock, INT32_MAX), kBlock, 0, as_hip(stream)>>>(state, channels);
+    return check_launch("tq_minmax_reset");
+}
+
+int tq_minmax_observe(const float* x, int64_t n, float* state, tq_stream_t stream) {
+    TQ_REQUIRE(n >= 0 && state, "tq_minmax_observe: bad arguments");
+    if (n == 0) return TQ_OK;
+    TQ_REQUIRE(x && aligned(state, 4), "tq_minmax_observe: null/misaligned pointer");
+    k_minmax_observe<<<grid_for(n, kBlock * 8, 4096), kBlock, 0, as_hip(stream)>>>(x, n, state);
+    return check_launch("tq_minmax_observe");
+}
+
+int tq_minmax_observe_per_channel(const float* x, int64_t n, int64_t channels, float* state,
+                                  tq_stream_t stream) {
+    TQ_REQUIRE(n >= 0 && channels > 0 && state, "tq_minmax_observe_per_channel: bad arguments");
+    TQ_REQUIRE(channels < (int64_t(1) << 31), "tq_minmax_observe_per_channel: too many channels");
+    const int64_t per = n / channels;
+    if (per == 0) return TQ_OK;
+    TQ_REQUIRE(x, "tq_minmax_observe_per_channel: null input");
+    k_minmax_observe_per_channel<<<static_cast<unsigned>(channels), kBlock, 0, as_hip(stream)>>>(x, per,
+                                                                                               state);
+    return check_launch("tq_minmax_observe_per_channel");
+}
+
+}  // extern "C"

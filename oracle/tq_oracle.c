@@ -1,0 +1,394 @@
+/*
+ * tq_oracle.c -- CPU restatement of neo-theano's quantized-inference path.
+ *
+ * TEST INFRASTRUCTURE ONLY: the parity checker for libtq.so (see tq_oracle.h
+ * for who may use it and how each function is pinned).  Compile with
+ * -O2 -ffp-contract=off and without -ffast-math so that every double
+ * operation rounds exactly like the reference's Rust f64 code.
+ *
+ * Citations are relative to the reference repository root.
+ */
+#include "tq_oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* ---- QuantDType ranges: crates/theano-quantize/src/qconfig.rs:12-41 ---- */
+
+int tqo_bits(int dtype) { return dtype == TQO_INT4 ? 4 : 8; }
+
+int tqo_is_signed(int dtype) { return dtype == TQO_INT8 || dtype == TQO_INT4; }
+
+double tqo_qmin(int dtype) {
+    switch (dtype) {
+    case TQO_INT8: return -128.0;
+    case TQO_UINT8: return 0.0;
+    case TQO_INT4: return -8.0;
+    default: return -448.0; /* FP8: range only, no encoding */
+    }
+}
+
+double tqo_qmax(int dtype) {
+    switch (dtype) {
+    case TQO_INT8: return 127.0;
+    case TQO_UINT8: return 255.0;
+    case TQO_INT4: return 7.0;
+    default: return 448.0;
+    }
+}
+
+/* Rust f64::clamp: below min -> min, above max -> max, NaN passes through. */
+static double rust_clamp(double x, double lo, double hi) {
+    if (x < lo) x = lo;
+    if (x > hi) x = hi;
+    return x;
+}
+
+/* Rust `f64 as i8/i32`: NaN -> 0, otherwise truncate and saturate. */
+static int32_t rust_as_int(double x, double lo, double hi) {
+    if (x != x) return 0;
+    if (x < lo) return (int32_t)lo;
+    if (x > hi) return (int32_t)hi;
+    return (int32_t)x;
+}
+
+/* ---- quantize.rs:8-19 quantize_tensor: q = round(x/scale + zp).clamp(qmin, qmax) ---- */
+void tqo_quantize_tensor(const double* x, int64_t n, double scale, double zero_point,
+                         int dtype, double* q) {
+    const double qmin = tqo_qmin(dtype), qmax = tqo_qmax(dtype);
+    for (int64_t i = 0; i < n; ++i)
+        q[i] = rust_clamp(round(x[i] / scale + zero_point), qmin, qmax);
+}
+
+/* ---- quantize.rs:22-27 dequantize_tensor: x = (q - zp) * scale ---- */
+void tqo_dequantize_tensor(const double* q, int64_t n, double scale, double zero_point,
+                           double* out) {
+    for (int64_t i = 0; i < n; ++i) out[i] = (q[i] - zero_point) * scale;
+}
+
+/* ---- quantize.rs:30-48 quantize_per_tensor (asymmetric, stats from the data) ---- */
+void tqo_quantize_per_tensor(const double* x, int64_t n, int dtype, double* q,
+                             double* scale_out, double* zp_out) {
+    double mn = INFINITY, mx = -INFINITY;
+    for (int64_t i = 0; i < n; ++i) mn = fmin(mn, x[i]);
+    for (int64_t i = 0; i < n; ++i) mx = fmax(mx, x[i]);
+    const double qmin = tqo_qmin(dtype), qmax = tqo_qmax(dtype);
+    const double scale = fmax((mx - mn) / (qmax - qmin), 1e-10);
+    const double zp = rust_clamp(round(qmin - mn / scale), qmin, qmax);
+    for (int64_t i = 0; i < n; ++i) q[i] = rust_clamp(round(x[i] / scale + zp), qmin, qmax);
+    *scale_out = scale;
+    *zp_out = zp;
+}
+
+/* ---- quantize.rs:51-55 fake_quantize = dequantize(quantize(x)) ---- */
+void tqo_fake_quantize(const double* x, int64_t n, double scale, double zero_point,
+                       int dtype, double* out) {
+    tqo_quantize_tensor(x, n, scale, zero_point, dtype, out);
+    tqo_dequantize_tensor(out, n, scale, zero_point, out);
+}
+
+/* ---- observer.rs:42-73 MinMaxObserver ---- */
+void tqo_minmax_observe(double* st, const double* values, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) {
+        st[0] = fmin(st[0], values[i]);
+        st[1] = fmax(st[1], values[i]);
+    }
+    st[2] = 1.0;
+}
+
+static void scale_zp_from_range(double mn, double mx, int dtype, double* scale, double* zp) {
+    const double qmin = tqo_qmin(dtype), qmax = tqo_qmax(dtype);
+    double s = (mx - mn) / (qmax - qmin);
+    s = fmax(s, 1e-10);
+    double z = qmin - mn / s;
+    *scale = s;
+    *zp = rust_clamp(round(z), qmin, qmax);
+}
+
+void tqo_minmax_scale_zp(const double* st, int dtype, double* scale, double* zp) {
+    if (st[2] == 0.0) {
+        *scale = 1.0;
+        *zp = 0.0;
+        return;
+    }
+    scale_zp_from_range(st[0], st[1], dtype, scale, zp);
+}
+
+/* ---- observer.rs:93-136 PerChannelMinMaxObserver (layout [channels, ...]) ---- */
+void tqo_perchannel_observe(double* mins, double* maxs, int64_t channels,
+                            const double* values, int64_t n) {
+    const int64_t per = n / channels;
+    for (int64_t c = 0; c < channels; ++c)
+        for (int64_t i = 0; i < per; ++i) {
+            const double v = values[c * per + i];
+            mins[c] = fmin(mins[c], v);
+            maxs[c] = fmax(maxs[c], v);
+        }
+}
+
+void tqo_perchannel_scales_zps(const double* mins, const double* maxs, int64_t channels,
+                               int dtype, double* scales, double* zps) {
+    for (int64_t c = 0; c < channels; ++c)
+        scale_zp_from_range(mins[c], maxs[c], dtype, &scales[c], &zps[c]);
+}
+
+void tqo_perchannel_global_scale_zp(const double* mins, const double* maxs,
+                                    int64_t channels, int dtype, double* scale, double* zp) {
+    double ss = 0.0, zz = 0.0;
+    for (int64_t c = 0; c < channels; ++c) {
+        double s, z;
+        scale_zp_from_range(mins[c], maxs[c], dtype, &s, &z);
+        ss += s;
+        zz += z;
+    }
+    *scale = ss / (double)channels;
+    *zp = zz / (double)channels;
+}
+
+/* ---- tensor_ops.rs:379-410 Tensor::mm: C[i,j] += A[i,p]*B[p,j], i-p-j order ---- */
+void tqo_mm(const double* a, const double* b, int64_t m, int64_t k, int64_t n, double* c) {
+    memset(c, 0, sizeof(double) * (size_t)(m * n));
+    for (int64_t i = 0; i < m; ++i)
+        for (int64_t p = 0; p < k; ++p) {
+            const double av = a[i * k + p];
+            const double* brow = b + p * n;
+            double* crow = c + i * n;
+            for (int64_t j = 0; j < n; ++j) crow[j] += av * brow[j];
+        }
+}
+
+/* ---- linear.rs:111-121 Linear::forward: y = x . W^T (+ b) ----
+ * W^T is materialised the way Tensor::mm's to_vec_f64 gathers the transposed
+ * view (tensor_view.rs:129-163, tensor_ops.rs:395-396); the bias add is the
+ * broadcast binary_op (tensor_ops.rs:125-147). */
+void tqo_linear(const double* x, int64_t m, const double* w, const float* bias,
+                int64_t n, int64_t k, double* y) {
+    double* wt = (double*)malloc(sizeof(double) * (size_t)(n * k));
+    for (int64_t p = 0; p < k; ++p)
+        for (int64_t j = 0; j < n; ++j) wt[p * n + j] = w[j * k + p];
+    tqo_mm(x, wt, m, k, n, y);
+    free(wt);
+    if (bias)
+        for (int64_t i = 0; i < m; ++i)
+            for (int64_t j = 0; j < n; ++j) y[i * n + j] = y[i * n + j] + (double)bias[j];
+}
+
+/* tensor_ops.rs:62-64 sigmoid = 1/(1+exp(-x)); activation.rs:70-74 SiLU = x*sigmoid(x) */
+double tqo_sigmoid(double x) { return 1.0 / (1.0 + exp(-x)); }
+
+double tqo_silu_module(double x) { return x * tqo_sigmoid(x); }
+
+/* ---- IEEE round-to-nearest-even conversions for the build-defined formats ---- */
+uint16_t tqo_f64_to_f16_bits(double x) {
+    const uint16_t sign = signbit(x) ? 0x8000u : 0u;
+    if (x != x) return (uint16_t)(sign | 0x7E00u);
+    const double a = fabs(x);
+    if (a >= 65520.0) return (uint16_t)(sign | 0x7C00u); /* past max + half ulp */
+    if (a < 0x1p-14) {                                    /* subnormal range, ulp 2^-24 */
+        const double m = nearbyint(a * 0x1p24);           /* exact scaling, RNE */
+        return (uint16_t)(sign | (uint16_t)m);            /* m == 1024 encodes 2^-14 */
+    }
+    int e2;
+    frexp(a, &e2);
+    int e = e2 - 1; /* a in [2^e, 2^(e+1)) */
+    double m = nearbyint(ldexp(a, 10 - e));
+    if (m == 2048.0) {
+        m = 1024.0;
+        e += 1;
+    }
+    if (e > 15) return (uint16_t)(sign | 0x7C00u);
+    return (uint16_t)(sign | (uint16_t)((e + 15) << 10) | (uint16_t)(m - 1024.0));
+}
+
+double tqo_f16_bits_to_f64(uint16_t h) {
+    const double sign = (h & 0x8000u) ? -1.0 : 1.0;
+    const int e = (h >> 10) & 0x1F;
+    const int m = h & 0x3FF;
+    if (e == 0x1F) return m ? NAN : sign * INFINITY;
+    if (e == 0) return sign * ldexp((double)m, -24);
+    return sign * ldexp((double)(m + 1024), e - 25);
+}
+
+uint16_t tqo_f32_to_bf16_bits(float x) {
+    uint32_t u;
+    memcpy(&u, &x, 4);
+    if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (uint16_t)((u >> 16) | 0x0040u);
+    u += 0x7FFFu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+double tqo_bf16_bits_to_f64(uint16_t b) {
+    const uint32_t u = (uint32_t)b << 16;
+    float f;
+    memcpy(&f, &u, 4);
+    return (double)f;
+}
+
+/* ---- build-defined: symmetric absmax from the observer statistics ----
+ * absmax = max(|min|, |max|) with min/max folded as in
+ * PerChannelMinMaxObserver::observe (observer.rs:110-121).  A row with no
+ * non-NaN value keeps min=+inf, max=-inf, so absmax = +inf. */
+static double absmax_of(const float* v, int64_t n) {
+    double mn = INFINITY, mx = -INFINITY;
+    for (int64_t i = 0; i < n; ++i) {
+        mn = fmin(mn, (double)v[i]);
+        mx = fmax(mx, (double)v[i]);
+    }
+    return fmax(fabs(mn), fabs(mx));
+}
+
+/* Build-defined symmetric per-row INT8:
+ *   s_r = f32(max(absmax_r / 127, 1e-10))            (the 1e-10 floor of quantize.rs:39)
+ *   q   = quantize_tensor(row, f64(s_r), 0, Int8) as i8   (quantize.rs:8-19) */
+void tqo_quantize_i8_rowwise(const float* w, int64_t rows, int64_t k, int8_t* q, float* s) {
+    for (int64_t r = 0; r < rows; ++r) {
+        const float* row = w + r * k;
+        const double sc = fmax(absmax_of(row, k) / 127.0, 1e-10);
+        const float sf = (float)sc;
+        s[r] = sf;
+        for (int64_t i = 0; i < k; ++i) {
+            const double qd = rust_clamp(round((double)row[i] / (double)sf + 0.0), -128.0, 127.0);
+            q[r * k + i] = (int8_t)rust_as_int(qd, -128.0, 127.0);
+        }
+    }
+}
+
+/* dequantize_tensor (quantize.rs:22-27) with zp = 0, result stored as f32 */
+void tqo_dequantize_i8_rowwise(const int8_t* q, const float* s, int64_t rows, int64_t k,
+                               float* w_hat) {
+    for (int64_t r = 0; r < rows; ++r)
+        for (int64_t i = 0; i < k; ++i)
+            w_hat[r * k + i] = (float)(((double)q[r * k + i] - 0.0) * (double)s[r]);
+}
+
+/* Build-defined symmetric INT4, groups of 128 along K:
+ *   s = max(f16_rne(absmax_g / 7), 2^-24)   (2^-24 = smallest positive f16; the
+ *       f16 counterpart of the reference's 1e-10 floor, which f16 flushes to 0)
+ *   q = quantize_tensor(group, f64(s), 0, Int4) as i8 in [-8, 7]
+ *   byte[r, j] = (q[r, 2j] & 0xF) | (q[r, 2j+1] & 0xF) << 4   (low nibble = even k) */
+void tqo_quantize_i4_g128(const float* w, int64_t rows, int64_t k, uint8_t* packed,
+                          uint16_t* s_f16) {
+    const int64_t groups = k / 128;
+    for (int64_t r = 0; r < rows; ++r)
+        for (int64_t g = 0; g < groups; ++g) {
+            const float* grp = w + r * k + g * 128;
+            uint16_t h = tqo_f64_to_f16_bits(absmax_of(grp, 128) / 7.0);
+            if (h == 0) h = 1;
+            s_f16[r * groups + g] = h;
+            const double sv = tqo_f16_bits_to_f64(h);
+            for (int i = 0; i < 128; i += 2) {
+                const double q0 = rust_clamp(round((double)grp[i] / sv + 0.0), -8.0, 7.0);
+                const double q1 = rust_clamp(round((double)grp[i + 1] / sv + 0.0), -8.0, 7.0);
+                const int c0 = rust_as_int(q0, -8.0, 7.0), c1 = rust_as_int(q1, -8.0, 7.0);
+                packed[r * (k / 2) + g * 64 + i / 2] = (uint8_t)((c0 & 0xF) | ((c1 & 0xF) << 4));
+            }
+        }
+}
+
+static int nibble_value(uint8_t byte, int hi) {
+    const int v = hi ? (byte >> 4) : (byte & 0xF);
+    return v >= 8 ? v - 16 : v;
+}
+
+void tqo_dequantize_i4_g128(const uint8_t* packed, const uint16_t* s_f16, int64_t rows,
+                            int64_t k, float* w_hat) {
+    const int64_t groups = k / 128;
+    for (int64_t r = 0; r < rows; ++r)
+        for (int64_t i = 0; i < k; ++i) {
+            const int q = nibble_value(packed[r * (k / 2) + i / 2], (int)(i & 1));
+            const double sv = tqo_f16_bits_to_f64(s_f16[r * groups + i / 128]);
+            w_hat[r * k + i] = (float)(((double)q - 0.0) * sv);
+        }
+}
+
+/* dequantized weight in f64, as Linear::from_tensors receives it (linear.rs:65-75) */
+static double* deq_w8_f64(const int8_t* q, const float* s, int64_t n, int64_t k) {
+    double* w = (double*)malloc(sizeof(double) * (size_t)(n * k));
+    for (int64_t r = 0; r < n; ++r)
+        for (int64_t i = 0; i < k; ++i) w[r * k + i] = ((double)q[r * k + i] - 0.0) * (double)s[r];
+    return w;
+}
+
+static double* deq_w4_f64(const uint8_t* packed, const uint16_t* s_f16, int64_t n, int64_t k) {
+    double* w = (double*)malloc(sizeof(double) * (size_t)(n * k));
+    const int64_t groups = k / 128;
+    for (int64_t r = 0; r < n; ++r)
+        for (int64_t i = 0; i < k; ++i) {
+            const int q = nibble_value(packed[r * (k / 2) + i / 2], (int)(i & 1));
+            w[r * k + i] = ((double)q - 0.0) * tqo_f16_bits_to_f64(s_f16[r * groups + i / 128]);
+        }
+    return w;
+}
+
+void tqo_linear_w8(const float* x, int64_t m, const int8_t* q, const float* s,
+                   const float* bias, int64_t n, int64_t k, double* y) {
+    double* xd = (double*)malloc(sizeof(double) * (size_t)(m * k));
+    for (int64_t i = 0; i < m * k; ++i) xd[i] = (double)x[i];
+    double* w = deq_w8_f64(q, s, n, k);
+    tqo_linear(xd, m, w, bias, n, k, y);
+    free(w);
+    free(xd);
+}
+
+void tqo_linear_w4g128_bf16(const uint16_t* x_bf16, int64_t m, const uint8_t* packed,
+                            const uint16_t* s_f16, const float* bias, int64_t n, int64_t k,
+                            double* y) {
+    double* xd = (double*)malloc(sizeof(double) * (size_t)(m * k));
+    for (int64_t i = 0; i < m * k; ++i) xd[i] = tqo_bf16_bits_to_f64(x_bf16[i]);
+    double* w = deq_w4_f64(packed, s_f16, n, k);
+    tqo_linear(xd, m, w, bias, n, k, y);
+    free(w);
+    free(xd);
+}
+
+void tqo_linear_w4g128_f32(const float* x, int64_t m, const uint8_t* packed,
+                           const uint16_t* s_f16, const float* bias, int64_t n, int64_t k,
+                           double* y) {
+    double* xd = (double*)malloc(sizeof(double) * (size_t)(m * k));
+    for (int64_t i = 0; i < m * k; ++i) xd[i] = (double)x[i];
+    double* w = deq_w4_f64(packed, s_f16, n, k);
+    tqo_linear(xd, m, w, bias, n, k, y);
+    free(w);
+    free(xd);
+}
+
+/* Build-defined W8A8 accumulators: Tensor::mm over integral f64 codes is exact
+ * (|acc| <= K*128*128 < 2^53), so the int32 result is the exact integer sum. */
+void tqo_gemm_w8a8_acc(const int8_t* qa, const int8_t* qw, int64_t m, int64_t n, int64_t k,
+                       int32_t* acc) {
+    for (int64_t i = 0; i < m; ++i)
+        for (int64_t j = 0; j < n; ++j) {
+            int64_t t = 0;
+            for (int64_t p = 0; p < k; ++p) t += (int64_t)qa[i * k + p] * (int64_t)qw[j * k + p];
+            acc[i * n + j] = (int32_t)t;
+        }
+}
+
+/* Reference value of the W8A8 product: mm(deq(qa), deq(qw)^T) (+ b) in f64. */
+void tqo_linear_w8a8(const int8_t* qa, const float* sa, const int8_t* qw, const float* sw,
+                     const float* bias, int64_t m, int64_t n, int64_t k, double* y) {
+    double* a = deq_w8_f64(qa, sa, m, k);
+    double* w = deq_w8_f64(qw, sw, n, k);
+    tqo_linear(a, m, w, bias, n, k, y);
+    free(w);
+    free(a);
+}
+
+/* Build-defined quantized FFN composed from Linear (linear.rs:111-121), SiLU
+ * (activation.rs:70-74) and Tensor::mul (tensor_ops.rs:155-157), all in f64:
+ *   h = SiLU(x Wg^T) * (x Wu^T);  y = h Wd^T */
+void tqo_mlp_w4g128(const uint16_t* x_bf16, int64_t m, int64_t d, int64_t f,
+                    const uint8_t* pg, const uint16_t* sg, const uint8_t* pu,
+                    const uint16_t* su, const uint8_t* pd, const uint16_t* sd, double* y) {
+    double* g = (double*)malloc(sizeof(double) * (size_t)(m * f));
+    double* u = (double*)malloc(sizeof(double) * (size_t)(m * f));
+    tqo_linear_w4g128_bf16(x_bf16, m, pg, sg, NULL, f, d, g);
+    tqo_linear_w4g128_bf16(x_bf16, m, pu, su, NULL, f, d, u);
+    for (int64_t i = 0; i < m * f; ++i) g[i] = tqo_silu_module(g[i]) * u[i];
+    free(u);
+    double* w = deq_w4_f64(pd, sd, d, f);
+    tqo_linear(g, m, w, NULL, d, f, y);
+    free(w);
+    free(g);
+}

@@ -1,0 +1,114 @@
+"""CPU checks of the C ABI: libtq.so loads, exports every entry point that
+include/tq.h declares, and its host-only paths (ranges, observer scale math,
+argument validation) behave like the reference.  No kernel is launched here:
+every call below fails validation or is host-only."""
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "tq.h")
+
+
+def declared_symbols():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\*?\s+\**(tq_\w+)\s*\(", text, flags=re.M)))
+
+
+@pytest.fixture(scope="module")
+def abi():
+    from theano_quantize import _abi
+
+    return _abi
+
+
+def test_header_declares_entry_points():
+    syms = declared_symbols()
+    assert "tq_quantize_i8_rowwise" in syms and "tq_gemm_w8a8" in syms and len(syms) >= 20
+
+
+def test_library_exports_every_declared_symbol(abi):
+    L = abi.lib()
+    missing = [s for s in declared_symbols() if not hasattr(L, s)]
+    assert not missing, missing
+
+
+def test_binding_covers_every_declared_symbol(abi):
+    assert sorted(abi.SIGNATURES) == declared_symbols()
+
+
+def test_version_and_status_strings(abi):
+    L = abi.lib()
+    assert L.tq_version() >= 100
+    assert L.tq_status_string(0) == b"TQ_OK" and L.tq_status_string(1) == b"TQ_EINVAL"
+
+
+def test_qdtype_info_reference_ranges(abi):
+    # crates/theano-quantize/src/qconfig.rs:82-108
+    from theano_quantize import QuantDType
+
+    assert [d.bits() for d in QuantDType] == [8, 8, 4, 8]
+    assert [d.is_signed() for d in QuantDType] == [True, False, True, False]
+    assert [d.qmin() for d in QuantDType] == [-128.0, 0.0, -8.0, -448.0]
+    assert [d.qmax() for d in QuantDType] == [127.0, 255.0, 7.0, 448.0]
+    with pytest.raises(ValueError):
+        abi.call("tq_qdtype_info", 9, None, None, None, None)
+
+
+def test_qconfig_defaults_reference():
+    # qconfig.rs:110-148
+    from theano_quantize import QConfig, QuantDType
+
+    c = QConfig.default_int8()
+    assert (c.weight_dtype, c.activation_dtype, c.symmetric, c.per_channel) == (
+        QuantDType.Int8, QuantDType.UInt8, True, False)
+    c = QConfig.default_int4()
+    assert (c.weight_dtype, c.activation_dtype, c.symmetric, c.per_channel) == (
+        QuantDType.Int4, QuantDType.Int8, True, True)
+    assert QConfig.default() == QConfig.default_int8()
+
+
+def test_observer_scale_zp_matches_oracle(abi, oracle):
+    s, z = ctypes.c_double(), ctypes.c_double()
+    for mn, mx, dt in [(-1.0, 3.0, 0), (0.0, 1.0, 1), (-0.2, 0.7, 2), (5.0, 5.0, 0),
+                       (float("inf"), float("-inf"), 0), (-448.0, 100.0, 3)]:
+        abi.call("tq_observer_scale_zp", mn, mx, 1, dt, ctypes.byref(s), ctypes.byref(z))
+        o = oracle.MinMaxObserver()
+        o.state[:] = [mn, mx, 1.0]
+        assert (s.value, z.value) == o.compute_scale_zero_point(dt)
+    abi.call("tq_observer_scale_zp", 0.0, 1.0, 0, 0, ctypes.byref(s), ctypes.byref(z))
+    assert (s.value, z.value) == (1.0, 0.0)  # uninitialized, observer.rs:52-54
+
+
+@pytest.mark.parametrize("call", [
+    ("tq_quantize_i4_g128", [None, 4, 100, None, None, None]),            # K % 128
+    ("tq_dequantize_i4_g128", [None, None, 2, 130, None, None]),
+    ("tq_quantize_i8_rowwise", [None, -1, 16, None, None, None]),         # negative rows
+    ("tq_quantize_i8_rowwise", [None, 4, 16, None, None, None]),          # null pointers
+    ("tq_gemv_w4g128", [None, 17, None, None, None, 16, 128, None, None]),  # M > 16
+    ("tq_gemv_w8", [None, 1, None, None, None, 16, 20, None, None]),       # K % 16
+    ("tq_gemm_w8a8", [None, None, None, None, None, 4, 20, 64, None, None, None]),  # N % 16
+    ("tq_gemm_w8a8", [None, None, None, None, None, 4, 16, 65, None, None, None]),  # K % 16
+    ("tq_gemm_w4g128_bf16", [None, 4, None, None, None, 16, 100, None, None]),
+    ("tq_mlp_w4g128", [None, 4, 100, 128, None, None, None, None, None, None, None, None, None]),
+    ("tq_quantize_tensor", [None, 10, 1.0, 0.0, 7, None, None]),          # bad QuantDType
+    ("tq_quantize_per_tensor", [None, 10, 0, None, None, None, None]),
+    ("tq_minmax_reset", [None, 0, None]),
+])
+def test_invalid_arguments_are_rejected(abi, call):
+    from theano_quantize import InvalidArgument
+
+    name, args = call
+    with pytest.raises(InvalidArgument):
+        abi.call(name, *args)
+    assert abi.lib().tq_last_error()  # a message was recorded
+
+
+def test_zero_sizes_are_noops(abi):
+    # empty inputs enqueue nothing and succeed
+    assert abi.call("tq_quantize_i8_rowwise", None, 0, 16, None, None, None) == 0
+    assert abi.call("tq_gemv_w8", None, 0, None, None, None, 16, 16, None, None) == 0
+    assert abi.call("tq_quantize_tensor", None, 0, 1.0, 0.0, 0, None, None) == 0

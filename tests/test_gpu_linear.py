@@ -1,0 +1,237 @@
+"""GPU parity: quantized Linear (GEMV, W8A8 GEMM, W4A16 GEMM) and the
+quantized FFN vs the oracle's f64 reference (Linear::forward over the
+dequantized weight).  Integer accumulators are bit-exact; float outputs are
+checked at |got - ref| <= 1e-4 + 1e-3 * |ref|.
+
+At full W8A8 size (M=2048) the oracle runs on sampled rows and every row is
+checked by exact int64 checksums: row sums, column sums and a random
+projection of the int32 accumulators."""
+import numpy as np
+import pytest
+
+from conftest import assert_close
+
+pytestmark = pytest.mark.gpu
+
+RTOL, ATOL = 1e-3, 1e-4
+
+
+def dev_tensor(a):
+    import torch
+
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def host(t):
+    import torch
+
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def normal(seed, shape, std=1.0, stream=0):
+    from theano_quantize.synth import normal_f32
+
+    return normal_f32(seed, shape, std, stream)
+
+
+def bf16_dev(bits):
+    import torch
+
+    return dev_tensor(bits.view(np.int16)).view(torch.bfloat16)
+
+
+def to_bf16_bits(x):
+    from theano_quantize.synth import f32_to_bf16_bits
+
+    return f32_to_bf16_bits(x)
+
+
+# ------------------------------------------------------------------ GEMV
+@pytest.fixture(scope="module")
+def c2(tq, oracle):
+    """Config 2: INT8 per-channel weight [4096, 4096] ~ N(0, 0.02), x [16, 4096] ~ N(0, 1)."""
+    w = normal(1, (4096, 4096), 0.02)
+    x = normal(1, (16, 4096), 1.0, stream=1)
+    q, s = tq.quantize_per_channel_i8(dev_tensor(w))
+    rq, rs = oracle.quantize_i8_rowwise(w)
+    assert np.array_equal(host(q), rq) and np.array_equal(host(s), rs)
+    ref = oracle.linear_w8(x, rq, rs)
+    return x, q, s, ref
+
+
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 8, 16])
+def test_gemv_w8_config2(tq, c2, m):
+    from theano_quantize import _abi
+    from theano_quantize._tensor import ptr, stream
+    import torch
+
+    x, q, s, ref = c2
+    y = torch.empty((m, 4096), dtype=torch.float32, device="cuda")
+    xd = dev_tensor(x[:m])
+    _abi.call("tq_gemv_w8", ptr(xd), m, ptr(q), ptr(s), None, 4096, 4096, ptr(y), stream())
+    assert_close(host(y), ref[:m], RTOL, ATOL, f"gemv_w8 M={m}")
+
+
+@pytest.mark.parametrize("n,k,m", [(1000, 1024, 1), (17, 16, 2), (333, 3088, 3), (64, 8192, 4), (5, 2000, 16)])
+def test_gemv_w8_shapes_bias(tq, oracle, n, k, m):
+    w = normal(50, (n, k), 0.02)
+    x = normal(50, (m, k), 1.0, stream=1)
+    b = normal(50, (n,), 0.1, stream=2)
+    lin = tq.QuantizedLinear.from_tensors(dev_tensor(w), dev_tensor(b), tq.QConfig.default_int8())
+    y = host(lin(dev_tensor(x)))
+    rq, rs = oracle.quantize_i8_rowwise(w)
+    assert_close(y, oracle.linear_w8(x, rq, rs, b), RTOL, ATOL, f"QuantizedLinear w8 {n}x{k} M={m}")
+
+
+@pytest.fixture(scope="module")
+def c3(tq, oracle):
+    """Config 3: INT4 g128 weight [14336, 4096] ~ N(0, 0.02), x bf16 [16, 4096] ~ N(0, 1)."""
+    w = normal(2, (14336, 4096), 0.02)
+    xb = to_bf16_bits(normal(2, (16, 4096), 1.0, stream=1))
+    p, s = tq.quantize_i4_g128(dev_tensor(w))
+    rp, rs = oracle.quantize_i4_g128(w)
+    assert np.array_equal(host(p), rp) and np.array_equal(host(s).view(np.uint16), rs)
+    ref = oracle.linear_w4g128_bf16(xb, rp, rs)
+    return xb, p, s, ref
+
+
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 8, 16])
+def test_gemv_w4g128_config3(tq, c3, m):
+    from theano_quantize import _abi
+    from theano_quantize._tensor import ptr, stream
+    import torch
+
+    xb, p, s, ref = c3
+    y = torch.empty((m, 14336), dtype=torch.float32, device="cuda")
+    xd = bf16_dev(xb[:m])
+    _abi.call("tq_gemv_w4g128", ptr(xd), m, ptr(p), ptr(s), None, 14336, 4096, ptr(y), stream())
+    assert_close(host(y), ref[:m], RTOL, ATOL, f"gemv_w4g128 M={m}")
+
+
+@pytest.mark.parametrize("n,k,m", [(100, 128, 1), (7, 2176, 2), (256, 14336, 1), (48, 16384, 3), (9, 4096, 16)])
+def test_gemv_w4g128_shapes_bias(tq, oracle, n, k, m):
+    w = normal(51, (n, k), 0.02)
+    xb = to_bf16_bits(normal(51, (m, k), 1.0, stream=1))
+    b = normal(51, (n,), 0.1, stream=2)
+    lin = tq.QuantizedLinear.from_tensors(dev_tensor(w), dev_tensor(b), tq.QConfig.default_int4())
+    y = host(lin(bf16_dev(xb)))
+    rp, rs = oracle.quantize_i4_g128(w)
+    assert_close(y, oracle.linear_w4g128_bf16(xb, rp, rs, b), RTOL, ATOL, f"QuantizedLinear w4 {n}x{k} M={m}")
+
+
+# ------------------------------------------------------------------ W8A8
+def checksums_ok(acc, qa, qw, seed=0):
+    a = qa.astype(np.int64)
+    w = qw.astype(np.int64)
+    acc = acc.astype(np.int64)
+    rows = np.array_equal(acc.sum(axis=1), a @ w.sum(axis=0))
+    cols = np.array_equal(acc.sum(axis=0), a.sum(axis=0) @ w.T)
+    r = np.random.default_rng(seed).integers(-3, 4, acc.shape[1]).astype(np.int64)
+    proj = np.array_equal(acc @ r, a @ (w.T @ r))
+    return rows and cols and proj
+
+
+def run_w8a8(tq, x, w, bias=None, with_acc=True):
+    import torch
+    from theano_quantize import _abi
+    from theano_quantize._tensor import ptr, stream
+
+    m, k = x.shape
+    n = w.shape[0]
+    qa, sa = tq.quantize_per_channel_i8(dev_tensor(x))
+    qw, sw = tq.quantize_per_channel_i8(dev_tensor(w))
+    acc = torch.empty((m, n), dtype=torch.int32, device="cuda") if with_acc else None
+    y = torch.empty((m, n), dtype=torch.float32, device="cuda")
+    bd = None if bias is None else dev_tensor(bias)
+    _abi.call("tq_gemm_w8a8", ptr(qa), ptr(sa), ptr(qw), ptr(sw), ptr(bd), m, n, k, ptr(acc), ptr(y), stream())
+    return host(qa), host(sa), host(qw), host(sw), (host(acc) if with_acc else None), host(y)
+
+
+def test_w8a8_config4_full(tq, oracle):
+    x = normal(3, (2048, 4096), 1.0)
+    w = normal(3, (4096, 4096), 0.02, stream=1)
+    qa, sa, qw, sw, acc, y = run_w8a8(tq, x, w)
+    rqa, rsa = oracle.quantize_i8_rowwise(x)
+    rqw, rsw = oracle.quantize_i8_rowwise(w)
+    assert np.array_equal(qa, rqa) and np.array_equal(sa, rsa)
+    assert np.array_equal(qw, rqw) and np.array_equal(sw, rsw)
+    assert checksums_ok(acc, qa, qw)
+    rows = np.array([0, 1, 127, 128, 1000, 2047])
+    assert np.array_equal(acc[rows], oracle.gemm_w8a8_acc(qa[rows], qw))
+    assert_close(y[rows], oracle.linear_w8a8(qa[rows], sa[rows], qw, sw), RTOL, ATOL, "w8a8 y")
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 16, 16), (130, 48, 208), (7, 272, 1024), (257, 128, 4096), (64, 160, 80)])
+def test_w8a8_shapes_bias(tq, oracle, m, n, k):
+    x = normal(52, (m, k), 1.0)
+    w = normal(52, (n, k), 0.02, stream=1)
+    b = normal(52, (n,), 0.1, stream=2)
+    qa, sa, qw, sw, acc, y = run_w8a8(tq, x, w, b)
+    assert np.array_equal(acc, oracle.gemm_w8a8_acc(qa, qw))
+    assert_close(y, oracle.linear_w8a8(qa, sa, qw, sw, b), RTOL, ATOL, f"w8a8 {m}x{n}x{k}")
+    _, _, _, _, _, y2 = run_w8a8(tq, x, w, b, with_acc=False)
+    assert np.array_equal(y, y2)
+
+
+def test_w8a8_extreme_codes(tq, oracle):
+    # every code -128/127 paths: rows of constant sign reach |acc| = K*127*128
+    x = np.where(normal(53, (32, 4096), 1.0) > 0, 1.0, -1.0).astype(np.float32)
+    w = np.where(normal(53, (64, 4096), 1.0, stream=1) > 0, 1.0, -1.0).astype(np.float32)
+    x[0] = 1.0
+    w[0] = 1.0
+    qa, sa, qw, sw, acc, y = run_w8a8(tq, x, w)
+    assert np.array_equal(acc, oracle.gemm_w8a8_acc(qa, qw))
+    assert acc[0, 0] == 4096 * 127 * 127
+
+
+def test_quantized_linear_w8a8_module(tq, oracle):
+    from theano_quantize import QConfig, QuantDType
+
+    w = normal(54, (256, 512), 0.02)
+    x = normal(54, (100, 512), 1.0, stream=1)
+    cfg = QConfig(QuantDType.Int8, QuantDType.Int8, True, True)
+    lin = tq.QuantizedLinear.from_tensors(dev_tensor(w), None, cfg)
+    y = host(lin(dev_tensor(x)))
+    rqa, rsa = oracle.quantize_i8_rowwise(x)
+    rqw, rsw = oracle.quantize_i8_rowwise(w)
+    assert_close(y, oracle.linear_w8a8(rqa, rsa, rqw, rsw), RTOL, ATOL, "QuantizedLinear w8a8")
+    assert lin.num_parameters() == 256 * 512
+
+
+# ----------------------------------------------------------------- W4A16
+@pytest.mark.parametrize("m,n,k", [(17, 256, 512), (130, 64, 4096), (300, 128, 1024), (33, 16, 128)])
+def test_gemm_w4g128_bf16_shapes(tq, oracle, m, n, k):
+    w = normal(55, (n, k), 0.02)
+    xb = to_bf16_bits(normal(55, (m, k), 1.0, stream=1))
+    b = normal(55, (n,), 0.1, stream=2)
+    lin = tq.QuantizedLinear.from_tensors(dev_tensor(w), dev_tensor(b), tq.QConfig.default_int4())
+    y = host(lin(bf16_dev(xb)))
+    rp, rs = oracle.quantize_i4_g128(w)
+    assert_close(y, oracle.linear_w4g128_bf16(xb, rp, rs, b), RTOL, ATOL, f"w4a16 {m}x{n}x{k}")
+
+
+# ------------------------------------------------------------------- MLP
+@pytest.mark.parametrize("m,d,f", [(5, 256, 384), (1, 128, 128), (70, 512, 1024)])
+def test_mlp_small(tq, oracle, m, d, f):
+    wg = normal(56, (f, d), 0.02)
+    wu = normal(56, (f, d), 0.02, stream=1)
+    wd = normal(56, (d, f), 0.02, stream=2)
+    xb = to_bf16_bits(normal(56, (m, d), 1.0, stream=3))
+    mlp = tq.QuantizedMLP.from_tensors(dev_tensor(wg), dev_tensor(wu), dev_tensor(wd))
+    y = host(mlp(bf16_dev(xb)))
+    args = [a for t in (mlp.gate, mlp.up, mlp.down) for a in (host(t[0]), host(t[1]).view(np.uint16))]
+    assert_close(y, oracle.mlp_w4g128(xb, *args), RTOL, ATOL, f"mlp {m}x{d}x{f}")
+
+
+def test_mlp_config5_sampled_rows(tq, oracle):
+    d, f, m = 4096, 14336, 512
+    wg = normal(4, (f, d), 0.02)
+    wu = normal(4, (f, d), 0.02, stream=1)
+    wd = normal(4, (d, f), 0.02, stream=2)
+    xb = to_bf16_bits(normal(4, (m, d), 1.0, stream=3))
+    mlp = tq.QuantizedMLP.from_tensors(dev_tensor(wg), dev_tensor(wu), dev_tensor(wd))
+    y = host(mlp(bf16_dev(xb)))
+    rows = np.array([0, 129, 511])
+    args = [a for t in (mlp.gate, mlp.up, mlp.down) for a in (host(t[0]), host(t[1]).view(np.uint16))]
+    assert_close(y[rows], oracle.mlp_w4g128(xb[rows], *args), RTOL, ATOL, "mlp config 5")

@@ -142,17 +142,23 @@ def main():
     w4_bytes = n3 * k3 // 2 + 2 * n3 * (k3 // 128)         # packed + f16 scales
     w4_bytes_m = lambda m: w4_bytes + 2 * m * k3 + 4 * m * n3  # + x bf16 + y f32
     if want("gemv_w4") or want("gemv_w4_m") or only is None:
-        log("setup: config 3 INT4 g128 weights [14336, 4096]")
+        log("setup: config 3 INT4 g128 weights [14336, 4096], decode kernel layout")
         w = normal_f32(2, (n3, k3), 0.02)
-        copies = quant_copies(w, tq.quantize_i4_g128, rotation(w4_bytes))
-        del w
+        p0, s0 = tq.quantize_i4_g128(dt(w))
+        pt0, st0, tile = tq.repack_i4_g128_tiled(p0, s0)
+        copies = [(pt0.clone(), st0.clone(), p0.clone(), s0.clone()) for _ in range(rotation(2 * w4_bytes))]
+        del w, p0, s0, pt0, st0
         x = bf16(normal_f32(2, (16, k3), 1.0, stream=1))
         y = torch.empty((16, n3), dtype=torch.float32, device=dev)
 
         def gemv_w4(m):
-            def launch(i):
-                p, s = copies[i % len(copies)]
-                _abi.call("tq_gemv_w4g128", ptr(x), m, ptr(p), ptr(s), None, n3, k3, ptr(y), stream())
+            def launch(i):  # same dispatch as QuantizedLinear: tiled up to 4 tokens, MFMA beyond
+                pt, st, p, s = copies[i % len(copies)]
+                if m <= tq.nn.TILED_MAX_M:
+                    _abi.call("tq_gemv_w4g128_tiled", ptr(x), m, ptr(pt), ptr(st), None, n3, k3, tile, ptr(y),
+                              stream())
+                else:
+                    _abi.call("tq_gemv_w4g128", ptr(x), m, ptr(p), ptr(s), None, n3, k3, ptr(y), stream())
             return launch
 
         if want("gemv_w4"):
@@ -324,7 +330,7 @@ def main():
         "dtype": "int4xbf16",
         "data": "synthetic (numpy PCG64 normals, seeded; weights rotate over copies > 2x MALL)",
         "config": {"workload": "int4_g128_dequant_gemv", "baseline_config": 3, "n": n3, "k": k3, "m": 1,
-                   "group": 128, "timing": headline["mode"]},
+                   "group": 128, "weight_layout": "row-tiled", "timing": headline["mode"]},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "algorithmic_bytes_per_launch": w4_bytes_m(1)},

@@ -156,11 +156,29 @@ int tq_dequantize_i4_g128(const uint8_t* packed, const uint16_t* s_f16, int64_t 
 int tq_gemv_w8(const float* x, int64_t m, const int8_t* q, const float* s,
                const float* bias, int64_t n, int64_t k, float* y, tq_stream_t stream);
 
-/* Decode-shaped GEMV, INT4 g128 weights, bf16 activations x [M, K] (bf16 bits),
- * M <= 16, K % 128 == 0. */
+/* Decode-shaped GEMV, INT4 g128 weights (canonical layout), bf16 activations
+ * x [M, K] (bf16 bits), M <= 16, K % 128 == 0, K <= 16384. */
 int tq_gemv_w4g128(const uint16_t* x_bf16, int64_t m, const uint8_t* packed,
                    const uint16_t* s_f16, const float* bias, int64_t n, int64_t k,
                    float* y, tq_stream_t stream);
+
+/* Row-tiled kernel layout of an INT4 g128 weight for the decode GEMV (a pure
+ * permutation of the canonical bytes; rows padded to a multiple of tile_rows
+ * with zero bytes and zero scales).  With C = K/32 16-byte chunks per row,
+ * G = K/128 groups and T = tile_rows:
+ *   packed_t[((t*C + c)*T + r)*16 + b] = packed[t*T + r][16c + b]
+ *   s_t[(t*G + g)*T + r]               = s[t*T + r][g]
+ * Buffer sizes: packed_t ceil(N/T)*T*K/2 bytes, s_t ceil(N/T)*T*K/128 halves.
+ * tq_w4g128_tile_rows picks T (a multiple of 8 in [8, 64]) so that the tiles
+ * about match the compute units of the current device (host-only). */
+int64_t tq_w4g128_tile_rows(int64_t n);
+int tq_repack_w4g128_tiled(const uint8_t* packed, const uint16_t* s_f16, int64_t n, int64_t k,
+                           int64_t tile_rows, uint8_t* packed_t, uint16_t* s_t, tq_stream_t stream);
+/* Decode-shaped GEMV on the tiled layout: same result as tq_gemv_w4g128.
+ * M <= 16, K % 128 == 0, K <= 16384. */
+int tq_gemv_w4g128_tiled(const uint16_t* x_bf16, int64_t m, const uint8_t* packed_t,
+                         const uint16_t* s_t, const float* bias, int64_t n, int64_t k,
+                         int64_t tile_rows, float* y, tq_stream_t stream);
 
 /* Prefill-shaped W8A8: activations already quantized per row (use
  * tq_quantize_i8_rowwise on X).  acc[i,j] = sum_p qa[i,p]*qw[j,p] (int32,

@@ -1,0 +1,263 @@
+// tq_decode_tiled.hip -- decode-shaped INT4 group-128 Linear on a row-tiled
+// copy of the packed weight, for gfx950.  Same result as tq_gemv_w4g128 (the
+// reference's Linear::forward over the dequantized weight,
+// crates/theano-nn/src/linear.rs:111-121, quantize.rs:22-27); only the byte
+// order of the weight differs.
+//
+// Tiled layout (a permutation of the canonical [N, K/2] bytes; T rows per tile,
+// C = K/32 chunks of 16 bytes per row, G = K/128 groups, rows padded to a
+// multiple of T with zero bytes and zero scales):
+//   packed_t[((t*C + c)*T + r)*16 + b] = packed[t*T + r][16c + b]
+//   s_t[(t*G + g)*T + r]               = s[t*T + r][g]
+// so the 16-byte chunk c of the T rows of a tile is one contiguous T*16-byte run.
+//
+// Kernel: one block (16 waves) per tile, lane = row, waves split the chunks.
+// x is wave-uniform, so each wave permutes its slice of x once into a private
+// LDS strip and reads it back with broadcast ds_read_b128; no cross-lane
+// reduction is needed per row.  Nibbles become bf16 with bit operations
+// ((q+8) | 0x4300 is the bf16 of 136+q), v_dot2_f32_bf16 multiplies them by x
+// pairs, 136*sum(x) of each 32-element chunk is subtracted before the f16
+// group scale is applied.  Weight loads are unconditional (clamped addresses)
+// and run kWin chunks ahead of the arithmetic; the waves' partial sums meet in
+// LDS in a fixed order.
+#include "tq_internal.h"
+
+namespace tq {
+namespace {
+
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kWaves = 16;
+constexpr int kBlock = 64 * kWaves;
+constexpr int kWin = 2;
+constexpr int kMaxCPW = 32;   // chunks per wave: K <= 32 * 16 * 32 = 16384
+constexpr int kMaxTok = 4;    // tokens per pass
+
+__device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a), __builtin_bit_cast(bf16x2, b), c,
+                                           false);
+}
+
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); }
+
+// Per-wave LDS strip for token j: kCPW chunks x 16 dwords, each 8-block stored
+// as (x0,x2)(x1,x3)(x4,x6)(x5,x7); then 136*chunk sums [kM][kCPW] f32.
+template <int kM, int kCPW>
+struct Strip {
+    static constexpr int kXBytes = kM * kCPW * 64;
+    static constexpr int kBytes = kXBytes + kM * kCPW * 4;
+};
+
+template <int kM, int kCPW>
+__global__ __launch_bounds__(kBlock) void k_decode_tiled(const uint16_t* __restrict__ x,
+                                                         const uint8_t* __restrict__ pt,
+                                                         const uint16_t* __restrict__ st,
+                                                         const float* __restrict__ bias, int64_t n,
+                                                         int64_t k, int tile_rows,
+                                                         float* __restrict__ y) {
+    using S = Strip<kM, kCPW>;
+    __shared__ __attribute__((aligned(16))) uint8_t strips[kWaves][S::kBytes];
+    __shared__ float part[kWaves][kM][64];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int64_t tile = blockIdx.x;
+    const int64_t C = k >> 5, G = k >> 7;
+    const int T = tile_rows;
+    const int ln = lane < T ? lane : T - 1;  // lanes past the tile re-read its last row; never stored
+    const int64_t c0 = static_cast<int64_t>(wave) * kCPW;
+    uint32_t* sx = reinterpret_cast<uint32_t*>(strips[wave]);
+    float* ssum = reinterpret_cast<float*>(strips[wave] + S::kXBytes);
+
+    // scales of this wave's groups, then the first window of weight chunks
+    constexpr int kGPW = (kCPW + 3) / 4;
+    uint16_t sh[kGPW];
+#pragma unroll
+    for (int i = 0; i < kGPW; ++i) {
+        const int64_t g = min<int64_t>((c0 >> 2) + i, G - 1);
+        sh[i] = st[(tile * G + g) * T + ln];
+    }
+    const uint8_t* wbase = pt + (tile * C * T + ln) * 16;
+    u32x4 w[kWin];
+#pragma unroll
+    for (int i = 0; i < kWin && i < kCPW; ++i) {
+        const int64_t c = min<int64_t>(c0 + i, C - 1);
+        w[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wbase + c * T * 16));
+    }
+
+    // stage this wave's x slice: item = 4 values (half an 8-block) of token j
+    for (int it = lane; it < kM * kCPW * 8; it += kWave) {
+        const int j = it / (kCPW * 8), r = it - j * (kCPW * 8);
+        const int64_t kx = min<int64_t>(c0 * 32 + r * 4, k - 4);
+        const uint2 v = *reinterpret_cast<const uint2*>(x + j * k + kx);
+        // (x0,x1),(x2,x3) -> (x0,x2),(x1,x3); the odd half of the 8-block lands after the even one
+        *reinterpret_cast<uint2*>(sx + j * kCPW * 16 + 2 * r) =
+            make_uint2((v.x & 0xFFFFu) | (v.y << 16), (v.x >> 16) | (v.y & 0xFFFF0000u));
+        float s = bf16_lo(v.x) + bf16_hi(v.x) + bf16_lo(v.y) + bf16_hi(v.y);
+        s += __shfl_xor(s, 1, kWave);
+        s += __shfl_xor(s, 2, kWave);
+        s += __shfl_xor(s, 4, kWave);
+        if ((r & 7) == 0) ssum[j * kCPW + (r >> 3)] = 136.0f * s;
+    }
+    // the strip is private to this wave: LDS accesses of one wave complete in order
+
+    float acc[kM];
+#pragma unroll
+    for (int j = 0; j < kM; ++j) acc[j] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kCPW; ++i) {
+        const int slot = i % kWin;
+        const uint32_t ws[4] = {w[slot].x, w[slot].y, w[slot].z, w[slot].w};
+        uint32_t lo[4], hi[4];
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+            lo[d] = (ws[d] ^ 0x88888888u) & 0x0F0F0F0Fu;         // q+8 of k, k+2, k+4, k+6
+            hi[d] = ((ws[d] >> 4) ^ 0x08888888u) & 0x0F0F0F0Fu;  // q+8 of k+1, k+3, k+5, k+7
+        }
+        const bool live = c0 + i < C;
+        const float sc = live ? __half2float(__ushort_as_half(sh[i >> 2])) : 0.0f;
+#pragma unroll
+        for (int j = 0; j < kM; ++j) {
+            float p = 0.0f;
+#pragma unroll
+            for (int d = 0; d < 4; ++d) {
+                // strip dwords of 8-block d: (x0,x2), (x1,x3), (x4,x6), (x5,x7)
+                const u32x4 xq = *reinterpret_cast<const u32x4*>(sx + j * kCPW * 16 + i * 16 + 4 * d);
+                p = dot2_bf16(__builtin_amdgcn_perm(0x43434343u, lo[d], 0x04010400u), xq.x, p);
+                p = dot2_bf16(__builtin_amdgcn_perm(0x43434343u, hi[d], 0x04010400u), xq.y, p);
+                p = dot2_bf16(__builtin_amdgcn_perm(0x43434343u, lo[d], 0x04030402u), xq.z, p);
+                p = dot2_bf16(__builtin_amdgcn_perm(0x43434343u, hi[d], 0x04030402u), xq.w, p);
+            }
+            acc[j] = fmaf(sc, p - ssum[j * kCPW + i], acc[j]);
+        }
+        if (i + kWin < kCPW) {  // compile-time: refill this slot kWin chunks ahead
+            const int64_t c = min<int64_t>(c0 + i + kWin, C - 1);
+            w[slot] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wbase + c * T * 16));
+        }
+    }
+
+#pragma unroll
+    for (int j = 0; j < kM; ++j) part[wave][j][lane] = acc[j];
+    __syncthreads();
+    for (int i = threadIdx.x; i < kM * 64; i += kBlock) {
+        const int j = i >> 6, r = i & 63;
+        const int64_t row = tile * T + r;
+        if (r >= T || row >= n) continue;
+        float s = 0.0f;
+#pragma unroll
+        for (int v = 0; v < kWaves; ++v) s += part[v][j][r];
+        y[j * n + row] = s + (bias ? bias[row] : 0.0f);
+    }
+}
+
+// 16-byte chunks move from row-major rows into tiles; rows past n become zeros.
+__global__ __launch_bounds__(256) void k_repack_tiled(const uint8_t* __restrict__ packed,
+                                                      const uint16_t* __restrict__ s16, int64_t n,
+                                                      int64_t k, int tile_rows, int64_t tiles,
+                                                      uint8_t* __restrict__ pt, uint16_t* __restrict__ st) {
+    const int64_t C = k >> 5, G = k >> 7, T = tile_rows;
+    const int64_t total = tiles * C * T;
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * 256;
+    for (int64_t o = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; o < total; o += stride) {
+        const int64_t r = o % T, tc = o / T, c = tc % C, t = tc / C;
+        const int64_t row = t * T + r;
+        u32x4 v = u32x4{0u, 0u, 0u, 0u};
+        if (row < n) v = *reinterpret_cast<const u32x4*>(packed + row * (k >> 1) + c * 16);
+        reinterpret_cast<u32x4*>(pt)[o] = v;
+    }
+    const int64_t stotal = tiles * G * T;
+    for (int64_t o = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; o < stotal; o += stride) {
+        const int64_t r = o % T, tg = o / T, g = tg % G, t = tg / G;
+        const int64_t row = t * T + r;
+        st[o] = row < n ? s16[row * G + g] : uint16_t(0);
+    }
+}
+
+template <int kM, int kCPW>
+void launch_tiled(int64_t tiles, hipStream_t s, const uint16_t* x, const uint8_t* pt, const uint16_t* st,
+                  const float* b, int64_t n, int64_t k, int T, float* y) {
+    k_decode_tiled<kM, kCPW><<<static_cast<unsigned>(tiles), kBlock, 0, s>>>(x, pt, st, b, n, k, T, y);
+}
+
+// dispatch on chunks-per-wave (kCPW in {1, 2, 4, 8, 16, 32}: a wave may own a
+// few chunks past K, which are clamped and masked)
+template <int kM>
+void dispatch_tiled(int64_t cpw, int64_t tiles, hipStream_t s, const uint16_t* x, const uint8_t* pt,
+                    const uint16_t* st, const float* b, int64_t n, int64_t k, int T, float* y) {
+    if (cpw <= 1) launch_tiled<kM, 1>(tiles, s, x, pt, st, b, n, k, T, y);
+    else if (cpw <= 2) launch_tiled<kM, 2>(tiles, s, x, pt, st, b, n, k, T, y);
+    else if (cpw <= 4) launch_tiled<kM, 4>(tiles, s, x, pt, st, b, n, k, T, y);
+    else if (cpw <= 8) launch_tiled<kM, 8>(tiles, s, x, pt, st, b, n, k, T, y);
+    else if (cpw <= 16) launch_tiled<kM, 16>(tiles, s, x, pt, st, b, n, k, T, y);
+    else launch_tiled<kM, 32>(tiles, s, x, pt, st, b, n, k, T, y);
+}
+
+}  // namespace
+}  // namespace tq
+
+using namespace tq;
+
+extern "C" {
+
+int64_t tq_w4g128_tile_rows(int64_t n) {
+    if (n <= 0) return 8;
+    const int64_t cus = device_cu_count();
+    int64_t t = (n + cus - 1) / cus;  // one tile per CU where possible
+    t = (t + 7) / 8 * 8;
+    return t < 8 ? 8 : (t > 64 ? 64 : t);
+}
+
+int tq_repack_w4g128_tiled(const uint8_t* packed, const uint16_t* s_f16, int64_t n, int64_t k,
+                           int64_t tile_rows, uint8_t* packed_t, uint16_t* s_t, tq_stream_t stream) {
+    TQ_REQUIRE(n >= 0 && k >= 0, "tq_repack_w4g128_tiled: negative shape");
+    TQ_REQUIRE(k % 128 == 0, "tq_repack_w4g128_tiled: K=%lld is not a multiple of 128", (long long)k);
+    TQ_REQUIRE(tile_rows >= 8 && tile_rows <= 64 && tile_rows % 8 == 0,
+               "tq_repack_w4g128_tiled: tile_rows=%lld must be a multiple of 8 in [8, 64]", (long long)tile_rows);
+    if (n == 0 || k == 0) return TQ_OK;
+    TQ_REQUIRE(packed && s_f16 && packed_t && s_t, "tq_repack_w4g128_tiled: null pointer");
+    TQ_REQUIRE(aligned(packed, 16) && aligned(packed_t, 16) && aligned(s_f16, 2) && aligned(s_t, 2),
+               "tq_repack_w4g128_tiled: misaligned pointer (packed buffers need 16 B)");
+    const int64_t tiles = (n + tile_rows - 1) / tile_rows;
+    const int64_t total = tiles * (k >> 5) * tile_rows;
+    int64_t blocks = (total + 255) / 256;
+    if (blocks > 65536) blocks = 65536;
+    k_repack_tiled<<<static_cast<unsigned>(blocks), 256, 0, as_hip(stream)>>>(packed, s_f16, n, k,
+                                                                             static_cast<int>(tile_rows), tiles,
+                                                                             packed_t, s_t);
+    return check_launch("tq_repack_w4g128_tiled");
+}
+
+int tq_gemv_w4g128_tiled(const uint16_t* x_bf16, int64_t m, const uint8_t* packed_t, const uint16_t* s_t,
+                         const float* bias, int64_t n, int64_t k, int64_t tile_rows, float* y,
+                         tq_stream_t stream) {
+    TQ_REQUIRE(m >= 0 && n >= 0 && k >= 0, "tq_gemv_w4g128_tiled: negative shape");
+    TQ_REQUIRE(m <= 16, "tq_gemv_w4g128_tiled: M=%lld > 16", (long long)m);
+    TQ_REQUIRE(k % 128 == 0, "tq_gemv_w4g128_tiled: K=%lld is not a multiple of 128", (long long)k);
+    TQ_REQUIRE(tile_rows >= 8 && tile_rows <= 64 && tile_rows % 8 == 0,
+               "tq_gemv_w4g128_tiled: tile_rows=%lld must be a multiple of 8 in [8, 64]", (long long)tile_rows);
+    if (m == 0 || n == 0) return TQ_OK;
+    TQ_REQUIRE(k > 0 && y, "tq_gemv_w4g128_tiled: K=0 or null y");
+    const int64_t cpw = ((k >> 5) + kWaves - 1) / kWaves;
+    TQ_REQUIRE(cpw <= kMaxCPW, "tq_gemv_w4g128_tiled: K=%lld > %d", (long long)k, kMaxCPW * kWaves * 32);
+    TQ_REQUIRE(x_bf16 && packed_t && s_t, "tq_gemv_w4g128_tiled: null pointer");
+    TQ_REQUIRE(aligned(x_bf16, 8) && aligned(packed_t, 16) && aligned(s_t, 2) && (!bias || aligned(bias, 4)) &&
+                   aligned(y, 4),
+               "tq_gemv_w4g128_tiled: misaligned pointer (packed_t needs 16 B, x 8 B)");
+    const int64_t tiles = (n + tile_rows - 1) / tile_rows;
+    const int T = static_cast<int>(tile_rows);
+    const hipStream_t st = as_hip(stream);
+    for (int64_t m0 = 0; m0 < m; m0 += kMaxTok) {
+        const int64_t mm = (m - m0) < kMaxTok ? (m - m0) : kMaxTok;
+        const uint16_t* xp = x_bf16 + m0 * k;
+        float* yp = y + m0 * n;
+        if (mm == 1) dispatch_tiled<1>(cpw, tiles, st, xp, packed_t, s_t, bias, n, k, T, yp);
+        else if (mm == 2) dispatch_tiled<2>(cpw, tiles, st, xp, packed_t, s_t, bias, n, k, T, yp);
+        else if (mm == 3) dispatch_tiled<3>(cpw, tiles, st, xp, packed_t, s_t, bias, n, k, T, yp);
+        else dispatch_tiled<4>(cpw, tiles, st, xp, packed_t, s_t, bias, n, k, T, yp);
+        const int rc = check_launch("tq_gemv_w4g128_tiled");
+        if (rc != TQ_OK) return rc;
+    }
+    return TQ_OK;
+}
+
+}  // extern "C"

@@ -14,6 +14,8 @@ from .formats import (
     fake_quantize_per_channel_i8,
     quantize_i4_g128,
     quantize_per_channel_i8,
+    repack_i4_g128_tiled,
+    tile_rows_for,
 )
 from .nn import Module, QuantizedLinear, QuantizedMLP
 from .observer import MinMaxObserver, Observer, PerChannelMinMaxObserver
@@ -25,5 +27,5 @@ __all__ = [
     "QuantDType", "QConfig", "Observer", "MinMaxObserver", "PerChannelMinMaxObserver",
     "quantize_tensor", "dequantize_tensor", "quantize_per_tensor", "fake_quantize",
     "quantize_per_channel_i8", "dequantize_per_channel_i8", "fake_quantize_per_channel_i8",
-    "quantize_i4_g128", "dequantize_i4_g128", "Module", "QuantizedLinear", "QuantizedMLP",
+    "quantize_i4_g128", "dequantize_i4_g128", "repack_i4_g128_tiled", "tile_rows_for", "Module", "QuantizedLinear", "QuantizedMLP",
 ]

@@ -41,11 +41,15 @@ SIGNATURES = {
     "tq_dequantize_i4_g128": [_p, _p, _i64, _i64, _p, _p],
     "tq_gemv_w8": [_p, _i64, _p, _p, _p, _i64, _i64, _p, _p],
     "tq_gemv_w4g128": [_p, _i64, _p, _p, _p, _i64, _i64, _p, _p],
+    "tq_w4g128_tile_rows": [_i64],
+    "tq_repack_w4g128_tiled": [_p, _p, _i64, _i64, _i64, _p, _p, _p],
+    "tq_gemv_w4g128_tiled": [_p, _i64, _p, _p, _p, _i64, _i64, _i64, _p, _p],
     "tq_gemm_w8a8": [_p, _p, _p, _p, _p, _i64, _i64, _i64, _p, _p, _p],
     "tq_gemm_w4g128_bf16": [_p, _i64, _p, _p, _p, _i64, _i64, _p, _p],
     "tq_mlp_w4g128": [_p, _i64, _i64, _i64, _p, _p, _p, _p, _p, _p, _p, _p, _p],
 }
-_RESTYPE = {"tq_status_string": ctypes.c_char_p, "tq_last_error": ctypes.c_char_p}
+_RESTYPE = {"tq_status_string": ctypes.c_char_p, "tq_last_error": ctypes.c_char_p,
+            "tq_w4g128_tile_rows": ctypes.c_int64}
 
 _lib = None
 
@@ -67,7 +71,7 @@ def lib():
 
 
 def call(name, *args):
-    """Calls an entry point and raises the mapped exception on a bad status."""
+    """Calls a status-returning entry point and raises the mapped exception."""
     L = lib()
     st = getattr(L, name)(*args)
     if st != 0:

@@ -74,3 +74,23 @@ def dequantize_i4_g128(packed, scales):
     out = torch.empty((n, 2 * kh), dtype=torch.float32, device=p.device)
     _abi.call("tq_dequantize_i4_g128", ptr(p), ptr(s), n, 2 * kh, ptr(out), stream())
     return out
+
+
+def tile_rows_for(n: int) -> int:
+    """Tile height of the decode kernel layout for an N-row weight on this device."""
+    return int(_abi.lib().tq_w4g128_tile_rows(int(n)))
+
+
+def repack_i4_g128_tiled(packed, scales, tile_rows=None):
+    """Row-tiled kernel layout of a canonical INT4 g128 weight (a pure permutation,
+    rows padded to a multiple of tile_rows).  Returns (packed_t, s_t, tile_rows)."""
+    p = on_device(packed, torch.uint8, "repack_i4_g128_tiled")
+    s = on_device(scales, torch.float16, "repack_i4_g128_tiled")
+    n, kh = p.shape
+    k = 2 * kh
+    t = tile_rows_for(n) if tile_rows is None else int(tile_rows)
+    tiles = (n + t - 1) // t
+    pt = torch.empty(tiles * t * kh, dtype=torch.uint8, device=p.device)
+    st = torch.empty(tiles * t * (k // GROUP), dtype=torch.float16, device=p.device)
+    _abi.call("tq_repack_w4g128_tiled", ptr(p), ptr(s), n, k, t, ptr(pt), ptr(st), stream())
+    return pt, st, t

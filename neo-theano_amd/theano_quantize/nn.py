@@ -23,10 +23,11 @@ import torch
 from . import _abi
 from ._tensor import on_device, ptr, stream
 from .errors import InvalidArgument
-from .formats import quantize_i4_g128, quantize_per_channel_i8
+from .formats import quantize_i4_g128, quantize_per_channel_i8, repack_i4_g128_tiled
 from .qconfig import QConfig, QuantDType
 
 DECODE_MAX_M = 16
+TILED_MAX_M = 4  # the row-tiled GEMV wins up to 4 tokens, the MFMA decode kernel beyond
 
 
 class Module:
@@ -69,6 +70,10 @@ class QuantizedLinear(Module):
         self.qweight = qweight
         self.scales = scales
         self.bias = bias
+        self.tiled = None
+        if mode == "w4" and self.in_features <= 16384:
+            # decode kernel layout (a permutation of qweight) for M <= 16
+            self.tiled = repack_i4_g128_tiled(qweight, scales)
 
     @staticmethod
     def from_tensors(weight, bias=None, qconfig: QConfig | None = None) -> "QuantizedLinear":
@@ -111,9 +116,14 @@ class QuantizedLinear(Module):
         y = torch.empty((m, self.out_features), dtype=torch.float32, device=x.device)
         n, k = self.out_features, self.in_features
         if self.mode == "w4":
-            fn = "tq_gemv_w4g128" if m <= DECODE_MAX_M else "tq_gemm_w4g128_bf16"
-            _abi.call(fn, ptr(x), m, ptr(self.qweight), ptr(self.scales), ptr(self.bias), n, k,
-                      ptr(y), stream())
+            if m <= TILED_MAX_M and self.tiled is not None:
+                pt, st, t = self.tiled
+                _abi.call("tq_gemv_w4g128_tiled", ptr(x), m, ptr(pt), ptr(st), ptr(self.bias), n, k, t,
+                          ptr(y), stream())
+            else:
+                fn = "tq_gemv_w4g128" if m <= DECODE_MAX_M else "tq_gemm_w4g128_bf16"
+                _abi.call(fn, ptr(x), m, ptr(self.qweight), ptr(self.scales), ptr(self.bias), n, k,
+                          ptr(y), stream())
         elif self.mode == "w8":
             for m0 in range(0, m, DECODE_MAX_M):
                 mm = min(DECODE_MAX_M, m - m0)

@@ -109,6 +109,58 @@ def test_gemv_w4g128_config3(tq, c3, m):
     assert_close(host(y), ref[:m], RTOL, ATOL, f"gemv_w4g128 M={m}")
 
 
+def untile(pt, st, n, k, t):
+    """Inverse of the row-tiled kernel layout (numpy), for bit-exact checks."""
+    tiles = (n + t - 1) // t
+    p = pt.reshape(tiles, k // 32, t, 16).transpose(0, 2, 1, 3).reshape(tiles * t, k // 2)
+    s = st.reshape(tiles, k // 128, t).transpose(0, 2, 1).reshape(tiles * t, k // 128)
+    return p, s
+
+
+@pytest.mark.parametrize("n,k,t", [(14336, 4096, None), (100, 256, 8), (77, 1024, 64), (4096, 4096, None)])
+def test_repack_tiled_is_a_permutation(tq, n, k, t):
+    w = normal(57, (n, k), 0.02)
+    p, s = tq.quantize_i4_g128(dev_tensor(w))
+    pt, st, tr = tq.repack_i4_g128_tiled(p, s, t)
+    assert tr % 8 == 0 and 8 <= tr <= 64
+    up, us = untile(host(pt), host(st).view(np.uint16), n, k, tr)
+    assert np.array_equal(up[:n], host(p)) and np.array_equal(us[:n], host(s).view(np.uint16))
+    assert not up[n:].any() and not us[n:].any()  # padding rows are zero
+
+
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 8, 16])
+def test_gemv_w4g128_tiled_config3(tq, c3, m):
+    from theano_quantize import _abi
+    from theano_quantize._tensor import ptr, stream
+    import torch
+
+    xb, p, s, ref = c3
+    pt, st, t = tq.repack_i4_g128_tiled(p, s)
+    y = torch.empty((m, 14336), dtype=torch.float32, device="cuda")
+    xd = bf16_dev(xb[:m])
+    _abi.call("tq_gemv_w4g128_tiled", ptr(xd), m, ptr(pt), ptr(st), None, 14336, 4096, t, ptr(y), stream())
+    assert_close(host(y), ref[:m], RTOL, ATOL, f"gemv_w4g128_tiled M={m} T={t}")
+
+
+@pytest.mark.parametrize("n,k,m,t", [(100, 128, 1, 8), (7, 2176, 2, 8), (256, 14336, 1, 16), (48, 16384, 3, 24),
+                                     (1000, 4096, 4, 64), (333, 640, 2, 40)])
+def test_gemv_w4g128_tiled_shapes(tq, oracle, n, k, m, t):
+    from theano_quantize import _abi
+    from theano_quantize._tensor import ptr, stream
+    import torch
+
+    w = normal(58, (n, k), 0.02)
+    xb = to_bf16_bits(normal(58, (m, k), 1.0, stream=1))
+    b = normal(58, (n,), 0.1, stream=2)
+    p, s = tq.quantize_i4_g128(dev_tensor(w))
+    pt, st, tr = tq.repack_i4_g128_tiled(p, s, t)
+    y = torch.empty((m, n), dtype=torch.float32, device="cuda")
+    bd, xd = dev_tensor(b), bf16_dev(xb)
+    _abi.call("tq_gemv_w4g128_tiled", ptr(xd), m, ptr(pt), ptr(st), ptr(bd), n, k, tr, ptr(y), stream())
+    rp, rs = oracle.quantize_i4_g128(w)
+    assert_close(host(y), oracle.linear_w4g128_bf16(xb, rp, rs, b), RTOL, ATOL, f"tiled {n}x{k} M={m} T={t}")
+
+
 @pytest.mark.parametrize("n,k,m", [(100, 128, 1), (7, 2176, 2), (256, 14336, 1), (48, 16384, 3), (9, 4096, 16)])
 def test_gemv_w4g128_shapes_bias(tq, oracle, n, k, m):
     w = normal(51, (n, k), 0.02)

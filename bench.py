@@ -146,7 +146,7 @@ def main():
         w = normal_f32(2, (n3, k3), 0.02)
         p0, s0 = tq.quantize_i4_g128(dt(w))
         pt0, st0, tile = tq.repack_i4_g128_tiled(p0, s0)
-        copies = [(pt0.clone(), st0.clone(), p0.clone(), s0.clone()) for _ in range(rotation(2 * w4_bytes))]
+        copies = [(pt0.clone(), st0.clone(), p0.clone(), s0.clone()) for _ in range(rotation(w4_bytes))]
         del w, p0, s0, pt0, st0
         x = bf16(normal_f32(2, (16, k3), 1.0, stream=1))
         y = torch.empty((16, n3), dtype=torch.float32, device=dev)

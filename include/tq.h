@@ -183,7 +183,8 @@ int tq_gemv_w4g128_tiled(const uint16_t* x_bf16, int64_t m, const uint8_t* packe
 /* Prefill-shaped W8A8: activations already quantized per row (use
  * tq_quantize_i8_rowwise on X).  acc[i,j] = sum_p qa[i,p]*qw[j,p] (int32,
  * bit-exact); y = f32(acc) * sa[i] * sw[j] (+ bias[j]).  acc may be NULL.
- * K % 64 == 0, N % 16 == 0 (tile constraints), any M. */
+ * K % 16 == 0, N % 16 == 0 (tile constraints), any M; qa, qw, sw, bias, y and
+ * acc 16-byte aligned. */
 int tq_gemm_w8a8(const int8_t* qa, const float* sa, const int8_t* qw, const float* sw,
                  const float* bias, int64_t m, int64_t n, int64_t k, int32_t* acc,
                  float* y, tq_stream_t stream);

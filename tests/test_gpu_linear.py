@@ -214,7 +214,12 @@ def test_w8a8_config4_full(tq, oracle):
     assert_close(y[rows], oracle.linear_w8a8(qa[rows], sa[rows], qw, sw), RTOL, ATOL, "w8a8 y")
 
 
-@pytest.mark.parametrize("m,n,k", [(1, 16, 16), (130, 48, 208), (7, 272, 1024), (257, 128, 4096), (64, 160, 80)])
+# K % 128 == 0 takes the LDS-DMA kernel (1, 2, 3 and more stages; M, N tails; tile
+# groups with and without the XCD remap), other K the general kernel.
+@pytest.mark.parametrize("m,n,k", [(1, 16, 16), (130, 48, 208), (64, 160, 80),
+                                   (7, 272, 1024), (257, 128, 4096), (300, 512, 128),
+                                   (129, 4096, 256), (100, 272, 384), (384, 2048, 256),
+                                   (1, 256, 640), (1031, 528, 512)])
 def test_w8a8_shapes_bias(tq, oracle, m, n, k):
     x = normal(52, (m, k), 1.0)
     w = normal(52, (n, k), 0.02, stream=1)

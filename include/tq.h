@@ -74,20 +74,31 @@ int tq_qdtype_info(int qdtype, int* bits, int* is_signed, double* qmin, double* 
  * Vec<f64> (integral, within +-448, -0.0 and NaN included) is exactly
  * representable in f32, so the f32 buffer holds the reference's codes
  * bit-for-bit after widening.  Arithmetic is done in f64 on the GPU.
+ * Each primitive also has an _f64 form with f64 data in and out (the
+ * reference's own element type: Tensor storage and Vec<f64>), which returns
+ * exactly the reference's f64 results for any f64 input; the f32 forms are
+ * the device-native ones for f32 tensors.
  * ------------------------------------------------------------------------ */
 
 /* quantize_tensor (crates/theano-quantize/src/quantize.rs:8-19):
  *   q[i] = clamp(round(x[i]/scale + zero_point), qmin, qmax) */
 int tq_quantize_tensor(const float* x, int64_t n, double scale, double zero_point,
                        int qdtype, float* q, tq_stream_t stream);
+int tq_quantize_tensor_f64(const double* x, int64_t n, double scale, double zero_point,
+                           int qdtype, double* q, tq_stream_t stream);
 
 /* dequantize_tensor (quantize.rs:22-27): out[i] = f32((q[i] - zero_point) * scale) */
 int tq_dequantize_tensor(const float* q, int64_t n, double scale, double zero_point,
                          float* out, tq_stream_t stream);
+/* out[i] = (q[i] - zero_point) * scale in f64 (the reference's Vec<f64> result) */
+int tq_dequantize_tensor_f64(const double* q, int64_t n, double scale, double zero_point,
+                             double* out, tq_stream_t stream);
 
 /* fake_quantize (quantize.rs:51-55): out = f32(dequantize(quantize(x))) */
 int tq_fake_quantize(const float* x, int64_t n, double scale, double zero_point,
                      int qdtype, float* out, tq_stream_t stream);
+int tq_fake_quantize_f64(const double* x, int64_t n, double scale, double zero_point,
+                         int qdtype, double* out, tq_stream_t stream);
 
 /* quantize_per_tensor (quantize.rs:30-48): asymmetric scale/zero point from the
  * data's min/max, then quantize_tensor.  scale_zp (device, 2 doubles) receives
@@ -96,6 +107,8 @@ int tq_fake_quantize(const float* x, int64_t n, double scale, double zero_point,
 #define TQ_PER_TENSOR_WORKSPACE 64
 int tq_quantize_per_tensor(const float* x, int64_t n, int qdtype, float* q,
                            double* scale_zp, void* workspace, tq_stream_t stream);
+int tq_quantize_per_tensor_f64(const double* x, int64_t n, int qdtype, double* q,
+                               double* scale_zp, void* workspace, tq_stream_t stream);
 
 /* MinMaxObserver::{reset, observe} (crates/theano-quantize/src/observer.rs:42-73).
  * state (device, 2 floats) = {min, max}; reset sets {+inf, -inf}; observe
@@ -103,12 +116,17 @@ int tq_quantize_per_tensor(const float* x, int64_t n, int qdtype, float* q,
  * (see tq_observer_scale_zp). */
 int tq_minmax_reset(float* state, int64_t channels, tq_stream_t stream);
 int tq_minmax_observe(const float* x, int64_t n, float* state, tq_stream_t stream);
+/* the same with f64 values and an f64 state (channels x {min, max} doubles) */
+int tq_minmax_reset_f64(double* state, int64_t channels, tq_stream_t stream);
+int tq_minmax_observe_f64(const double* x, int64_t n, double* state, tq_stream_t stream);
 
 /* PerChannelMinMaxObserver::observe (observer.rs:110-121): values laid out
  * [channels, n/channels] (a trailing remainder is ignored, as in the
  * reference); state (device) = channels x {min, max}. */
 int tq_minmax_observe_per_channel(const float* x, int64_t n, int64_t channels,
                                   float* state, tq_stream_t stream);
+int tq_minmax_observe_per_channel_f64(const double* x, int64_t n, int64_t channels,
+                                      double* state, tq_stream_t stream);
 
 /* compute_scale_zero_point for one {min,max} pair (observer.rs:51-66,93-106).
  * Host-only scalar helper; initialized=0 gives (1, 0) as the reference does. */
@@ -152,12 +170,17 @@ int tq_dequantize_i4_g128(const uint8_t* packed, const uint16_t* s_f16, int64_t 
  * y is f32 [M, N]; bias (f32 [N]) may be NULL.
  * ------------------------------------------------------------------------ */
 
-/* Decode-shaped GEMV, INT8 per-row weights, f32 activations x [M, K], M <= 16. */
+/* Decode-shaped GEMV, INT8 per-row weights, f32 activations x [M, K], M <= 16
+ * (longer inputs run in chunks of 16 rows).  Any N, K; f32 pointers 4-byte
+ * aligned.  The tuned kernel serves K % 16 == 0, K <= 8192 with x and q 16-byte
+ * aligned; other shapes take a shape-general kernel. */
 int tq_gemv_w8(const float* x, int64_t m, const int8_t* q, const float* s,
                const float* bias, int64_t n, int64_t k, float* y, tq_stream_t stream);
 
 /* Decode-shaped GEMV, INT4 g128 weights (canonical layout), bf16 activations
- * x [M, K] (bf16 bits), M <= 16, K % 128 == 0, K <= 16384. */
+ * x [M, K] (bf16 bits), M <= 16, K % 128 == 0 (the format), any N.  The MFMA
+ * kernel serves K <= 16384 with x and packed 16-byte aligned; other cases take
+ * a shape-general kernel. */
 int tq_gemv_w4g128(const uint16_t* x_bf16, int64_t m, const uint8_t* packed,
                    const uint16_t* s_f16, const float* bias, int64_t n, int64_t k,
                    float* y, tq_stream_t stream);
@@ -183,15 +206,17 @@ int tq_gemv_w4g128_tiled(const uint16_t* x_bf16, int64_t m, const uint8_t* packe
 /* Prefill-shaped W8A8: activations already quantized per row (use
  * tq_quantize_i8_rowwise on X).  acc[i,j] = sum_p qa[i,p]*qw[j,p] (int32,
  * bit-exact); y = f32(acc) * sa[i] * sw[j] (+ bias[j]).  acc may be NULL.
- * K % 16 == 0, N % 16 == 0 (tile constraints), any M; qa, qw, sw, bias, y and
- * acc 16-byte aligned. */
+ * Any M, N, K.  The MFMA kernels serve N % 16 == 0 and K % 16 == 0 (the LDS-DMA
+ * kernel K % 128 == 0) with 16-byte aligned qa, qw, sw, bias, y and acc; other
+ * cases take a shape-general kernel. */
 int tq_gemm_w8a8(const int8_t* qa, const float* sa, const int8_t* qw, const float* sw,
                  const float* bias, int64_t m, int64_t n, int64_t k, int32_t* acc,
                  float* y, tq_stream_t stream);
 
 /* Prefill-shaped W4A16: x bf16 [M, K], INT4 g128 weights, f32 accumulation with
  * the group scale applied to each 128-long partial sum; y f32 [M, N].
- * K % 128 == 0, N % 16 == 0. */
+ * K % 128 == 0 (the format), any M, N.  The MFMA kernel serves N % 16 == 0 with
+ * 16-byte aligned x, packed, y and bias; other cases take a shape-general kernel. */
 int tq_gemm_w4g128_bf16(const uint16_t* x_bf16, int64_t m, const uint8_t* packed,
                         const uint16_t* s_f16, const float* bias, int64_t n, int64_t k,
                         float* y, tq_stream_t stream);

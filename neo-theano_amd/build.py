@@ -35,7 +35,7 @@ HIP_FLAGS = [
     f"-I{os.path.join(ROOT, 'include')}",
 ]
 
-SOURCES = ["tq_api.hip", "tq_quant.hip", "tq_gemv.hip", "tq_decode_w4.hip", "tq_decode_tiled.hip", "tq_gemm.hip", "tq_mlp.hip"]
+SOURCES = ["tq_api.hip", "tq_quant.hip", "tq_gemv.hip", "tq_decode_w4.hip", "tq_decode_tiled.hip", "tq_gemm.hip", "tq_mlp.hip", "tq_generic.hip"]
 
 
 def _run(cmd):
@@ -81,6 +81,23 @@ def build_host(verbose=False):
     return HOSTLIB
 
 
+def build_cpp_tests(verbose=False):
+    """C++ tests of the host layer (test infrastructure: links the C oracle)."""
+    src = os.path.join(ROOT, "tests", "cpp", "test_theano_quantize.cpp")
+    if not os.path.exists(src) or not os.path.exists(HOSTLIB):
+        return None
+    out = os.path.join(ROOT, "tests", "cpp", "test_theano_quantize")
+    tmp = out + ".tmp"
+    odir = os.path.join(ROOT, "oracle")
+    log = _run([HIPCC, "-O2", "-std=c++17", "-Wall", f"-I{os.path.join(ROOT, 'include')}", f"-I{HOST}", src,
+                "-o", tmp, f"-L{PKG}", "-ltheano_quantize_rocm", "-ltq", f"-L{odir}", "-ltq_oracle",
+                "-Wl,-rpath,$ORIGIN/../../neo-theano_amd", "-Wl,-rpath,$ORIGIN/../../oracle"])
+    if verbose and log.strip():
+        print(log)
+    os.replace(tmp, out)
+    return out
+
+
 def build_oracle():
     """The C oracle (test infrastructure) -- compiled, never linked into libtq."""
     odir = os.path.join(ROOT, "oracle")
@@ -99,6 +116,9 @@ def build_all(verbose=False):
     h = build_host(verbose=verbose)
     if h:
         libs.append(h)
+        t = build_cpp_tests(verbose=verbose)
+        if t:
+            libs.append(t)
     return libs
 
 

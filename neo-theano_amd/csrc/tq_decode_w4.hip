@@ -195,13 +195,13 @@ extern "C" int tq_gemv_w4g128(const uint16_t* x_bf16, int64_t m, const uint8_t* 
     TQ_REQUIRE(k % 128 == 0, "tq_gemv_w4g128: K=%lld is not a multiple of 128", (long long)k);
     if (m == 0 || n == 0) return TQ_OK;
     TQ_REQUIRE(y, "tq_gemv_w4g128: null y");
-    if (k == 0) return fail(TQ_EINVAL, "tq_gemv_w4g128: K=0");
+    TQ_REQUIRE(k == 0 || (x_bf16 && packed && s_f16), "tq_gemv_w4g128: null pointer");
+    TQ_REQUIRE(aligned(x_bf16, 2) && aligned(s_f16, 2) && (!bias || aligned(bias, 4)) && aligned(y, 4),
+               "tq_gemv_w4g128: misaligned pointer");
     const int64_t gpw = ((k >> 7) + kWaves - 1) / kWaves;
-    TQ_REQUIRE(gpw <= kMaxGPW, "tq_gemv_w4g128: K=%lld > %d", (long long)k, kMaxGPW * kWaves * 128);
-    TQ_REQUIRE(x_bf16 && packed && s_f16, "tq_gemv_w4g128: null pointer");
-    TQ_REQUIRE(aligned(x_bf16, 16) && aligned(packed, 16) && aligned(s_f16, 2) &&
-                   (!bias || aligned(bias, 4)) && aligned(y, 4),
-               "tq_gemv_w4g128: misaligned pointer (x and packed need 16 B)");
+    // the MFMA kernel keeps the tokens' K in LDS and streams 16-byte weight vectors
+    if (k == 0 || gpw > kMaxGPW || !aligned(x_bf16, 16) || !aligned(packed, 16))
+        return launch_linear_w4_generic(x_bf16, m, packed, s_f16, bias, n, k, y, as_hip(stream));
     const int64_t blocks = (n + kRowsPerBlock - 1) / kRowsPerBlock;
     TQ_REQUIRE(blocks < (int64_t(1) << 31), "tq_gemv_w4g128: N too large");
     const size_t lds_cap = 160 * 1024;

@@ -367,14 +367,15 @@ extern "C" int tq_gemm_w8a8(const int8_t* qa, const float* sa, const int8_t* qw,
                             const float* bias, int64_t m, int64_t n, int64_t k, int32_t* acc,
                             float* y, tq_stream_t stream) {
     TQ_REQUIRE(m >= 0 && n >= 0 && k >= 0, "tq_gemm_w8a8: negative shape");
-    TQ_REQUIRE(n % 16 == 0, "tq_gemm_w8a8: N=%lld is not a multiple of 16", (long long)n);
-    TQ_REQUIRE(k % 16 == 0, "tq_gemm_w8a8: K=%lld is not a multiple of 16", (long long)k);
     if (m == 0 || n == 0) return TQ_OK;
-    TQ_REQUIRE(k > 0, "tq_gemm_w8a8: K=0");
-    TQ_REQUIRE(qa && sa && qw && sw && y, "tq_gemm_w8a8: null pointer");
-    TQ_REQUIRE(aligned(qa, 16) && aligned(qw, 16) && aligned(sw, 16) && aligned(y, 16) &&
-                   (!acc || aligned(acc, 16)) && (!bias || aligned(bias, 16)) && aligned(sa, 4),
-               "tq_gemm_w8a8: misaligned pointer (qa, qw, sw, bias, y, acc need 16 B)");
+    TQ_REQUIRE(sa && sw && y && (k == 0 || (qa && qw)), "tq_gemm_w8a8: null pointer");
+    TQ_REQUIRE(aligned(sa, 4) && aligned(sw, 4) && aligned(y, 4) && (!acc || aligned(acc, 4)) &&
+                   (!bias || aligned(bias, 4)),
+               "tq_gemm_w8a8: misaligned pointer");
+    // the MFMA kernels tile N by 16 rows, K by 16-byte vectors, and store 16-byte vectors
+    if (k == 0 || n % 16 != 0 || k % 16 != 0 || !aligned(qa, 16) || !aligned(qw, 16) || !aligned(sw, 16) ||
+        !aligned(y, 16) || (acc && !aligned(acc, 16)) || (bias && !aligned(bias, 16)))
+        return launch_gemm_w8a8_generic(qa, sa, qw, sw, bias, m, n, k, acc, y, as_hip(stream));
     if (k % kDmaBK == 0 && m < (int64_t(1) << 31) && n < (int64_t(1) << 31) && k < (int64_t(1) << 31)) {
         const int64_t tm = (m + kDmaBM - 1) / kDmaBM, tn = (n + kDmaBN - 1) / kDmaBN;
         if (tm * tn < (int64_t(1) << 31)) {

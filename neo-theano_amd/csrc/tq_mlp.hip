@@ -333,13 +333,14 @@ int tq_gemm_w4g128_bf16(const uint16_t* x_bf16, int64_t m, const uint8_t* packed
                         tq_stream_t stream) {
     TQ_REQUIRE(m >= 0 && n >= 0 && k >= 0, "tq_gemm_w4g128_bf16: negative shape");
     TQ_REQUIRE(k % 128 == 0, "tq_gemm_w4g128_bf16: K=%lld is not a multiple of 128", (long long)k);
-    TQ_REQUIRE(n % 16 == 0, "tq_gemm_w4g128_bf16: N=%lld is not a multiple of 16", (long long)n);
     if (m == 0 || n == 0) return TQ_OK;
-    TQ_REQUIRE(k > 0, "tq_gemm_w4g128_bf16: K=0");
-    TQ_REQUIRE(x_bf16 && packed && s_f16 && y, "tq_gemm_w4g128_bf16: null pointer");
-    TQ_REQUIRE(aligned(x_bf16, 16) && aligned(packed, 16) && aligned(y, 16) && aligned(s_f16, 2) &&
-                   (!bias || aligned(bias, 16)),
-               "tq_gemm_w4g128_bf16: misaligned pointer (x, packed, y, bias need 16 B)");
+    TQ_REQUIRE(y && (k == 0 || (x_bf16 && packed && s_f16)), "tq_gemm_w4g128_bf16: null pointer");
+    TQ_REQUIRE(aligned(x_bf16, 2) && aligned(s_f16, 2) && aligned(y, 4) && (!bias || aligned(bias, 4)),
+               "tq_gemm_w4g128_bf16: misaligned pointer");
+    // the MFMA kernel tiles N by 16 rows and moves 16-byte vectors
+    if (k == 0 || n % 16 != 0 || !aligned(x_bf16, 16) || !aligned(packed, 16) || !aligned(y, 16) ||
+        (bias && !aligned(bias, 16)))
+        return launch_linear_w4_generic(x_bf16, m, packed, s_f16, bias, n, k, y, as_hip(stream));
     return launch_w4<kBF16, false, 128>(x_bf16, packed, s_f16, nullptr, nullptr, bias, m, n, k, y, n,
                                         as_hip(stream), "tq_gemm_w4g128_bf16");
 }

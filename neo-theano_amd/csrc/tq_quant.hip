@@ -32,17 +32,6 @@ __device__ __forceinline__ float block_max(float v, float* red) {
     return r;
 }
 
-__device__ __forceinline__ float block_min(float v, float* red) {
-    v = wave_min(v);
-    const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
-    if (lane == 0) red[wid] = v;
-    __syncthreads();
-    float r = red[0];
-#pragma unroll
-    for (int i = 1; i < kWavesPerBlock; ++i) r = fminf(r, red[i]);
-    return r;
-}
-
 // Symmetric absmax from a NaN-ignoring fold of |x| started at -inf: a row with
 // no non-NaN value folds to -inf, which the observer form
 // max(|min|, |max|) with min=+inf, max=-inf turns into +inf.
@@ -253,160 +242,208 @@ __device__ __forceinline__ double rust_clamp(double v, double lo, double hi) {
     return v;
 }
 
-__global__ __launch_bounds__(kBlock) void k_quantize_tensor(const float* __restrict__ x, int64_t n,
-                                                            double scale, double zp, double qmin,
-                                                            double qmax, float* __restrict__ q) {
+// ---- generic primitives: f64 arithmetic, elements f32 or f64 (TI in, TO out) ----
+
+template <typename TI, typename TO>
+__global__ __launch_bounds__(kBlock) void k_quantize_tensor(const TI* __restrict__ x, int64_t n, double scale,
+                                                            double zp, double qmin, double qmax,
+                                                            TO* __restrict__ q) {
     const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlock;
     for (int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; i < n; i += stride)
-        q[i] = static_cast<float>(rust_clamp(round(static_cast<double>(x[i]) / scale + zp), qmin, qmax));
+        q[i] = static_cast<TO>(rust_clamp(round(static_cast<double>(x[i]) / scale + zp), qmin, qmax));
 }
 
-__global__ __launch_bounds__(kBlock) void k_dequantize_tensor(const float* __restrict__ q, int64_t n,
-                                                              double scale, double zp,
-                                                              float* __restrict__ out) {
+template <typename TI, typename TO>
+__global__ __launch_bounds__(kBlock) void k_dequantize_tensor(const TI* __restrict__ q, int64_t n, double scale,
+                                                              double zp, TO* __restrict__ out) {
     const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlock;
     for (int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; i < n; i += stride)
-        out[i] = static_cast<float>((static_cast<double>(q[i]) - zp) * scale);
+        out[i] = static_cast<TO>((static_cast<double>(q[i]) - zp) * scale);
 }
 
-__global__ __launch_bounds__(kBlock) void k_fake_quantize(const float* __restrict__ x, int64_t n,
-                                                          double scale, double zp, double qmin,
-                                                          double qmax, float* __restrict__ out) {
+template <typename TI, typename TO>
+__global__ __launch_bounds__(kBlock) void k_fake_quantize(const TI* __restrict__ x, int64_t n, double scale,
+                                                          double zp, double qmin, double qmax,
+                                                          TO* __restrict__ out) {
     const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlock;
     for (int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; i < n; i += stride) {
         const double c = rust_clamp(round(static_cast<double>(x[i]) / scale + zp), qmin, qmax);
-        out[i] = static_cast<float>((c - zp) * scale);
+        out[i] = static_cast<TO>((c - zp) * scale);
     }
 }
 
-// Order-preserving int keys for non-NaN floats (atomic min/max on ints).
-__device__ __forceinline__ int float_key(float f) {
-    const int b = __float_as_int(f);
-    return b >= 0 ? b : b ^ 0x7FFFFFFF;
-}
-__device__ __forceinline__ float key_float(int k) { return __int_as_float(k >= 0 ? k : k ^ 0x7FFFFFFF); }
+// NaN-ignoring min / max (f64::min / f64::max, fminf / fmin)
+__device__ __forceinline__ float vmin(float a, float b) { return fminf(a, b); }
+__device__ __forceinline__ float vmax(float a, float b) { return fmaxf(a, b); }
+__device__ __forceinline__ double vmin(double a, double b) { return fmin(a, b); }
+__device__ __forceinline__ double vmax(double a, double b) { return fmax(a, b); }
 
-// workspace layout for quantize_per_tensor: int keys {min, max}
-__global__ void k_per_tensor_init(int* ws) {
+// Block-wide NaN-ignoring min and max, results valid in thread 0.
+template <typename T>
+__device__ __forceinline__ void block_minmax(T& mn, T& mx, T* red) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        mn = vmin(mn, __shfl_xor(mn, o, kWave));
+        mx = vmax(mx, __shfl_xor(mx, o, kWave));
+    }
+    const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
+    if (lane == 0) {
+        red[2 * wid] = mn;
+        red[2 * wid + 1] = mx;
+    }
+    __syncthreads();
     if (threadIdx.x == 0) {
-        ws[0] = float_key(INFINITY);
-        ws[1] = float_key(-INFINITY);
+#pragma unroll
+        for (int i = 1; i < kWavesPerBlock; ++i) {
+            mn = vmin(mn, red[2 * i]);
+            mx = vmax(mx, red[2 * i + 1]);
+        }
     }
 }
 
-// NaN-ignoring min/max of x folded into int keys (one atomic pair per block).
-__global__ __launch_bounds__(kBlock) void k_minmax_keys(const float* __restrict__ x, int64_t n,
-                                                        int* ws) {
-    __shared__ float red[kWavesPerBlock];
-    float mn = INFINITY, mx = -INFINITY;
+// Order-preserving integer keys of non-NaN values (atomic min/max on integers).
+template <typename T>
+struct OrderedKey;
+template <>
+struct OrderedKey<float> {
+    using K = int;
+    __device__ static K key(float f) {
+        const int b = __float_as_int(f);
+        return b >= 0 ? b : b ^ 0x7FFFFFFF;
+    }
+    __device__ static float val(K k) { return __int_as_float(k >= 0 ? k : k ^ 0x7FFFFFFF); }
+};
+template <>
+struct OrderedKey<double> {
+    using K = long long;
+    __device__ static K key(double f) {
+        const long long b = __double_as_longlong(f);
+        return b >= 0 ? b : b ^ 0x7FFFFFFFFFFFFFFFLL;
+    }
+    __device__ static double val(K k) { return __longlong_as_double(k >= 0 ? k : k ^ 0x7FFFFFFFFFFFFFFFLL); }
+};
+
+// workspace layout for quantize_per_tensor: keys {min, max}
+template <typename T>
+__global__ void k_per_tensor_init(typename OrderedKey<T>::K* ws) {
+    if (threadIdx.x == 0) {
+        ws[0] = OrderedKey<T>::key(static_cast<T>(INFINITY));
+        ws[1] = OrderedKey<T>::key(static_cast<T>(-INFINITY));
+    }
+}
+
+// NaN-ignoring min/max of x folded into keys (one atomic pair per block).
+template <typename T>
+__global__ __launch_bounds__(kBlock) void k_minmax_keys(const T* __restrict__ x, int64_t n,
+                                                        typename OrderedKey<T>::K* ws) {
+    __shared__ T red[2 * kWavesPerBlock];
+    T mn = static_cast<T>(INFINITY), mx = static_cast<T>(-INFINITY);
     const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlock;
     for (int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; i < n; i += stride) {
-        const float v = x[i];
-        mn = fminf(mn, v);
-        mx = fmaxf(mx, v);
+        const T v = x[i];
+        mn = vmin(mn, v);
+        mx = vmax(mx, v);
     }
-    mn = block_min(mn, red);
-    __syncthreads();
-    mx = block_max(mx, red);
+    block_minmax(mn, mx, red);
     if (threadIdx.x == 0) {
-        atomicMin(ws, float_key(mn));
-        atomicMax(ws + 1, float_key(mx));
+        atomicMin(ws, OrderedKey<T>::key(mn));
+        atomicMax(ws + 1, OrderedKey<T>::key(mx));
     }
 }
 
 // quantize.rs:33-40: scale = max((max-min)/(qmax-qmin), 1e-10), zp = clamp(round(qmin - min/scale))
-__device__ __forceinline__ void per_tensor_params(const int* ws, double qmin, double qmax,
+template <typename T>
+__device__ __forceinline__ void per_tensor_params(const typename OrderedKey<T>::K* ws, double qmin, double qmax,
                                                   double* scale, double* zp) {
-    const double mn = static_cast<double>(key_float(ws[0]));
-    const double mx = static_cast<double>(key_float(ws[1]));
+    const double mn = static_cast<double>(OrderedKey<T>::val(ws[0]));
+    const double mx = static_cast<double>(OrderedKey<T>::val(ws[1]));
     const double s = fmax((mx - mn) / (qmax - qmin), 1e-10);
     *scale = s;
     *zp = rust_clamp(round(qmin - mn / s), qmin, qmax);
 }
 
-__global__ __launch_bounds__(kBlock) void k_per_tensor_quantize(const float* __restrict__ x,
-                                                                int64_t n, const int* ws,
-                                                                double qmin, double qmax,
-                                                                float* __restrict__ q,
+template <typename T>
+__global__ __launch_bounds__(kBlock) void k_per_tensor_quantize(const T* __restrict__ x, int64_t n,
+                                                                const typename OrderedKey<T>::K* ws,
+                                                                double qmin, double qmax, T* __restrict__ q,
                                                                 double* scale_zp) {
     double s, zp;
-    per_tensor_params(ws, qmin, qmax, &s, &zp);
+    per_tensor_params<T>(ws, qmin, qmax, &s, &zp);
     if (blockIdx.x == 0 && threadIdx.x == 0) {
         scale_zp[0] = s;
         scale_zp[1] = zp;
     }
     const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlock;
     for (int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; i < n; i += stride)
-        q[i] = static_cast<float>(rust_clamp(round(static_cast<double>(x[i]) / s + zp), qmin, qmax));
+        q[i] = static_cast<T>(rust_clamp(round(static_cast<double>(x[i]) / s + zp), qmin, qmax));
 }
 
-// ---- observers: state = channels x {min, max} floats ----
-__global__ void k_minmax_reset(float* state, int64_t channels) {
+// ---- observers: state = channels x {min, max} ----
+template <typename T>
+__global__ void k_minmax_reset(T* state, int64_t channels) {
     const int64_t c = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
     if (c < channels) {
-        state[2 * c] = INFINITY;
-        state[2 * c + 1] = -INFINITY;
+        state[2 * c] = static_cast<T>(INFINITY);
+        state[2 * c + 1] = static_cast<T>(-INFINITY);
     }
 }
 
-// Folds the per-tensor min/max into state[0..1] with CAS loops (one per block).
-__device__ void atomic_fold_min(float* addr, float v) {
-    unsigned int* a = reinterpret_cast<unsigned int*>(addr);
-    unsigned int old = __atomic_load_n(a, __ATOMIC_RELAXED);
-    while (v < __uint_as_float(old)) {
-        const unsigned int prev = atomicCAS(a, old, __float_as_uint(v));
+// Folds a block's min/max into state[0..1] with compare-and-swap loops.
+__device__ __forceinline__ unsigned int as_bits(float v) { return __float_as_uint(v); }
+__device__ __forceinline__ unsigned long long as_bits(double v) {
+    return static_cast<unsigned long long>(__double_as_longlong(v));
+}
+__device__ __forceinline__ float from_bits(unsigned int b, float) { return __uint_as_float(b); }
+__device__ __forceinline__ double from_bits(unsigned long long b, double) {
+    return __longlong_as_double(static_cast<long long>(b));
+}
+
+template <bool kMax, typename T>
+__device__ void atomic_fold(T* addr, T v) {
+    using U = decltype(as_bits(v));
+    U* a = reinterpret_cast<U*>(addr);
+    U old = __atomic_load_n(a, __ATOMIC_RELAXED);
+    while (kMax ? (v > from_bits(old, v)) : (v < from_bits(old, v))) {
+        const U prev = atomicCAS(a, old, as_bits(v));
         if (prev == old) break;
         old = prev;
     }
 }
 
-__device__ void atomic_fold_max(float* addr, float v) {
-    unsigned int* a = reinterpret_cast<unsigned int*>(addr);
-    unsigned int old = __atomic_load_n(a, __ATOMIC_RELAXED);
-    while (v > __uint_as_float(old)) {
-        const unsigned int prev = atomicCAS(a, old, __float_as_uint(v));
-        if (prev == old) break;
-        old = prev;
-    }
-}
-
-__global__ __launch_bounds__(kBlock) void k_minmax_observe(const float* __restrict__ x, int64_t n,
-                                                           float* state) {
-    __shared__ float red[kWavesPerBlock];
-    float mn = INFINITY, mx = -INFINITY;
+template <typename T>
+__global__ __launch_bounds__(kBlock) void k_minmax_observe(const T* __restrict__ x, int64_t n, T* state) {
+    __shared__ T red[2 * kWavesPerBlock];
+    T mn = static_cast<T>(INFINITY), mx = static_cast<T>(-INFINITY);
     const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlock;
     for (int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; i < n; i += stride) {
-        const float v = x[i];
-        mn = fminf(mn, v);
-        mx = fmaxf(mx, v);
+        const T v = x[i];
+        mn = vmin(mn, v);
+        mx = vmax(mx, v);
     }
-    mn = block_min(mn, red);
-    __syncthreads();
-    mx = block_max(mx, red);
+    block_minmax(mn, mx, red);
     if (threadIdx.x == 0) {
-        atomic_fold_min(state, mn);
-        atomic_fold_max(state + 1, mx);
+        atomic_fold<false>(state, mn);
+        atomic_fold<true>(state + 1, mx);
     }
 }
 
 // One block per channel; channel c covers x[c*per, (c+1)*per).
-__global__ __launch_bounds__(kBlock) void k_minmax_observe_per_channel(const float* __restrict__ x,
-                                                                       int64_t per, float* state) {
-    __shared__ float red[kWavesPerBlock];
+template <typename T>
+__global__ __launch_bounds__(kBlock) void k_minmax_observe_per_channel(const T* __restrict__ x, int64_t per,
+                                                                       T* state) {
+    __shared__ T red[2 * kWavesPerBlock];
     const int64_t c = blockIdx.x;
-    const float* src = x + c * per;
-    float mn = INFINITY, mx = -INFINITY;
+    const T* src = x + c * per;
+    T mn = static_cast<T>(INFINITY), mx = static_cast<T>(-INFINITY);
     for (int64_t i = threadIdx.x; i < per; i += kBlock) {
-        const float v = src[i];
-        mn = fminf(mn, v);
-        mx = fmaxf(mx, v);
+        const T v = src[i];
+        mn = vmin(mn, v);
+        mx = vmax(mx, v);
     }
-    mn = block_min(mn, red);
-    __syncthreads();
-    mx = block_max(mx, red);
+    block_minmax(mn, mx, red);
     if (threadIdx.x == 0) {
-        state[2 * c] = fminf(state[2 * c], mn);
-        state[2 * c + 1] = fmaxf(state[2 * c + 1], mx);
+        state[2 * c] = vmin(state[2 * c], mn);
+        state[2 * c + 1] = vmax(state[2 * c + 1], mx);
     }
 }
 
@@ -508,85 +545,159 @@ int tq_dequantize_i4_g128(const uint8_t* packed, const uint16_t* s_f16, int64_t 
     return check_launch("tq_dequantize_i4_g128");
 }
 
-int tq_quantize_tensor(const float* x, int64_t n, double scale, double zero_point, int qdtype,
-                       float* q, tq_stream_t stream) {
+}  // extern "C"
+
+namespace tq {
+namespace {
+
+template <typename TI, typename TO>
+int quantize_tensor_impl(const TI* x, int64_t n, double scale, double zero_point, int qdtype, TO* q,
+                         tq_stream_t stream, const char* what) {
     double qmin, qmax;
     const int st = qrange(qdtype, &qmin, &qmax);
     if (st != TQ_OK) return st;
-    TQ_REQUIRE(n >= 0, "tq_quantize_tensor: negative size");
+    TQ_REQUIRE(n >= 0, "%s: negative size", what);
     if (n == 0) return TQ_OK;
-    TQ_REQUIRE(x && q, "tq_quantize_tensor: null pointer");
-    k_quantize_tensor<<<grid_for(n, kBlock, 65536), kBlock, 0, as_hip(stream)>>>(x, n, scale, zero_point,
-                                                                                 qmin, qmax, q);
-    return check_launch("tq_quantize_tensor");
+    TQ_REQUIRE(x && q, "%s: null pointer", what);
+    k_quantize_tensor<TI, TO><<<grid_for(n, kBlock, 65536), kBlock, 0, as_hip(stream)>>>(x, n, scale, zero_point,
+                                                                                         qmin, qmax, q);
+    return check_launch(what);
+}
+
+template <typename TI, typename TO>
+int dequantize_tensor_impl(const TI* q, int64_t n, double scale, double zero_point, TO* out, tq_stream_t stream,
+                           const char* what) {
+    TQ_REQUIRE(n >= 0, "%s: negative size", what);
+    if (n == 0) return TQ_OK;
+    TQ_REQUIRE(q && out, "%s: null pointer", what);
+    k_dequantize_tensor<TI, TO><<<grid_for(n, kBlock, 65536), kBlock, 0, as_hip(stream)>>>(q, n, scale,
+                                                                                           zero_point, out);
+    return check_launch(what);
+}
+
+template <typename TI, typename TO>
+int fake_quantize_impl(const TI* x, int64_t n, double scale, double zero_point, int qdtype, TO* out,
+                       tq_stream_t stream, const char* what) {
+    double qmin, qmax;
+    const int st = qrange(qdtype, &qmin, &qmax);
+    if (st != TQ_OK) return st;
+    TQ_REQUIRE(n >= 0, "%s: negative size", what);
+    if (n == 0) return TQ_OK;
+    TQ_REQUIRE(x && out, "%s: null pointer", what);
+    k_fake_quantize<TI, TO><<<grid_for(n, kBlock, 65536), kBlock, 0, as_hip(stream)>>>(x, n, scale, zero_point,
+                                                                                       qmin, qmax, out);
+    return check_launch(what);
+}
+
+template <typename T>
+int quantize_per_tensor_impl(const T* x, int64_t n, int qdtype, T* q, double* scale_zp, void* workspace,
+                             tq_stream_t stream, const char* what) {
+    double qmin, qmax;
+    const int st = qrange(qdtype, &qmin, &qmax);
+    if (st != TQ_OK) return st;
+    TQ_REQUIRE(n >= 0, "%s: negative size", what);
+    TQ_REQUIRE(scale_zp && workspace, "%s: null scale_zp/workspace", what);
+    TQ_REQUIRE(n == 0 || (x && q), "%s: null pointer", what);
+    TQ_REQUIRE(aligned(workspace, 16) && aligned(scale_zp, 8), "%s: misaligned workspace/scale_zp", what);
+    const hipStream_t s = as_hip(stream);
+    using K = typename OrderedKey<T>::K;
+    K* ws = static_cast<K*>(workspace);
+    k_per_tensor_init<T><<<1, kWave, 0, s>>>(ws);
+    if (n > 0) k_minmax_keys<T><<<grid_for(n, kBlock * 8, 4096), kBlock, 0, s>>>(x, n, ws);
+    k_per_tensor_quantize<T><<<grid_for(n, kBlock, 65536), kBlock, 0, s>>>(x, n, ws, qmin, qmax, q, scale_zp);
+    return check_launch(what);
+}
+
+template <typename T>
+int minmax_reset_impl(T* state, int64_t channels, tq_stream_t stream, const char* what) {
+    TQ_REQUIRE(state && channels > 0, "%s: null state or channels <= 0", what);
+    k_minmax_reset<T><<<grid_for(channels, kBlock, INT32_MAX), kBlock, 0, as_hip(stream)>>>(state, channels);
+    return check_launch(what);
+}
+
+template <typename T>
+int minmax_observe_impl(const T* x, int64_t n, T* state, tq_stream_t stream, const char* what) {
+    TQ_REQUIRE(n >= 0 && state, "%s: bad arguments", what);
+    if (n == 0) return TQ_OK;
+    TQ_REQUIRE(x && aligned(state, sizeof(T)), "%s: null/misaligned pointer", what);
+    k_minmax_observe<T><<<grid_for(n, kBlock * 8, 4096), kBlock, 0, as_hip(stream)>>>(x, n, state);
+    return check_launch(what);
+}
+
+template <typename T>
+int minmax_observe_per_channel_impl(const T* x, int64_t n, int64_t channels, T* state, tq_stream_t stream,
+                                    const char* what) {
+    TQ_REQUIRE(n >= 0 && channels > 0 && state, "%s: bad arguments", what);
+    TQ_REQUIRE(channels < (int64_t(1) << 31), "%s: too many channels", what);
+    const int64_t per = n / channels;
+    if (per == 0) return TQ_OK;
+    TQ_REQUIRE(x, "%s: null input", what);
+    k_minmax_observe_per_channel<T><<<static_cast<unsigned>(channels), kBlock, 0, as_hip(stream)>>>(x, per, state);
+    return check_launch(what);
+}
+
+}  // namespace
+}  // namespace tq
+
+extern "C" {
+
+int tq_quantize_tensor(const float* x, int64_t n, double scale, double zero_point, int qdtype, float* q,
+                       tq_stream_t stream) {
+    return quantize_tensor_impl(x, n, scale, zero_point, qdtype, q, stream, "tq_quantize_tensor");
+}
+int tq_quantize_tensor_f64(const double* x, int64_t n, double scale, double zero_point, int qdtype, double* q,
+                           tq_stream_t stream) {
+    return quantize_tensor_impl(x, n, scale, zero_point, qdtype, q, stream, "tq_quantize_tensor_f64");
 }
 
 int tq_dequantize_tensor(const float* q, int64_t n, double scale, double zero_point, float* out,
                          tq_stream_t stream) {
-    TQ_REQUIRE(n >= 0, "tq_dequantize_tensor: negative size");
-    if (n == 0) return TQ_OK;
-    TQ_REQUIRE(q && out, "tq_dequantize_tensor: null pointer");
-    k_dequantize_tensor<<<grid_for(n, kBlock, 65536), kBlock, 0, as_hip(stream)>>>(q, n, scale, zero_point,
-                                                                                   out);
-    return check_launch("tq_dequantize_tensor");
+    return dequantize_tensor_impl(q, n, scale, zero_point, out, stream, "tq_dequantize_tensor");
+}
+int tq_dequantize_tensor_f64(const double* q, int64_t n, double scale, double zero_point, double* out,
+                             tq_stream_t stream) {
+    return dequantize_tensor_impl(q, n, scale, zero_point, out, stream, "tq_dequantize_tensor_f64");
 }
 
-int tq_fake_quantize(const float* x, int64_t n, double scale, double zero_point, int qdtype,
-                     float* out, tq_stream_t stream) {
-    double qmin, qmax;
-    const int st = qrange(qdtype, &qmin, &qmax);
-    if (st != TQ_OK) return st;
-    TQ_REQUIRE(n >= 0, "tq_fake_quantize: negative size");
-    if (n == 0) return TQ_OK;
-    TQ_REQUIRE(x && out, "tq_fake_quantize: null pointer");
-    k_fake_quantize<<<grid_for(n, kBlock, 65536), kBlock, 0, as_hip(stream)>>>(x, n, scale, zero_point,
-                                                                               qmin, qmax, out);
-    return check_launch("tq_fake_quantize");
+int tq_fake_quantize(const float* x, int64_t n, double scale, double zero_point, int qdtype, float* out,
+                     tq_stream_t stream) {
+    return fake_quantize_impl(x, n, scale, zero_point, qdtype, out, stream, "tq_fake_quantize");
+}
+int tq_fake_quantize_f64(const double* x, int64_t n, double scale, double zero_point, int qdtype, double* out,
+                         tq_stream_t stream) {
+    return fake_quantize_impl(x, n, scale, zero_point, qdtype, out, stream, "tq_fake_quantize_f64");
 }
 
-int tq_quantize_per_tensor(const float* x, int64_t n, int qdtype, float* q, double* scale_zp,
-                           void* workspace, tq_stream_t stream) {
-    double qmin, qmax;
-    const int st = qrange(qdtype, &qmin, &qmax);
-    if (st != TQ_OK) return st;
-    TQ_REQUIRE(n >= 0, "tq_quantize_per_tensor: negative size");
-    TQ_REQUIRE(scale_zp && workspace, "tq_quantize_per_tensor: null scale_zp/workspace");
-    TQ_REQUIRE(n == 0 || (x && q), "tq_quantize_per_tensor: null pointer");
-    TQ_REQUIRE(aligned(workspace, 16) && aligned(scale_zp, 8),
-               "tq_quantize_per_tensor: misaligned workspace/scale_zp");
-    const hipStream_t s = as_hip(stream);
-    int* ws = static_cast<int*>(workspace);
-    k_per_tensor_init<<<1, kWave, 0, s>>>(ws);
-    if (n > 0) k_minmax_keys<<<grid_for(n, kBlock * 8, 4096), kBlock, 0, s>>>(x, n, ws);
-    k_per_tensor_quantize<<<grid_for(n, kBlock, 65536), kBlock, 0, s>>>(x, n, ws, qmin, qmax, q,
-                                                                        scale_zp);
-    return check_launch("tq_quantize_per_tensor");
+int tq_quantize_per_tensor(const float* x, int64_t n, int qdtype, float* q, double* scale_zp, void* workspace,
+                           tq_stream_t stream) {
+    return quantize_per_tensor_impl(x, n, qdtype, q, scale_zp, workspace, stream, "tq_quantize_per_tensor");
+}
+int tq_quantize_per_tensor_f64(const double* x, int64_t n, int qdtype, double* q, double* scale_zp,
+                               void* workspace, tq_stream_t stream) {
+    return quantize_per_tensor_impl(x, n, qdtype, q, scale_zp, workspace, stream, "tq_quantize_per_tensor_f64");
 }
 
 int tq_minmax_reset(float* state, int64_t channels, tq_stream_t stream) {
-    TQ_REQUIRE(state && channels > 0, "tq_minmax_reset: null state or channels <= 0");
-    k_minmax_reset<<<grid_for(channels, kBlock, INT32_MAX), kBlock, 0, as_hip(stream)>>>(state, channels);
-    return check_launch("tq_minmax_reset");
+    return minmax_reset_impl(state, channels, stream, "tq_minmax_reset");
+}
+int tq_minmax_reset_f64(double* state, int64_t channels, tq_stream_t stream) {
+    return minmax_reset_impl(state, channels, stream, "tq_minmax_reset_f64");
 }
 
 int tq_minmax_observe(const float* x, int64_t n, float* state, tq_stream_t stream) {
-    TQ_REQUIRE(n >= 0 && state, "tq_minmax_observe: bad arguments");
-    if (n == 0) return TQ_OK;
-    TQ_REQUIRE(x && aligned(state, 4), "tq_minmax_observe: null/misaligned pointer");
-    k_minmax_observe<<<grid_for(n, kBlock * 8, 4096), kBlock, 0, as_hip(stream)>>>(x, n, state);
-    return check_launch("tq_minmax_observe");
+    return minmax_observe_impl(x, n, state, stream, "tq_minmax_observe");
+}
+int tq_minmax_observe_f64(const double* x, int64_t n, double* state, tq_stream_t stream) {
+    return minmax_observe_impl(x, n, state, stream, "tq_minmax_observe_f64");
 }
 
 int tq_minmax_observe_per_channel(const float* x, int64_t n, int64_t channels, float* state,
                                   tq_stream_t stream) {
-    TQ_REQUIRE(n >= 0 && channels > 0 && state, "tq_minmax_observe_per_channel: bad arguments");
-    TQ_REQUIRE(channels < (int64_t(1) << 31), "tq_minmax_observe_per_channel: too many channels");
-    const int64_t per = n / channels;
-    if (per == 0) return TQ_OK;
-    TQ_REQUIRE(x, "tq_minmax_observe_per_channel: null input");
-    k_minmax_observe_per_channel<<<static_cast<unsigned>(channels), kBlock, 0, as_hip(stream)>>>(x, per,
-                                                                                               state);
-    return check_launch("tq_minmax_observe_per_channel");
+    return minmax_observe_per_channel_impl(x, n, channels, state, stream, "tq_minmax_observe_per_channel");
+}
+int tq_minmax_observe_per_channel_f64(const double* x, int64_t n, int64_t channels, double* state,
+                                      tq_stream_t stream) {
+    return minmax_observe_per_channel_impl(x, n, channels, state, stream, "tq_minmax_observe_per_channel_f64");
 }
 
 }  // extern "C"

@@ -1,0 +1,674 @@
+// theano_quantize.cpp -- C++ host layer over libtq.so (see theano_quantize.hpp).
+#include "theano_quantize.hpp"
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <numeric>
+
+namespace theano {
+
+namespace {
+
+// Throws the TheanoError of a failed libtq call (a GPU failure has no
+// Result to go into in the crate's infallible signatures either).
+void check(int status, const char* what) {
+    if (status != TQ_OK) throw TheanoError::from_status(status, what);
+}
+
+void check_hip(hipError_t e, const char* what) {
+    if (e == hipErrorOutOfMemory) throw TheanoError::out_of_memory(std::string(what) + ": out of device memory");
+    if (e != hipSuccess) throw TheanoError::runtime(std::string("HIP kernel launch error: ") + what + ": " +
+                                                    hipGetErrorString(e));
+}
+
+size_t shape_numel(const std::vector<size_t>& shape) {
+    return std::accumulate(shape.begin(), shape.end(), size_t{1}, [](size_t a, size_t b) { return a * b; });
+}
+
+std::string shape_str(const std::vector<size_t>& shape) {
+    std::string s = "[";
+    for (size_t i = 0; i < shape.size(); ++i) s += (i ? ", " : "") + std::to_string(shape[i]);
+    return s + "]";
+}
+
+// Runs `f` and turns a thrown TheanoError into an Err.
+template <class T, class F>
+Result<T> capture(F&& f) {
+    try {
+        return f();
+    } catch (const TheanoError& e) {
+        return e;
+    }
+}
+
+}  // namespace
+
+TheanoError TheanoError::from_status(int status, const char* what) {
+    const std::string msg = std::string(what) + ": " + tq_last_error();
+    switch (status) {
+        case TQ_EINVAL:
+            return invalid_argument(msg);
+        case TQ_ENOMEM:
+            return out_of_memory(msg);
+        default:
+            return runtime("HIP kernel launch error: " + msg);
+    }
+}
+
+// ----------------------------------------------------------------- Tensor
+
+Tensor Tensor::from_slice(std::vector<double> data, std::vector<size_t> shape) {
+    if (shape_numel(shape) != data.size())
+        throw TheanoError::shape_mismatch("Tensor::from_slice: " + std::to_string(data.size()) +
+                                          " values for shape " + shape_str(shape));
+    Tensor t;
+    t.data_ = std::move(data);
+    t.shape_ = std::move(shape);
+    return t;
+}
+
+Tensor Tensor::zeros(std::vector<size_t> shape) {
+    std::vector<double> d(shape_numel(shape), 0.0);
+    return from_slice(std::move(d), std::move(shape));
+}
+
+Tensor Tensor::ones(std::vector<size_t> shape) {
+    std::vector<double> d(shape_numel(shape), 1.0);
+    return from_slice(std::move(d), std::move(shape));
+}
+
+Result<double> Tensor::item() const {
+    if (data_.size() != 1)
+        return TheanoError::invalid_argument("item(): tensor has " + std::to_string(data_.size()) + " elements");
+    return data_[0];
+}
+
+// ----------------------------------------------------------------- DeviceBuffer
+
+namespace rocm {
+
+template <class T>
+DeviceBuffer<T>::DeviceBuffer(size_t n) : n_(n) {
+    if (n) check_hip(hipMalloc(reinterpret_cast<void**>(&p_), n * sizeof(T)), "hipMalloc");
+}
+
+template <class T>
+DeviceBuffer<T>::~DeviceBuffer() {
+    if (p_) (void)hipFree(p_);
+}
+
+template <class T>
+DeviceBuffer<T>& DeviceBuffer<T>::operator=(DeviceBuffer&& o) noexcept {
+    if (this != &o) {
+        if (p_) (void)hipFree(p_);
+        p_ = o.p_;
+        n_ = o.n_;
+        o.p_ = nullptr;
+        o.n_ = 0;
+    }
+    return *this;
+}
+
+template <class T>
+void DeviceBuffer<T>::upload(const T* src, size_t n, hipStream_t stream) {
+    if (n > n_) throw TheanoError::invalid_argument("DeviceBuffer::upload: too many elements");
+    if (!n) return;
+    check_hip(hipMemcpyAsync(p_, src, n * sizeof(T), hipMemcpyHostToDevice, stream), "upload");
+    check_hip(hipStreamSynchronize(stream), "upload");
+}
+
+template <class T>
+void DeviceBuffer<T>::download(T* dst, size_t n, hipStream_t stream) const {
+    if (n > n_) throw TheanoError::invalid_argument("DeviceBuffer::download: too many elements");
+    if (!n) return;
+    check_hip(hipMemcpyAsync(dst, p_, n * sizeof(T), hipMemcpyDeviceToHost, stream), "download");
+    check_hip(hipStreamSynchronize(stream), "download");
+}
+
+template <class T>
+std::vector<T> DeviceBuffer<T>::to_host(hipStream_t stream) const {
+    std::vector<T> v(n_);
+    download(v.data(), n_, stream);
+    return v;
+}
+
+template class DeviceBuffer<double>;
+template class DeviceBuffer<float>;
+template class DeviceBuffer<int8_t>;
+template class DeviceBuffer<uint8_t>;
+template class DeviceBuffer<uint16_t>;
+template class DeviceBuffer<int32_t>;
+
+}  // namespace rocm
+
+using rocm::DeviceBuffer;
+
+namespace quantize {
+
+// ----------------------------------------------------------------- QuantDType
+
+namespace {
+struct DTypeInfo {
+    int bits, is_signed;
+    double qmin, qmax;
+};
+DTypeInfo info(int q) {
+    DTypeInfo d{};
+    check(tq_qdtype_info(q, &d.bits, &d.is_signed, &d.qmin, &d.qmax), "QuantDType");
+    return d;
+}
+}  // namespace
+
+size_t QuantDType::bits() const { return static_cast<size_t>(info(abi()).bits); }
+bool QuantDType::is_signed() const { return info(abi()).is_signed != 0; }
+double QuantDType::qmin() const { return info(abi()).qmin; }
+double QuantDType::qmax() const { return info(abi()).qmax; }
+const char* QuantDType::name() const {
+    switch (k_) {
+        case Int8_:
+            return "Int8";
+        case UInt8_:
+            return "UInt8";
+        case Int4_:
+            return "Int4";
+        default:
+            return "FP8";
+    }
+}
+
+// ----------------------------------------------------------------- primitives
+
+Result<std::vector<double>> quantize_tensor(const Tensor& tensor, double scale, double zero_point,
+                                            QuantDType dtype) {
+    return capture<std::vector<double>>([&]() -> Result<std::vector<double>> {
+        const size_t n = tensor.numel();
+        DeviceBuffer<double> x(n), q(n);
+        x.upload(tensor.data(), n, nullptr);
+        const int st = tq_quantize_tensor_f64(x.data(), static_cast<int64_t>(n), scale, zero_point, dtype.abi(),
+                                              q.data(), nullptr);
+        if (st != TQ_OK) return TheanoError::from_status(st, "quantize_tensor");
+        return q.to_host(nullptr);
+    });
+}
+
+std::vector<double> dequantize_tensor(const std::vector<double>& quantized, double scale, double zero_point) {
+    const size_t n = quantized.size();
+    DeviceBuffer<double> q(n), out(n);
+    q.upload(quantized.data(), n, nullptr);
+    check(tq_dequantize_tensor_f64(q.data(), static_cast<int64_t>(n), scale, zero_point, out.data(), nullptr),
+          "dequantize_tensor");
+    return out.to_host(nullptr);
+}
+
+Result<std::tuple<std::vector<double>, double, double>> quantize_per_tensor(const Tensor& tensor,
+                                                                            QuantDType dtype) {
+    using R = std::tuple<std::vector<double>, double, double>;
+    return capture<R>([&]() -> Result<R> {
+        const size_t n = tensor.numel();
+        DeviceBuffer<double> x(n), q(n), szp(2);
+        DeviceBuffer<uint8_t> ws(TQ_PER_TENSOR_WORKSPACE);
+        x.upload(tensor.data(), n, nullptr);
+        const int st = tq_quantize_per_tensor_f64(x.data(), static_cast<int64_t>(n), dtype.abi(), q.data(),
+                                                  szp.data(), ws.data(), nullptr);
+        if (st != TQ_OK) return TheanoError::from_status(st, "quantize_per_tensor");
+        const std::vector<double> sz = szp.to_host(nullptr);
+        return R{q.to_host(nullptr), sz[0], sz[1]};
+    });
+}
+
+Result<Tensor> fake_quantize(const Tensor& tensor, double scale, double zero_point, QuantDType dtype) {
+    return capture<Tensor>([&]() -> Result<Tensor> {
+        const size_t n = tensor.numel();
+        DeviceBuffer<double> x(n), out(n);
+        x.upload(tensor.data(), n, nullptr);
+        const int st = tq_fake_quantize_f64(x.data(), static_cast<int64_t>(n), scale, zero_point, dtype.abi(),
+                                            out.data(), nullptr);
+        if (st != TQ_OK) return TheanoError::from_status(st, "fake_quantize");
+        return Tensor::from_slice(out.to_host(nullptr), tensor.shape());
+    });
+}
+
+// ----------------------------------------------------------------- observers
+
+namespace {
+std::pair<double, double> scale_zp(double mn, double mx, bool initialized, QuantDType dtype) {
+    double s = 0, z = 0;
+    check(tq_observer_scale_zp(mn, mx, initialized ? 1 : 0, dtype.abi(), &s, &z), "compute_scale_zero_point");
+    return {s, z};
+}
+}  // namespace
+
+MinMaxObserver::MinMaxObserver() : state_(2) { reset(); }
+
+void MinMaxObserver::observe(const std::vector<double>& values) {
+    DeviceBuffer<double> x(values.size());
+    x.upload(values.data(), values.size(), nullptr);
+    check(tq_minmax_observe_f64(x.data(), static_cast<int64_t>(values.size()), state_.data(), nullptr),
+          "MinMaxObserver::observe");
+    check_hip(hipStreamSynchronize(nullptr), "MinMaxObserver::observe");
+    initialized_ = true;
+}
+
+double MinMaxObserver::min_val() const { return state_.to_host(nullptr)[0]; }
+double MinMaxObserver::max_val() const { return state_.to_host(nullptr)[1]; }
+
+std::pair<double, double> MinMaxObserver::compute_scale_zero_point(QuantDType dtype) const {
+    const std::vector<double> st = state_.to_host(nullptr);
+    return scale_zp(st[0], st[1], initialized_, dtype);
+}
+
+void MinMaxObserver::reset() {
+    check(tq_minmax_reset_f64(state_.data(), 1, nullptr), "MinMaxObserver::reset");
+    initialized_ = false;
+}
+
+PerChannelMinMaxObserver::PerChannelMinMaxObserver(size_t num_channels)
+    : channels_(num_channels), state_(2 * num_channels) {
+    if (num_channels == 0) throw TheanoError::invalid_argument("PerChannelMinMaxObserver: zero channels");
+    reset();
+}
+
+void PerChannelMinMaxObserver::observe(const std::vector<double>& values) {
+    DeviceBuffer<double> x(values.size());
+    x.upload(values.data(), values.size(), nullptr);
+    check(tq_minmax_observe_per_channel_f64(x.data(), static_cast<int64_t>(values.size()),
+                                            static_cast<int64_t>(channels_), state_.data(), nullptr),
+          "PerChannelMinMaxObserver::observe");
+    check_hip(hipStreamSynchronize(nullptr), "PerChannelMinMaxObserver::observe");
+}
+
+std::vector<std::pair<double, double>> PerChannelMinMaxObserver::scales_and_zero_points(QuantDType dtype) const {
+    const std::vector<double> st = state_.to_host(nullptr);
+    std::vector<std::pair<double, double>> out;
+    out.reserve(channels_);
+    // observer.rs:93-106 has no `initialized` check
+    for (size_t c = 0; c < channels_; ++c) out.push_back(scale_zp(st[2 * c], st[2 * c + 1], true, dtype));
+    return out;
+}
+
+std::pair<double, double> PerChannelMinMaxObserver::compute_scale_zero_point(QuantDType dtype) const {
+    const auto sz = scales_and_zero_points(dtype);
+    double s = 0, z = 0;
+    for (const auto& p : sz) s += p.first;
+    for (const auto& p : sz) z += p.second;
+    return {s / static_cast<double>(sz.size()), z / static_cast<double>(sz.size())};
+}
+
+void PerChannelMinMaxObserver::reset() {
+    check(tq_minmax_reset_f64(state_.data(), static_cast<int64_t>(channels_), nullptr),
+          "PerChannelMinMaxObserver::reset");
+}
+
+// ----------------------------------------------------------------- weight formats
+
+namespace {
+
+// [rows, cols] view of a 2-D tensor's values rounded to f32
+std::vector<float> as_f32_matrix(const Tensor& w, const char* what, size_t* rows, size_t* cols) {
+    if (w.ndim() != 2)
+        throw TheanoError::invalid_argument(std::string(what) + ": weight must be 2-D, got " + shape_str(w.shape()));
+    *rows = w.shape()[0];
+    *cols = w.shape()[1];
+    std::vector<float> f(w.numel());
+    for (size_t i = 0; i < f.size(); ++i) f[i] = static_cast<float>(w.data()[i]);
+    return f;
+}
+
+Tensor to_tensor(const std::vector<float>& v, std::vector<size_t> shape) {
+    return Tensor::from_slice(std::vector<double>(v.begin(), v.end()), std::move(shape));
+}
+
+}  // namespace
+
+Result<Int8Weight> quantize_per_channel_i8(const Tensor& weight, hipStream_t stream) {
+    return capture<Int8Weight>([&]() -> Result<Int8Weight> {
+        Int8Weight w;
+        const std::vector<float> f = as_f32_matrix(weight, "quantize_per_channel_i8", &w.rows, &w.cols);
+        DeviceBuffer<float> src(f.size());
+        src.upload(f.data(), f.size(), stream);
+        w.codes = DeviceBuffer<int8_t>(w.rows * w.cols);
+        w.scales = DeviceBuffer<float>(w.rows);
+        const int st = tq_quantize_i8_rowwise(src.data(), static_cast<int64_t>(w.rows), static_cast<int64_t>(w.cols),
+                                              w.codes.data(), w.scales.data(),
+                                              reinterpret_cast<tq_stream_t>(stream));
+        if (st != TQ_OK) return TheanoError::from_status(st, "quantize_per_channel_i8");
+        check_hip(hipStreamSynchronize(stream), "quantize_per_channel_i8");
+        return std::move(w);
+    });
+}
+
+Result<Int4Weight> quantize_i4_g128(const Tensor& weight, hipStream_t stream) {
+    return capture<Int4Weight>([&]() -> Result<Int4Weight> {
+        Int4Weight w;
+        const std::vector<float> f = as_f32_matrix(weight, "quantize_i4_g128", &w.rows, &w.cols);
+        if (w.cols % 128 != 0)
+            return TheanoError::invalid_argument("quantize_i4_g128: K=" + std::to_string(w.cols) +
+                                                 " is not a multiple of the group size 128");
+        DeviceBuffer<float> src(f.size());
+        src.upload(f.data(), f.size(), stream);
+        w.packed = DeviceBuffer<uint8_t>(w.rows * w.cols / 2);
+        w.scales = DeviceBuffer<uint16_t>(w.rows * w.cols / 128);
+        const auto ts = reinterpret_cast<tq_stream_t>(stream);
+        int st = tq_quantize_i4_g128(src.data(), static_cast<int64_t>(w.rows), static_cast<int64_t>(w.cols),
+                                     w.packed.data(), w.scales.data(), ts);
+        if (st != TQ_OK) return TheanoError::from_status(st, "quantize_i4_g128");
+        if (w.cols <= 16384 && w.rows > 0) {
+            // row-tiled copy for the decode GEMV (a permutation of the packed bytes)
+            const int64_t t = tq_w4g128_tile_rows(static_cast<int64_t>(w.rows));
+            if (t <= 0) return TheanoError::runtime("quantize_i4_g128: tile size query failed");
+            const size_t padded = (w.rows + t - 1) / t * t;
+            w.packed_tiled = DeviceBuffer<uint8_t>(padded * w.cols / 2);
+            w.scales_tiled = DeviceBuffer<uint16_t>(padded * w.cols / 128);
+            st = tq_repack_w4g128_tiled(w.packed.data(), w.scales.data(), static_cast<int64_t>(w.rows),
+                                        static_cast<int64_t>(w.cols), t, w.packed_tiled.data(),
+                                        w.scales_tiled.data(), ts);
+            if (st != TQ_OK) return TheanoError::from_status(st, "quantize_i4_g128");
+            w.tile_rows = t;
+        }
+        check_hip(hipStreamSynchronize(stream), "quantize_i4_g128");
+        return std::move(w);
+    });
+}
+
+Result<Tensor> dequantize(const Int8Weight& w, hipStream_t stream) {
+    return capture<Tensor>([&]() -> Result<Tensor> {
+        DeviceBuffer<float> out(w.rows * w.cols);
+        const int st = tq_dequantize_i8_rowwise(w.codes.data(), w.scales.data(), static_cast<int64_t>(w.rows),
+                                                static_cast<int64_t>(w.cols), out.data(),
+                                                reinterpret_cast<tq_stream_t>(stream));
+        if (st != TQ_OK) return TheanoError::from_status(st, "dequantize");
+        return to_tensor(out.to_host(stream), {w.rows, w.cols});
+    });
+}
+
+Result<Tensor> dequantize(const Int4Weight& w, hipStream_t stream) {
+    return capture<Tensor>([&]() -> Result<Tensor> {
+        DeviceBuffer<float> out(w.rows * w.cols);
+        const int st = tq_dequantize_i4_g128(w.packed.data(), w.scales.data(), static_cast<int64_t>(w.rows),
+                                             static_cast<int64_t>(w.cols), out.data(),
+                                             reinterpret_cast<tq_stream_t>(stream));
+        if (st != TQ_OK) return TheanoError::from_status(st, "dequantize");
+        return to_tensor(out.to_host(stream), {w.rows, w.cols});
+    });
+}
+
+}  // namespace quantize
+
+// ----------------------------------------------------------------- nn
+
+namespace nn {
+
+using quantize::Int4Weight;
+using quantize::Int8Weight;
+using quantize::QConfig;
+using quantize::QuantDType;
+
+uint16_t f32_to_bf16(float x) {
+    uint32_t b;
+    std::memcpy(&b, &x, 4);
+    if ((b & 0x7F800000u) == 0x7F800000u && (b & 0x007FFFFFu)) return static_cast<uint16_t>((b >> 16) | 0x40);
+    b += 0x7FFFu + ((b >> 16) & 1u);  // round to nearest even
+    return static_cast<uint16_t>(b >> 16);
+}
+
+float bf16_to_f32(uint16_t h) {
+    const uint32_t b = static_cast<uint32_t>(h) << 16;
+    float f;
+    std::memcpy(&f, &b, 4);
+    return f;
+}
+
+std::vector<std::pair<std::string, Tensor>> Module::named_parameters() const {
+    std::vector<std::pair<std::string, Tensor>> out;
+    const auto ps = parameters();
+    for (size_t i = 0; i < ps.size(); ++i) out.emplace_back("param_" + std::to_string(i), ps[i]);
+    return out;
+}
+
+size_t Module::num_parameters() const {
+    size_t n = 0;
+    for (const auto& p : parameters()) n += p.numel();
+    return n;
+}
+
+std::map<std::string, Tensor> Module::state_dict() const {
+    std::map<std::string, Tensor> out;
+    for (auto& kv : named_parameters()) out.emplace(kv.first, kv.second);
+    return out;
+}
+
+namespace {
+
+// rows x cols activations of a 1-D or 2-D input; `squeeze` when 1-D
+std::vector<double> input_rows(const Tensor& x, size_t in, const char* what, size_t* m, bool* squeeze) {
+    if (x.ndim() == 1 && x.shape()[0] == in) {
+        *m = 1;
+        *squeeze = true;
+    } else if (x.ndim() == 2 && x.shape()[1] == in) {
+        *m = x.shape()[0];
+        *squeeze = false;
+    } else {
+        throw TheanoError::shape_mismatch(std::string(what) + ": expected [*, " + std::to_string(in) + "], got " +
+                                          shape_str(x.shape()));
+    }
+    return std::vector<double>(x.data(), x.data() + x.numel());
+}
+
+Tensor output_tensor(const std::vector<float>& y, size_t m, size_t n, bool squeeze) {
+    std::vector<double> d(y.begin(), y.end());
+    return squeeze ? Tensor::from_slice(std::move(d), {n}) : Tensor::from_slice(std::move(d), {m, n});
+}
+
+std::vector<uint16_t> to_bf16(const std::vector<double>& v) {
+    std::vector<uint16_t> out(v.size());
+    for (size_t i = 0; i < v.size(); ++i) out[i] = f32_to_bf16(static_cast<float>(v[i]));
+    return out;
+}
+
+}  // namespace
+
+Result<QuantizedLinear> QuantizedLinear::from_tensors(const Tensor& weight, const std::optional<Tensor>& bias,
+                                                      const QConfig& qconfig, hipStream_t stream) {
+    return capture<QuantizedLinear>([&]() -> Result<QuantizedLinear> {
+        QuantizedLinear l;
+        l.stream_ = stream;
+        if (qconfig.weight_dtype == QuantDType::Int4) {
+            l.mode_ = Mode::W4;
+            auto r = quantize::quantize_i4_g128(weight, stream);
+            if (r.is_err()) return r.unwrap_err();
+            l.w4_ = std::move(r).unwrap();
+            l.out_ = l.w4_.rows;
+            l.in_ = l.w4_.cols;
+        } else if (qconfig.weight_dtype == QuantDType::Int8) {
+            l.mode_ = qconfig.activation_dtype == QuantDType::Int8 ? Mode::W8A8 : Mode::W8;
+            auto r = quantize::quantize_per_channel_i8(weight, stream);
+            if (r.is_err()) return r.unwrap_err();
+            l.w8_ = std::move(r).unwrap();
+            l.out_ = l.w8_.rows;
+            l.in_ = l.w8_.cols;
+        } else {
+            return TheanoError::invalid_argument(std::string("QuantizedLinear: unsupported weight dtype ") +
+                                                 qconfig.weight_dtype.name());
+        }
+        if (bias) {
+            if (bias->numel() != l.out_)
+                return TheanoError::shape_mismatch("QuantizedLinear: bias " + shape_str(bias->shape()) +
+                                                   " for " + std::to_string(l.out_) + " outputs");
+            std::vector<float> b(l.out_);
+            for (size_t i = 0; i < l.out_; ++i) b[i] = static_cast<float>(bias->data()[i]);
+            l.bias_.emplace(l.out_);
+            l.bias_->upload(b.data(), b.size(), stream);
+        }
+        return std::move(l);
+    });
+}
+
+Result<void> QuantizedLinear::forward_device(const void* x, int64_t m, float* y, hipStream_t stream, int8_t* act_codes,
+                                             float* act_scales) const {
+    const auto ts = reinterpret_cast<tq_stream_t>(stream);
+    const float* b = bias_ ? bias_->data() : nullptr;
+    const int64_t n = static_cast<int64_t>(out_), k = static_cast<int64_t>(in_);
+    int st = TQ_OK;
+    switch (mode_) {
+        case Mode::W4: {
+            const auto* xb = static_cast<const uint16_t*>(x);
+            if (m <= 4 && w4_.tile_rows > 0)
+                st = tq_gemv_w4g128_tiled(xb, m, w4_.packed_tiled.data(), w4_.scales_tiled.data(), b, n, k,
+                                          w4_.tile_rows, y, ts);
+            else if (m <= 16)
+                st = tq_gemv_w4g128(xb, m, w4_.packed.data(), w4_.scales.data(), b, n, k, y, ts);
+            else
+                st = tq_gemm_w4g128_bf16(xb, m, w4_.packed.data(), w4_.scales.data(), b, n, k, y, ts);
+            break;
+        }
+        case Mode::W8: {
+            const auto* xf = static_cast<const float*>(x);
+            for (int64_t m0 = 0; m0 < m && st == TQ_OK; m0 += 16) {
+                const int64_t mm = std::min<int64_t>(16, m - m0);
+                st = tq_gemv_w8(xf + m0 * k, mm, w8_.codes.data(), w8_.scales.data(), b, n, k, y + m0 * n, ts);
+            }
+            break;
+        }
+        case Mode::W8A8: {
+            if (!act_codes || !act_scales)
+                return TheanoError::invalid_argument("QuantizedLinear::forward_device: w8a8 needs activation scratch");
+            st = tq_quantize_i8_rowwise(static_cast<const float*>(x), m, k, act_codes, act_scales, ts);
+            if (st == TQ_OK)
+                st = tq_gemm_w8a8(act_codes, act_scales, w8_.codes.data(), w8_.scales.data(), b, m, n, k, nullptr, y,
+                                  ts);
+            break;
+        }
+    }
+    if (st != TQ_OK) return TheanoError::from_status(st, "QuantizedLinear::forward");
+    return {};
+}
+
+Result<Tensor> QuantizedLinear::try_forward(const Tensor& input) const {
+    return capture<Tensor>([&]() -> Result<Tensor> {
+        size_t m = 0;
+        bool squeeze = false;
+        const std::vector<double> xv = input_rows(input, in_, "QuantizedLinear::forward", &m, &squeeze);
+        DeviceBuffer<float> y(m * out_);
+        Result<void> r;
+        if (mode_ == Mode::W4) {
+            const std::vector<uint16_t> xb = to_bf16(xv);
+            DeviceBuffer<uint16_t> xd(xb.size());
+            xd.upload(xb.data(), xb.size(), stream_);
+            r = forward_device(xd.data(), static_cast<int64_t>(m), y.data(), stream_);
+        } else {
+            const std::vector<float> xf(xv.begin(), xv.end());
+            DeviceBuffer<float> xd(xf.size());
+            xd.upload(xf.data(), xf.size(), stream_);
+            if (mode_ == Mode::W8A8) {
+                DeviceBuffer<int8_t> qa(m * in_);
+                DeviceBuffer<float> sa(m);
+                r = forward_device(xd.data(), static_cast<int64_t>(m), y.data(), stream_, qa.data(), sa.data());
+                if (r.is_ok()) check_hip(hipStreamSynchronize(stream_), "QuantizedLinear::forward");
+            } else {
+                r = forward_device(xd.data(), static_cast<int64_t>(m), y.data(), stream_);
+            }
+        }
+        if (r.is_err()) return r.unwrap_err();
+        return output_tensor(y.to_host(stream_), m, out_, squeeze);
+    });
+}
+
+Tensor QuantizedLinear::forward(const Tensor& input) const { return try_forward(input).unwrap(); }
+
+std::vector<std::pair<std::string, Tensor>> QuantizedLinear::named_parameters() const {
+    // codes and scales as f64 tensors, like the crate's f64 parameter data
+    std::vector<std::pair<std::string, Tensor>> out;
+    if (mode_ == Mode::W4) {
+        const auto p = w4_.packed.to_host(stream_);
+        const auto s = w4_.scales.to_host(stream_);
+        std::vector<double> codes(out_ * in_), sc(s.size());
+        for (size_t i = 0; i < p.size(); ++i) {
+            codes[2 * i] = static_cast<double>(static_cast<int8_t>(static_cast<uint8_t>(p[i] << 4)) >> 4);
+            codes[2 * i + 1] = static_cast<double>(static_cast<int8_t>(p[i]) >> 4);
+        }
+        for (size_t i = 0; i < s.size(); ++i) {
+            // f16 bits -> value
+            const uint16_t h = s[i];
+            const int e = (h >> 10) & 0x1F, f = h & 0x3FF;
+            const double mag = e ? std::ldexp(1.0 + f / 1024.0, e - 15) : std::ldexp(f / 1024.0, -14);
+            sc[i] = (h & 0x8000) ? -mag : mag;
+        }
+        out.emplace_back("weight", Tensor::from_slice(std::move(codes), {out_, in_}));
+        out.emplace_back("weight_scale", Tensor::from_slice(std::move(sc), {out_, in_ / 128}));
+    } else {
+        const auto q = w8_.codes.to_host(stream_);
+        const auto s = w8_.scales.to_host(stream_);
+        out.emplace_back("weight", Tensor::from_slice(std::vector<double>(q.begin(), q.end()), {out_, in_}));
+        out.emplace_back("weight_scale", Tensor::from_slice(std::vector<double>(s.begin(), s.end()), {out_}));
+    }
+    if (bias_) {
+        const auto b = bias_->to_host(stream_);
+        out.emplace_back("bias", Tensor::from_slice(std::vector<double>(b.begin(), b.end()), {out_}));
+    }
+    return out;
+}
+
+std::vector<Tensor> QuantizedLinear::parameters() const {
+    std::vector<Tensor> out;
+    for (auto& kv : named_parameters()) out.push_back(kv.second);
+    return out;
+}
+
+size_t QuantizedLinear::num_parameters() const { return in_ * out_ + (bias_ ? out_ : 0); }
+
+Result<QuantizedMLP> QuantizedMLP::from_tensors(const Tensor& gate, const Tensor& up, const Tensor& down,
+                                                hipStream_t stream) {
+    return capture<QuantizedMLP>([&]() -> Result<QuantizedMLP> {
+        if (gate.ndim() != 2 || up.shape() != gate.shape() || down.ndim() != 2 || down.shape()[0] != gate.shape()[1] ||
+            down.shape()[1] != gate.shape()[0])
+            return TheanoError::shape_mismatch("QuantizedMLP: gate/up must be [F, D] and down [D, F]");
+        QuantizedMLP mlp;
+        mlp.stream_ = stream;
+        mlp.f_ = gate.shape()[0];
+        mlp.d_ = gate.shape()[1];
+        for (auto [src, dst] : {std::pair{&gate, &mlp.gate_}, std::pair{&up, &mlp.up_}, std::pair{&down, &mlp.down_}}) {
+            auto r = quantize::quantize_i4_g128(*src, stream);
+            if (r.is_err()) return r.unwrap_err();
+            *dst = std::move(r).unwrap();
+        }
+        return std::move(mlp);
+    });
+}
+
+Result<void> QuantizedMLP::forward_device(const uint16_t* x, int64_t m, float* h, float* y, hipStream_t stream) const {
+    const int st = tq_mlp_w4g128(x, m, static_cast<int64_t>(d_), static_cast<int64_t>(f_), gate_.packed.data(),
+                                 gate_.scales.data(), up_.packed.data(), up_.scales.data(), down_.packed.data(),
+                                 down_.scales.data(), h, y, reinterpret_cast<tq_stream_t>(stream));
+    if (st != TQ_OK) return TheanoError::from_status(st, "QuantizedMLP::forward");
+    return {};
+}
+
+Result<Tensor> QuantizedMLP::try_forward(const Tensor& input) const {
+    return capture<Tensor>([&]() -> Result<Tensor> {
+        size_t m = 0;
+        bool squeeze = false;
+        const std::vector<double> xv = input_rows(input, d_, "QuantizedMLP::forward", &m, &squeeze);
+        const std::vector<uint16_t> xb = to_bf16(xv);
+        DeviceBuffer<uint16_t> xd(xb.size());
+        xd.upload(xb.data(), xb.size(), stream_);
+        DeviceBuffer<float> h(m * f_), y(m * d_);
+        auto r = forward_device(xd.data(), static_cast<int64_t>(m), h.data(), y.data(), stream_);
+        if (r.is_err()) return r.unwrap_err();
+        return output_tensor(y.to_host(stream_), m, d_, squeeze);
+    });
+}
+
+Tensor QuantizedMLP::forward(const Tensor& input) const { return try_forward(input).unwrap(); }
+
+std::vector<Tensor> QuantizedMLP::parameters() const {
+    std::vector<Tensor> out;
+    for (const Int4Weight* w : {&gate_, &up_, &down_}) {
+        auto t = quantize::dequantize(*w, stream_);
+        out.push_back(std::move(t).unwrap());
+    }
+    return out;
+}
+
+}  // namespace nn
+}  // namespace theano

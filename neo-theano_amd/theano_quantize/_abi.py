@@ -33,6 +33,13 @@ SIGNATURES = {
     "tq_minmax_reset": [_p, _i64, _p],
     "tq_minmax_observe": [_p, _i64, _p, _p],
     "tq_minmax_observe_per_channel": [_p, _i64, _i64, _p, _p],
+    "tq_quantize_tensor_f64": [_p, _i64, _dbl, _dbl, _int, _p, _p],
+    "tq_dequantize_tensor_f64": [_p, _i64, _dbl, _dbl, _p, _p],
+    "tq_fake_quantize_f64": [_p, _i64, _dbl, _dbl, _int, _p, _p],
+    "tq_quantize_per_tensor_f64": [_p, _i64, _int, _p, _p, _p, _p],
+    "tq_minmax_reset_f64": [_p, _i64, _p],
+    "tq_minmax_observe_f64": [_p, _i64, _p, _p],
+    "tq_minmax_observe_per_channel_f64": [_p, _i64, _i64, _p, _p],
     "tq_observer_scale_zp": [_dbl, _dbl, _int, _int, _p, _p],
     "tq_quantize_i8_rowwise": [_p, _i64, _i64, _p, _p, _p],
     "tq_dequantize_i8_rowwise": [_p, _p, _i64, _i64, _p, _p],

@@ -1,0 +1,522 @@
+// C++ tests of the host layer (neo-theano_amd/host/theano_quantize.hpp).
+//
+// The first groups restate the reference crate's own unit tests with the same
+// inputs and asserts (crates/theano-quantize/src/{qconfig,quantize,observer}.rs
+// and crates/theano-nn/src/linear.rs), run on the GPU through the C++ API.
+// The parity group compares the API's results with the C oracle (oracle/,
+// test infrastructure) on seeded inputs: f64 results bit-exact, Linear outputs
+// within 1e-3 relative / 1e-4 absolute of the oracle's f64 result.
+//
+// Usage: test_theano_quantize [--cpu]   (--cpu: only the tests that need no GPU)
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <functional>
+#include <random>
+#include <string>
+#include <vector>
+
+#include "../../oracle/tq_oracle.h"
+#include "theano_quantize.hpp"
+
+using namespace theano;
+using namespace theano::quantize;
+using theano::nn::QuantizedLinear;
+using theano::nn::QuantizedMLP;
+
+namespace {
+
+struct Case {
+    const char* name;
+    bool gpu;
+    std::function<void()> fn;
+};
+std::vector<Case>& registry() {
+    static std::vector<Case> r;
+    return r;
+}
+struct Reg {
+    Reg(const char* n, bool gpu, std::function<void()> f) { registry().push_back({n, gpu, std::move(f)}); }
+};
+
+struct Failure : std::runtime_error {
+    using std::runtime_error::runtime_error;
+};
+
+#define TEST_CPU(name)                                     \
+    void name();                                           \
+    static Reg reg_##name(#name, false, name);             \
+    void name()
+#define TEST_GPU(name)                                     \
+    void name();                                           \
+    static Reg reg_##name(#name, true, name);              \
+    void name()
+#define ASSERT(cond)                                                                                    \
+    do {                                                                                                \
+        if (!(cond)) throw Failure(std::string(__FILE__) + ":" + std::to_string(__LINE__) + ": " #cond); \
+    } while (0)
+#define ASSERT_EQ(a, b) ASSERT((a) == (b))
+
+// bitwise equality of f64 vectors (signed zeros included); any NaN equals any NaN
+bool same_bits(const std::vector<double>& a, const std::vector<double>& b) {
+    if (a.size() != b.size()) return false;
+    for (size_t i = 0; i < a.size(); ++i) {
+        if (std::isnan(a[i]) && std::isnan(b[i])) continue;
+        if (std::memcmp(&a[i], &b[i], 8) != 0) return false;
+    }
+    return true;
+}
+
+std::vector<double> randn(size_t n, double std, uint64_t seed) {
+    std::mt19937_64 g(seed);
+    std::normal_distribution<double> d(0.0, std);
+    std::vector<double> v(n);
+    for (auto& x : v) x = d(g);
+    return v;
+}
+
+void assert_close(const std::vector<double>& got, const std::vector<double>& ref, const char* what) {
+    ASSERT_EQ(got.size(), ref.size());
+    for (size_t i = 0; i < got.size(); ++i)
+        if (!(std::fabs(got[i] - ref[i]) <= 1e-4 + 1e-3 * std::fabs(ref[i])))
+            throw Failure(std::string(what) + ": element " + std::to_string(i) + " got " + std::to_string(got[i]) +
+                          " ref " + std::to_string(ref[i]));
+}
+
+// ------------------------------------------------------------ qconfig.rs:82-148
+
+TEST_CPU(test_quant_dtype_bits) {
+    ASSERT_EQ(QuantDType::Int8.bits(), 8u);
+    ASSERT_EQ(QuantDType::UInt8.bits(), 8u);
+    ASSERT_EQ(QuantDType::Int4.bits(), 4u);
+    ASSERT_EQ(QuantDType::FP8.bits(), 8u);
+}
+
+TEST_CPU(test_quant_dtype_signed) {
+    ASSERT(QuantDType::Int8.is_signed());
+    ASSERT(!QuantDType::UInt8.is_signed());
+    ASSERT(QuantDType::Int4.is_signed());
+    ASSERT(!QuantDType::FP8.is_signed());
+}
+
+TEST_CPU(test_quant_dtype_range) {
+    ASSERT_EQ(QuantDType::Int8.qmin(), -128.0);
+    ASSERT_EQ(QuantDType::Int8.qmax(), 127.0);
+    ASSERT_EQ(QuantDType::UInt8.qmin(), 0.0);
+    ASSERT_EQ(QuantDType::UInt8.qmax(), 255.0);
+    ASSERT_EQ(QuantDType::Int4.qmin(), -8.0);
+    ASSERT_EQ(QuantDType::Int4.qmax(), 7.0);
+    ASSERT_EQ(QuantDType::FP8.qmin(), -448.0);
+    ASSERT_EQ(QuantDType::FP8.qmax(), 448.0);
+}
+
+TEST_CPU(test_qconfig_default_int8) {
+    const QConfig cfg = QConfig::default_int8();
+    ASSERT(cfg.weight_dtype == QuantDType::Int8);
+    ASSERT(cfg.activation_dtype == QuantDType::UInt8);
+    ASSERT(cfg.symmetric);
+    ASSERT(!cfg.per_channel);
+}
+
+TEST_CPU(test_qconfig_default_int4) {
+    const QConfig cfg = QConfig::default_int4();
+    ASSERT(cfg.weight_dtype == QuantDType::Int4);
+    ASSERT(cfg.activation_dtype == QuantDType::Int8);
+    ASSERT(cfg.symmetric);
+    ASSERT(cfg.per_channel);
+}
+
+TEST_CPU(test_qconfig_default_trait) { ASSERT(QConfig::default_().weight_dtype == QuantDType::Int8); }
+
+TEST_CPU(test_quant_dtype_equality) {
+    ASSERT(QuantDType::Int8 == QuantDType::Int8);
+    ASSERT(QuantDType::Int8 != QuantDType::UInt8);
+}
+
+TEST_CPU(test_qconfig_clone) {
+    const QConfig cfg = QConfig::default_int8();
+    const QConfig cloned = cfg;
+    ASSERT(cloned.weight_dtype == cfg.weight_dtype);
+    ASSERT(cloned.activation_dtype == cfg.activation_dtype);
+    ASSERT_EQ(cloned.symmetric, cfg.symmetric);
+    ASSERT_EQ(cloned.per_channel, cfg.per_channel);
+}
+
+TEST_CPU(test_tensor_from_slice_checks_shape) {
+    bool threw = false;
+    try {
+        Tensor::from_slice({1.0, 2.0, 3.0}, {2, 2});
+    } catch (const TheanoError& e) {
+        threw = e.kind() == TheanoError::Kind::ShapeMismatch;
+    }
+    ASSERT(threw);
+    ASSERT_EQ(Tensor::scalar(2.5).item().unwrap(), 2.5);
+    ASSERT(Tensor::ones({2, 3}).item().is_err());
+}
+
+// ------------------------------------------------------------ quantize.rs:61-136
+
+TEST_GPU(test_quantize_dequantize_roundtrip) {
+    const Tensor tensor = Tensor::from_slice({0.0, 0.5, 1.0, -0.5, -1.0}, {5});
+    auto [quantized, scale, zp] = quantize_per_tensor(tensor, QuantDType::Int8).unwrap();
+    const auto dequantized = dequantize_tensor(quantized, scale, zp);
+    const auto original = tensor.to_vec_f64().unwrap();
+    for (size_t i = 0; i < original.size(); ++i) ASSERT(std::fabs(original[i] - dequantized[i]) < 0.05);
+}
+
+TEST_GPU(test_fake_quantize) {
+    const Tensor tensor = Tensor::from_slice({0.1, 0.5, 0.9}, {3});
+    const Tensor result = fake_quantize(tensor, 0.01, 0.0, QuantDType::Int8).unwrap();
+    ASSERT(result.shape() == std::vector<size_t>{3});
+}
+
+TEST_GPU(test_quantize_tensor_clamps) {
+    const Tensor tensor = Tensor::from_slice({1000.0, -1000.0}, {2});
+    const auto quantized = quantize_tensor(tensor, 1.0, 0.0, QuantDType::Int8).unwrap();
+    ASSERT_EQ(quantized[0], 127.0);
+    ASSERT_EQ(quantized[1], -128.0);
+}
+
+TEST_GPU(test_dequantize_tensor) {
+    const std::vector<double> quantized = {0.0, 64.0, 127.0};
+    const auto result = dequantize_tensor(quantized, 0.01, 0.0);
+    ASSERT_EQ(result.size(), 3u);
+    ASSERT(std::fabs(result[0] - 0.0) < 1e-10);
+    ASSERT(std::fabs(result[1] - 0.64) < 1e-10);
+    ASSERT(std::fabs(result[2] - 1.27) < 1e-10);
+}
+
+TEST_GPU(test_quantize_per_tensor_int4) {
+    const Tensor tensor = Tensor::from_slice({0.0, 0.5, 1.0}, {3});
+    auto [quantized, scale, zp] = quantize_per_tensor(tensor, QuantDType::Int4).unwrap();
+    ASSERT_EQ(quantized.size(), 3u);
+    for (double q : quantized) ASSERT(q >= -8.0 && q <= 7.0);
+    (void)scale;
+    (void)zp;
+}
+
+TEST_GPU(test_quantize_per_tensor_uint8) {
+    const Tensor tensor = Tensor::from_slice({0.0, 0.5, 1.0}, {3});
+    auto r = quantize_per_tensor(tensor, QuantDType::UInt8).unwrap();
+    for (double q : std::get<0>(r)) ASSERT(q >= 0.0 && q <= 255.0);
+}
+
+TEST_GPU(test_fake_quantize_preserves_shape) {
+    const Tensor tensor = Tensor::from_slice({1.0, 2.0, 3.0, 4.0, 5.0, 6.0}, {2, 3});
+    const Tensor result = fake_quantize(tensor, 0.1, 0.0, QuantDType::Int8).unwrap();
+    ASSERT((result.shape() == std::vector<size_t>{2, 3}));
+}
+
+TEST_GPU(test_quantize_single_value) {
+    const Tensor tensor = Tensor::from_slice({0.5, -0.5}, {2});
+    auto [quantized, scale, zp] = quantize_per_tensor(tensor, QuantDType::Int8).unwrap();
+    const auto dequantized = dequantize_tensor(quantized, scale, zp);
+    ASSERT(std::fabs(0.5 - dequantized[0]) < 0.05);
+    ASSERT(std::fabs(-0.5 - dequantized[1]) < 0.05);
+}
+
+// ------------------------------------------------------------ observer.rs:142-223
+
+TEST_GPU(test_minmax_observer_basic) {
+    MinMaxObserver obs;
+    obs.observe({1.0, 2.0, 3.0, -1.0});
+    ASSERT_EQ(obs.min_val(), -1.0);
+    ASSERT_EQ(obs.max_val(), 3.0);
+}
+
+TEST_GPU(test_minmax_observer_multiple_observations) {
+    MinMaxObserver obs;
+    obs.observe({1.0, 2.0});
+    obs.observe({-5.0, 10.0});
+    ASSERT_EQ(obs.min_val(), -5.0);
+    ASSERT_EQ(obs.max_val(), 10.0);
+}
+
+TEST_GPU(test_minmax_observer_uninitialized) {
+    const MinMaxObserver obs;
+    auto [scale, zp] = obs.compute_scale_zero_point(QuantDType::Int8);
+    ASSERT_EQ(scale, 1.0);
+    ASSERT_EQ(zp, 0.0);
+}
+
+TEST_GPU(test_minmax_observer_scale_zero_point) {
+    MinMaxObserver obs;
+    obs.observe({0.0, 1.0});
+    auto [scale, zp] = obs.compute_scale_zero_point(QuantDType::UInt8);
+    ASSERT(std::fabs(scale - 1.0 / 255.0) < 1e-6);
+    (void)zp;
+}
+
+TEST_GPU(test_minmax_observer_reset) {
+    MinMaxObserver obs;
+    obs.observe({1.0, 2.0});
+    obs.reset();
+    ASSERT_EQ(obs.min_val(), INFINITY);
+    ASSERT_EQ(obs.max_val(), -INFINITY);
+    auto [scale, zp] = obs.compute_scale_zero_point(QuantDType::Int8);
+    ASSERT_EQ(scale, 1.0);
+    ASSERT_EQ(zp, 0.0);
+}
+
+TEST_GPU(test_per_channel_observer) {
+    PerChannelMinMaxObserver obs(2);
+    obs.observe({1.0, 2.0, 3.0, -1.0, 0.0, 1.0});
+    ASSERT_EQ(obs.scales_and_zero_points(QuantDType::Int8).size(), 2u);
+}
+
+TEST_GPU(test_per_channel_observer_reset) {
+    PerChannelMinMaxObserver obs(3);
+    obs.observe({1.0, 2.0, 3.0});
+    obs.reset();
+    auto [scale, zp] = obs.compute_scale_zero_point(QuantDType::Int8);
+    ASSERT(scale > 0.0);
+    (void)zp;
+}
+
+TEST_GPU(test_minmax_observer_default) {
+    const MinMaxObserver obs = MinMaxObserver::default_();
+    ASSERT_EQ(obs.min_val(), INFINITY);
+    ASSERT_EQ(obs.max_val(), -INFINITY);
+}
+
+TEST_GPU(test_per_channel_compute_global_scale) {
+    PerChannelMinMaxObserver obs(2);
+    obs.observe({0.0, 1.0, 0.0, 2.0});
+    auto [scale, zp] = obs.compute_scale_zero_point(QuantDType::Int8);
+    ASSERT(scale > 0.0);
+    (void)zp;
+}
+
+// ------------------------------------------------------------ linear.rs:145-174 (quantized)
+
+TEST_GPU(test_quantized_linear_shape) {
+    const Tensor w = Tensor::from_slice(randn(5 * 10, 0.5, 1), {5, 10});
+    const Tensor b = Tensor::from_slice(randn(5, 0.1, 2), {5});
+    const QuantizedLinear layer = QuantizedLinear::from_tensors(w, b).unwrap();
+    ASSERT_EQ(layer.in_features(), 10u);
+    ASSERT_EQ(layer.out_features(), 5u);
+    ASSERT((layer.parameters()[0].shape() == std::vector<size_t>{5, 10}));
+    ASSERT_EQ(layer.parameters().size(), 3u);  // codes, scales, bias
+    ASSERT_EQ(layer.num_parameters(), 55u);
+}
+
+TEST_GPU(test_quantized_linear_forward_shape) {
+    const Tensor w = Tensor::from_slice(randn(2 * 3, 0.5, 3), {2, 3});
+    const QuantizedLinear layer = QuantizedLinear::from_tensors(w, std::nullopt).unwrap();
+    const Tensor out = layer.forward(Tensor::ones({4, 3}));
+    ASSERT((out.shape() == std::vector<size_t>{4, 2}));
+    ASSERT((layer.forward(Tensor::ones({3})).shape() == std::vector<size_t>{2}));
+}
+
+TEST_GPU(test_quantized_linear_errors) {
+    const Tensor w = Tensor::from_slice(randn(4 * 8, 0.5, 4), {4, 8});
+    const QuantizedLinear layer = QuantizedLinear::from_tensors(w, std::nullopt).unwrap();
+    auto r = layer.try_forward(Tensor::ones({2, 7}));
+    ASSERT(r.is_err() && r.unwrap_err().kind() == TheanoError::Kind::ShapeMismatch);
+    // INT4 g128 needs K % 128 == 0
+    auto r4 = QuantizedLinear::from_tensors(Tensor::ones({4, 100}), std::nullopt, QConfig::default_int4());
+    ASSERT(r4.is_err() && r4.unwrap_err().kind() == TheanoError::Kind::InvalidArgument);
+    auto rb = QuantizedLinear::from_tensors(w, Tensor::ones({3}));
+    ASSERT(rb.is_err() && rb.unwrap_err().kind() == TheanoError::Kind::ShapeMismatch);
+}
+
+// ------------------------------------------------------------ parity with the oracle
+
+TEST_GPU(test_parity_primitives_f64) {
+    // f64 inputs, including values no f32 holds, and exact ties
+    std::vector<double> x = randn(4099, 3.0, 11);
+    x[0] = 2.5;
+    x[1] = -2.5;
+    x[2] = 0.1 + 1e-12;
+    x[3] = NAN;
+    x[4] = -0.3;
+    x[5] = 1e300;
+    const Tensor t = Tensor::from_slice(x, {x.size()});
+    for (QuantDType dt : {QuantDType::Int8, QuantDType::UInt8, QuantDType::Int4, QuantDType::FP8}) {
+        const double s = 0.037, zp = dt == QuantDType::UInt8 ? 128.0 : 0.0;
+        std::vector<double> ref(x.size());
+        tqo_quantize_tensor(x.data(), static_cast<int64_t>(x.size()), s, zp, dt.abi(), ref.data());
+        const auto q = quantize_tensor(t, s, zp, dt).unwrap();
+        ASSERT(same_bits(q, ref));
+        std::vector<double> dref(x.size());
+        tqo_dequantize_tensor(ref.data(), static_cast<int64_t>(x.size()), s, zp, dref.data());
+        ASSERT(same_bits(dequantize_tensor(q, s, zp), dref));
+        std::vector<double> fref(x.size());
+        tqo_fake_quantize(x.data(), static_cast<int64_t>(x.size()), s, zp, dt.abi(), fref.data());
+        ASSERT(same_bits(fake_quantize(t, s, zp, dt).unwrap().to_vec_f64().unwrap(), fref));
+    }
+    std::vector<double> y = randn(1000, 2.0, 12);
+    y[7] = NAN;
+    const Tensor ty = Tensor::from_slice(y, {y.size()});
+    for (QuantDType dt : {QuantDType::Int8, QuantDType::UInt8, QuantDType::Int4}) {
+        std::vector<double> ref(y.size());
+        double rs = 0, rz = 0;
+        tqo_quantize_per_tensor(y.data(), static_cast<int64_t>(y.size()), dt.abi(), ref.data(), &rs, &rz);
+        auto [q, s, z] = quantize_per_tensor(ty, dt).unwrap();
+        ASSERT(same_bits(q, ref));
+        ASSERT_EQ(s, rs);
+        ASSERT_EQ(z, rz);
+    }
+}
+
+TEST_GPU(test_parity_observers_f64) {
+    const std::vector<double> a = randn(777, 1.5, 21), b = randn(333, 4.0, 22);
+    MinMaxObserver obs;
+    obs.observe(a);
+    obs.observe(b);
+    double st[3] = {INFINITY, -INFINITY, 0.0};
+    tqo_minmax_observe(st, a.data(), static_cast<int64_t>(a.size()));
+    tqo_minmax_observe(st, b.data(), static_cast<int64_t>(b.size()));
+    ASSERT_EQ(obs.min_val(), st[0]);
+    ASSERT_EQ(obs.max_val(), st[1]);
+    for (QuantDType dt : {QuantDType::Int8, QuantDType::UInt8, QuantDType::Int4}) {
+        double rs, rz;
+        tqo_minmax_scale_zp(st, dt.abi(), &rs, &rz);
+        auto [s, z] = obs.compute_scale_zero_point(dt);
+        ASSERT_EQ(s, rs);
+        ASSERT_EQ(z, rz);
+    }
+    const size_t ch = 7;
+    PerChannelMinMaxObserver pc(ch);
+    std::vector<double> mins(ch, INFINITY), maxs(ch, -INFINITY);
+    pc.observe(a);  // 777 = 7 x 111, no remainder
+    tqo_perchannel_observe(mins.data(), maxs.data(), ch, a.data(), static_cast<int64_t>(a.size()));
+    pc.observe(b);  // 333 = 7 x 47 + 4: the remainder is ignored
+    tqo_perchannel_observe(mins.data(), maxs.data(), ch, b.data(), static_cast<int64_t>(b.size()));
+    std::vector<double> rs(ch), rz(ch);
+    tqo_perchannel_scales_zps(mins.data(), maxs.data(), ch, TQ_QINT8, rs.data(), rz.data());
+    const auto sz = pc.scales_and_zero_points(QuantDType::Int8);
+    for (size_t c = 0; c < ch; ++c) {
+        ASSERT_EQ(sz[c].first, rs[c]);
+        ASSERT_EQ(sz[c].second, rz[c]);
+    }
+    double gs, gz;
+    tqo_perchannel_global_scale_zp(mins.data(), maxs.data(), ch, TQ_QINT8, &gs, &gz);
+    auto [s, z] = pc.compute_scale_zero_point(QuantDType::Int8);
+    ASSERT_EQ(s, gs);
+    ASSERT_EQ(z, gz);
+}
+
+// weights as the f32 values the device formats hold
+std::vector<float> f32(const std::vector<double>& v) { return std::vector<float>(v.begin(), v.end()); }
+
+TEST_GPU(test_parity_quantized_linear_w8) {
+    const size_t n = 300, k = 512, m = 3;
+    const auto wv = randn(n * k, 0.02, 31), xv = randn(m * k, 1.0, 32), bv = randn(n, 0.1, 33);
+    const QuantizedLinear layer =
+        QuantizedLinear::from_tensors(Tensor::from_slice(wv, {n, k}), Tensor::from_slice(bv, {n})).unwrap();
+    ASSERT(layer.mode() == QuantizedLinear::Mode::W8);
+    const auto y = layer.forward(Tensor::from_slice(xv, {m, k})).to_vec_f64().unwrap();
+    const auto w32 = f32(wv), x32 = f32(xv), b32 = f32(bv);
+    std::vector<int8_t> q(n * k);
+    std::vector<float> s(n);
+    tqo_quantize_i8_rowwise(w32.data(), n, k, q.data(), s.data());
+    std::vector<double> ref(m * n);
+    tqo_linear_w8(x32.data(), m, q.data(), s.data(), b32.data(), n, k, ref.data());
+    assert_close(y, ref, "w8 linear");
+}
+
+TEST_GPU(test_parity_quantized_linear_w4) {
+    const size_t n = 200, k = 1024;
+    const auto wv = randn(n * k, 0.02, 41);
+    const QuantizedLinear layer =
+        QuantizedLinear::from_tensors(Tensor::from_slice(wv, {n, k}), std::nullopt, QConfig::default_int4()).unwrap();
+    const auto w32 = f32(wv);
+    std::vector<uint8_t> p(n * k / 2);
+    std::vector<uint16_t> s(n * k / 128);
+    tqo_quantize_i4_g128(w32.data(), n, k, p.data(), s.data());
+    for (size_t m : {1u, 3u, 9u, 40u}) {  // tiled GEMV, MFMA GEMV, W4A16 GEMM
+        const auto xv = randn(m * k, 1.0, 42 + m);
+        const auto y = layer.forward(Tensor::from_slice(xv, {m, k})).to_vec_f64().unwrap();
+        std::vector<uint16_t> xb(m * k);
+        for (size_t i = 0; i < xb.size(); ++i) xb[i] = tqo_f32_to_bf16_bits(static_cast<float>(xv[i]));
+        std::vector<double> ref(m * n);
+        tqo_linear_w4g128_bf16(xb.data(), m, p.data(), s.data(), nullptr, n, k, ref.data());
+        assert_close(y, ref, "w4 linear");
+    }
+}
+
+TEST_GPU(test_parity_quantized_linear_w8a8) {
+    const size_t n = 272, k = 1024, m = 37;
+    const auto wv = randn(n * k, 0.02, 51), xv = randn(m * k, 1.0, 52);
+    const QConfig cfg{QuantDType::Int8, QuantDType::Int8, true, true};
+    const QuantizedLinear layer = QuantizedLinear::from_tensors(Tensor::from_slice(wv, {n, k}), std::nullopt, cfg).unwrap();
+    ASSERT(layer.mode() == QuantizedLinear::Mode::W8A8);
+    const auto y = layer.forward(Tensor::from_slice(xv, {m, k})).to_vec_f64().unwrap();
+    const auto w32 = f32(wv), x32 = f32(xv);
+    std::vector<int8_t> qw(n * k), qa(m * k);
+    std::vector<float> sw(n), sa(m);
+    tqo_quantize_i8_rowwise(w32.data(), n, k, qw.data(), sw.data());
+    tqo_quantize_i8_rowwise(x32.data(), m, k, qa.data(), sa.data());
+    std::vector<double> ref(m * n);
+    tqo_linear_w8a8(qa.data(), sa.data(), qw.data(), sw.data(), nullptr, m, n, k, ref.data());
+    assert_close(y, ref, "w8a8 linear");
+}
+
+TEST_GPU(test_parity_quantized_mlp) {
+    const size_t d = 256, f = 384, m = 5;
+    const auto gv = randn(f * d, 0.02, 61), uv = randn(f * d, 0.02, 62), dv = randn(d * f, 0.02, 63);
+    const auto xv = randn(m * d, 1.0, 64);
+    const QuantizedMLP mlp = QuantizedMLP::from_tensors(Tensor::from_slice(gv, {f, d}), Tensor::from_slice(uv, {f, d}),
+                                                        Tensor::from_slice(dv, {d, f}))
+                                 .unwrap();
+    const auto y = mlp.forward(Tensor::from_slice(xv, {m, d})).to_vec_f64().unwrap();
+    std::vector<uint8_t> pg(f * d / 2), pu(f * d / 2), pd(d * f / 2);
+    std::vector<uint16_t> sg(f * d / 128), su(f * d / 128), sd(d * f / 128);
+    const auto g32 = f32(gv), u32 = f32(uv), d32 = f32(dv);
+    tqo_quantize_i4_g128(g32.data(), f, d, pg.data(), sg.data());
+    tqo_quantize_i4_g128(u32.data(), f, d, pu.data(), su.data());
+    tqo_quantize_i4_g128(d32.data(), d, f, pd.data(), sd.data());
+    std::vector<uint16_t> xb(m * d);
+    for (size_t i = 0; i < xb.size(); ++i) xb[i] = tqo_f32_to_bf16_bits(static_cast<float>(xv[i]));
+    std::vector<double> ref(m * d);
+    tqo_mlp_w4g128(xb.data(), m, d, f, pg.data(), sg.data(), pu.data(), su.data(), pd.data(), sd.data(), ref.data());
+    assert_close(y, ref, "mlp");
+}
+
+TEST_GPU(test_parity_weight_formats) {
+    const size_t n = 33, k = 384;
+    auto wv = randn(n * k, 0.02, 71);
+    wv[5] = 0.0;
+    const Tensor w = Tensor::from_slice(wv, {n, k});
+    const auto w32 = f32(wv);
+    auto i8 = quantize_per_channel_i8(w).unwrap();
+    std::vector<int8_t> q(n * k);
+    std::vector<float> s(n);
+    tqo_quantize_i8_rowwise(w32.data(), n, k, q.data(), s.data());
+    ASSERT(i8.codes.to_host(nullptr) == q);
+    ASSERT(i8.scales.to_host(nullptr) == s);
+    auto i4 = quantize_i4_g128(w).unwrap();
+    std::vector<uint8_t> p(n * k / 2);
+    std::vector<uint16_t> s4(n * k / 128);
+    tqo_quantize_i4_g128(w32.data(), n, k, p.data(), s4.data());
+    ASSERT(i4.packed.to_host(nullptr) == p);
+    ASSERT(i4.scales.to_host(nullptr) == s4);
+    std::vector<float> wh(n * k);
+    tqo_dequantize_i4_g128(p.data(), s4.data(), n, k, wh.data());
+    const auto got = dequantize(i4).unwrap().to_vec_f64().unwrap();
+    for (size_t i = 0; i < wh.size(); ++i) ASSERT_EQ(got[i], static_cast<double>(wh[i]));
+}
+
+}  // namespace
+
+int main(int argc, char** argv) {
+    const bool cpu_only = argc > 1 && std::strcmp(argv[1], "--cpu") == 0;
+    int failed = 0, run = 0;
+    for (const Case& c : registry()) {
+        if (cpu_only && c.gpu) continue;
+        ++run;
+        std::printf("%-45s ", c.name);
+        std::fflush(stdout);
+        try {
+            c.fn();
+            std::printf("ok\n");
+        } catch (const std::exception& e) {
+            ++failed;
+            std::printf("FAILED: %s\n", e.what());
+        }
+        std::fflush(stdout);
+    }
+    std::printf("%d of %d tests passed\n", run - failed, run);
+    return failed ? 1 : 0;
+}

@@ -73,7 +73,9 @@ def test_gemv_w8_config2(tq, c2, m):
     assert_close(host(y), ref[:m], RTOL, ATOL, f"gemv_w8 M={m}")
 
 
-@pytest.mark.parametrize("n,k,m", [(1000, 1024, 1), (17, 16, 2), (333, 3088, 3), (64, 8192, 4), (5, 2000, 16)])
+# K % 16 != 0 and K > 8192 take the shape-general kernel (e.g. the reference's Linear(3, 2))
+@pytest.mark.parametrize("n,k,m", [(1000, 1024, 1), (17, 16, 2), (333, 3088, 3), (64, 8192, 4), (5, 2000, 16),
+                                   (2, 3, 4), (50, 100, 3), (64, 9000, 2)])
 def test_gemv_w8_shapes_bias(tq, oracle, n, k, m):
     w = normal(50, (n, k), 0.02)
     x = normal(50, (m, k), 1.0, stream=1)
@@ -161,7 +163,8 @@ def test_gemv_w4g128_tiled_shapes(tq, oracle, n, k, m, t):
     assert_close(host(y), oracle.linear_w4g128_bf16(xb, rp, rs, b), RTOL, ATOL, f"tiled {n}x{k} M={m} T={t}")
 
 
-@pytest.mark.parametrize("n,k,m", [(100, 128, 1), (7, 2176, 2), (256, 14336, 1), (48, 16384, 3), (9, 4096, 16)])
+@pytest.mark.parametrize("n,k,m", [(100, 128, 1), (7, 2176, 2), (256, 14336, 1), (48, 16384, 3), (9, 4096, 16),
+                                   (33, 16512, 2)])
 def test_gemv_w4g128_shapes_bias(tq, oracle, n, k, m):
     w = normal(51, (n, k), 0.02)
     xb = to_bf16_bits(normal(51, (m, k), 1.0, stream=1))
@@ -219,7 +222,8 @@ def test_w8a8_config4_full(tq, oracle):
 @pytest.mark.parametrize("m,n,k", [(1, 16, 16), (130, 48, 208), (64, 160, 80),
                                    (7, 272, 1024), (257, 128, 4096), (300, 512, 128),
                                    (129, 4096, 256), (100, 272, 384), (384, 2048, 256),
-                                   (1, 256, 640), (1031, 528, 512)])
+                                   (1, 256, 640), (1031, 528, 512),
+                                   (5, 8, 256), (33, 50, 100), (17, 16, 1000)])
 def test_w8a8_shapes_bias(tq, oracle, m, n, k):
     x = normal(52, (m, k), 1.0)
     w = normal(52, (n, k), 0.02, stream=1)
@@ -256,8 +260,36 @@ def test_quantized_linear_w8a8_module(tq, oracle):
     assert lin.num_parameters() == 256 * 512
 
 
+def test_misaligned_inputs_take_the_general_kernels(tq, oracle):
+    """Device views that start off a 16-byte boundary still give the oracle's result."""
+    import torch
+    from theano_quantize import _abi
+    from theano_quantize._tensor import ptr, stream
+
+    m, n, k = 3, 40, 256
+    w = normal(57, (n, k), 0.02)
+    x = normal(57, (m, k), 1.0, stream=1)
+    q, s = tq.quantize_per_channel_i8(dev_tensor(w))
+    big = torch.zeros(m * k + 1, dtype=torch.float32, device="cuda")
+    xv = big[1:].view(m, k)
+    xv.copy_(dev_tensor(x))
+    y = torch.empty((m, n), dtype=torch.float32, device="cuda")
+    _abi.call("tq_gemv_w8", ptr(xv), m, ptr(q), ptr(s), None, n, k, ptr(y), stream())
+    rq, rs = oracle.quantize_i8_rowwise(w)
+    assert_close(host(y), oracle.linear_w8(x, rq, rs), RTOL, ATOL, "gemv_w8 misaligned x")
+    xb = to_bf16_bits(x)
+    p4, s4 = tq.quantize_i4_g128(dev_tensor(w))
+    bigb = torch.zeros(m * k + 1, dtype=torch.int16, device="cuda")
+    xbv = bigb[1:].view(m, k)
+    xbv.copy_(dev_tensor(xb.view(np.int16)))
+    _abi.call("tq_gemv_w4g128", ptr(xbv), m, ptr(p4), ptr(s4), None, n, k, ptr(y), stream())
+    rp, rs4 = oracle.quantize_i4_g128(w)
+    assert_close(host(y), oracle.linear_w4g128_bf16(xb, rp, rs4), RTOL, ATOL, "gemv_w4 misaligned x")
+
+
 # ----------------------------------------------------------------- W4A16
-@pytest.mark.parametrize("m,n,k", [(17, 256, 512), (130, 64, 4096), (300, 128, 1024), (33, 16, 128)])
+@pytest.mark.parametrize("m,n,k", [(17, 256, 512), (130, 64, 4096), (300, 128, 1024), (33, 16, 128),
+                                   (40, 200, 1024), (20, 7, 256)])
 def test_gemm_w4g128_bf16_shapes(tq, oracle, m, n, k):
     w = normal(55, (n, k), 0.02)
     xb = to_bf16_bits(normal(55, (m, k), 1.0, stream=1))

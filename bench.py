@@ -152,7 +152,7 @@ def main():
         y = torch.empty((16, n3), dtype=torch.float32, device=dev)
 
         def gemv_w4(m):
-            def launch(i):  # same dispatch as QuantizedLinear: tiled up to 4 tokens, MFMA beyond
+            def launch(i):  # same dispatch as QuantizedLinear
                 pt, st, p, s = copies[i % len(copies)]
                 if m <= tq.nn.TILED_MAX_M:
                     _abi.call("tq_gemv_w4g128_tiled", ptr(x), m, ptr(pt), ptr(st), None, n3, k3, tile, ptr(y),

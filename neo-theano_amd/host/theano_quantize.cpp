@@ -513,7 +513,7 @@ Result<void> QuantizedLinear::forward_device(const void* x, int64_t m, float* y,
     switch (mode_) {
         case Mode::W4: {
             const auto* xb = static_cast<const uint16_t*>(x);
-            if (m <= 4 && w4_.tile_rows > 0)
+            if (m <= 16 && w4_.tile_rows > 0)
                 st = tq_gemv_w4g128_tiled(xb, m, w4_.packed_tiled.data(), w4_.scales_tiled.data(), b, n, k,
                                           w4_.tile_rows, y, ts);
             else if (m <= 16)

@@ -27,7 +27,7 @@ from .formats import quantize_i4_g128, quantize_per_channel_i8, repack_i4_g128_t
 from .qconfig import QConfig, QuantDType
 
 DECODE_MAX_M = 16
-TILED_MAX_M = 4  # the row-tiled GEMV wins up to 4 tokens, the MFMA decode kernel beyond
+TILED_MAX_M = 16  # decode shapes run on the row-tiled copy of an INT4 weight
 
 
 class Module:
@@ -72,7 +72,7 @@ class QuantizedLinear(Module):
         self.bias = bias
         self.tiled = None
         if mode == "w4" and self.in_features <= 16384:
-            # decode kernel layout (a permutation of qweight) for M <= 16
+            # row-tiled copy (a permutation of qweight) for the decode GEMV, M <= 16
             self.tiled = repack_i4_g128_tiled(qweight, scales)
 
     @staticmethod

@@ -130,7 +130,7 @@ def test_repack_tiled_is_a_permutation(tq, n, k, t):
     assert not up[n:].any() and not us[n:].any()  # padding rows are zero
 
 
-@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 8, 16])
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 8, 11, 16])
 def test_gemv_w4g128_tiled_config3(tq, c3, m):
     from theano_quantize import _abi
     from theano_quantize._tensor import ptr, stream
@@ -144,8 +144,13 @@ def test_gemv_w4g128_tiled_config3(tq, c3, m):
     assert_close(host(y), ref[:m], RTOL, ATOL, f"gemv_w4g128_tiled M={m} T={t}")
 
 
+# 1-2 tokens (and tiles that are not 16, 32 or 64 rows, or K ranges past the MFMA
+# kernel's budget) run the dot2 kernel; 3-16 tokens the MFMA kernel (token passes,
+# tail tiles, K up to 8192 with the two-position x staging)
 @pytest.mark.parametrize("n,k,m,t", [(100, 128, 1, 8), (7, 2176, 2, 8), (256, 14336, 1, 16), (48, 16384, 3, 24),
-                                     (1000, 4096, 4, 64), (333, 640, 2, 40)])
+                                     (1000, 4096, 4, 64), (333, 640, 2, 40),
+                                     (1000, 4096, 5, 64), (70, 1024, 16, 16), (200, 6144, 7, 32),
+                                     (130, 8192, 9, 16), (77, 384, 13, 64), (64, 8192, 3, 64)])
 def test_gemv_w4g128_tiled_shapes(tq, oracle, n, k, m, t):
     from theano_quantize import _abi
     from theano_quantize._tensor import ptr, stream

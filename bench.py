@@ -257,12 +257,12 @@ def main():
         mlp = tq.QuantizedMLP.from_tensors(dt(normal_f32(4, (f5, d5), 0.02)), dt(normal_f32(4, (f5, d5), 0.02, 1)),
                                            dt(normal_f32(4, (d5, f5), 0.02, 2)))
         x = bf16(normal_f32(4, (m5, d5), 1.0, stream=3))
-        h = torch.empty((m5, f5), dtype=torch.float32, device=dev)
+        ws = torch.empty((mlp.workspace_bytes(m5),), dtype=torch.uint8, device=dev)
         y = torch.empty((m5, d5), dtype=torch.float32, device=dev)
 
         def launch(i):
             _abi.call("tq_mlp_w4g128", ptr(x), m5, d5, f5, ptr(mlp.gate[0]), ptr(mlp.gate[1]), ptr(mlp.up[0]),
-                      ptr(mlp.up[1]), ptr(mlp.down[0]), ptr(mlp.down[1]), ptr(h), ptr(y), stream())
+                      ptr(mlp.up[1]), ptr(mlp.down[0]), ptr(mlp.down[1]), ptr(ws), ws.numel(), ptr(y), stream())
 
         steps = max(5, args.steps // 10)
         ms, _ = timer.run(launch, steps, 2)

@@ -223,15 +223,20 @@ int tq_gemm_w4g128_bf16(const uint16_t* x_bf16, int64_t m, const uint8_t* packed
 
 /* Quantized Llama-style FFN (build-defined composition of Linear, SiLU
  * (crates/theano-nn/src/activation.rs:66-79) and Tensor::mul):
- *   h = SiLU(x Wg^T) * (x Wu^T)  kept in f32 (h_workspace, f32 [M, F]);
- *   y = h Wd^T                   f32 [M, D].
+ *   h = SiLU(x Wg^T) * (x Wu^T);   y = h Wd^T   (f32 [M, D]).
  * x bf16 [M, D]; gate/up INT4 g128 [F, D]; down INT4 g128 [D, F];
- * D % 128 == 0, F % 128 == 0. */
+ * D % 128 == 0, F % 128 == 0.  `workspace` is device memory of at least
+ * tq_mlp_w4g128_workspace_bytes(M, D, F) bytes (intermediates: x in the
+ * kernels' k-order, h as bf16 hi + lo planes, group sums; or h as f32 [M, F]
+ * on the shape-general path), 16-byte aligned; the pipelined kernels run when
+ * D % 256 == 0, F % 256 == 0, the workspace is 256-byte aligned and the
+ * scales 4-byte aligned.  x, packed weights and y 16-byte aligned. */
+int64_t tq_mlp_w4g128_workspace_bytes(int64_t m, int64_t d, int64_t f);
 int tq_mlp_w4g128(const uint16_t* x_bf16, int64_t m, int64_t d, int64_t f,
                   const uint8_t* gate_packed, const uint16_t* gate_s,
                   const uint8_t* up_packed, const uint16_t* up_s,
                   const uint8_t* down_packed, const uint16_t* down_s,
-                  float* h_workspace, float* y, tq_stream_t stream);
+                  void* workspace, int64_t workspace_bytes, float* y, tq_stream_t stream);
 
 #ifdef __cplusplus
 }

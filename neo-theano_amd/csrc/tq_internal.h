@@ -47,6 +47,14 @@ int launch_gemm_w8a8_generic(const int8_t* qa, const float* sa, const int8_t* qw
                              const float* bias, int64_t m, int64_t n, int64_t k, int32_t* acc, float* y,
                              hipStream_t st);
 
+// FFN block for shapes the pipelined kernels of tq_ffn.hip do not take (D or F
+// not a multiple of 256, 2-byte aligned scales): 16x16x32 MFMA kernels of
+// tq_mlp.hip with h kept as f32 [M, F] in `h`.
+int launch_mlp_w4g128_general(const uint16_t* x_bf16, int64_t m, int64_t d, int64_t f, const uint8_t* gate_packed,
+                              const uint16_t* gate_s, const uint8_t* up_packed, const uint16_t* up_s,
+                              const uint8_t* down_packed, const uint16_t* down_s, float* h, float* y,
+                              hipStream_t st);
+
 #define TQ_REQUIRE(cond, ...)                                 \
     do {                                                      \
         if (!(cond)) return ::tq::fail(TQ_EINVAL, __VA_ARGS__); \

@@ -322,6 +322,20 @@ int launch_w4(const void* act, const uint8_t* p0, const uint16_t* s0, const uint
 }
 
 }  // namespace
+
+// Shape-general FFN (any M; D, F multiples of 128): gate/up then down on the
+// 16x16x32 kernels above, h kept as f32 [M, F] in `h`.
+int launch_mlp_w4g128_general(const uint16_t* x_bf16, int64_t m, int64_t d, int64_t f, const uint8_t* gate_packed,
+                              const uint16_t* gate_s, const uint8_t* up_packed, const uint16_t* up_s,
+                              const uint8_t* down_packed, const uint16_t* down_s, float* h, float* y,
+                              hipStream_t st) {
+    int rc = launch_w4<kBF16, true, 128>(x_bf16, gate_packed, gate_s, up_packed, up_s, nullptr, m, f, d, h, f, st,
+                                         "tq_mlp_w4g128 (gate/up)");
+    if (rc != TQ_OK) return rc;
+    return launch_w4<kF32Split, false, 64>(h, down_packed, down_s, nullptr, nullptr, nullptr, m, d, f, y, d, st,
+                                           "tq_mlp_w4g128 (down)");
+}
+
 }  // namespace tq
 
 using namespace tq;
@@ -343,28 +357,6 @@ int tq_gemm_w4g128_bf16(const uint16_t* x_bf16, int64_t m, const uint8_t* packed
         return launch_linear_w4_generic(x_bf16, m, packed, s_f16, bias, n, k, y, as_hip(stream));
     return launch_w4<kBF16, false, 128>(x_bf16, packed, s_f16, nullptr, nullptr, bias, m, n, k, y, n,
                                         as_hip(stream), "tq_gemm_w4g128_bf16");
-}
-
-int tq_mlp_w4g128(const uint16_t* x_bf16, int64_t m, int64_t d, int64_t f, const uint8_t* gate_packed,
-                  const uint16_t* gate_s, const uint8_t* up_packed, const uint16_t* up_s,
-                  const uint8_t* down_packed, const uint16_t* down_s, float* h_workspace, float* y,
-                  tq_stream_t stream) {
-    TQ_REQUIRE(m >= 0 && d >= 0 && f >= 0, "tq_mlp_w4g128: negative shape");
-    TQ_REQUIRE(d % 128 == 0 && f % 128 == 0,
-               "tq_mlp_w4g128: D=%lld and F=%lld must be multiples of 128", (long long)d, (long long)f);
-    if (m == 0 || d == 0) return TQ_OK;
-    TQ_REQUIRE(f > 0, "tq_mlp_w4g128: F=0");
-    TQ_REQUIRE(x_bf16 && gate_packed && gate_s && up_packed && up_s && down_packed && down_s && h_workspace && y,
-               "tq_mlp_w4g128: null pointer");
-    TQ_REQUIRE(aligned(x_bf16, 16) && aligned(gate_packed, 16) && aligned(up_packed, 16) &&
-                   aligned(down_packed, 16) && aligned(h_workspace, 16) && aligned(y, 16),
-               "tq_mlp_w4g128: misaligned pointer (16 B required)");
-    const hipStream_t st = as_hip(stream);
-    int rc = launch_w4<kBF16, true, 128>(x_bf16, gate_packed, gate_s, up_packed, up_s, nullptr, m, f, d,
-                                         h_workspace, f, st, "tq_mlp_w4g128 (gate/up)");
-    if (rc != TQ_OK) return rc;
-    return launch_w4<kF32Split, false, 64>(h_workspace, down_packed, down_s, nullptr, nullptr, nullptr, m, d, f, y,
-                                           d, st, "tq_mlp_w4g128 (down)");
 }
 
 }  // extern "C"

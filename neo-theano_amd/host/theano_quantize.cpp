@@ -636,10 +636,17 @@ Result<QuantizedMLP> QuantizedMLP::from_tensors(const Tensor& gate, const Tensor
     });
 }
 
-Result<void> QuantizedMLP::forward_device(const uint16_t* x, int64_t m, float* h, float* y, hipStream_t stream) const {
+size_t QuantizedMLP::workspace_bytes(int64_t m) const {
+    return static_cast<size_t>(
+        tq_mlp_w4g128_workspace_bytes(m, static_cast<int64_t>(d_), static_cast<int64_t>(f_)));
+}
+
+Result<void> QuantizedMLP::forward_device(const uint16_t* x, int64_t m, void* workspace, size_t workspace_bytes,
+                                          float* y, hipStream_t stream) const {
     const int st = tq_mlp_w4g128(x, m, static_cast<int64_t>(d_), static_cast<int64_t>(f_), gate_.packed.data(),
                                  gate_.scales.data(), up_.packed.data(), up_.scales.data(), down_.packed.data(),
-                                 down_.scales.data(), h, y, reinterpret_cast<tq_stream_t>(stream));
+                                 down_.scales.data(), workspace, static_cast<int64_t>(workspace_bytes), y,
+                                 reinterpret_cast<tq_stream_t>(stream));
     if (st != TQ_OK) return TheanoError::from_status(st, "QuantizedMLP::forward");
     return {};
 }
@@ -652,8 +659,9 @@ Result<Tensor> QuantizedMLP::try_forward(const Tensor& input) const {
         const std::vector<uint16_t> xb = to_bf16(xv);
         DeviceBuffer<uint16_t> xd(xb.size());
         xd.upload(xb.data(), xb.size(), stream_);
-        DeviceBuffer<float> h(m * f_), y(m * d_);
-        auto r = forward_device(xd.data(), static_cast<int64_t>(m), h.data(), y.data(), stream_);
+        DeviceBuffer<uint8_t> ws(std::max<size_t>(workspace_bytes(static_cast<int64_t>(m)), 1));
+        DeviceBuffer<float> y(m * d_);
+        auto r = forward_device(xd.data(), static_cast<int64_t>(m), ws.data(), ws.size(), y.data(), stream_);
         if (r.is_err()) return r.unwrap_err();
         return output_tensor(y.to_host(stream_), m, d_, squeeze);
     });

@@ -346,8 +346,11 @@ class QuantizedMLP : public Module {
                                              hipStream_t stream = nullptr);
     Tensor forward(const Tensor& input) const override;
     Result<Tensor> try_forward(const Tensor& input) const;
-    // x bf16 bits [m, d], h f32 [m, f] scratch, y f32 [m, d]
-    Result<void> forward_device(const uint16_t* x, int64_t m, float* h, float* y, hipStream_t stream) const;
+    // device bytes of intermediates for m tokens (tq_mlp_w4g128_workspace_bytes)
+    size_t workspace_bytes(int64_t m) const;
+    // x bf16 bits [m, d], workspace of workspace_bytes(m) bytes, y f32 [m, d]
+    Result<void> forward_device(const uint16_t* x, int64_t m, void* workspace, size_t workspace_bytes, float* y,
+                                hipStream_t stream) const;
     std::vector<Tensor> parameters() const override;
     size_t num_parameters() const override { return 3 * d_ * f_; }
     size_t hidden() const { return d_; }

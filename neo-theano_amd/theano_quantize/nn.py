@@ -167,15 +167,22 @@ class QuantizedMLP(Module):
     def num_parameters(self) -> int:
         return 3 * self.d * self.f
 
-    def forward(self, x, h_workspace=None):
+    def workspace_bytes(self, m: int) -> int:
+        """Device bytes of intermediates forward() needs for m tokens."""
+        return int(_abi.lib().tq_mlp_w4g128_workspace_bytes(m, self.d, self.f))
+
+    def forward(self, x, workspace=None):
+        """y = (SiLU(x Wg^T) * (x Wu^T)) Wd^T for x bf16 [M, D]; `workspace` is an
+        optional uint8 device tensor of at least workspace_bytes(M) bytes."""
         x = on_device(x, torch.bfloat16, "QuantizedMLP.forward")
         if x.dim() != 2 or x.shape[1] != self.d:
             raise InvalidArgument(f"QuantizedMLP.forward: expected [M, {self.d}], got {tuple(x.shape)}")
         m = x.shape[0]
-        if h_workspace is None:
-            h_workspace = torch.empty((m, self.f), dtype=torch.float32, device=x.device)
+        need = self.workspace_bytes(m)
+        if workspace is None:
+            workspace = torch.empty((max(need, 1),), dtype=torch.uint8, device=x.device)
         y = torch.empty((m, self.d), dtype=torch.float32, device=x.device)
         _abi.call("tq_mlp_w4g128", ptr(x), m, self.d, self.f, ptr(self.gate[0]), ptr(self.gate[1]),
                   ptr(self.up[0]), ptr(self.up[1]), ptr(self.down[0]), ptr(self.down[1]),
-                  ptr(h_workspace), ptr(y), stream())
+                  ptr(workspace), workspace.numel() * workspace.element_size(), ptr(y), stream())
         return y

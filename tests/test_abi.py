@@ -93,7 +93,9 @@ def test_observer_scale_zp_matches_oracle(abi, oracle):
     ("tq_gemm_w8a8", [None, None, None, None, None, 4, 20, 64, None, None, None]),  # N % 16
     ("tq_gemm_w8a8", [None, None, None, None, None, 4, 16, 65, None, None, None]),  # K % 16
     ("tq_gemm_w4g128_bf16", [None, 4, None, None, None, 16, 100, None, None]),
-    ("tq_mlp_w4g128", [None, 4, 100, 128, None, None, None, None, None, None, None, None, None]),
+    ("tq_mlp_w4g128", [None, 4, 100, 128, None, None, None, None, None, None, None, 0, None, None]),  # D % 128
+    ("tq_mlp_w4g128", [None, 4, 256, 256, None, None, None, None, None, None, None, 0, None, None]),  # nulls
+    ("tq_mlp_w4g128", [256, 4, 256, 256, 256, 256, 256, 256, 256, 256, 256, 16, 256, None]),  # workspace
     ("tq_quantize_tensor", [None, 10, 1.0, 0.0, 7, None, None]),          # bad QuantDType
     ("tq_quantize_per_tensor", [None, 10, 0, None, None, None, None]),
     ("tq_minmax_reset", [None, 0, None]),
@@ -105,6 +107,18 @@ def test_invalid_arguments_are_rejected(abi, call):
     with pytest.raises(InvalidArgument):
         abi.call(name, *args)
     assert abi.lib().tq_last_error()  # a message was recorded
+
+
+def test_mlp_workspace_bytes(abi):
+    ws = abi.lib().tq_mlp_w4g128_workspace_bytes
+    # x in k-order (M*D*2) + x group sums (D/128 * Mpad * 8) + h hi/lo (2 * M*F*2)
+    # + h group sums (F/128 * Mpad * 8), parts 256-byte aligned, Mpad = M rounded to 128
+    assert ws(512, 4096, 14336) == 4194304 + 131072 + 2 * 14680064 + 458752
+    m, d, f = 5, 256, 384
+    parts = [m * d * 2, (d // 128) * 128 * 8, m * f * 2, m * f * 2, (f // 128) * 128 * 8]
+    assert ws(m, d, f) == sum((p + 255) // 256 * 256 for p in parts)
+    assert ws(1, 128, 128) >= 4 * 1 * 128  # covers the f32 h [M, F] of the shape-general path
+    assert ws(0, 128, 128) == 0
 
 
 def test_zero_sizes_are_noops(abi):

@@ -306,7 +306,10 @@ def test_gemm_w4g128_bf16_shapes(tq, oracle, m, n, k):
 
 
 # ------------------------------------------------------------------- MLP
-@pytest.mark.parametrize("m,d,f", [(5, 256, 384), (1, 128, 128), (70, 512, 1024)])
+# (5, 256, 384) and (1, 128, 128) have an odd number of groups: shape-general
+# path; the others take the pipelined kernels (row tails at 64 / 128).
+@pytest.mark.parametrize("m,d,f", [(5, 256, 384), (1, 128, 128), (70, 512, 1024), (1, 256, 512),
+                                   (129, 768, 1536), (300, 1024, 2048), (64, 256, 256), (200, 512, 768)])
 def test_mlp_small(tq, oracle, m, d, f):
     wg = normal(56, (f, d), 0.02)
     wu = normal(56, (f, d), 0.02, stream=1)
@@ -329,3 +332,48 @@ def test_mlp_config5_sampled_rows(tq, oracle):
     rows = np.array([0, 129, 511])
     args = [a for t in (mlp.gate, mlp.up, mlp.down) for a in (host(t[0]), host(t[1]).view(np.uint16))]
     assert_close(y[rows], oracle.mlp_w4g128(xb[rows], *args), RTOL, ATOL, "mlp config 5")
+
+
+def _mlp_case(tq, m, d, f, seed=57):
+    wg = normal(seed, (f, d), 0.02)
+    wu = normal(seed, (f, d), 0.02, stream=1)
+    wd = normal(seed, (d, f), 0.02, stream=2)
+    xb = to_bf16_bits(normal(seed, (m, d), 1.0, stream=3))
+    mlp = tq.QuantizedMLP.from_tensors(dev_tensor(wg), dev_tensor(wu), dev_tensor(wd))
+    return mlp, xb
+
+
+def test_mlp_paths_agree(tq, oracle):
+    """A workspace that is 16- but not 256-byte aligned selects the shape-general
+    kernels; both paths meet the tolerance against the oracle."""
+    import torch
+
+    m, d, f = 96, 512, 1024
+    mlp, xb = _mlp_case(tq, m, d, f)
+    need = mlp.workspace_bytes(m)
+    raw = torch.empty((need + 256,), dtype=torch.uint8, device="cuda")
+    assert raw.data_ptr() % 256 == 0
+    y_fast = host(mlp.forward(bf16_dev(xb), raw[:need]))
+    y_gen = host(mlp.forward(bf16_dev(xb), raw[16:16 + need]))
+    args = [a for t in (mlp.gate, mlp.up, mlp.down) for a in (host(t[0]), host(t[1]).view(np.uint16))]
+    ref = oracle.mlp_w4g128(xb, *args)
+    assert_close(y_fast, ref, RTOL, ATOL, "mlp pipelined")
+    assert_close(y_gen, ref, RTOL, ATOL, "mlp shape-general")
+
+
+def test_mlp_workspace_reuse_and_size_check(tq, oracle):
+    """One workspace serves calls of decreasing M (stale intermediates of a larger
+    call must not leak into a smaller one); a short workspace is rejected."""
+    import torch
+    from theano_quantize import InvalidArgument
+
+    d, f = 256, 512
+    mlp, xb = _mlp_case(tq, 300, d, f, seed=58)
+    ws = torch.empty((mlp.workspace_bytes(300),), dtype=torch.uint8, device="cuda")
+    args = [a for t in (mlp.gate, mlp.up, mlp.down) for a in (host(t[0]), host(t[1]).view(np.uint16))]
+    for m in (300, 130, 7):
+        y = host(mlp.forward(bf16_dev(xb[:m]), ws))
+        assert_close(y, oracle.mlp_w4g128(xb[:m], *args), RTOL, ATOL, f"mlp reuse M={m}")
+    short = torch.empty((mlp.workspace_bytes(300) - 256,), dtype=torch.uint8, device="cuda")
+    with pytest.raises(InvalidArgument):
+        mlp.forward(bf16_dev(xb), short)

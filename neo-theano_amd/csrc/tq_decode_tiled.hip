@@ -22,13 +22,12 @@
 // group scale is applied.  Weight loads are unconditional (clamped addresses)
 // and run kWin chunks ahead of the arithmetic; the waves' partial sums meet in
 // LDS in a fixed order.  Its arithmetic grows with the token count.
-//  * k_decode_tiled_mfma (up to 16 tokens per pass, T a multiple of 16): the same
-//    unpacked bf16 weights feed v_mfma_f32_16x16x32_bf16 with the tokens as the
-//    other operand, so the cost is nearly flat in the token count.  A wave owns a
-//    16-row group and a range of 128-element groups; lane (row r, quarter q)
-//    loads chunk 4g + q of row r, MFMA j of group g takes its dword j.  All
-//    tokens' x is staged block-wide in LDS (same slot order), 136 * group sums
-//    are subtracted per group before the f16 scale, and the K ranges meet in LDS.
+//  * k_decode_tiled_mfma (3-16 tokens, T a multiple of 16): unpacked bf16
+//    weights feed v_mfma_f32_16x16x32_bf16 with the tokens as the other operand,
+//    so the cost is nearly flat in the token count.  Each wave owns the whole
+//    tile and a run of groups, reads its tokens' x straight from L2 (no LDS
+//    staging, no barrier before the arithmetic) and consumes its loads in
+//    order; the runs meet in LDS (details at the kernel).
 #include "tq_internal.h"
 
 namespace tq {
@@ -176,116 +175,125 @@ __global__ __launch_bounds__(kBlock) void k_decode_tiled(const uint16_t* __restr
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
-// kR row groups of 16 per tile (T = 16 kR); kS = 16 / kR waves split the groups,
-// kGPW groups each (padding groups are clamped and masked); kM token capacity
-// (tokens >= m read zeros and are not stored); kPos positions of 4 x values per
-// thread and token in the staging (K <= 4096 kPos).
-template <int kR, int kM, int kGPW, int kPos>
+// Packed dword of 8 nibbles (k .. k+7, two's complement) -> bf16 8 * (24 + q) in
+// the slot order (k, k+2), (k+1, k+3), (k+4, k+6), (k+5, k+7): q + 8 in the top
+// four mantissa bits of bf16 128.  The smaller offset (24 instead of the 136 of
+// a low-mantissa nibble) keeps the partial sums of a group near their size.
+__device__ __forceinline__ u32x4 unpack_w4_24(uint32_t w) {
+    const uint32_t lo = ((w << 3) & 0x78787878u) ^ 0x40404040u;
+    const uint32_t hi = ((w >> 1) & 0x78787878u) ^ 0x40404040u;
+    u32x4 a;
+    a.x = __builtin_amdgcn_perm(0x43434343u, lo, 0x04010400u);
+    a.y = __builtin_amdgcn_perm(0x43434343u, hi, 0x04010400u);
+    a.z = __builtin_amdgcn_perm(0x43434343u, lo, 0x04030402u);
+    a.w = __builtin_amdgcn_perm(0x43434343u, hi, 0x04030402u);
+    return a;
+}
+
+// 8 bf16 (x0..x7) -> the slot order (x0,x2)(x1,x3)(x4,x6)(x5,x7)
+__device__ __forceinline__ u32x4 pair_slots(u32x4 v) {
+    u32x4 o;
+    o.x = __builtin_amdgcn_perm(v.y, v.x, 0x05040100u);
+    o.y = __builtin_amdgcn_perm(v.y, v.x, 0x07060302u);
+    o.z = __builtin_amdgcn_perm(v.w, v.z, 0x05040100u);
+    o.w = __builtin_amdgcn_perm(v.w, v.z, 0x07060302u);
+    return o;
+}
+
+__device__ __forceinline__ f32x4 mfma16_bf16(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
+                                                   0, 0, 0);
+}
+
+// MFMA kernel for 3..16 tokens.  Block: one tile of T = 16 kR rows; its 16 waves
+// split K into runs of kGPW groups (no LDS staging of x, no barrier before the
+// arithmetic: every wave issues all of its loads at once and consumes them in
+// order).  Lane (r16 = l % 16, q = l / 16) holds, per group g, the 16 bytes of
+// chunk 4 g + q (k in [128 g + 32 q, +32)) of row r16 of each 16-row group, and
+// the same k of token r16's x (read from L2, zero past M).  MFMA step j of a
+// group takes dword j of each: weights as bf16 8 * (24 + q) (unpack_w4_24),
+// tokens as the other operand in the matching slot order.  One extra MFMA chain
+// per group with the constant -192 as the weight operand gives -192 * sum(x)
+// of the group for every token, the start value of each row group's chain, so
+// the offset cancels inside the MFMA accumulator; the f16 scale is applied per
+// group, the factor 1/8 at the end.  The K runs meet in LDS in a fixed order.
+template <int kR, int kGPW>
 __global__ __launch_bounds__(kBlock) void k_decode_tiled_mfma(const uint16_t* __restrict__ x, int m,
                                                               const uint8_t* __restrict__ pt,
                                                               const uint16_t* __restrict__ st,
                                                               const float* __restrict__ bias, int64_t n,
                                                               int64_t k, float* __restrict__ y) {
-    constexpr int kS = kWaves / kR;
     constexpr int T = 16 * kR;
-    // LDS: x strips [kM][C chunks][16 dwords] (slot order) | zero strip [kGPW * 4][16] |
-    //      136 * group sums [kM][G] | partial outputs [kS][T][16]
-    extern __shared__ __attribute__((aligned(16))) uint8_t lds_dyn[];
-    const int64_t C = k >> 5, G = k >> 7;
-    uint32_t* sx = reinterpret_cast<uint32_t*>(lds_dyn);
-    uint32_t* zero = sx + kM * C * 16;
-    float* gsum = reinterpret_cast<float*>(zero + kGPW * 4 * 16);
-    float* part = gsum + kM * G;
-
+    __shared__ float part[kWaves][T][16];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int rg = wave % kR, ks = wave / kR;
-    const int64_t tile = blockIdx.x;
     const int q = lane >> 4, r16 = lane & 15;
-    const int64_t g0 = static_cast<int64_t>(ks) * kGPW;
+    const int64_t tile = blockIdx.x;
+    const int64_t C = k >> 5, G = k >> 7;
+    const int64_t g0 = static_cast<int64_t>(wave) * kGPW;
 
-    // x first: token j (row min(j, m - 1)), position p = threadIdx.x + 1024 u < K / 4
-    const int cpos = static_cast<int>(C) * 8;
-    uint2 xv[kM][kPos];
-#pragma unroll
-    for (int j = 0; j < kM; ++j)
-#pragma unroll
-        for (int u = 0; u < kPos; ++u) {
-            const int pos = min(static_cast<int>(threadIdx.x) + u * kBlock, cpos - 1);
-            xv[j][u] = *reinterpret_cast<const uint2*>(x + min(j, m - 1) * k + pos * 4);
-        }
-    // weights: chunk 4 g + q of row r16 of the row group, per group (clamped past G)
-    const uint8_t* wbase = pt + (tile * C * T + rg * 16 + r16) * 16;
-    u32x4 w[kGPW];
+    // x of token r16 (zero past m); groups past G are clamped (and skipped below)
+    u32x4 xf[kGPW][4];
+    const bool tok = r16 < m;
+    const uint16_t* xr = x + static_cast<int64_t>(tok ? r16 : 0) * k + 32 * q;
 #pragma unroll
     for (int i = 0; i < kGPW; ++i) {
         const int64_t g = min<int64_t>(g0 + i, G - 1);
-        w[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wbase + (4 * g + q) * T * 16));
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            xf[i][j] = tok ? *reinterpret_cast<const u32x4*>(xr + g * 128 + 8 * j) : u32x4{0u, 0u, 0u, 0u};
     }
-    // f16 scales of rows 4 q .. 4 q + 3 of the row group (the lane's D rows), per group
-    uint2 sc[kGPW];
+    // f16 scales of the lane's D rows 16 r + 4 q .. + 3
+    uint2 sc[kGPW][kR];
 #pragma unroll
     for (int i = 0; i < kGPW; ++i) {
         const int64_t g = min<int64_t>(g0 + i, G - 1);
-        sc[i] = *reinterpret_cast<const uint2*>(st + (tile * G + g) * T + rg * 16 + 4 * q);
+#pragma unroll
+        for (int r = 0; r < kR; ++r)
+            sc[i][r] = *reinterpret_cast<const uint2*>(st + (tile * G + g) * T + 16 * r + 4 * q);
     }
-
-    // stage x block-wide (slot order), 136 * group sums (a group is 32 positions = 32 lanes)
-#pragma unroll
-    for (int j = 0; j < kM; ++j)
-#pragma unroll
-        for (int u = 0; u < kPos; ++u) {
-            const int pos = static_cast<int>(threadIdx.x) + u * kBlock;
-            const uint2 v = xv[j][u];
-            float sm = bf16_lo(v.x) + bf16_hi(v.x) + bf16_lo(v.y) + bf16_hi(v.y);
-#pragma unroll
-            for (int o = 1; o < 32; o <<= 1) sm += __shfl_xor(sm, o, kWave);
-            if (pos < cpos) {
-                *reinterpret_cast<uint2*>(sx + j * C * 16 + 2 * pos) =
-                    make_uint2((v.x & 0xFFFFu) | (v.y << 16), (v.x >> 16) | (v.y & 0xFFFF0000u));
-                if ((pos & 31) == 0) gsum[j * G + (pos >> 5)] = 136.0f * sm;
-            }
-        }
-    for (int i = threadIdx.x; i < kGPW * 4 * 16; i += kBlock) zero[i] = 0u;
-    __syncthreads();
-
-    const int tok = r16;
-    const bool tok_live = tok < m;
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    // weights
+    const uint8_t* wb = pt + (tile * C * T + r16) * 16;
+    u32x4 w[kGPW][kR];
 #pragma unroll
     for (int i = 0; i < kGPW; ++i) {
-        const int64_t g = g0 + i;
-        const bool live = g < G;
-        const int64_t gc = live ? g : G - 1;
-        const uint32_t* xc = tok_live ? sx + (tok * C + gc * 4 + q) * 16 : zero + (i * 4 + q) * 16;
-        const uint32_t ws[4] = {w[i].x, w[i].y, w[i].z, w[i].w};
-        f32x4 d = {0.f, 0.f, 0.f, 0.f};
+        const int64_t g = min<int64_t>(g0 + i, G - 1);
 #pragma unroll
-        for (int jd = 0; jd < 4; ++jd) {
-            const uint32_t lo = (ws[jd] ^ 0x88888888u) & 0x0F0F0F0Fu;
-            const uint32_t hi = ((ws[jd] >> 4) ^ 0x08888888u) & 0x0F0F0F0Fu;
-            u32x4 a;
-            a.x = __builtin_amdgcn_perm(0x43434343u, lo, 0x04010400u);
-            a.y = __builtin_amdgcn_perm(0x43434343u, hi, 0x04010400u);
-            a.z = __builtin_amdgcn_perm(0x43434343u, lo, 0x04030402u);
-            a.w = __builtin_amdgcn_perm(0x43434343u, hi, 0x04030402u);
-            const u32x4 b = *reinterpret_cast<const u32x4*>(xc + 4 * jd);
-            d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
-                                                        __builtin_bit_cast(bf16x8, b), d, 0, 0, 0);
+        for (int r = 0; r < kR; ++r)
+            w[i][r] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wb + ((4 * g + q) * T + 16 * r) * 16));
+    }
+
+    const u32x4 aoff = u32x4{0xC340C340u, 0xC340C340u, 0xC340C340u, 0xC340C340u};  // bf16 -192
+    f32x4 acc[kR];
+#pragma unroll
+    for (int r = 0; r < kR; ++r) acc[r] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < kGPW; ++i) {
+        if (g0 + i >= G) break;  // wave-uniform
+        u32x4 xb[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) xb[j] = pair_slots(xf[i][j]);
+        f32x4 xs = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) xs = mfma16_bf16(aoff, xb[j], xs);
+#pragma unroll
+        for (int r = 0; r < kR; ++r) {
+            const uint32_t ws[4] = {w[i][r].x, w[i][r].y, w[i][r].z, w[i][r].w};
+            f32x4 d = xs;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) d = mfma16_bf16(unpack_w4_24(ws[j]), xb[j], d);
+            const uint32_t s01 = sc[i][r].x, s23 = sc[i][r].y;
+            acc[r].x = fmaf(__half2float(__ushort_as_half(static_cast<uint16_t>(s01))), d.x, acc[r].x);
+            acc[r].y = fmaf(__half2float(__ushort_as_half(static_cast<uint16_t>(s01 >> 16))), d.y, acc[r].y);
+            acc[r].z = fmaf(__half2float(__ushort_as_half(static_cast<uint16_t>(s23))), d.z, acc[r].z);
+            acc[r].w = fmaf(__half2float(__ushort_as_half(static_cast<uint16_t>(s23 >> 16))), d.w, acc[r].w);
         }
-        // lane holds D[row 4 q + e][token r16]
-        const float gs = tok_live ? gsum[tok * G + gc] : 0.0f;
-        const float mk = live ? 1.0f : 0.0f;
-        const uint32_t s01 = sc[i].x, s23 = sc[i].y;
-        acc.x = fmaf(mk * __half2float(__ushort_as_half(static_cast<uint16_t>(s01))), d.x - gs, acc.x);
-        acc.y = fmaf(mk * __half2float(__ushort_as_half(static_cast<uint16_t>(s01 >> 16))), d.y - gs, acc.y);
-        acc.z = fmaf(mk * __half2float(__ushort_as_half(static_cast<uint16_t>(s23))), d.z - gs, acc.z);
-        acc.w = fmaf(mk * __half2float(__ushort_as_half(static_cast<uint16_t>(s23 >> 16))), d.w - gs, acc.w);
     }
-    if (tok_live) {
+    // lane holds D[row 16 r + 4 q + e][token r16]
 #pragma unroll
-        for (int e = 0; e < 4; ++e) part[(ks * T + rg * 16 + 4 * q + e) * 16 + tok] = acc[e];
-    }
+    for (int r = 0; r < kR; ++r)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) part[wave][16 * r + 4 * q + e][r16] = acc[r][e];
     __syncthreads();
     for (int i = threadIdx.x; i < T * m; i += kBlock) {
         const int row = i / m, t = i - row * m;
@@ -293,61 +301,24 @@ __global__ __launch_bounds__(kBlock) void k_decode_tiled_mfma(const uint16_t* __
         if (grow >= n) continue;
         float sum = 0.0f;
 #pragma unroll
-        for (int v = 0; v < kS; ++v) sum += part[(v * T + row) * 16 + t];
-        y[t * n + grow] = sum + (bias ? bias[grow] : 0.0f);
+        for (int v = 0; v < kWaves; ++v) sum += part[v][row][t];
+        y[t * n + grow] = 0.125f * sum + (bias ? bias[grow] : 0.0f);
     }
-}
-
-constexpr size_t kLdsCap = 160 * 1024;
-
-template <int kR, int kM, int kGPW, int kPos>
-size_t mfma_lds_bytes(int64_t k) {
-    constexpr int kS = kWaves / kR;
-    const int64_t C = k >> 5, G = k >> 7;
-    return (static_cast<size_t>(kM) * C * 16 + kGPW * 4 * 16) * 4 + static_cast<size_t>(kM) * G * 4 +
-           static_cast<size_t>(kS) * 16 * kR * 16 * 4;
-}
-
-template <int kR, int kM, int kGPW, int kPos>
-int launch_mfma(int64_t tiles, hipStream_t s, const uint16_t* x, int m, const uint8_t* pt, const uint16_t* st,
-                const float* b, int64_t n, int64_t k, float* y) {
-    const size_t bytes = mfma_lds_bytes<kR, kM, kGPW, kPos>(k);
-    if (bytes > kLdsCap) return fail(TQ_EINVAL, "tq_gemv_w4g128_tiled: LDS budget exceeded");
-    auto* fn = k_decode_tiled_mfma<kR, kM, kGPW, kPos>;
-    static bool attr_set = false;  // per instantiation; the attribute is per device function
-    if (!attr_set) {
-        if (hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                static_cast<int>(kLdsCap)) != hipSuccess)
-            return fail(TQ_EHIP, "tq_gemv_w4g128_tiled: hipFuncSetAttribute failed");
-        attr_set = true;
-    }
-    fn<<<static_cast<unsigned>(tiles), kBlock, bytes, s>>>(x, m, pt, st, b, n, k, y);
-    return check_launch("tq_gemv_w4g128_tiled");
-}
-
-// kGPW in {4, 8}: groups per wave rounded up (more would not fit the register
-// budget of 16 waves per CU)
-template <int kR, int kM, int kPos>
-int dispatch_mfma_gpw(int64_t gpw, int64_t tiles, hipStream_t s, const uint16_t* x, int m, const uint8_t* pt,
-                      const uint16_t* st, const float* b, int64_t n, int64_t k, float* y) {
-    if (gpw <= 4) return launch_mfma<kR, kM, 4, kPos>(tiles, s, x, m, pt, st, b, n, k, y);
-    return launch_mfma<kR, kM, 8, kPos>(tiles, s, x, m, pt, st, b, n, k, y);
 }
 
 template <int kR>
-int dispatch_mfma(int64_t m, int64_t gpw, int64_t tiles, hipStream_t s, const uint16_t* x, const uint8_t* pt,
-                  const uint16_t* st, const float* b, int64_t n, int64_t k, float* y) {
-    const int mi = static_cast<int>(m);
-    if (k <= 4096) {
-        if (m <= 4) return dispatch_mfma_gpw<kR, 4, 1>(gpw, tiles, s, x, mi, pt, st, b, n, k, y);
-        if (m <= 8) return dispatch_mfma_gpw<kR, 8, 1>(gpw, tiles, s, x, mi, pt, st, b, n, k, y);
-        return dispatch_mfma_gpw<kR, 16, 1>(gpw, tiles, s, x, mi, pt, st, b, n, k, y);
-    }
-    if (m <= 4) return dispatch_mfma_gpw<kR, 4, 2>(gpw, tiles, s, x, mi, pt, st, b, n, k, y);
-    return dispatch_mfma_gpw<kR, 8, 2>(gpw, tiles, s, x, mi, pt, st, b, n, k, y);
+int launch_mfma(int64_t gpw, int64_t tiles, hipStream_t s, const uint16_t* x, int m, const uint8_t* pt,
+                const uint16_t* st, const float* b, int64_t n, int64_t k, float* y) {
+    const unsigned grid = static_cast<unsigned>(tiles);
+    if (gpw <= 1)
+        k_decode_tiled_mfma<kR, 1><<<grid, kBlock, 0, s>>>(x, m, pt, st, b, n, k, y);
+    else if (gpw <= 2)
+        k_decode_tiled_mfma<kR, 2><<<grid, kBlock, 0, s>>>(x, m, pt, st, b, n, k, y);
+    else
+        k_decode_tiled_mfma<kR, 4><<<grid, kBlock, 0, s>>>(x, m, pt, st, b, n, k, y);
+    return check_launch("tq_gemv_w4g128_tiled");
 }
 
-// 16-byte chunks move from row-major rows into tiles; rows past n become zeros.
 __global__ __launch_bounds__(256) void k_repack_tiled(const uint8_t* __restrict__ packed,
                                                       const uint16_t* __restrict__ s16, int64_t n,
                                                       int64_t k, int tile_rows, int64_t tiles,
@@ -443,27 +414,15 @@ int tq_gemv_w4g128_tiled(const uint16_t* x_bf16, int64_t m, const uint8_t* packe
     const int64_t tiles = (n + tile_rows - 1) / tile_rows;
     const int T = static_cast<int>(tile_rows);
     const hipStream_t st = as_hip(stream);
-    // 3..16 tokens: the MFMA kernel where the tile is 16, 32 or 64 rows, a wave's K range
-    // is at most 8 groups and the tokens' x fits its LDS staging (K <= 8192; 16 tokens
-    // per pass for K <= 4096, 8 above)
+    // 3..16 tokens: the MFMA kernel where the tile is 16, 32 or 64 rows, the 16 waves'
+    // K runs are at most 4 groups (K <= 8192) and x rows are 16-byte aligned
     const int kr = T == 16 ? 1 : (T == 32 ? 2 : (T == 64 ? 4 : 0));
-    if (m >= 3 && kr && k <= 8192 && aligned(s_t, 8)) {
-        const int64_t G = k >> 7, ks = kWaves / kr;
-        const int64_t gpw = (G + ks - 1) / ks;
-        const int64_t per_pass = k <= 4096 ? 16 : 8;
-        if (gpw <= 8) {
-            for (int64_t m0 = 0; m0 < m; m0 += per_pass) {
-                const int64_t mm = (m - m0) < per_pass ? (m - m0) : per_pass;
-                const uint16_t* xp = x_bf16 + m0 * k;
-                float* yp = y + m0 * n;
-                int rc;
-                if (kr == 1) rc = dispatch_mfma<1>(mm, gpw, tiles, st, xp, packed_t, s_t, bias, n, k, yp);
-                else if (kr == 2) rc = dispatch_mfma<2>(mm, gpw, tiles, st, xp, packed_t, s_t, bias, n, k, yp);
-                else rc = dispatch_mfma<4>(mm, gpw, tiles, st, xp, packed_t, s_t, bias, n, k, yp);
-                if (rc != TQ_OK) return rc;
-            }
-            return TQ_OK;
-        }
+    const int64_t gpw = ((k >> 7) + kWaves - 1) / kWaves;
+    if (m >= 3 && kr && gpw <= 4 && aligned(x_bf16, 16) && aligned(s_t, 8)) {
+        const int mi = static_cast<int>(m);
+        if (kr == 1) return launch_mfma<1>(gpw, tiles, st, x_bf16, mi, packed_t, s_t, bias, n, k, y);
+        if (kr == 2) return launch_mfma<2>(gpw, tiles, st, x_bf16, mi, packed_t, s_t, bias, n, k, y);
+        return launch_mfma<4>(gpw, tiles, st, x_bf16, mi, packed_t, s_t, bias, n, k, y);
     }
     for (int64_t m0 = 0; m0 < m; m0 += kMaxTok) {
         const int64_t mm = (m - m0) < kMaxTok ? (m - m0) : kMaxTok;

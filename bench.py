@@ -230,12 +230,14 @@ def main():
         q = torch.empty((n1, k1), dtype=torch.int8, device=dev)
         s = torch.empty(n1, dtype=torch.float32, device=dev)
         wh = torch.empty((n1, k1), dtype=torch.float32, device=dev)
+        # dequantize input: codes rotating over copies as well, so that its reads come from HBM
+        qs = [torch.randint(-127, 128, (n1, k1), dtype=torch.int8, device=dev) for _ in range(rotation(n1 * k1))]
 
         def lq(i):
             _abi.call("tq_quantize_i8_rowwise", ptr(ins[i % len(ins)]), n1, k1, ptr(q), ptr(s), stream())
 
         def ld(i):
-            _abi.call("tq_dequantize_i8_rowwise", ptr(q), ptr(s), n1, k1, ptr(wh), stream())
+            _abi.call("tq_dequantize_i8_rowwise", ptr(qs[i % len(qs)]), ptr(s), n1, k1, ptr(wh), stream())
 
         def lf(i):
             _abi.call("tq_fake_quantize_i8_rowwise", ptr(ins[i % len(ins)]), n1, k1, ptr(q), ptr(s), ptr(wh),
@@ -249,7 +251,7 @@ def main():
             res[name] = {"us": round(ms * 1e3, 3), "GB/s": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
             log(f"roundtrip {name}: {ms * 1e3:.2f} us  {gbs:.0f} GB/s")
         secondary["roundtrip_i8_4096x4096"] = res
-        del ins
+        del ins, qs
 
     # --------------------------------------------------------- MLP (C5)
     if not args.no_secondary and want("mlp"):

@@ -48,9 +48,24 @@ __device__ __forceinline__ int code_i8(float x, float s, float inv_s, float half
     return signed_code(x, n, -128, 127);
 }
 
+// INT8 code of x for its row's own scale s = f32(max(absmax/127, 1e-10)) (finite):
+// |x| / s <= 127 (1 + 2^-22), so the code stays in [-127, 127] before the clamp.
+// fmax(NaN, 0) = 0 sends NaN to code 0 without a separate test; the rounding is
+// rhaz_div's (candidate, exact residual, +-1).
+__device__ __forceinline__ int code_i8_row(float x, float s, float inv_s, float half_s) {
+    const float a = fabsf(x);
+    float n = floorf(fmaxf(a * inv_s, 0.0f) + 0.5f);
+    const float r = fmaf(-n, s, a);
+    n = (r >= half_s) ? n + 1.0f : n;
+    n = (r < -half_s) ? n - 1.0f : n;
+    const int c = static_cast<int>(copysignf(n, x));
+    return min(max(c, -128), 127);
+}
+
 __device__ __forceinline__ uint32_t pack4_i8(int a, int b, int c, int d) {
-    return (uint32_t)(a & 0xFF) | ((uint32_t)(b & 0xFF) << 8) | ((uint32_t)(c & 0xFF) << 16) |
-           ((uint32_t)(d & 0xFF) << 24);
+    // low bytes of a, b (bytes 0, 1) and c, d (bytes 2, 3)
+    return __builtin_amdgcn_perm(static_cast<uint32_t>(b), static_cast<uint32_t>(a), 0x0c0c0400u) |
+           __builtin_amdgcn_perm(static_cast<uint32_t>(d), static_cast<uint32_t>(c), 0x04000c0cu);
 }
 
 // ---- per-row INT8, register-cached row (K % 4 == 0, K <= 1024 * kItems) ----
@@ -87,19 +102,19 @@ __global__ __launch_bounds__(kBlock) void k_quant_i8_rows_vec(const float* __res
         if (idx < k4) {
             int c0 = 0, c1 = 0, c2 = 0, c3 = 0;
             if (finite) {
-                c0 = code_i8(v[i].x, sc, inv, half);
-                c1 = code_i8(v[i].y, sc, inv, half);
-                c2 = code_i8(v[i].z, sc, inv, half);
-                c3 = code_i8(v[i].w, sc, inv, half);
+                c0 = code_i8_row(v[i].x, sc, inv, half);
+                c1 = code_i8_row(v[i].y, sc, inv, half);
+                c2 = code_i8_row(v[i].z, sc, inv, half);
+                c3 = code_i8_row(v[i].w, sc, inv, half);
             }
-            if (q) qd[idx] = pack4_i8(c0, c1, c2, c3);
+            if (q) __builtin_nontemporal_store(pack4_i8(c0, c1, c2, c3), qd + idx);
             if (w_hat) {
                 f32x4 o;
                 o.x = static_cast<float>(c0) * sc;
                 o.y = static_cast<float>(c1) * sc;
                 o.z = static_cast<float>(c2) * sc;
                 o.w = static_cast<float>(c3) * sc;
-                wd[idx] = o;
+                __builtin_nontemporal_store(o, wd + idx);
             }
         }
     }
@@ -129,26 +144,32 @@ __global__ __launch_bounds__(kBlock) void k_quant_i8_rows_generic(const float* _
 
 // ---- per-row INT8 dequant: w_hat = f32(q * s[row]) ----
 // Vector form: 16 codes per thread (K % 16 == 0, aligned).
+// Thread t of a block handles 4-element units t + 256 j (j < kDqUnits): every
+// wave-wide load reads 256 contiguous code bytes, every store writes 1 KB.
+constexpr int kDqUnits = 4;
 __global__ __launch_bounds__(kBlock) void k_dequant_i8_rows_vec(const int8_t* __restrict__ q,
                                                                 const float* __restrict__ s,
-                                                                int64_t k, int64_t n16,
+                                                                int64_t k, int64_t n4,
                                                                 float* __restrict__ w_hat) {
-    const int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
-    if (i >= n16) return;
-    const int64_t row = (i * 16) / k;
-    const float sc = s[row];
-    const i32x4 c = __builtin_nontemporal_load(reinterpret_cast<const i32x4*>(q) + i);
-    const int words[4] = {c.x, c.y, c.z, c.w};
-    f32x4* dst = reinterpret_cast<f32x4*>(w_hat) + i * 4;
+    const int64_t u0 = static_cast<int64_t>(blockIdx.x) * (kBlock * kDqUnits) + threadIdx.x;
+    int32_t c[kDqUnits];
+    float sc[kDqUnits];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int wv = words[j];
+    for (int j = 0; j < kDqUnits; ++j) {
+        const int64_t u = min<int64_t>(u0 + j * kBlock, n4 - 1);
+        c[j] = __builtin_nontemporal_load(reinterpret_cast<const int32_t*>(q) + u);
+        sc[j] = s[(u * 4) / k];
+    }
+#pragma unroll
+    for (int j = 0; j < kDqUnits; ++j) {
+        const int64_t u = u0 + j * kBlock;
+        if (u >= n4) break;
         f32x4 o;
-        o.x = static_cast<float>(static_cast<int8_t>(wv & 0xFF)) * sc;
-        o.y = static_cast<float>(static_cast<int8_t>((wv >> 8) & 0xFF)) * sc;
-        o.z = static_cast<float>(static_cast<int8_t>((wv >> 16) & 0xFF)) * sc;
-        o.w = static_cast<float>(static_cast<int8_t>((wv >> 24) & 0xFF)) * sc;
-        dst[j] = o;
+        o.x = static_cast<float>(static_cast<int8_t>(c[j] & 0xFF)) * sc[j];
+        o.y = static_cast<float>(static_cast<int8_t>((c[j] >> 8) & 0xFF)) * sc[j];
+        o.z = static_cast<float>(static_cast<int8_t>((c[j] >> 16) & 0xFF)) * sc[j];
+        o.w = static_cast<float>(static_cast<int8_t>((c[j] >> 24) & 0xFF)) * sc[j];
+        __builtin_nontemporal_store(o, reinterpret_cast<f32x4*>(w_hat) + u);
     }
 }
 
@@ -508,8 +529,8 @@ int tq_dequantize_i8_rowwise(const int8_t* q, const float* s, int64_t rows, int6
     TQ_REQUIRE(q && s && w_hat, "tq_dequantize_i8_rowwise: null pointer");
     const hipStream_t st = as_hip(stream);
     if (k % 16 == 0 && aligned(q, 16) && aligned(w_hat, 16)) {
-        const int64_t n16 = total / 16;
-        k_dequant_i8_rows_vec<<<grid_for(n16, kBlock, INT32_MAX), kBlock, 0, st>>>(q, s, k, n16, w_hat);
+        const int64_t n4 = total / 4;
+        k_dequant_i8_rows_vec<<<grid_for(n4, kBlock * kDqUnits, INT32_MAX), kBlock, 0, st>>>(q, s, k, n4, w_hat);
     } else {
         k_dequant_i8_rows_generic<<<grid_for(total, kBlock, INT32_MAX), kBlock, 0, st>>>(q, s, k, total, w_hat);
     }

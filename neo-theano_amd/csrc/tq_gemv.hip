@@ -5,10 +5,10 @@
 //
 // HBM-bound weight stream.  The grid is persistent: every
 // wave owns a contiguous range of output rows, keeps its slice of x in
-// registers for its whole life, and issues the loads of kRows rows at once
-// (global_load_dwordx4, non-temporal) so that each CU keeps tens of KB in
-// flight.  Lane l owns 16-byte slices of a row at byte 16*l of every 1 KB
-// chunk, so each wave-wide load is 1 KB contiguous; a row's partial dot
+// registers for its whole life (staged once per block through LDS), and keeps
+// the loads of the next kRows rows in flight (global_load_dwordx4,
+// non-temporal).  Lane l owns 16-byte slices of a row at byte 16*l of every
+// 1 KB chunk, so each wave-wide load is 1 KB contiguous; a row's partial dot
 // products meet in one wave64 butterfly.  Up to 4 tokens per pass.
 #include "tq_internal.h"
 
@@ -21,56 +21,79 @@ __device__ __forceinline__ int64_t uniform(int64_t v) {
     return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
 }
 
-constexpr int kBlock = 256;
-constexpr int kWaves = kBlock / kWave;
-constexpr int kWavesPerCU = 8;
 
 // ------------------------------------------------------------------- INT8
 // Chunk c covers k in [1024c, 1024c + 1024): lane l owns the 16 codes at
 // k = 1024c + 16l.  y = s[row] * sum(q * x) + b.
+//
+// One 512-thread block per CU (persistent), 8 waves, each owning a contiguous
+// run of rows.  A wave first issues the weight loads of its first kRows rows
+// (unconditional: rows past its run re-read its last row and are not
+// stored), then the block stages x in LDS once (f32, K-contiguous per token)
+// and every lane copies its 16-value slices into registers; rows are then
+// consumed kRows at a time with the next group's loads issued before the
+// current group's arithmetic.  x crosses L2 once per block instead of once per
+// wave.
+constexpr int kBlockW8 = 512;
+constexpr int kWavesW8 = kBlockW8 / kWave;
+
 template <int kM, int kChunks, int kRows>
-__global__ __launch_bounds__(kBlock) void k_gemv_w8(const float* __restrict__ x, int64_t x_stride,
-                                                    const int8_t* __restrict__ q,
-                                                    const float* __restrict__ s,
-                                                    const float* __restrict__ bias, int64_t n,
-                                                    int64_t k, float* __restrict__ y,
-                                                    int64_t y_stride, int64_t rows_per_wave) {
+__global__ __launch_bounds__(kBlockW8) void k_gemv_w8(const float* __restrict__ x, int64_t x_stride,
+                                                      const int8_t* __restrict__ q,
+                                                      const float* __restrict__ s,
+                                                      const float* __restrict__ bias, int64_t n,
+                                                      int64_t k, float* __restrict__ y,
+                                                      int64_t y_stride, int64_t rows_per_wave) {
+    __shared__ f32x4 xs[kM][kChunks * 256];
     const int lane = threadIdx.x & (kWave - 1);
-    const int64_t wave = uniform(static_cast<int64_t>(blockIdx.x) * kWaves + (threadIdx.x >> 6));
+    const int64_t wave = uniform(static_cast<int64_t>(blockIdx.x) * kWavesW8 + (threadIdx.x >> 6));
     const int64_t row_begin = wave * rows_per_wave;
     const int64_t row_end = min(n, row_begin + rows_per_wave);
-    if (row_begin >= row_end) return;
+    const int64_t row_last = max(row_begin, row_end - 1);  // clamp target (valid when the run is empty too)
+    const int64_t row_clamp = min(row_last, n - 1);
 
+    auto load_rows = [&](int64_t row0, i32x4 (&wq)[kRows][kChunks]) {
+#pragma unroll
+        for (int r = 0; r < kRows; ++r)
+#pragma unroll
+            for (int c = 0; c < kChunks; ++c) {
+                const int64_t row = min(row0 + r, row_clamp);
+                const int64_t kb = min<int64_t>(1024 * c + 16 * lane, k - 16);
+                wq[r][c] = __builtin_nontemporal_load(reinterpret_cast<const i32x4*>(q + row * k + kb));
+            }
+    };
+    i32x4 wq[kRows][kChunks];
+    load_rows(row_begin, wq);
+
+    // x -> LDS (zero past K), then each lane's 16-value slices -> registers
+    const int k4 = static_cast<int>(k >> 2);
+    for (int i = threadIdx.x; i < kM * kChunks * 256; i += kBlockW8) {
+        const int m = i / (kChunks * 256), j = i - m * (kChunks * 256);
+        xs[m][j] = j < k4 ? *reinterpret_cast<const f32x4*>(x + m * x_stride + 4 * j) : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    __syncthreads();
     float xr[kM][kChunks][16];
 #pragma unroll
-    for (int c = 0; c < kChunks; ++c) {
-        const int64_t kb = 1024 * c + 16 * lane;
-        const bool valid = kb < k;
+    for (int m = 0; m < kM; ++m)
 #pragma unroll
-        for (int m = 0; m < kM; ++m)
+        for (int c = 0; c < kChunks; ++c)
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                f32x4 v = f32x4{0.f, 0.f, 0.f, 0.f};
-                if (valid) v = *reinterpret_cast<const f32x4*>(x + m * x_stride + kb + 4 * j);
+                const f32x4 v = xs[m][c * 256 + 4 * lane + j];
                 xr[m][c][4 * j + 0] = v.x;
                 xr[m][c][4 * j + 1] = v.y;
                 xr[m][c][4 * j + 2] = v.z;
                 xr[m][c][4 * j + 3] = v.w;
             }
-    }
+    if (row_begin >= row_end) return;
 
     for (int64_t row0 = row_begin; row0 < row_end; row0 += kRows) {
-        i32x4 wq[kRows][kChunks];
+        i32x4 cur[kRows][kChunks];
 #pragma unroll
         for (int r = 0; r < kRows; ++r)
 #pragma unroll
-            for (int c = 0; c < kChunks; ++c) {
-                const int64_t row = row0 + r;
-                const int64_t kb = 1024 * c + 16 * lane;
-                wq[r][c] = (row < row_end && kb < k)
-                               ? __builtin_nontemporal_load(reinterpret_cast<const i32x4*>(q + row * k + kb))
-                               : i32x4{0, 0, 0, 0};
-            }
+            for (int c = 0; c < kChunks; ++c) cur[r][c] = wq[r][c];
+        if (row0 + kRows < row_end) load_rows(row0 + kRows, wq);
 #pragma unroll
         for (int r = 0; r < kRows; ++r) {
             float acc[kM];
@@ -78,7 +101,7 @@ __global__ __launch_bounds__(kBlock) void k_gemv_w8(const float* __restrict__ x,
             for (int m = 0; m < kM; ++m) acc[m] = 0.0f;
 #pragma unroll
             for (int c = 0; c < kChunks; ++c) {
-                const int words[4] = {wq[r][c].x, wq[r][c].y, wq[r][c].z, wq[r][c].w};
+                const int words[4] = {cur[r][c].x, cur[r][c].y, cur[r][c].z, cur[r][c].w};
 #pragma unroll
                 for (int j = 0; j < 4; ++j)
 #pragma unroll
@@ -89,7 +112,7 @@ __global__ __launch_bounds__(kBlock) void k_gemv_w8(const float* __restrict__ x,
                     }
             }
             const int64_t row = row0 + r;
-            const float sc = row < row_end ? s[row] : 0.0f;
+            const float sc = s[min(row, row_clamp)];
 #pragma unroll
             for (int m = 0; m < kM; ++m) {
                 const float v = wave_sum(acc[m]);
@@ -99,25 +122,28 @@ __global__ __launch_bounds__(kBlock) void k_gemv_w8(const float* __restrict__ x,
     }
 }
 
-// Persistent grid: kWavesPerCU waves per CU, contiguous row ranges per wave.
+// Persistent grid: one block per CU (fewer if there are few rows), contiguous
+// row runs per wave, a multiple of kRows each.
 template <int kRows>
 void grid_for_rows(int64_t n, int64_t* blocks, int64_t* rows_per_wave) {
-    const int64_t slots = static_cast<int64_t>(device_cu_count()) * kWavesPerCU;
+    const int64_t slots = static_cast<int64_t>(device_cu_count()) * kWavesW8;
     int64_t waves = (n + kRows - 1) / kRows;
     if (waves > slots) waves = slots;
-    *rows_per_wave = (n + waves - 1) / waves;
-    waves = (n + *rows_per_wave - 1) / *rows_per_wave;
-    *blocks = (waves + kWaves - 1) / kWaves;
+    int64_t rpw = (n + waves - 1) / waves;
+    rpw = (rpw + kRows - 1) / kRows * kRows;
+    *rows_per_wave = rpw;
+    waves = (n + rpw - 1) / rpw;
+    *blocks = (waves + kWavesW8 - 1) / kWavesW8;
 }
 
 template <int kM, int kChunks>
 void launch_w8(const float* x, int64_t xs, const int8_t* q, const float* s, const float* b,
                int64_t n, int64_t k, float* y, int64_t ys, hipStream_t st) {
-    constexpr int kRows = (kM * kChunks <= 4) ? 4 : 2;
+    constexpr int kRows = 2;
     int64_t blocks, rpw;
     grid_for_rows<kRows>(n, &blocks, &rpw);
-    k_gemv_w8<kM, kChunks, kRows><<<static_cast<unsigned>(blocks), kBlock, 0, st>>>(x, xs, q, s, b, n, k, y,
-                                                                                  ys, rpw);
+    k_gemv_w8<kM, kChunks, kRows><<<static_cast<unsigned>(blocks), kBlockW8, 0, st>>>(x, xs, q, s, b, n, k, y,
+                                                                                    ys, rpw);
 }
 
 template <int kM>

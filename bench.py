@@ -273,7 +273,22 @@ def main():
         secondary["mlp_w4g128_m512"] = {"us": round(ms * 1e3, 2), "tokens/s": round(m5 / (ms * 1e-3), 1),
                                         "TFLOP/s": round(tf, 1), "bf16_mfma_frac": round(tf / BF16_PEAK_TFLOPS, 4)}
         log(f"mlp M=512: {ms * 1e3:.1f} us  {m5 / (ms * 1e-3):.0f} tok/s  {tf:.0f} TFLOP/s")
-        del mlp
+
+        # prefill INT4 Linear on the gate weight alone: [512, 4096] x [14336, 4096]^T
+        nbl = int(_abi.lib().tq_gemm_w4g128_bf16_workspace_bytes(m5, d5))
+        wsl = torch.empty((nbl,), dtype=torch.uint8, device=dev)
+        yl = torch.empty((m5, f5), dtype=torch.float32, device=dev)
+
+        def launch_lin(i):
+            _abi.call("tq_gemm_w4g128_bf16_ws", ptr(x), m5, ptr(mlp.gate[0]), ptr(mlp.gate[1]), None, f5, d5,
+                      ptr(wsl), nbl, ptr(yl), stream())
+
+        ms, _ = timer.run(launch_lin, steps, 2)
+        tf = 2.0 * m5 * f5 * d5 / (ms * 1e-3) / 1e12
+        secondary["w4a16_linear_m512_n14336_k4096"] = {"us": round(ms * 1e3, 2), "TFLOP/s": round(tf, 1),
+                                                       "bf16_mfma_frac": round(tf / BF16_PEAK_TFLOPS, 4)}
+        log(f"w4a16 linear M=512 N=14336 K=4096: {ms * 1e3:.1f} us  {tf:.0f} TFLOP/s")
+        del mlp, wsl, yl
 
     # ------------------------------------------ copy (PMC calibration)
     if only == "copy":

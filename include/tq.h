@@ -221,6 +221,21 @@ int tq_gemm_w4g128_bf16(const uint16_t* x_bf16, int64_t m, const uint8_t* packed
                         const uint16_t* s_f16, const float* bias, int64_t n, int64_t k,
                         float* y, tq_stream_t stream);
 
+/* The same Linear (crates/theano-nn/src/linear.rs:111-121 over the dequantized
+ * weight) on the pipelined FFN kernels: x in the kernels' k-order and
+ * its group sums go to `workspace` (at least
+ * tq_gemm_w4g128_bf16_workspace_bytes(M, K) bytes, 256-byte aligned).  Runs when
+ * K % 256 == 0 and N % 256 == 0 with 16-byte aligned x, packed and y and
+ * 4-byte aligned scales; other shapes take tq_gemm_w4g128_bf16.  When twice
+ * the output tiles still fit the CUs in one round, K is split in two halves
+ * added into y (zeroed first; two addends onto zero, so the result is
+ * deterministic). */
+int64_t tq_gemm_w4g128_bf16_workspace_bytes(int64_t m, int64_t k);
+int tq_gemm_w4g128_bf16_ws(const uint16_t* x_bf16, int64_t m, const uint8_t* packed,
+                           const uint16_t* s_f16, const float* bias, int64_t n, int64_t k,
+                           void* workspace, int64_t workspace_bytes, float* y,
+                           tq_stream_t stream);
+
 /* Quantized Llama-style FFN (build-defined composition of Linear, SiLU
  * (crates/theano-nn/src/activation.rs:66-79) and Tensor::mul):
  *   h = SiLU(x Wg^T) * (x Wu^T);   y = h Wd^T   (f32 [M, D]).

@@ -109,10 +109,16 @@ __device__ __forceinline__ f32x16 mfma(u32x4 a, u32x4 b, f32x16 c) {
                                                    0, 0, 0);
 }
 
-// 16 lanes per (row, group): 8 values each.
+// 16 lanes per (row, group): 8 values each.  Also zeroes y [M, ny] when given
+// (grid-stride, 16 bytes per step).
 __global__ __launch_bounds__(256) void k_ffn_prep(const uint16_t* __restrict__ x, int64_t m, int64_t d, int64_t mpad,
                                                   uint16_t* __restrict__ xp, uint32_t* __restrict__ xs,
-                                                  float* __restrict__ yzero) {
+                                                  float* __restrict__ yzero, int64_t ny) {
+    if (yzero) {
+        const int64_t n4 = m * ny / 4, stride = static_cast<int64_t>(gridDim.x) * 256;
+        for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n4; i += stride)
+            reinterpret_cast<f32x4*>(yzero)[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
     const int64_t G = d >> 7;
     const int64_t item = static_cast<int64_t>(blockIdx.x) * 16 + (threadIdx.x >> 4);
     if (item >= m * G) return;
@@ -131,8 +137,6 @@ __global__ __launch_bounds__(256) void k_ffn_prep(const uint16_t* __restrict__ x
     o.w = __builtin_amdgcn_perm(v.w, v.z, 0x07060302u);
     *reinterpret_cast<u32x4*>(xp + off) = o;
     if (l == 0) *reinterpret_cast<uint2*>(xs + (g * mpad + row) * 2) = split3(-kOffset * s);
-    *reinterpret_cast<f32x4*>(yzero + off) = f32x4{0.f, 0.f, 0.f, 0.f};
-    *reinterpret_cast<f32x4*>(yzero + off + 4) = f32x4{0.f, 0.f, 0.f, 0.f};
 }
 
 struct FfnArgs {
@@ -145,7 +149,8 @@ struct FfnArgs {
     const uint16_t* s1;
     int64_t m, n, k, mpad;
     int tiles_m, tiles_n;
-    float* y;        // down: f32 [M, N], zeroed
+    float* y;        // down / Linear: f32 [M, N], zeroed when K is split
+    const float* bias;  // Linear: f32 [N] or null
     uint16_t* h_hi;  // gate/up: h planes [M, N] bf16 in xp order
     uint16_t* h_lo;
     uint32_t* hs;    // gate/up: -192 * group sums of h, planes [N/128][mpad][2]
@@ -396,7 +401,7 @@ __global__ __launch_bounds__(64 * kWavesM * kWavesN, 1) void k_ffn(FfnArgs p) {
                 for (int e = 0; e < 16; ++e) {
                     const int64_t mm = m0 + wm * 32 * kWM + i * 32 + 8 * (e >> 2) + 4 * lh + (e & 3);
                     if (mm < p.m) {
-                        const float v = (kUnit * sprev[t]) * dg[i][t][e];
+                        const float v = (kUnit * sprev[t]) * dg[i][t][e] + (p.bias && ks == 0 ? p.bias[nn] : 0.0f);
                         if constexpr (kSplit == 1)
                             p.y[mm * p.n + nn] = v;
                         else
@@ -458,6 +463,10 @@ using GuCfg = FfnCfg<kGuWM, kGuWN, kGuTM, kGuTN, 2, 1>;
 // down: 2 x 4 waves of 32 rows x 64 columns on two h planes -> 64 x 256 y per block, K in two halves
 constexpr int kDnWM = 2, kDnWN = 4, kDnTM = 1, kDnTN = 2, kDnSplit = 2;
 using DnCfg = FfnCfg<kDnWM, kDnWN, kDnTM, kDnTN, 1, 2>;
+
+// prefill Linear: 2 x 4 waves of 64 rows x 64 columns -> 128 x 256 y per block
+constexpr int kLnWM = 2, kLnWN = 4, kLnTM = 2, kLnTN = 2;
+using LinCfg = FfnCfg<kLnWM, kLnWN, kLnTM, kLnTN, 1, 1>;
 
 struct FfnWorkspace {
     int64_t mpad, xp, xs, hh, hl, hs, bytes;  // byte offsets of the parts, total
@@ -532,7 +541,7 @@ int tq_mlp_w4g128(const uint16_t* x_bf16, int64_t m, int64_t d, int64_t f, const
     const int64_t dn_tiles = ((m + DnCfg::BM - 1) / DnCfg::BM) * (d / DnCfg::BN) * kDnSplit;
     TQ_REQUIRE(gu_tiles < (int64_t(1) << 31) && dn_tiles < (int64_t(1) << 31), "tq_mlp_w4g128: problem too large");
 
-    k_ffn_prep<<<static_cast<unsigned>((items + 15) / 16), 256, 0, st>>>(x_bf16, m, d, w.mpad, xp, xs, y);
+    k_ffn_prep<<<static_cast<unsigned>((items + 15) / 16), 256, 0, st>>>(x_bf16, m, d, w.mpad, xp, xs, y, d);
     int rc = check_launch("tq_mlp_w4g128 (prep)");
     if (rc != TQ_OK) return rc;
 
@@ -571,6 +580,68 @@ int tq_mlp_w4g128(const uint16_t* x_bf16, int64_t m, int64_t d, int64_t f, const
     b.y = y;
     k_ffn<kDnWM, kDnWN, kDnTM, kDnTN, 1, 2, kDnSplit><<<static_cast<unsigned>(dn_tiles), DnCfg::kThreads, 0, st>>>(b);
     return check_launch("tq_mlp_w4g128 (down)");
+}
+
+// ---- prefill W4A16 Linear on the same kernels (one weight matrix, one plane) ----
+
+int64_t tq_gemm_w4g128_bf16_workspace_bytes(int64_t m, int64_t k) {
+    if (m <= 0 || k <= 0) return 0;
+    const int64_t mpad = (m + 127) / 128 * 128;
+    return align256(m * k * 2) + align256((k / 128) * mpad * 8);
+}
+
+int tq_gemm_w4g128_bf16_ws(const uint16_t* x_bf16, int64_t m, const uint8_t* packed, const uint16_t* s_f16,
+                           const float* bias, int64_t n, int64_t k, void* workspace, int64_t workspace_bytes,
+                           float* y, tq_stream_t stream) {
+    TQ_REQUIRE(m >= 0 && n >= 0 && k >= 0, "tq_gemm_w4g128_bf16_ws: negative shape");
+    TQ_REQUIRE(k % 128 == 0, "tq_gemm_w4g128_bf16_ws: K=%lld is not a multiple of 128", (long long)k);
+    if (m == 0 || n == 0) return TQ_OK;
+    const int64_t need = tq_gemm_w4g128_bf16_workspace_bytes(m, k);
+    TQ_REQUIRE(k == 0 || (workspace && workspace_bytes >= need),
+               "tq_gemm_w4g128_bf16_ws: workspace of %lld bytes, %lld needed", (long long)workspace_bytes,
+               (long long)need);
+    // the pipelined kernel: scale pairs as dwords (K % 256), 256-column tiles,
+    // 16-byte vectors; anything else runs the workspace-free entry point
+    const bool fast = k > 0 && k % 256 == 0 && n % LinCfg::BN == 0 && x_bf16 && packed && s_f16 && y &&
+                      aligned(x_bf16, 16) && aligned(packed, 16) && aligned(s_f16, 4) && aligned(y, 16) &&
+                      (!bias || aligned(bias, 4)) && aligned(workspace, 256);
+    if (!fast) return tq_gemm_w4g128_bf16(x_bf16, m, packed, s_f16, bias, n, k, y, stream);
+    const hipStream_t st = as_hip(stream);
+    const int64_t mpad = (m + 127) / 128 * 128;
+    uint16_t* xp = static_cast<uint16_t*>(workspace);
+    uint32_t* xs = reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(workspace) + align256(m * k * 2));
+    const int64_t tiles_m = (m + LinCfg::BM - 1) / LinCfg::BM, tiles_n = n / LinCfg::BN;
+    // K halves are added into y when the doubled grid still fits one round on the CUs
+    // and each half keeps at least 8 groups (two addends onto zero: the sum does not
+    // depend on their order)
+    const bool split = 2 * tiles_m * tiles_n <= device_cu_count() && k / 128 >= 16;
+    const int64_t items = m * (k / 128);
+    TQ_REQUIRE((items + 15) / 16 < (int64_t(1) << 31) && tiles_m * tiles_n * 2 < (int64_t(1) << 31),
+               "tq_gemm_w4g128_bf16_ws: problem too large");
+    k_ffn_prep<<<static_cast<unsigned>((items + 15) / 16), 256, 0, st>>>(x_bf16, m, k, mpad, xp, xs,
+                                                                       split ? y : nullptr, n);
+    int rc = check_launch("tq_gemm_w4g128_bf16_ws (prep)");
+    if (rc != TQ_OK) return rc;
+    FfnArgs a{};
+    a.a0 = xp;
+    a.xs = xs;
+    a.w0 = packed;
+    a.s0 = s_f16;
+    a.m = m;
+    a.n = n;
+    a.k = k;
+    a.mpad = mpad;
+    a.tiles_m = static_cast<int>(tiles_m);
+    a.tiles_n = static_cast<int>(tiles_n);
+    a.y = y;
+    a.bias = bias;
+    if (split)
+        k_ffn<kLnWM, kLnWN, kLnTM, kLnTN, 1, 1, 2>
+            <<<static_cast<unsigned>(tiles_m * tiles_n * 2), LinCfg::kThreads, 0, st>>>(a);
+    else
+        k_ffn<kLnWM, kLnWN, kLnTM, kLnTN, 1, 1, 1>
+            <<<static_cast<unsigned>(tiles_m * tiles_n), LinCfg::kThreads, 0, st>>>(a);
+    return check_launch("tq_gemm_w4g128_bf16_ws");
 }
 
 }  // extern "C"

@@ -504,8 +504,13 @@ Result<QuantizedLinear> QuantizedLinear::from_tensors(const Tensor& weight, cons
     });
 }
 
+size_t QuantizedLinear::workspace_bytes(int64_t m) const {
+    if (mode_ != Mode::W4 || m <= 16) return 0;
+    return static_cast<size_t>(tq_gemm_w4g128_bf16_workspace_bytes(m, static_cast<int64_t>(in_)));
+}
+
 Result<void> QuantizedLinear::forward_device(const void* x, int64_t m, float* y, hipStream_t stream, int8_t* act_codes,
-                                             float* act_scales) const {
+                                             float* act_scales, void* workspace, size_t workspace_bytes) const {
     const auto ts = reinterpret_cast<tq_stream_t>(stream);
     const float* b = bias_ ? bias_->data() : nullptr;
     const int64_t n = static_cast<int64_t>(out_), k = static_cast<int64_t>(in_);
@@ -518,6 +523,9 @@ Result<void> QuantizedLinear::forward_device(const void* x, int64_t m, float* y,
                                           w4_.tile_rows, y, ts);
             else if (m <= 16)
                 st = tq_gemv_w4g128(xb, m, w4_.packed.data(), w4_.scales.data(), b, n, k, y, ts);
+            else if (workspace)
+                st = tq_gemm_w4g128_bf16_ws(xb, m, w4_.packed.data(), w4_.scales.data(), b, n, k, workspace,
+                                            static_cast<int64_t>(workspace_bytes), y, ts);
             else
                 st = tq_gemm_w4g128_bf16(xb, m, w4_.packed.data(), w4_.scales.data(), b, n, k, y, ts);
             break;
@@ -555,7 +563,10 @@ Result<Tensor> QuantizedLinear::try_forward(const Tensor& input) const {
             const std::vector<uint16_t> xb = to_bf16(xv);
             DeviceBuffer<uint16_t> xd(xb.size());
             xd.upload(xb.data(), xb.size(), stream_);
-            r = forward_device(xd.data(), static_cast<int64_t>(m), y.data(), stream_);
+            const size_t wsb = workspace_bytes(static_cast<int64_t>(m));
+            DeviceBuffer<uint8_t> ws(std::max<size_t>(wsb, 1));
+            r = forward_device(xd.data(), static_cast<int64_t>(m), y.data(), stream_, nullptr, nullptr,
+                               wsb ? ws.data() : nullptr, wsb);
         } else {
             const std::vector<float> xf(xv.begin(), xv.end());
             DeviceBuffer<float> xd(xf.size());

@@ -316,9 +316,13 @@ class QuantizedLinear : public Module {
     Result<Tensor> try_forward(const Tensor& input) const;
     // Device-resident forward: x is f32 [m, in] (w8, w8a8) or bf16 bits [m, in] (w4),
     // y is f32 [m, out]; enqueued on `stream`, no host synchronisation.  w8a8
-    // needs `act_codes` (int8 [m, in]) and `act_scales` (f32 [m]) device scratch.
+    // needs `act_codes` (int8 [m, in]) and `act_scales` (f32 [m]) device scratch;
+    // w4 with m > 16 uses `workspace` (workspace_bytes(m) bytes) when given.
     Result<void> forward_device(const void* x, int64_t m, float* y, hipStream_t stream,
-                                int8_t* act_codes = nullptr, float* act_scales = nullptr) const;
+                                int8_t* act_codes = nullptr, float* act_scales = nullptr,
+                                void* workspace = nullptr, size_t workspace_bytes = 0) const;
+    // device scratch of the w4 prefill path for m tokens (0 for other modes / m <= 16)
+    size_t workspace_bytes(int64_t m) const;
 
     std::vector<Tensor> parameters() const override;
     std::vector<std::pair<std::string, Tensor>> named_parameters() const override;

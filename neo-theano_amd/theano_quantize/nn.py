@@ -120,10 +120,15 @@ class QuantizedLinear(Module):
                 pt, st, t = self.tiled
                 _abi.call("tq_gemv_w4g128_tiled", ptr(x), m, ptr(pt), ptr(st), ptr(self.bias), n, k, t,
                           ptr(y), stream())
-            else:
-                fn = "tq_gemv_w4g128" if m <= DECODE_MAX_M else "tq_gemm_w4g128_bf16"
-                _abi.call(fn, ptr(x), m, ptr(self.qweight), ptr(self.scales), ptr(self.bias), n, k,
+            elif m <= DECODE_MAX_M:
+                _abi.call("tq_gemv_w4g128", ptr(x), m, ptr(self.qweight), ptr(self.scales), ptr(self.bias), n, k,
                           ptr(y), stream())
+            else:
+                # prefill: pipelined kernels with x's k-order and group sums in a workspace
+                nb = int(_abi.lib().tq_gemm_w4g128_bf16_workspace_bytes(m, k))
+                ws = torch.empty((max(nb, 1),), dtype=torch.uint8, device=x.device)
+                _abi.call("tq_gemm_w4g128_bf16_ws", ptr(x), m, ptr(self.qweight), ptr(self.scales), ptr(self.bias),
+                          n, k, ptr(ws), nb, ptr(y), stream())
         elif self.mode == "w8":
             for m0 in range(0, m, DECODE_MAX_M):
                 mm = min(DECODE_MAX_M, m - m0)

@@ -436,6 +436,30 @@ TEST_GPU(test_parity_quantized_linear_w4) {
     }
 }
 
+TEST_GPU(test_parity_quantized_linear_w4_prefill) {
+    // N % 256 == 0 and K % 256 == 0: the pipelined kernels (K split in two for the
+    // small grid at M = 40), with bias
+    const size_t n = 512, k = 2048;
+    const auto wv = randn(n * k, 0.02, 71), bv = randn(n, 0.1, 72);
+    const QuantizedLinear layer = QuantizedLinear::from_tensors(Tensor::from_slice(wv, {n, k}),
+                                                                Tensor::from_slice(bv, {n}), QConfig::default_int4())
+                                      .unwrap();
+    ASSERT(layer.workspace_bytes(40) > 0);
+    const auto w32 = f32(wv), b32 = f32(bv);
+    std::vector<uint8_t> p(n * k / 2);
+    std::vector<uint16_t> s(n * k / 128);
+    tqo_quantize_i4_g128(w32.data(), n, k, p.data(), s.data());
+    for (size_t m : {40u, 300u}) {
+        const auto xv = randn(m * k, 1.0, 73 + m);
+        const auto y = layer.forward(Tensor::from_slice(xv, {m, k})).to_vec_f64().unwrap();
+        std::vector<uint16_t> xb(m * k);
+        for (size_t i = 0; i < xb.size(); ++i) xb[i] = tqo_f32_to_bf16_bits(static_cast<float>(xv[i]));
+        std::vector<double> ref(m * n);
+        tqo_linear_w4g128_bf16(xb.data(), m, p.data(), s.data(), b32.data(), n, k, ref.data());
+        assert_close(y, ref, "w4 prefill linear");
+    }
+}
+
 TEST_GPU(test_parity_quantized_linear_w8a8) {
     const size_t n = 272, k = 1024, m = 37;
     const auto wv = randn(n * k, 0.02, 51), xv = randn(m * k, 1.0, 52);

@@ -293,8 +293,12 @@ def test_misaligned_inputs_take_the_general_kernels(tq, oracle):
 
 
 # ----------------------------------------------------------------- W4A16
+# (17, 256, 512), (300, 512, 768), (64, 1024, 4096), (129, 768, 2048) run the
+# pipelined kernels (K split in two where the grid is small); the rest the
+# 16x16x32 / shape-general kernels
 @pytest.mark.parametrize("m,n,k", [(17, 256, 512), (130, 64, 4096), (300, 128, 1024), (33, 16, 128),
-                                   (40, 200, 1024), (20, 7, 256)])
+                                   (40, 200, 1024), (20, 7, 256), (300, 512, 768), (64, 1024, 4096),
+                                   (129, 768, 2048)])
 def test_gemm_w4g128_bf16_shapes(tq, oracle, m, n, k):
     w = normal(55, (n, k), 0.02)
     xb = to_bf16_bits(normal(55, (m, k), 1.0, stream=1))
@@ -377,3 +381,31 @@ def test_mlp_workspace_reuse_and_size_check(tq, oracle):
     short = torch.empty((mlp.workspace_bytes(300) - 256,), dtype=torch.uint8, device="cuda")
     with pytest.raises(InvalidArgument):
         mlp.forward(bf16_dev(xb), short)
+
+
+def test_gemm_w4g128_bf16_entry_points_agree(tq, oracle):
+    """The workspace entry point (pipelined kernels) and the workspace-free one
+    (16x16x32 kernel) both meet the tolerance; a short workspace is rejected."""
+    import torch
+    from theano_quantize import InvalidArgument, _abi
+    from theano_quantize._tensor import ptr, stream
+
+    m, n, k = 200, 512, 2048
+    w = normal(59, (n, k), 0.02)
+    b = normal(59, (n,), 0.1, stream=2)
+    xb = to_bf16_bits(normal(59, (m, k), 1.0, stream=1))
+    q, s = tq.quantize_i4_g128(dev_tensor(w))
+    x, bias = bf16_dev(xb), dev_tensor(b)
+    y1 = torch.empty((m, n), dtype=torch.float32, device="cuda")
+    y2 = torch.empty_like(y1)
+    nb = int(_abi.lib().tq_gemm_w4g128_bf16_workspace_bytes(m, k))
+    ws = torch.empty((nb,), dtype=torch.uint8, device="cuda")
+    _abi.call("tq_gemm_w4g128_bf16_ws", ptr(x), m, ptr(q), ptr(s), ptr(bias), n, k, ptr(ws), nb, ptr(y1), stream())
+    _abi.call("tq_gemm_w4g128_bf16", ptr(x), m, ptr(q), ptr(s), ptr(bias), n, k, ptr(y2), stream())
+    rp, rs = oracle.quantize_i4_g128(w)
+    ref = oracle.linear_w4g128_bf16(xb, rp, rs, b)
+    assert_close(host(y1), ref, RTOL, ATOL, "w4a16 pipelined")
+    assert_close(host(y2), ref, RTOL, ATOL, "w4a16 16x16x32")
+    with pytest.raises(InvalidArgument):
+        _abi.call("tq_gemm_w4g128_bf16_ws", ptr(x), m, ptr(q), ptr(s), ptr(bias), n, k, ptr(ws), nb - 256,
+                  ptr(y1), stream())

@@ -73,7 +73,8 @@ def build_host(verbose=False):
         return None
     tmp = HOSTLIB + ".tmp"
     out = _run([HIPCC, "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall",
-                f"-I{os.path.join(ROOT, 'include')}", f"-I{HOST}", src, "-o", tmp,
+                f"-I{os.path.join(ROOT, 'include')}", f"-I{HOST}", src, os.path.join(HOST, "theano_serialize.cpp"),
+                "-o", tmp,
                 f"-L{PKG}", "-ltq", "-Wl,-rpath,$ORIGIN"])
     if verbose and out.strip():
         print(out)

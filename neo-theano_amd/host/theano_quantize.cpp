@@ -1,5 +1,6 @@
 // theano_quantize.cpp -- C++ host layer over libtq.so (see theano_quantize.hpp).
 #include "theano_quantize.hpp"
+#include "theano_serialize.hpp"
 
 #include <algorithm>
 #include <cmath>
@@ -338,6 +339,8 @@ Result<Int8Weight> quantize_per_channel_i8(const Tensor& weight, hipStream_t str
     });
 }
 
+void make_tiled(Int4Weight& w, hipStream_t stream);
+
 Result<Int4Weight> quantize_i4_g128(const Tensor& weight, hipStream_t stream) {
     return capture<Int4Weight>([&]() -> Result<Int4Weight> {
         Int4Weight w;
@@ -353,22 +356,25 @@ Result<Int4Weight> quantize_i4_g128(const Tensor& weight, hipStream_t stream) {
         int st = tq_quantize_i4_g128(src.data(), static_cast<int64_t>(w.rows), static_cast<int64_t>(w.cols),
                                      w.packed.data(), w.scales.data(), ts);
         if (st != TQ_OK) return TheanoError::from_status(st, "quantize_i4_g128");
-        if (w.cols <= 16384 && w.rows > 0) {
-            // row-tiled copy for the decode GEMV (a permutation of the packed bytes)
-            const int64_t t = tq_w4g128_tile_rows(static_cast<int64_t>(w.rows));
-            if (t <= 0) return TheanoError::runtime("quantize_i4_g128: tile size query failed");
-            const size_t padded = (w.rows + t - 1) / t * t;
-            w.packed_tiled = DeviceBuffer<uint8_t>(padded * w.cols / 2);
-            w.scales_tiled = DeviceBuffer<uint16_t>(padded * w.cols / 128);
-            st = tq_repack_w4g128_tiled(w.packed.data(), w.scales.data(), static_cast<int64_t>(w.rows),
-                                        static_cast<int64_t>(w.cols), t, w.packed_tiled.data(),
-                                        w.scales_tiled.data(), ts);
-            if (st != TQ_OK) return TheanoError::from_status(st, "quantize_i4_g128");
-            w.tile_rows = t;
-        }
+        make_tiled(w, stream);
         check_hip(hipStreamSynchronize(stream), "quantize_i4_g128");
         return std::move(w);
     });
+}
+
+void make_tiled(Int4Weight& w, hipStream_t stream) {
+    if (w.cols > 16384 || w.rows == 0) return;
+    // row-tiled copy for the decode GEMV (a permutation of the packed bytes)
+    const int64_t t = tq_w4g128_tile_rows(static_cast<int64_t>(w.rows));
+    if (t <= 0) throw TheanoError::runtime("tiled INT4 copy: tile size query failed");
+    const size_t padded = (w.rows + t - 1) / t * t;
+    w.packed_tiled = DeviceBuffer<uint8_t>(padded * w.cols / 2);
+    w.scales_tiled = DeviceBuffer<uint16_t>(padded * w.cols / 128);
+    check(tq_repack_w4g128_tiled(w.packed.data(), w.scales.data(), static_cast<int64_t>(w.rows),
+                                 static_cast<int64_t>(w.cols), t, w.packed_tiled.data(), w.scales_tiled.data(),
+                                 reinterpret_cast<tq_stream_t>(stream)),
+          "tiled INT4 copy");
+    w.tile_rows = t;
 }
 
 Result<Tensor> dequantize(const Int8Weight& w, hipStream_t stream) {
@@ -687,6 +693,160 @@ std::vector<Tensor> QuantizedMLP::parameters() const {
         out.push_back(std::move(t).unwrap());
     }
     return out;
+}
+
+}  // namespace nn
+}  // namespace theano
+
+// ------------------------------------------------------ quantized checkpoints
+namespace theano {
+namespace nn {
+namespace {
+
+using serialize::SafeTensorsFile;
+
+std::string meta(const SafeTensorsFile& f, const std::string& key) {
+    const auto it = f.metadata.find(key);
+    if (it == f.metadata.end()) throw TheanoError::runtime("checkpoint: missing metadata '" + key + "'");
+    return it->second;
+}
+
+size_t meta_size(const SafeTensorsFile& f, const std::string& key) {
+    const std::string v = meta(f, key);
+    try {
+        return static_cast<size_t>(std::stoull(v));
+    } catch (...) {
+        throw TheanoError::runtime("checkpoint: metadata '" + key + "' is not a size: " + v);
+    }
+}
+
+template <class T>
+std::vector<uint8_t> bytes_of(const DeviceBuffer<T>& b, hipStream_t stream) {
+    const std::vector<T> h = b.to_host(stream);
+    std::vector<uint8_t> out(h.size() * sizeof(T));
+    std::memcpy(out.data(), h.data(), out.size());
+    return out;
+}
+
+template <class T>
+DeviceBuffer<T> device_of(const std::vector<uint8_t>& raw, hipStream_t stream) {
+    DeviceBuffer<T> b(raw.size() / sizeof(T));
+    b.upload(reinterpret_cast<const T*>(raw.data()), raw.size() / sizeof(T), stream);
+    return b;
+}
+
+template <class T>
+std::vector<uint8_t> get(const SafeTensorsFile& f, const std::string& name, const char* dtype,
+                         std::vector<size_t> shape) {
+    auto r = f.get_raw(name, dtype, shape);
+    if (r.is_err()) throw r.unwrap_err();
+    return std::move(r).unwrap();
+}
+
+void put(SafeTensorsFile& f, const std::string& name, const char* dtype, std::vector<size_t> shape,
+         const std::vector<uint8_t>& raw) {
+    auto r = f.add_raw(name, dtype, std::move(shape), raw.data(), raw.size());
+    if (r.is_err()) throw r.unwrap_err();
+}
+
+void put_int4(SafeTensorsFile& f, const std::string& name, const Int4Weight& w, hipStream_t stream) {
+    put(f, name + ".weight", "U8", {w.rows, w.cols / 2}, bytes_of(w.packed, stream));
+    put(f, name + ".weight_scale", "F16", {w.rows, w.cols / 128}, bytes_of(w.scales, stream));
+}
+
+Int4Weight get_int4(const SafeTensorsFile& f, const std::string& name, size_t rows, size_t cols,
+                    hipStream_t stream) {
+    if (cols % 128 != 0) throw TheanoError::runtime("checkpoint: '" + name + "' K is not a multiple of 128");
+    Int4Weight w;
+    w.rows = rows;
+    w.cols = cols;
+    w.packed = device_of<uint8_t>(get<uint8_t>(f, name + ".weight", "U8", {rows, cols / 2}), stream);
+    w.scales = device_of<uint16_t>(get<uint16_t>(f, name + ".weight_scale", "F16", {rows, cols / 128}), stream);
+    quantize::make_tiled(w, stream);
+    check_hip(hipStreamSynchronize(stream), "checkpoint");
+    return w;
+}
+
+}  // namespace
+
+Result<void> QuantizedLinear::save(SafeTensorsFile& f, const std::string& name) const {
+    return capture<void>([&]() -> Result<void> {
+        f.metadata["format"] = serialize::kFormat;
+        f.metadata[name + ".in_features"] = std::to_string(in_);
+        f.metadata[name + ".out_features"] = std::to_string(out_);
+        if (mode_ == Mode::W4) {
+            f.metadata[name + ".quant"] = "int4_g128";
+            f.metadata[name + ".group_size"] = "128";
+            put_int4(f, name, w4_, stream_);
+        } else {
+            f.metadata[name + ".quant"] = mode_ == Mode::W8 ? "int8_per_channel" : "int8_per_channel_a8";
+            put(f, name + ".weight", "I8", {out_, in_}, bytes_of(w8_.codes, stream_));
+            put(f, name + ".weight_scale", "F32", {out_}, bytes_of(w8_.scales, stream_));
+        }
+        if (bias_) put(f, name + ".bias", "F32", {out_}, bytes_of(*bias_, stream_));
+        return {};
+    });
+}
+
+Result<QuantizedLinear> QuantizedLinear::load(const SafeTensorsFile& f, const std::string& name,
+                                              hipStream_t stream) {
+    return capture<QuantizedLinear>([&]() -> Result<QuantizedLinear> {
+        if (meta(f, "format") != serialize::kFormat)
+            return TheanoError::runtime("checkpoint: format is not " + std::string(serialize::kFormat));
+        QuantizedLinear l;
+        l.stream_ = stream;
+        l.in_ = meta_size(f, name + ".in_features");
+        l.out_ = meta_size(f, name + ".out_features");
+        const std::string q = meta(f, name + ".quant");
+        if (q == "int4_g128") {
+            if (meta(f, name + ".group_size") != "128")
+                return TheanoError::runtime("checkpoint: '" + name + "' group size is not 128");
+            l.mode_ = Mode::W4;
+            l.w4_ = get_int4(f, name, l.out_, l.in_, stream);
+        } else if (q == "int8_per_channel" || q == "int8_per_channel_a8") {
+            l.mode_ = q == "int8_per_channel" ? Mode::W8 : Mode::W8A8;
+            l.w8_.rows = l.out_;
+            l.w8_.cols = l.in_;
+            l.w8_.codes = device_of<int8_t>(get<int8_t>(f, name + ".weight", "I8", {l.out_, l.in_}), stream);
+            l.w8_.scales = device_of<float>(get<float>(f, name + ".weight_scale", "F32", {l.out_}), stream);
+        } else {
+            return TheanoError::runtime("checkpoint: '" + name + "' has unknown scheme " + q);
+        }
+        if (f.tensors.count(name + ".bias"))
+            l.bias_.emplace(device_of<float>(get<float>(f, name + ".bias", "F32", {l.out_}), stream));
+        return std::move(l);
+    });
+}
+
+Result<void> QuantizedMLP::save(SafeTensorsFile& f, const std::string& name) const {
+    return capture<void>([&]() -> Result<void> {
+        f.metadata["format"] = serialize::kFormat;
+        f.metadata[name + ".quant"] = "mlp_int4_g128";
+        f.metadata[name + ".group_size"] = "128";
+        f.metadata[name + ".hidden"] = std::to_string(d_);
+        f.metadata[name + ".intermediate"] = std::to_string(f_);
+        put_int4(f, name + ".gate", gate_, stream_);
+        put_int4(f, name + ".up", up_, stream_);
+        put_int4(f, name + ".down", down_, stream_);
+        return {};
+    });
+}
+
+Result<QuantizedMLP> QuantizedMLP::load(const SafeTensorsFile& f, const std::string& name, hipStream_t stream) {
+    return capture<QuantizedMLP>([&]() -> Result<QuantizedMLP> {
+        if (meta(f, "format") != serialize::kFormat)
+            return TheanoError::runtime("checkpoint: format is not " + std::string(serialize::kFormat));
+        if (meta(f, name + ".quant") != "mlp_int4_g128")
+            return TheanoError::runtime("checkpoint: '" + name + "' is not an INT4 MLP");
+        QuantizedMLP m;
+        m.stream_ = stream;
+        m.d_ = meta_size(f, name + ".hidden");
+        m.f_ = meta_size(f, name + ".intermediate");
+        m.gate_ = get_int4(f, name + ".gate", m.f_, m.d_, stream);
+        m.up_ = get_int4(f, name + ".up", m.f_, m.d_, stream);
+        m.down_ = get_int4(f, name + ".down", m.d_, m.f_, stream);
+        return std::move(m);
+    });
 }
 
 }  // namespace nn

@@ -284,6 +284,10 @@ Result<Tensor> dequantize(const Int4Weight& w, hipStream_t stream = nullptr);
 
 }  // namespace quantize
 
+namespace serialize {
+class SafeTensorsFile;  // theano_serialize.hpp
+}
+
 namespace nn {
 
 // Module (crates/theano-nn/src/module.rs:8-55) over host tensors: the quantized
@@ -323,6 +327,11 @@ class QuantizedLinear : public Module {
                                 void* workspace = nullptr, size_t workspace_bytes = 0) const;
     // device scratch of the w4 prefill path for m tokens (0 for other modes / m <= 16)
     size_t workspace_bytes(int64_t m) const;
+    // Quantized checkpoint entries under `name` (layout in theano_serialize.hpp):
+    // codes and scales as stored on the device, loaded back without re-quantizing.
+    Result<void> save(serialize::SafeTensorsFile& file, const std::string& name) const;
+    static Result<QuantizedLinear> load(const serialize::SafeTensorsFile& file, const std::string& name,
+                                        hipStream_t stream = nullptr);
 
     std::vector<Tensor> parameters() const override;
     std::vector<std::pair<std::string, Tensor>> named_parameters() const override;
@@ -357,6 +366,10 @@ class QuantizedMLP : public Module {
                                 hipStream_t stream) const;
     std::vector<Tensor> parameters() const override;
     size_t num_parameters() const override { return 3 * d_ * f_; }
+    // Quantized checkpoint entries under `name` (layout in theano_serialize.hpp)
+    Result<void> save(serialize::SafeTensorsFile& file, const std::string& name) const;
+    static Result<QuantizedMLP> load(const serialize::SafeTensorsFile& file, const std::string& name,
+                                     hipStream_t stream = nullptr);
     size_t hidden() const { return d_; }
     size_t intermediate() const { return f_; }
 

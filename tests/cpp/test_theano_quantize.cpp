@@ -18,11 +18,17 @@
 
 #include "../../oracle/tq_oracle.h"
 #include "theano_quantize.hpp"
+#include "theano_serialize.hpp"
+
+#include <fstream>
+#include <map>
+#include <unistd.h>
 
 using namespace theano;
 using namespace theano::quantize;
 using theano::nn::QuantizedLinear;
 using theano::nn::QuantizedMLP;
+namespace ser = theano::serialize;
 
 namespace {
 
@@ -523,6 +529,181 @@ TEST_GPU(test_parity_weight_formats) {
 }
 
 }  // namespace
+
+
+// ------------------------------------------------- safetensors.rs:240-286
+
+TEST_CPU(test_safetensors_roundtrip) {
+    std::map<std::string, Tensor> tensors;
+    tensors.emplace("weight", Tensor::from_slice({1.0, 2.0, 3.0, 4.0}, {2, 2}));
+    tensors.emplace("bias", Tensor::from_slice({5.0, 6.0}, {2}));
+    const auto bytes = ser::save_safetensors(tensors);
+    const auto loaded = ser::load_safetensors(bytes).unwrap();
+    ASSERT_EQ(loaded.size(), 2u);
+    ASSERT(loaded.at("weight").shape() == (std::vector<size_t>{2, 2}));
+    ASSERT(loaded.at("weight").to_vec_f64().unwrap() == (std::vector<double>{1.0, 2.0, 3.0, 4.0}));
+    ASSERT(loaded.at("bias").to_vec_f64().unwrap() == (std::vector<double>{5.0, 6.0}));
+}
+
+TEST_CPU(test_safetensors_file_api) {
+    ser::SafeTensorsFile file;
+    file.add_tensor("x", Tensor::ones({3, 3}));
+    ASSERT_EQ(file.tensor_names().size(), 1u);
+    const Tensor t = file.get_tensor("x").unwrap();
+    ASSERT(t.shape() == (std::vector<size_t>{3, 3}));
+}
+
+TEST_CPU(test_safetensors_empty) {
+    const auto bytes = ser::save_safetensors({});
+    ASSERT_EQ(ser::load_safetensors(bytes).unwrap().size(), 0u);
+}
+
+// The reference's own bytes: f64 payloads under DType names, header keys sorted,
+// data in insertion order (safetensors.rs:36-54, 83-135).
+TEST_CPU(test_safetensors_reference_dialect) {
+    const std::vector<double> w = {1.0, 2.0, 3.0, 4.0}, b = {5.0, 6.0};
+    std::vector<uint8_t> data(48);
+    std::memcpy(data.data(), b.data(), 16);       // bias inserted first
+    std::memcpy(data.data() + 16, w.data(), 32);
+    const std::string h = "{\"bias\":{\"dtype\":\"float32\",\"shape\":[2],\"data_offsets\":[0,16]},"
+                          "\"weight\":{\"dtype\":\"float64\",\"shape\":[2,2],\"data_offsets\":[16,48]}}";
+    std::vector<uint8_t> bytes(8);
+    const uint64_t n = h.size();
+    std::memcpy(bytes.data(), &n, 8);
+    bytes.insert(bytes.end(), h.begin(), h.end());
+    bytes.insert(bytes.end(), data.begin(), data.end());
+    const auto loaded = ser::load_safetensors(bytes).unwrap();
+    ASSERT(loaded.at("weight").to_vec_f64().unwrap() == w);
+    ASSERT(loaded.at("bias").to_vec_f64().unwrap() == b);
+}
+
+TEST_CPU(test_safetensors_raw_payloads) {
+    ser::SafeTensorsFile f;
+    const int8_t i8[4] = {-128, -1, 0, 127};
+    const uint16_t f16[2] = {0x3800, 0xBC00};  // 0.5, -1.0
+    ASSERT(f.add_raw("a", "I8", {2, 2}, i8, 4).is_ok());
+    ASSERT(f.add_raw("b", "F16", {2}, f16, 4).is_ok());
+    ASSERT(f.add_raw("c", "F32", {3}, i8, 4).is_err());      // size mismatch
+    ASSERT(f.add_raw("d", "float32", {1}, i8, 4).is_err());  // not a standard code
+    f.metadata["a.quant"] = "int8_per_channel";
+    const auto bytes = f.to_bytes();
+    uint64_t hl;
+    std::memcpy(&hl, bytes.data(), 8);
+    ASSERT_EQ(hl % 8, 0u);
+    const auto g = ser::SafeTensorsFile::from_bytes(bytes).unwrap();
+    ASSERT(g.metadata.at("a.quant") == "int8_per_channel");
+    const auto raw = g.get_raw("a", "I8", {2, 2}).unwrap();
+    ASSERT(std::memcmp(raw.data(), i8, 4) == 0);
+    ASSERT(g.get_raw("a", "U8", {2, 2}).is_err());
+    ASSERT(g.get_tensor("a").unwrap().to_vec_f64().unwrap() == (std::vector<double>{-128, -1, 0, 127}));
+    ASSERT(g.get_tensor("b").unwrap().to_vec_f64().unwrap() == (std::vector<double>{0.5, -1.0}));
+}
+
+TEST_CPU(test_safetensors_malformed) {
+    ASSERT(ser::SafeTensorsFile::from_bytes({1, 0}).is_err());
+    std::vector<uint8_t> b(8);
+    const uint64_t big = 100;
+    std::memcpy(b.data(), &big, 8);
+    ASSERT(ser::SafeTensorsFile::from_bytes(b).is_err());  // truncated header
+    auto make = [](const std::string& h, size_t data) {
+        std::vector<uint8_t> v(8);
+        const uint64_t n = h.size();
+        std::memcpy(v.data(), &n, 8);
+        v.insert(v.end(), h.begin(), h.end());
+        v.resize(v.size() + data);
+        return v;
+    };
+    ASSERT(ser::SafeTensorsFile::from_bytes(make("[]", 0)).is_err());
+    ASSERT(ser::SafeTensorsFile::from_bytes(make("{\"t\":{\"dtype\":\"F32\",\"shape\":[2],\"data_offsets\":[0,12]}}", 8))
+               .is_err());  // offsets past the data
+    ASSERT(ser::SafeTensorsFile::from_bytes(make("{\"t\":{\"dtype\":\"F32\",\"shape\":[3],\"data_offsets\":[0,8]}}", 8))
+               .is_err());  // size != shape x element
+    ASSERT(ser::SafeTensorsFile::from_bytes(make("{\"t\":{\"dtype\":\"X9\",\"shape\":[1],\"data_offsets\":[0,4]}}", 4))
+               .is_err());  // unknown dtype
+    ASSERT(ser::SafeTensorsFile::from_bytes(make("{\"t\":{\"dtype\":\"F32\",\"shape\":[1]", 4)).is_err());
+}
+
+std::vector<uint8_t> golden_checkpoint() {
+    char exe[4096];
+    const ssize_t n = readlink("/proc/self/exe", exe, sizeof exe - 1);
+    ASSERT(n > 0);
+    std::string dir(exe, static_cast<size_t>(n));
+    dir = dir.substr(0, dir.rfind('/'));
+    std::ifstream in(dir + "/../golden/checkpoint_int4_16x256.safetensors", std::ios::binary);
+    ASSERT(in.good());
+    return std::vector<uint8_t>((std::istreambuf_iterator<char>(in)), std::istreambuf_iterator<char>());
+}
+
+// written by the independent `safetensors` package (tests/golden/make_golden.py)
+TEST_CPU(test_safetensors_independent_writer) {
+    const auto f = ser::SafeTensorsFile::from_bytes(golden_checkpoint()).unwrap();
+    ASSERT(f.get_tensor("const.f64").unwrap().to_vec_f64().unwrap() == (std::vector<double>{1.5, -2.0, 3.25}));
+    ASSERT(f.get_tensor("const.i8").unwrap().to_vec_f64().unwrap() == (std::vector<double>{-128, 0, 127}));
+    ASSERT(f.get_tensor("const.f16").unwrap().to_vec_f64().unwrap() == (std::vector<double>{0.5, -1.0, 65504.0}));
+    const Tensor u8 = f.get_tensor("const.u8").unwrap();
+    ASSERT(u8.shape() == (std::vector<size_t>{2, 2}));
+    ASSERT(u8.to_vec_f64().unwrap() == (std::vector<double>{0, 255, 7, 128}));
+    ASSERT(f.metadata.at("proj.quant") == "int4_g128");
+    ASSERT(f.get_raw("proj.weight", "U8", {16, 128}).is_ok());
+    ASSERT(f.get_raw("proj.weight_scale", "F16", {16, 2}).is_ok());
+}
+
+TEST_GPU(test_checkpoint_linear_and_mlp_roundtrip) {
+    const size_t n = 256, k = 512;
+    const auto wv = randn(n * k, 0.02, 91), bv = randn(n, 0.1, 92);
+    const QConfig a8{QuantDType::Int8, QuantDType::Int8, true, true};
+    const std::vector<std::pair<std::string, QConfig>> cfgs = {
+        {"l4", QConfig::default_int4()}, {"l8", QConfig::default_int8()}, {"l8a8", a8}};
+    ser::SafeTensorsFile file;
+    std::vector<QuantizedLinear> layers;
+    for (const auto& [name, cfg] : cfgs) {
+        layers.push_back(QuantizedLinear::from_tensors(Tensor::from_slice(wv, {n, k}),
+                                                       name == "l8a8" ? std::optional<Tensor>{}
+                                                                      : std::optional<Tensor>{Tensor::from_slice(bv, {n})},
+                                                       cfg)
+                             .unwrap());
+        ASSERT(layers.back().save(file, name).is_ok());
+    }
+    const QuantizedMLP mlp = QuantizedMLP::from_tensors(Tensor::from_slice(randn(512 * 256, 0.02, 93), {512, 256}),
+                                                        Tensor::from_slice(randn(512 * 256, 0.02, 94), {512, 256}),
+                                                        Tensor::from_slice(randn(256 * 512, 0.02, 95), {256, 512}))
+                                 .unwrap();
+    ASSERT(mlp.save(file, "mlp").is_ok());
+    const auto back = ser::SafeTensorsFile::from_bytes(file.to_bytes()).unwrap();
+    for (size_t i = 0; i < cfgs.size(); ++i) {
+        const QuantizedLinear l = QuantizedLinear::load(back, cfgs[i].first).unwrap();
+        ASSERT(l.mode() == layers[i].mode() && l.in_features() == k && l.out_features() == n);
+        for (size_t m : {1u, 5u, 40u}) {
+            const Tensor x = Tensor::from_slice(randn(m * k, 1.0, 96 + m), {m, k});
+            ASSERT(same_bits(l.forward(x).to_vec_f64().unwrap(), layers[i].forward(x).to_vec_f64().unwrap()));
+        }
+    }
+    const QuantizedMLP m2 = QuantizedMLP::load(back, "mlp").unwrap();
+    const Tensor x = Tensor::from_slice(randn(7 * 256, 1.0, 97), {7, 256});
+    ASSERT(same_bits(m2.forward(x).to_vec_f64().unwrap(), mlp.forward(x).to_vec_f64().unwrap()));
+    ASSERT(QuantizedLinear::load(back, "missing").is_err());
+}
+
+// the independent writer's checkpoint through QuantizedLinear::load vs the oracle
+TEST_GPU(test_checkpoint_independent_writer_forward) {
+    const auto f = ser::SafeTensorsFile::from_bytes(golden_checkpoint()).unwrap();
+    const QuantizedLinear l = QuantizedLinear::load(f, "proj").unwrap();
+    const size_t n = 16, k = 256, m = 3;
+    const auto p = f.get_raw("proj.weight", "U8", {n, k / 2}).unwrap();
+    const auto sraw = f.get_raw("proj.weight_scale", "F16", {n, k / 128}).unwrap();
+    const auto braw = f.get_raw("proj.bias", "F32", {n}).unwrap();
+    std::vector<uint16_t> s(n * k / 128);
+    std::memcpy(s.data(), sraw.data(), sraw.size());
+    std::vector<float> b(n);
+    std::memcpy(b.data(), braw.data(), braw.size());
+    const auto xv = randn(m * k, 1.0, 98);
+    const auto y = l.forward(Tensor::from_slice(xv, {m, k})).to_vec_f64().unwrap();
+    std::vector<uint16_t> xb(m * k);
+    for (size_t i = 0; i < xb.size(); ++i) xb[i] = tqo_f32_to_bf16_bits(static_cast<float>(xv[i]));
+    std::vector<double> ref(m * n);
+    tqo_linear_w4g128_bf16(xb.data(), m, p.data(), s.data(), b.data(), n, k, ref.data());
+    assert_close(y, ref, "checkpoint linear");
+}
 
 int main(int argc, char** argv) {
     const bool cpu_only = argc > 1 && std::strcmp(argv[1], "--cpu") == 0;

@@ -14,6 +14,9 @@ Two kinds of data:
   pin the generator).  The oracle is itself pinned by tests/test_oracle.py;
   these files freeze its outputs so that the GPU kernels and any later change
   of the oracle are checked against the same bytes.
+* checkpoint_int4_16x256.safetensors -- the INT4 case as a quantized Linear
+  checkpoint, written by the independent `safetensors` package, for the
+  checkpoint readers (Python and C++).
 
 Run from the repository root:  python tests/golden/make_golden.py
 """
@@ -146,6 +149,23 @@ def main():
     np.savez(os.path.join(HERE, "w8a8_4x256x8.npz"), x=xa, w=ww, qa=qa, sa=sa, qw=qw, sw=sw, acc=acc, y=y)
 
     np.savez(os.path.join(HERE, "synth_prefixes.npz"), **synth_prefixes())
+
+    # a quantized checkpoint written by the independent `safetensors` package:
+    # the INT4 case above as a Linear "proj" (+ bias) and a few constants whose
+    # values the C++ and Python readers assert
+    from safetensors.numpy import save as st_save
+
+    tensors = {
+        "proj.weight": p4, "proj.weight_scale": s4.view(np.float16),
+        "proj.bias": synth.normal_f32(103, (16,), 0.1),
+        "const.f64": np.array([1.5, -2.0, 3.25]), "const.i8": np.array([-128, 0, 127], dtype=np.int8),
+        "const.f16": np.array([0.5, -1.0, 65504.0], dtype=np.float16),
+        "const.u8": np.array([[0, 255], [7, 128]], dtype=np.uint8),
+    }
+    meta = {"format": "theano-quantize/1", "proj.quant": "int4_g128", "proj.group_size": "128",
+            "proj.in_features": "256", "proj.out_features": "16"}
+    with open(os.path.join(HERE, "checkpoint_int4_16x256.safetensors"), "wb") as f:
+        f.write(st_save(tensors, metadata=meta))
     print("wrote fixtures to", HERE)
 
 

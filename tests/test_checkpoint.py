@@ -128,3 +128,15 @@ def _one(entry, data):
 def test_malformed_entries_are_rejected(entry, data):
     with pytest.raises(InvalidArgument):
         load_safetensors(_one(entry, data))
+
+
+def test_golden_checkpoint_fixture():
+    """tests/golden/checkpoint_int4_16x256.safetensors (written by the
+    `safetensors` package) decodes to the INT4 fixture's codes and scales."""
+    here = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+    got, meta = load_safetensors(open(os.path.join(here, "checkpoint_int4_16x256.safetensors"), "rb").read())
+    ref = np.load(os.path.join(here, "int4_g128_16x256.npz"))
+    assert np.array_equal(got["proj.weight"], ref["packed"])
+    assert np.array_equal(got["proj.weight_scale"].view(np.uint16), ref["s_f16"])
+    assert meta["proj.quant"] == "int4_g128" and meta["proj.group_size"] == "128"
+    assert got["const.f16"].tolist() == [0.5, -1.0, 65504.0]

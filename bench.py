@@ -9,7 +9,8 @@ streams them from HBM.  The timed region is a HIP graph of `--steps`
 launches bracketed by events on the launch stream.
 
 Secondary workloads (reported in `secondary`): INT8 GEMV (config 2), INT4
-GEMV at M=2..16, W8A8 GEMM at M=2048 (config 4), per-row INT8 quantize /
+GEMV at M=2..16, W8A8 GEMM at M=2048 (config 4) in INT8 and in FP8 e4m3,
+per-row INT8 quantize /
 dequantize round trip (config 1) and the INT4 FFN block (config 5).
 
 `cpu_baseline` times the C restatement of the reference CPU path
@@ -30,6 +31,7 @@ sys.path.insert(0, os.path.join(ROOT, "neo-theano_amd"))
 
 HBM_PEAK_GBS = 8000.0        # MI355X HBM3E
 I8_PEAK_TOPS = 5000.0        # dense int8 MFMA, 5.0 POP/s
+FP8_PEAK_TFLOPS = 5000.0     # dense fp8 MFMA, 5.0 PFLOP/s
 BF16_PEAK_TFLOPS = 2500.0    # dense bf16 MFMA
 MALL_BYTES = 256 << 20
 METRIC = "INT4/INT8 dequant-GEMV GB/s (% HBM peak) + W8A8 GEMM TOPS (% MFMA peak)"
@@ -41,7 +43,7 @@ def parse_args():
     p.add_argument("--steps", type=int, default=200)
     p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--only", default=None,
-                   help="run one workload: gemv_w4, gemv_w8, gemv_w4_m, w8a8, roundtrip, mlp, copy")
+                   help="run one workload: gemv_w4, gemv_w8, gemv_w4_m, w8a8, fp8, roundtrip, mlp, copy")
     p.add_argument("--no-secondary", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=12.0, help="bound of the CPU baseline sample (0: skip)")
     p.add_argument("--eager", action="store_true", help="time eager launches instead of a HIP graph")
@@ -221,6 +223,32 @@ def main():
             "us": round(ms * 1e3, 3), "TOPS": round(tops, 1), "i8_mfma_frac": round(tops / I8_PEAK_TOPS, 4),
             "act_quant_us": round(msq * 1e3, 3), "act_quant_GB/s": round(qbytes / (msq * 1e-3) / 1e9, 1)}
         log(f"w8a8 M=2048: {ms * 1e3:.2f} us  {tops:.0f} TOPS; act quant {msq * 1e3:.2f} us")
+        del qa, qw, y, xd
+
+    # ------------------------------------------------ FP8 W8A8 (C4 shape)
+    if not args.no_secondary and want("fp8"):
+        m4, n4, k4 = 2048, 4096, 4096
+        xd = dt(normal_f32(3, (m4, k4), 1.0))
+        qa, sa = tq.quantize_per_channel_fp8(xd)
+        qw, sw = tq.quantize_per_channel_fp8(dt(normal_f32(3, (n4, k4), 0.02, stream=1)))
+        y = torch.empty((m4, n4), dtype=torch.float32, device=dev)
+
+        def launch(i):
+            _abi.call("tq_gemm_fp8", ptr(qa), ptr(sa), ptr(qw), ptr(sw), None, m4, n4, k4, ptr(y), stream())
+
+        steps = max(10, args.steps // 4)
+        ms, mode = timer.run(launch, steps, max(2, args.warmup // 4))
+        tf = 2.0 * m4 * n4 * k4 / (ms * 1e-3) / 1e12
+        qbytes = 4 * m4 * k4 + m4 * k4 + 4 * m4
+
+        def launch_q(i):
+            _abi.call("tq_quantize_fp8_rowwise", ptr(xd), m4, k4, ptr(qa), ptr(sa), stream())
+
+        msq, _ = timer.run(launch_q, steps, 2)
+        secondary["fp8_gemm_m2048"] = {
+            "us": round(ms * 1e3, 3), "TFLOP/s": round(tf, 1), "fp8_mfma_frac": round(tf / FP8_PEAK_TFLOPS, 4),
+            "act_quant_us": round(msq * 1e3, 3), "act_quant_GB/s": round(qbytes / (msq * 1e-3) / 1e9, 1)}
+        log(f"fp8 M=2048: {ms * 1e3:.2f} us  {tf:.0f} TFLOP/s; act quant {msq * 1e3:.2f} us")
         del qa, qw, y, xd
 
     # ------------------------------------------------ round trip (C1)

@@ -152,6 +152,21 @@ int tq_dequantize_i8_rowwise(const int8_t* q, const float* s, int64_t rows, int6
 int tq_fake_quantize_i8_rowwise(const float* w, int64_t rows, int64_t k, int8_t* q,
                                 float* s, float* w_hat, tq_stream_t stream);
 
+/* Symmetric per-row FP8, OCP E4M3 (bias 7, largest finite 448, S.1111.111 =
+ * NaN): the 8-bit float behind QuantDType::FP8, whose range the reference
+ * states as [-448, 448] (qconfig.rs:29,38) without an encoding.
+ *   s[r]   = f32(max(absmax_r / 448, 1e-10))   (absmax as for INT8 above)
+ *   q[r,k] = e4m3_rne(clamp(f32(w[r,k] / s[r]), -448, 448)),  NaN -> 0x7F
+ * W [rows, K] f32 -> q u8 [rows, K] (e4m3 bit patterns), s f32 [rows]. */
+int tq_quantize_fp8_rowwise(const float* w, int64_t rows, int64_t k, uint8_t* q, float* s,
+                            tq_stream_t stream);
+/* w_hat = f32(e4m3(q) * s[r]) (one rounding of an exact product). */
+int tq_dequantize_fp8_rowwise(const uint8_t* q, const float* s, int64_t rows, int64_t k,
+                              float* w_hat, tq_stream_t stream);
+/* Both in one pass (fake_quantize per row with the FP8 grid). */
+int tq_fake_quantize_fp8_rowwise(const float* w, int64_t rows, int64_t k, uint8_t* q,
+                                 float* s, float* w_hat, tq_stream_t stream);
+
 /* Symmetric INT4 with groups of 128 along K (K % 128 == 0):
  *   s[r,g] = max(f16_rne(absmax_{r,g} / 7), 2^-24)   (f16 bits)
  *   q      = quantize_tensor(group, f64(s), 0, Int4)  in [-8, 7]
@@ -212,6 +227,15 @@ int tq_gemv_w4g128_tiled(const uint16_t* x_bf16, int64_t m, const uint8_t* packe
 int tq_gemm_w8a8(const int8_t* qa, const float* sa, const int8_t* qw, const float* sw,
                  const float* bias, int64_t m, int64_t n, int64_t k, int32_t* acc,
                  float* y, tq_stream_t stream);
+
+/* Prefill-shaped FP8 W8A8 (both operands per-row E4M3, tq_quantize_fp8_rowwise):
+ * y[i,j] = f32(sum_p e4m3(qa[i,p]) * e4m3(qw[j,p])) * sa[i] * sw[j] (+ bias[j]);
+ * products exact, f32 accumulation.  The reference value is Linear over the
+ * dequantized operands (linear.rs:111-121, tensor_ops.rs:379-410).  Any M, N,
+ * K.  The FP8 MFMA kernel serves K % 128 == 0 and N % 16 == 0 with 16-byte
+ * aligned qa, qw, sw, bias and y; other cases take a shape-general kernel. */
+int tq_gemm_fp8(const uint8_t* qa, const float* sa, const uint8_t* qw, const float* sw,
+                const float* bias, int64_t m, int64_t n, int64_t k, float* y, tq_stream_t stream);
 
 /* Prefill-shaped W4A16: x bf16 [M, K], INT4 g128 weights, f32 accumulation with
  * the group scale applied to each 128-long partial sum; y f32 [M, N].

@@ -46,7 +46,6 @@ namespace tq {
 namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef __attribute__((address_space(3))) int8_t lds_i8;
 
 constexpr float kOffset = 192.0f;  // 8 * 24: weight operand 8 * (24 + q)

@@ -94,6 +94,27 @@ __global__ __launch_bounds__(kGenBlock) void k_gemm_w8a8_generic(const int8_t* _
     }
 }
 
+// FP8 (e4m3) codes: products exact in f32, f32 sum over K, then the scales.
+__global__ __launch_bounds__(kGenBlock) void k_gemm_fp8_generic(const uint8_t* __restrict__ qa,
+                                                                const float* __restrict__ sa,
+                                                                const uint8_t* __restrict__ qw,
+                                                                const float* __restrict__ sw,
+                                                                const float* __restrict__ bias, int64_t m,
+                                                                int64_t n, int64_t k, float* __restrict__ y) {
+    const int64_t out = static_cast<int64_t>(blockIdx.x) * kGenWaves + threadIdx.x / kWave;
+    if (out >= m * n) return;  // wave-uniform
+    const int lane = threadIdx.x & (kWave - 1);
+    const int64_t i = out / n, j = out % n;
+    const uint8_t* ar = qa + i * k;
+    const uint8_t* wr = qw + j * k;
+    float acc = 0.f;
+    for (int64_t p = lane; p < k; p += kWave)
+        acc += __builtin_amdgcn_cvt_f32_fp8(static_cast<int>(ar[p]), 0) *
+               __builtin_amdgcn_cvt_f32_fp8(static_cast<int>(wr[p]), 0);
+    acc = wave_sum(acc);
+    if (lane == 0) y[out] = acc * sa[i] * sw[j] + (bias ? bias[j] : 0.f);
+}
+
 unsigned generic_grid(int64_t outputs) { return static_cast<unsigned>((outputs + kGenWaves - 1) / kGenWaves); }
 
 }  // namespace
@@ -121,6 +142,14 @@ int launch_gemm_w8a8_generic(const int8_t* qa, const float* sa, const int8_t* qw
     TQ_REQUIRE(m * n / kGenWaves < (int64_t(1) << 31), "gemm_w8a8 (generic): too many outputs");
     k_gemm_w8a8_generic<<<generic_grid(m * n), kGenBlock, 0, st>>>(qa, sa, qw, sw, bias, m, n, k, acc, y);
     return check_launch("gemm_w8a8 (generic)");
+}
+
+int launch_gemm_fp8_generic(const uint8_t* qa, const float* sa, const uint8_t* qw, const float* sw,
+                            const float* bias, int64_t m, int64_t n, int64_t k, float* y, hipStream_t st) {
+    if (m == 0 || n == 0) return TQ_OK;
+    TQ_REQUIRE(m * n / kGenWaves < (int64_t(1) << 31), "gemm_fp8 (generic): too many outputs");
+    k_gemm_fp8_generic<<<generic_grid(m * n), kGenBlock, 0, st>>>(qa, sa, qw, sw, bias, m, n, k, y);
+    return check_launch("gemm_fp8 (generic)");
 }
 
 }  // namespace tq

@@ -17,7 +17,9 @@ namespace tq {
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+typedef int32_t i32x8 __attribute__((ext_vector_type(8)));
 typedef int32_t i32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 // ---------------------------------------------------------------- host side
 
@@ -46,6 +48,8 @@ int launch_linear_w4_generic(const uint16_t* x, int64_t m, const uint8_t* packed
 int launch_gemm_w8a8_generic(const int8_t* qa, const float* sa, const int8_t* qw, const float* sw,
                              const float* bias, int64_t m, int64_t n, int64_t k, int32_t* acc, float* y,
                              hipStream_t st);
+int launch_gemm_fp8_generic(const uint8_t* qa, const float* sa, const uint8_t* qw, const float* sw,
+                            const float* bias, int64_t m, int64_t n, int64_t k, float* y, hipStream_t st);
 
 // FFN block for shapes the pipelined kernels of tq_ffn.hip do not take (D or F
 // not a multiple of 256, 2-byte aligned scales): 16x16x32 MFMA kernels of

@@ -37,11 +37,6 @@ __device__ __forceinline__ float block_max(float v, float* red) {
 // max(|min|, |max|) with min=+inf, max=-inf turns into +inf.
 __device__ __forceinline__ float absmax_finish(float m) { return (m == -INFINITY) ? INFINITY : m; }
 
-// s = f32(max(absmax / 127, 1e-10)), division in f64 (correctly rounded).
-__device__ __forceinline__ float scale_i8(float absmax) {
-    return static_cast<float>(fmax(static_cast<double>(absmax) / 127.0, 1e-10));
-}
-
 // INT8 code of x for scale s (finite, > 0).
 __device__ __forceinline__ int code_i8(float x, float s, float inv_s, float half_s) {
     const float n = rhaz_div(fabsf(x), s, inv_s, half_s, 256.0f);
@@ -68,14 +63,85 @@ __device__ __forceinline__ uint32_t pack4_i8(int a, int b, int c, int d) {
            __builtin_amdgcn_perm(static_cast<uint32_t>(d), static_cast<uint32_t>(c), 0x04000c0cu);
 }
 
-// ---- per-row INT8, register-cached row (K % 4 == 0, K <= 1024 * kItems) ----
+// ---- per-row symmetric formats ----
+// Each format gives its qmax (s = f32(max(absmax / qmax, 1e-10))), a per-row
+// coder built from s, and the value of a code: value(code) * s is the
+// dequantized element.
+
+// INT8: code = clamp(rhaz(x / s), -128, 127), NaN -> 0; an infinite scale (a row
+// holding an infinity) gives all-zero codes (|x| / inf = 0, inf / inf = NaN -> 0).
+struct FmtI8 {
+    typedef int8_t code_t;
+    static constexpr double kQmax = 127.0;
+    struct Row {
+        float s, inv, half;
+        bool finite;
+        __device__ explicit Row(float sc) : s(sc), inv(1.0f / sc), half(0.5f * sc), finite(sc < INFINITY) {}
+        __device__ uint32_t code4(f32x4 v) const {
+            if (!finite) return 0u;
+            return pack4_i8(code_i8_row(v.x, s, inv, half), code_i8_row(v.y, s, inv, half),
+                            code_i8_row(v.z, s, inv, half), code_i8_row(v.w, s, inv, half));
+        }
+        __device__ code_t code1(float x) const { return static_cast<code_t>(finite ? code_i8(x, s, inv, half) : 0); }
+    };
+    __device__ static f32x4 value4(uint32_t c, float sc) {
+        f32x4 o;
+        o.x = static_cast<float>(static_cast<int8_t>(c & 0xFF)) * sc;
+        o.y = static_cast<float>(static_cast<int8_t>((c >> 8) & 0xFF)) * sc;
+        o.z = static_cast<float>(static_cast<int8_t>((c >> 16) & 0xFF)) * sc;
+        o.w = static_cast<float>(static_cast<int8_t>((c >> 24) & 0xFF)) * sc;
+        return o;
+    }
+    __device__ static float value1(code_t c, float sc) { return static_cast<float>(c) * sc; }
+};
+
+// FP8 (OCP e4m3: bias 7, largest finite 448, S.1111.111 = NaN):
+// code = e4m3_rne(clamp(f32(x / s), -448, 448)), NaN -> 0x7F.  x / s is IEEE
+// division (correctly rounded); v_cvt_pk_fp8_f32 rounds to nearest even and,
+// after the clamp, never overflows.
+__device__ __forceinline__ float sat448(float t) { return fminf(fmaxf(t, -448.0f), 448.0f); }
+
+__device__ __forceinline__ uint32_t pack4_e4m3(float t0, float t1, float t2, float t3) {
+    uint32_t w = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(sat448(t0), sat448(t1), 0, false));
+    w = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(sat448(t2), sat448(t3), static_cast<int>(w), true));
+    const uint32_t nan = (t0 != t0 ? 0x000000FFu : 0u) | (t1 != t1 ? 0x0000FF00u : 0u) |
+                         (t2 != t2 ? 0x00FF0000u : 0u) | (t3 != t3 ? 0xFF000000u : 0u);
+    return (w & ~nan) | (0x7F7F7F7Fu & nan);
+}
+
+struct FmtFp8 {
+    typedef uint8_t code_t;
+    static constexpr double kQmax = 448.0;
+    struct Row {
+        float s;
+        __device__ explicit Row(float sc) : s(sc) {}
+        __device__ uint32_t code4(f32x4 v) const { return pack4_e4m3(v.x / s, v.y / s, v.z / s, v.w / s); }
+        __device__ code_t code1(float x) const { return static_cast<code_t>(pack4_e4m3(x / s, 0.f, 0.f, 0.f) & 0xFF); }
+    };
+    __device__ static f32x4 value4(uint32_t c, float sc) {
+        const int ci = static_cast<int>(c);
+        f32x4 o;
+        o.x = __builtin_amdgcn_cvt_f32_fp8(ci, 0) * sc;
+        o.y = __builtin_amdgcn_cvt_f32_fp8(ci, 1) * sc;
+        o.z = __builtin_amdgcn_cvt_f32_fp8(ci, 2) * sc;
+        o.w = __builtin_amdgcn_cvt_f32_fp8(ci, 3) * sc;
+        return o;
+    }
+    __device__ static float value1(code_t c, float sc) { return __builtin_amdgcn_cvt_f32_fp8(static_cast<int>(c), 0) * sc; }
+};
+
+// s = f32(max(absmax / qmax, 1e-10)), division in f64 (correctly rounded).
+template <class Fmt>
+__device__ __forceinline__ float row_scale(float absmax) {
+    return static_cast<float>(fmax(static_cast<double>(absmax) / Fmt::kQmax, 1e-10));
+}
+
+// ---- per-row quantize, register-cached row (K % 4 == 0, K <= 1024 * kItems) ----
 // One 256-thread block per row; each thread holds kItems f32x4 of the row.
-template <int kItems>
-__global__ __launch_bounds__(kBlock) void k_quant_i8_rows_vec(const float* __restrict__ w,
-                                                              int64_t k,
-                                                              int8_t* __restrict__ q,
-                                                              float* __restrict__ s,
-                                                              float* __restrict__ w_hat) {
+template <class Fmt, int kItems>
+__global__ __launch_bounds__(kBlock) void k_quant_rows_vec(const float* __restrict__ w, int64_t k,
+                                                           typename Fmt::code_t* __restrict__ q,
+                                                           float* __restrict__ s, float* __restrict__ w_hat) {
     __shared__ float red[kWavesPerBlock];
     const int64_t row = blockIdx.x;
     const int k4 = static_cast<int>(k >> 2);
@@ -90,96 +156,75 @@ __global__ __launch_bounds__(kBlock) void k_quant_i8_rows_vec(const float* __res
             m = fmaxf(m, fmaxf(fmaxf(fabsf(v[i].x), fabsf(v[i].y)), fmaxf(fabsf(v[i].z), fabsf(v[i].w))));
         }
     }
-    const float sc = scale_i8(absmax_finish(block_max(m, red)));
+    const float sc = row_scale<Fmt>(absmax_finish(block_max(m, red)));
     if (threadIdx.x == 0) s[row] = sc;
-    const bool finite = sc < INFINITY;  // row-uniform: an infinite scale gives all-zero codes
-    const float inv = 1.0f / sc, half = 0.5f * sc;
+    const typename Fmt::Row coder(sc);
     uint32_t* qd = reinterpret_cast<uint32_t*>(q + row * k);
     f32x4* wd = reinterpret_cast<f32x4*>(w_hat + row * k);
 #pragma unroll
     for (int i = 0; i < kItems; ++i) {
         const int idx = threadIdx.x + i * kBlock;
         if (idx < k4) {
-            int c0 = 0, c1 = 0, c2 = 0, c3 = 0;
-            if (finite) {
-                c0 = code_i8_row(v[i].x, sc, inv, half);
-                c1 = code_i8_row(v[i].y, sc, inv, half);
-                c2 = code_i8_row(v[i].z, sc, inv, half);
-                c3 = code_i8_row(v[i].w, sc, inv, half);
-            }
-            if (q) __builtin_nontemporal_store(pack4_i8(c0, c1, c2, c3), qd + idx);
-            if (w_hat) {
-                f32x4 o;
-                o.x = static_cast<float>(c0) * sc;
-                o.y = static_cast<float>(c1) * sc;
-                o.z = static_cast<float>(c2) * sc;
-                o.w = static_cast<float>(c3) * sc;
-                __builtin_nontemporal_store(o, wd + idx);
-            }
+            const uint32_t c = coder.code4(v[i]);
+            if (q) __builtin_nontemporal_store(c, qd + idx);
+            if (w_hat) __builtin_nontemporal_store(Fmt::value4(c, sc), wd + idx);
         }
     }
 }
 
-// ---- per-row INT8, any K / alignment: two passes over the row ----
-__global__ __launch_bounds__(kBlock) void k_quant_i8_rows_generic(const float* __restrict__ w,
-                                                                  int64_t k,
-                                                                  int8_t* __restrict__ q,
-                                                                  float* __restrict__ s,
-                                                                  float* __restrict__ w_hat) {
+// ---- per-row quantize, any K / alignment: two passes over the row ----
+template <class Fmt>
+__global__ __launch_bounds__(kBlock) void k_quant_rows_generic(const float* __restrict__ w, int64_t k,
+                                                               typename Fmt::code_t* __restrict__ q,
+                                                               float* __restrict__ s, float* __restrict__ w_hat) {
     __shared__ float red[kWavesPerBlock];
     const int64_t row = blockIdx.x;
     const float* src = w + row * k;
     float m = -INFINITY;
     for (int64_t i = threadIdx.x; i < k; i += kBlock) m = fmaxf(m, fabsf(src[i]));
-    const float sc = scale_i8(absmax_finish(block_max(m, red)));
+    const float sc = row_scale<Fmt>(absmax_finish(block_max(m, red)));
     if (threadIdx.x == 0) s[row] = sc;
-    const bool finite = sc < INFINITY;
-    const float inv = 1.0f / sc, half = 0.5f * sc;
+    const typename Fmt::Row coder(sc);
     for (int64_t i = threadIdx.x; i < k; i += kBlock) {
-        const int c = finite ? code_i8(src[i], sc, inv, half) : 0;
-        if (q) q[row * k + i] = static_cast<int8_t>(c);
-        if (w_hat) w_hat[row * k + i] = static_cast<float>(c) * sc;
+        const typename Fmt::code_t c = coder.code1(src[i]);
+        if (q) q[row * k + i] = c;
+        if (w_hat) w_hat[row * k + i] = Fmt::value1(c, sc);
     }
 }
 
-// ---- per-row INT8 dequant: w_hat = f32(q * s[row]) ----
+// ---- per-row dequant: w_hat = f32(value(q) * s[row]) ----
 // Vector form: 16 codes per thread (K % 16 == 0, aligned).
 // Thread t of a block handles 4-element units t + 256 j (j < kDqUnits): every
 // wave-wide load reads 256 contiguous code bytes, every store writes 1 KB.
 constexpr int kDqUnits = 4;
-__global__ __launch_bounds__(kBlock) void k_dequant_i8_rows_vec(const int8_t* __restrict__ q,
-                                                                const float* __restrict__ s,
-                                                                int64_t k, int64_t n4,
-                                                                float* __restrict__ w_hat) {
+template <class Fmt>
+__global__ __launch_bounds__(kBlock) void k_dequant_rows_vec(const typename Fmt::code_t* __restrict__ q,
+                                                             const float* __restrict__ s, int64_t k, int64_t n4,
+                                                             float* __restrict__ w_hat) {
     const int64_t u0 = static_cast<int64_t>(blockIdx.x) * (kBlock * kDqUnits) + threadIdx.x;
-    int32_t c[kDqUnits];
+    uint32_t c[kDqUnits];
     float sc[kDqUnits];
 #pragma unroll
     for (int j = 0; j < kDqUnits; ++j) {
         const int64_t u = min<int64_t>(u0 + j * kBlock, n4 - 1);
-        c[j] = __builtin_nontemporal_load(reinterpret_cast<const int32_t*>(q) + u);
+        c[j] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(q) + u);
         sc[j] = s[(u * 4) / k];
     }
 #pragma unroll
     for (int j = 0; j < kDqUnits; ++j) {
         const int64_t u = u0 + j * kBlock;
         if (u >= n4) break;
-        f32x4 o;
-        o.x = static_cast<float>(static_cast<int8_t>(c[j] & 0xFF)) * sc[j];
-        o.y = static_cast<float>(static_cast<int8_t>((c[j] >> 8) & 0xFF)) * sc[j];
-        o.z = static_cast<float>(static_cast<int8_t>((c[j] >> 16) & 0xFF)) * sc[j];
-        o.w = static_cast<float>(static_cast<int8_t>((c[j] >> 24) & 0xFF)) * sc[j];
-        __builtin_nontemporal_store(o, reinterpret_cast<f32x4*>(w_hat) + u);
+        __builtin_nontemporal_store(Fmt::value4(c[j], sc[j]), reinterpret_cast<f32x4*>(w_hat) + u);
     }
 }
 
-__global__ __launch_bounds__(kBlock) void k_dequant_i8_rows_generic(const int8_t* __restrict__ q,
-                                                                    const float* __restrict__ s,
-                                                                    int64_t k, int64_t total,
-                                                                    float* __restrict__ w_hat) {
+template <class Fmt>
+__global__ __launch_bounds__(kBlock) void k_dequant_rows_generic(const typename Fmt::code_t* __restrict__ q,
+                                                                 const float* __restrict__ s, int64_t k,
+                                                                 int64_t total, float* __restrict__ w_hat) {
     const int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
     if (i >= total) return;
-    w_hat[i] = static_cast<float>(q[i]) * s[i / k];
+    w_hat[i] = Fmt::value1(q[i], s[i / k]);
 }
 
 // ---- INT4 group-128: 16 lanes per group, 8 consecutive elements per lane ----
@@ -478,8 +523,9 @@ int qrange(int qdtype, double* qmin, double* qmax) {
     return tq_qdtype_info(qdtype, nullptr, nullptr, qmin, qmax);
 }
 
-int launch_quant_i8_rows(const float* w, int64_t rows, int64_t k, int8_t* q, float* s,
-                         float* w_hat, hipStream_t st, const char* what) {
+template <class Fmt>
+int launch_quant_rows(const float* w, int64_t rows, int64_t k, typename Fmt::code_t* q, float* s, float* w_hat,
+                      hipStream_t st, const char* what) {
     TQ_REQUIRE(rows >= 0 && k >= 0, "%s: negative shape [%lld, %lld]", what, (long long)rows,
                (long long)k);
     TQ_REQUIRE(rows < (int64_t(1) << 31), "%s: too many rows (%lld)", what, (long long)rows);
@@ -490,13 +536,29 @@ int launch_quant_i8_rows(const float* w, int64_t rows, int64_t k, int8_t* q, flo
     const dim3 grid(static_cast<unsigned>(rows)), block(kBlock);
     if (vec) {
         const int64_t items = (k / 4 + kBlock - 1) / kBlock;
-        if (items <= 1) k_quant_i8_rows_vec<1><<<grid, block, 0, st>>>(w, k, q, s, w_hat);
-        else if (items <= 2) k_quant_i8_rows_vec<2><<<grid, block, 0, st>>>(w, k, q, s, w_hat);
-        else if (items <= 4) k_quant_i8_rows_vec<4><<<grid, block, 0, st>>>(w, k, q, s, w_hat);
-        else if (items <= 8) k_quant_i8_rows_vec<8><<<grid, block, 0, st>>>(w, k, q, s, w_hat);
-        else k_quant_i8_rows_vec<16><<<grid, block, 0, st>>>(w, k, q, s, w_hat);
+        if (items <= 1) k_quant_rows_vec<Fmt, 1><<<grid, block, 0, st>>>(w, k, q, s, w_hat);
+        else if (items <= 2) k_quant_rows_vec<Fmt, 2><<<grid, block, 0, st>>>(w, k, q, s, w_hat);
+        else if (items <= 4) k_quant_rows_vec<Fmt, 4><<<grid, block, 0, st>>>(w, k, q, s, w_hat);
+        else if (items <= 8) k_quant_rows_vec<Fmt, 8><<<grid, block, 0, st>>>(w, k, q, s, w_hat);
+        else k_quant_rows_vec<Fmt, 16><<<grid, block, 0, st>>>(w, k, q, s, w_hat);
     } else {
-        k_quant_i8_rows_generic<<<grid, block, 0, st>>>(w, k, q, s, w_hat);
+        k_quant_rows_generic<Fmt><<<grid, block, 0, st>>>(w, k, q, s, w_hat);
+    }
+    return check_launch(what);
+}
+
+template <class Fmt>
+int launch_dequant_rows(const typename Fmt::code_t* q, const float* s, int64_t rows, int64_t k, float* w_hat,
+                        hipStream_t st, const char* what) {
+    TQ_REQUIRE(rows >= 0 && k >= 0, "%s: negative shape", what);
+    const int64_t total = rows * k;
+    if (total == 0) return TQ_OK;
+    TQ_REQUIRE(q && s && w_hat, "%s: null pointer", what);
+    if (k % 16 == 0 && aligned(q, 16) && aligned(w_hat, 16)) {
+        const int64_t n4 = total / 4;
+        k_dequant_rows_vec<Fmt><<<grid_for(n4, kBlock * kDqUnits, INT32_MAX), kBlock, 0, st>>>(q, s, k, n4, w_hat);
+    } else {
+        k_dequant_rows_generic<Fmt><<<grid_for(total, kBlock, INT32_MAX), kBlock, 0, st>>>(q, s, k, total, w_hat);
     }
     return check_launch(what);
 }
@@ -511,30 +573,37 @@ extern "C" {
 int tq_quantize_i8_rowwise(const float* w, int64_t rows, int64_t k, int8_t* q, float* s,
                            tq_stream_t stream) {
     if (rows > 0 && k > 0 && !q) return fail(TQ_EINVAL, "tq_quantize_i8_rowwise: null q");
-    return launch_quant_i8_rows(w, rows, k, q, s, nullptr, as_hip(stream), "tq_quantize_i8_rowwise");
+    return launch_quant_rows<FmtI8>(w, rows, k, q, s, nullptr, as_hip(stream), "tq_quantize_i8_rowwise");
 }
 
 int tq_fake_quantize_i8_rowwise(const float* w, int64_t rows, int64_t k, int8_t* q, float* s,
                                 float* w_hat, tq_stream_t stream) {
     if (rows > 0 && k > 0 && (!q || !w_hat))
         return fail(TQ_EINVAL, "tq_fake_quantize_i8_rowwise: null output");
-    return launch_quant_i8_rows(w, rows, k, q, s, w_hat, as_hip(stream), "tq_fake_quantize_i8_rowwise");
+    return launch_quant_rows<FmtI8>(w, rows, k, q, s, w_hat, as_hip(stream), "tq_fake_quantize_i8_rowwise");
 }
 
 int tq_dequantize_i8_rowwise(const int8_t* q, const float* s, int64_t rows, int64_t k,
                              float* w_hat, tq_stream_t stream) {
-    TQ_REQUIRE(rows >= 0 && k >= 0, "tq_dequantize_i8_rowwise: negative shape");
-    const int64_t total = rows * k;
-    if (total == 0) return TQ_OK;
-    TQ_REQUIRE(q && s && w_hat, "tq_dequantize_i8_rowwise: null pointer");
-    const hipStream_t st = as_hip(stream);
-    if (k % 16 == 0 && aligned(q, 16) && aligned(w_hat, 16)) {
-        const int64_t n4 = total / 4;
-        k_dequant_i8_rows_vec<<<grid_for(n4, kBlock * kDqUnits, INT32_MAX), kBlock, 0, st>>>(q, s, k, n4, w_hat);
-    } else {
-        k_dequant_i8_rows_generic<<<grid_for(total, kBlock, INT32_MAX), kBlock, 0, st>>>(q, s, k, total, w_hat);
-    }
-    return check_launch("tq_dequantize_i8_rowwise");
+    return launch_dequant_rows<FmtI8>(q, s, rows, k, w_hat, as_hip(stream), "tq_dequantize_i8_rowwise");
+}
+
+int tq_quantize_fp8_rowwise(const float* w, int64_t rows, int64_t k, uint8_t* q, float* s,
+                            tq_stream_t stream) {
+    if (rows > 0 && k > 0 && !q) return fail(TQ_EINVAL, "tq_quantize_fp8_rowwise: null q");
+    return launch_quant_rows<FmtFp8>(w, rows, k, q, s, nullptr, as_hip(stream), "tq_quantize_fp8_rowwise");
+}
+
+int tq_fake_quantize_fp8_rowwise(const float* w, int64_t rows, int64_t k, uint8_t* q, float* s,
+                                 float* w_hat, tq_stream_t stream) {
+    if (rows > 0 && k > 0 && (!q || !w_hat))
+        return fail(TQ_EINVAL, "tq_fake_quantize_fp8_rowwise: null output");
+    return launch_quant_rows<FmtFp8>(w, rows, k, q, s, w_hat, as_hip(stream), "tq_fake_quantize_fp8_rowwise");
+}
+
+int tq_dequantize_fp8_rowwise(const uint8_t* q, const float* s, int64_t rows, int64_t k,
+                              float* w_hat, tq_stream_t stream) {
+    return launch_dequant_rows<FmtFp8>(q, s, rows, k, w_hat, as_hip(stream), "tq_dequantize_fp8_rowwise");
 }
 
 int tq_quantize_i4_g128(const float* w, int64_t rows, int64_t k, uint8_t* packed,

@@ -44,6 +44,9 @@ SIGNATURES = {
     "tq_quantize_i8_rowwise": [_p, _i64, _i64, _p, _p, _p],
     "tq_dequantize_i8_rowwise": [_p, _p, _i64, _i64, _p, _p],
     "tq_fake_quantize_i8_rowwise": [_p, _i64, _i64, _p, _p, _p, _p],
+    "tq_quantize_fp8_rowwise": [_p, _i64, _i64, _p, _p, _p],
+    "tq_dequantize_fp8_rowwise": [_p, _p, _i64, _i64, _p, _p],
+    "tq_fake_quantize_fp8_rowwise": [_p, _i64, _i64, _p, _p, _p, _p],
     "tq_quantize_i4_g128": [_p, _i64, _i64, _p, _p, _p],
     "tq_dequantize_i4_g128": [_p, _p, _i64, _i64, _p, _p],
     "tq_gemv_w8": [_p, _i64, _p, _p, _p, _i64, _i64, _p, _p],
@@ -52,6 +55,7 @@ SIGNATURES = {
     "tq_repack_w4g128_tiled": [_p, _p, _i64, _i64, _i64, _p, _p, _p],
     "tq_gemv_w4g128_tiled": [_p, _i64, _p, _p, _p, _i64, _i64, _i64, _p, _p],
     "tq_gemm_w8a8": [_p, _p, _p, _p, _p, _i64, _i64, _i64, _p, _p, _p],
+    "tq_gemm_fp8": [_p, _p, _p, _p, _p, _i64, _i64, _i64, _p, _p],
     "tq_gemm_w4g128_bf16": [_p, _i64, _p, _p, _p, _i64, _i64, _p, _p],
     "tq_gemm_w4g128_bf16_workspace_bytes": [_i64, _i64],
     "tq_gemm_w4g128_bf16_ws": [_p, _i64, _p, _p, _p, _i64, _i64, _p, _i64, _p, _p],

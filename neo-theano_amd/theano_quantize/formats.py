@@ -4,6 +4,10 @@
   q = quantize_tensor(row, s_r, 0, Int8)  (quantize.rs:8-19, 39; observer.rs:110-121)
 * INT4, groups of 128 along K: s = max(f16_rne(absmax/7), 2^-24),
   q = quantize_tensor(group, s, 0, Int4), two nibbles per byte, low nibble = even k.
+* per-row symmetric FP8 (OCP e4m3, the 8-bit float behind QuantDType::FP8 and
+  its [-448, 448] range, qconfig.rs:29,38): s_r = f32(max(absmax_r/448, 1e-10)),
+  q = e4m3_rne(clamp(f32(x/s_r), -448, 448)), NaN -> 0x7F.  Codes are kept as
+  uint8 bit patterns (``q.view(torch.float8_e4m3fn)`` reads them as floats).
 """
 from __future__ import annotations
 
@@ -51,6 +55,37 @@ def fake_quantize_per_channel_i8(weight):
     s = torch.empty(n, dtype=torch.float32, device=w.device)
     out = torch.empty((n, k), dtype=torch.float32, device=w.device)
     _abi.call("tq_fake_quantize_i8_rowwise", ptr(w), n, k, ptr(q), ptr(s), ptr(out), stream())
+    return q, s, out
+
+
+def quantize_per_channel_fp8(weight):
+    """Symmetric per-row FP8 e4m3 -> (codes uint8 [N, K], scales f32 [N])."""
+    w = _as_2d(weight, "quantize_per_channel_fp8")
+    n, k = w.shape
+    q = torch.empty((n, k), dtype=torch.uint8, device=w.device)
+    s = torch.empty(n, dtype=torch.float32, device=w.device)
+    _abi.call("tq_quantize_fp8_rowwise", ptr(w), n, k, ptr(q), ptr(s), stream())
+    return q, s
+
+
+def dequantize_per_channel_fp8(q, s):
+    """w_hat = f32(e4m3(q) * s[row])."""
+    q = on_device(q, torch.uint8, "dequantize_per_channel_fp8")
+    s = on_device(s, torch.float32, "dequantize_per_channel_fp8")
+    n, k = q.shape
+    out = torch.empty((n, k), dtype=torch.float32, device=q.device)
+    _abi.call("tq_dequantize_fp8_rowwise", ptr(q), ptr(s), n, k, ptr(out), stream())
+    return out
+
+
+def fake_quantize_per_channel_fp8(weight):
+    """FP8 codes, scales and the dequantized tensor in one pass."""
+    w = _as_2d(weight, "fake_quantize_per_channel_fp8")
+    n, k = w.shape
+    q = torch.empty((n, k), dtype=torch.uint8, device=w.device)
+    s = torch.empty(n, dtype=torch.float32, device=w.device)
+    out = torch.empty((n, k), dtype=torch.float32, device=w.device)
+    _abi.call("tq_fake_quantize_fp8_rowwise", ptr(w), n, k, ptr(q), ptr(s), ptr(out), stream())
     return q, s, out
 
 

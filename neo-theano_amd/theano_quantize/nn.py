@@ -12,9 +12,11 @@ Modes (chosen from the QConfig):
   * "w8a8" INT8 weights and per-row dynamic INT8 activations
            (QConfig with activation_dtype Int8 and weight_dtype Int8);
   * "w4"   weight-only INT4 group-128, bf16 activations
-           (QConfig.default_int4()).
+           (QConfig.default_int4());
+  * "fp8"  FP8 e4m3 weights per output channel and per-row dynamic FP8
+           activations (QConfig with weight_dtype FP8).
 Decode shapes (M <= 16 tokens) run the dequant-GEMV kernels; prefill shapes run
-the i8-MFMA W8A8 GEMM or the bf16-MFMA W4A16 GEMM.
+the i8-MFMA W8A8 GEMM or the bf16-MFMA W4A16 GEMM; FP8 runs the FP8-MFMA GEMM.
 """
 from __future__ import annotations
 
@@ -23,7 +25,7 @@ import torch
 from . import _abi
 from ._tensor import on_device, ptr, stream
 from .errors import InvalidArgument
-from .formats import quantize_i4_g128, quantize_per_channel_i8, repack_i4_g128_tiled
+from .formats import quantize_i4_g128, quantize_per_channel_fp8, quantize_per_channel_i8, repack_i4_g128_tiled
 from .qconfig import QConfig, QuantDType
 
 DECODE_MAX_M = 16
@@ -57,6 +59,8 @@ def _mode_of(qconfig: QConfig) -> str:
         return "w4"
     if qconfig.weight_dtype == QuantDType.Int8:
         return "w8a8" if qconfig.activation_dtype == QuantDType.Int8 else "w8"
+    if qconfig.weight_dtype == QuantDType.FP8:
+        return "fp8"
     raise InvalidArgument(f"QuantizedLinear: unsupported weight dtype {qconfig.weight_dtype!r}")
 
 
@@ -86,6 +90,8 @@ class QuantizedLinear(Module):
         out_f, in_f = w.shape
         if mode == "w4":
             q, s = quantize_i4_g128(w)
+        elif mode == "fp8":
+            q, s = quantize_per_channel_fp8(w)
         else:
             q, s = quantize_per_channel_i8(w)
         b = None if bias is None else on_device(bias, torch.float32, "bias")
@@ -134,6 +140,12 @@ class QuantizedLinear(Module):
                 mm = min(DECODE_MAX_M, m - m0)
                 _abi.call("tq_gemv_w8", ptr(x[m0:m0 + mm]), mm, ptr(self.qweight), ptr(self.scales),
                           ptr(self.bias), n, k, ptr(y[m0:m0 + mm]), stream())
+        elif self.mode == "fp8":
+            qa = torch.empty((m, k), dtype=torch.uint8, device=x.device)
+            sa = torch.empty(m, dtype=torch.float32, device=x.device)
+            _abi.call("tq_quantize_fp8_rowwise", ptr(x), m, k, ptr(qa), ptr(sa), stream())
+            _abi.call("tq_gemm_fp8", ptr(qa), ptr(sa), ptr(self.qweight), ptr(self.scales),
+                      ptr(self.bias), m, n, k, ptr(y), stream())
         else:
             qa = torch.empty((m, k), dtype=torch.int8, device=x.device)
             sa = torch.empty(m, dtype=torch.float32, device=x.device)

@@ -3,7 +3,7 @@
 TEST INFRASTRUCTURE ONLY: the parity checker.  Only tests/, the smoke check in
 __graft_entry__.py and bench.py's cpu_baseline leg may import this module, and
 only to check or to time the CPU restatement of the reference -- never as a
-product path.  Build the library with ``oracle.build.build_oracle()``.
+product path.  The library is built by ``build_oracle()`` in neo-theano_amd/build.py.
 """
 from __future__ import annotations
 
@@ -59,6 +59,11 @@ def lib():
             "tqo_gemm_w8a8_acc": ([p, p, i64, i64, i64, p], None),
             "tqo_linear_w8a8": ([p, p, p, p, p, i64, i64, i64, p], None),
             "tqo_mlp_w4g128": ([p, i64, i64, i64, p, p, p, p, p, p, p], None),
+            "tqo_e4m3_to_f64": ([ctypes.c_uint8], d),
+            "tqo_f32_to_e4m3": ([ctypes.c_float], ctypes.c_uint8),
+            "tqo_quantize_fp8_rowwise": ([p, i64, i64, p, p], None),
+            "tqo_dequantize_fp8_rowwise": ([p, p, i64, i64, p], None),
+            "tqo_linear_fp8": ([p, p, p, p, p, i64, i64, i64, p], None),
         }
         for name, (args, res) in sig.items():
             fn = getattr(L, name)
@@ -315,4 +320,45 @@ def mlp_w4g128(x_bf16_bits, pg, sg, pu, su, pd, sd):
             _c(pd, np.uint8), _c(sd, np.uint16)]
     y = np.empty((m, d))
     lib().tqo_mlp_w4g128(_ptr(x), m, d, f, *[_ptr(a) for a in args], _ptr(y))
+    return y
+
+
+# ---- build-defined FP8 (OCP e4m3) ----
+
+def e4m3_to_f64(b):
+    return lib().tqo_e4m3_to_f64(int(b))
+
+
+def f32_to_e4m3(x):
+    return lib().tqo_f32_to_e4m3(float(x))
+
+
+def quantize_fp8_rowwise(w):
+    w = _c(w, np.float32)
+    n, k = w.shape
+    q = np.empty((n, k), np.uint8)
+    s = np.empty(n, np.float32)
+    lib().tqo_quantize_fp8_rowwise(_ptr(w), n, k, _ptr(q), _ptr(s))
+    return q, s
+
+
+def dequantize_fp8_rowwise(q, s):
+    q = _c(q, np.uint8)
+    s = _c(s, np.float32)
+    n, k = q.shape
+    out = np.empty((n, k), np.float32)
+    lib().tqo_dequantize_fp8_rowwise(_ptr(q), _ptr(s), n, k, _ptr(out))
+    return out
+
+
+def linear_fp8(qa, sa, qw, sw, bias=None):
+    qa = _c(qa, np.uint8)
+    qw = _c(qw, np.uint8)
+    sa = _c(sa, np.float32)
+    sw = _c(sw, np.float32)
+    b = None if bias is None else _c(bias, np.float32)
+    m, k = qa.shape
+    n = qw.shape[0]
+    y = np.empty((m, n))
+    lib().tqo_linear_fp8(_ptr(qa), _ptr(sa), _ptr(qw), _ptr(sw), _ptr(b), m, n, k, _ptr(y))
     return y

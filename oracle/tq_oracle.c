@@ -392,3 +392,86 @@ void tqo_mlp_w4g128(const uint16_t* x_bf16, int64_t m, int64_t d, int64_t f,
     free(w);
     free(g);
 }
+
+/* ---- build-defined FP8: OCP 8-bit float E4M3 ("e4m3fn") ----
+ * Bits S.EEEE.MMM, exponent bias 7, no infinities, S.1111.111 = NaN.
+ * Normal (E >= 1): (1 + M/8) * 2^(E-7); subnormal (E == 0): M * 2^-9.
+ * Largest finite value 448 = 0x7E, the range of QuantDType::FP8
+ * (crates/theano-quantize/src/qconfig.rs:29,38). */
+double tqo_e4m3_to_f64(uint8_t b) {
+    const double sign = (b & 0x80u) ? -1.0 : 1.0;
+    const int e = (b >> 3) & 0xF;
+    const int m = b & 7;
+    if (e == 15 && m == 7) return NAN;
+    if (e == 0) return sign * ldexp((double)m, -9);
+    return sign * ldexp((double)(8 + m), e - 10);
+}
+
+/* Round to nearest, ties to even, on the e4m3 grid extended past 448 by one
+ * step (480); a result of 480 or more, an infinity or a NaN encodes NaN with
+ * the input's sign.  So 464 (the tie between 448 and 480) gives 448 and
+ * anything above 464 gives NaN. */
+uint8_t tqo_f32_to_e4m3(float x) {
+    const uint8_t sign = signbit(x) ? 0x80u : 0u;
+    if (x != x || isinf(x)) return (uint8_t)(sign | 0x7Fu);
+    const double a = fabs((double)x);
+    if (a < 0x1p-6) { /* subnormal range, ulp 2^-9; m == 8 is the smallest normal 0x08 */
+        const double m = nearbyint(a * 0x1p9);
+        return (uint8_t)(sign | (uint8_t)m);
+    }
+    int e2;
+    frexp(a, &e2);
+    int e = e2 - 1; /* a in [2^e, 2^(e+1)) */
+    double m = nearbyint(ldexp(a, 3 - e)); /* in [8, 16] */
+    if (m == 16.0) {
+        m = 8.0;
+        e += 1;
+    }
+    if (e + 7 > 15) return (uint8_t)(sign | 0x7Fu);
+    return (uint8_t)(sign | (uint8_t)((e + 7) << 3) | (uint8_t)(m - 8.0)); /* e = 8, m = 15: 0x7F NaN */
+}
+
+/* Build-defined symmetric per-row FP8 (dynamic per-token for activations):
+ *   s_r = f32(max(absmax_r / 448, 1e-10))     (qmax of QuantDType::FP8, the
+ *                                              1e-10 floor of quantize.rs:39)
+ *   q   = e4m3(clamp(f32(x / s_r), -448, 448)), NaN -> 0x7F
+ * x / s_r is the correctly rounded f32 quotient (the f64 quotient rounded to
+ * f32 is that: 53 >= 2 * 24 + 2), and the clamp keeps NaN (f64::clamp). */
+void tqo_quantize_fp8_rowwise(const float* w, int64_t rows, int64_t k, uint8_t* q, float* s) {
+    for (int64_t r = 0; r < rows; ++r) {
+        const float* row = w + r * k;
+        const float sf = (float)fmax(absmax_of(row, k) / 448.0, 1e-10);
+        s[r] = sf;
+        for (int64_t i = 0; i < k; ++i) {
+            const float v = (float)((double)row[i] / (double)sf);
+            q[r * k + i] = v != v ? 0x7Fu : tqo_f32_to_e4m3((float)rust_clamp(v, -448.0, 448.0));
+        }
+    }
+}
+
+/* w_hat = f32(e4m3(q) * s[row]) (the f64 product of a 4-bit and a 24-bit
+ * significand is exact, so this is one f32 rounding) */
+void tqo_dequantize_fp8_rowwise(const uint8_t* q, const float* s, int64_t rows, int64_t k,
+                                float* w_hat) {
+    for (int64_t r = 0; r < rows; ++r)
+        for (int64_t i = 0; i < k; ++i)
+            w_hat[r * k + i] = (float)(tqo_e4m3_to_f64(q[r * k + i]) * (double)s[r]);
+}
+
+static double* deq_fp8_f64(const uint8_t* q, const float* s, int64_t n, int64_t k) {
+    double* w = (double*)malloc(sizeof(double) * (size_t)(n * k));
+    for (int64_t r = 0; r < n; ++r)
+        for (int64_t i = 0; i < k; ++i) w[r * k + i] = tqo_e4m3_to_f64(q[r * k + i]) * (double)s[r];
+    return w;
+}
+
+/* Reference value of the FP8 W8A8 product: mm(deq(qa), deq(qw)^T) (+ b) in f64
+ * (tensor_ops.rs:379-410, linear.rs:111-121). */
+void tqo_linear_fp8(const uint8_t* qa, const float* sa, const uint8_t* qw, const float* sw,
+                    const float* bias, int64_t m, int64_t n, int64_t k, double* y) {
+    double* a = deq_fp8_f64(qa, sa, m, k);
+    double* w = deq_fp8_f64(qw, sw, n, k);
+    tqo_linear(a, m, w, bias, n, k, y);
+    free(w);
+    free(a);
+}

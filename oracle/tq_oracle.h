@@ -29,6 +29,10 @@
  *   rowwise / g128 quant   exact-rational rounding (fractions.Fraction),
  *                          numpy float16 RNE, pack/unpack bijection
  *   w8a8 accumulators      numpy int64 matmul
+ *   e4m3 encode / decode   torch.float8_e4m3fn on all 256 codes and on every
+ *                          midpoint / boundary / special value; rowwise FP8
+ *                          quantize: exact-rational checks of the scale and
+ *                          of |x/s - decode(q)| <= half a step
  *   silu / mlp             closed forms (sigmoid(0)=1/2, limits), math.exp
  */
 #ifndef TQ_ORACLE_H
@@ -106,6 +110,15 @@ void tqo_gemm_w8a8_acc(const int8_t* qa, const int8_t* qw, int64_t m, int64_t n,
                        int32_t* acc);
 void tqo_linear_w8a8(const int8_t* qa, const float* sa, const int8_t* qw, const float* sw,
                      const float* bias_or_null, int64_t m, int64_t n, int64_t k, double* y);
+
+/* build-defined FP8 (OCP e4m3, bias 7, max 448, S.1111.111 = NaN), per-row scales */
+double tqo_e4m3_to_f64(uint8_t b);
+uint8_t tqo_f32_to_e4m3(float x);
+void tqo_quantize_fp8_rowwise(const float* w, int64_t rows, int64_t k, uint8_t* q, float* s);
+void tqo_dequantize_fp8_rowwise(const uint8_t* q, const float* s, int64_t rows, int64_t k,
+                                float* w_hat);
+void tqo_linear_fp8(const uint8_t* qa, const float* sa, const uint8_t* qw, const float* sw,
+                    const float* bias_or_null, int64_t m, int64_t n, int64_t k, double* y);
 
 /* build-defined quantized Llama FFN: y = (SiLU(x Wg^T) * (x Wu^T)) Wd^T */
 void tqo_mlp_w4g128(const uint16_t* x_bf16, int64_t m, int64_t d, int64_t f,

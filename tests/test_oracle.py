@@ -354,3 +354,133 @@ def test_mlp_matches_numpy_composition(oracle):
     h = g * (1.0 / (1.0 + np.exp(-g))) * u
     ref = h @ oracle.dequantize_i4_g128(pd, sd).astype(np.float64).T
     np.testing.assert_allclose(y, ref, rtol=1e-11, atol=1e-12)
+
+
+# ------------------------------------------------------------- FP8 (OCP e4m3)
+# torch.float8_e4m3fn is an independent implementation of the same OCP format.
+def _torch_e4m3(x):
+    import torch
+
+    return torch.from_numpy(np.asarray(x, np.float32)).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+
+
+def _torch_decode(codes):
+    import torch
+
+    return torch.from_numpy(np.asarray(codes, np.uint8)).view(torch.float8_e4m3fn).to(torch.float32).numpy()
+
+
+def _e4m3_probe_values():
+    finite = _torch_decode(np.arange(256, dtype=np.uint8))
+    grid = np.unique(finite[np.isfinite(finite) & (finite >= 0)].astype(np.float64))
+    grid = np.append(grid, 480.0)  # one step past 448: the rounding boundary at 464
+    mids = (grid[:-1] + grid[1:]) / 2  # every tie, exact in f32
+    pts = np.concatenate([grid, mids]).astype(np.float32)
+    up = np.nextafter(pts, np.float32(np.inf))
+    dn = np.nextafter(pts, np.float32(-np.inf))
+    rng = np.random.default_rng(7)
+    wide = (rng.standard_normal(20000) * np.exp2(rng.uniform(-14, 10, 20000))).astype(np.float32)
+    special = np.array([0.0, 2.0 ** -10, 2.0 ** -11, 1e-30, 1e-45, 447.9, 448.0, 463.99, 464.0, 464.01, 479.0,
+                        480.0, 500.0, 1e30, np.inf, np.nan], np.float32)
+    v = np.concatenate([pts, up, dn, wide, special])
+    return np.concatenate([v, -v])
+
+
+def test_e4m3_decode_all_codes_vs_torch(oracle):
+    t = _torch_decode(np.arange(256, dtype=np.uint8)).astype(np.float64)
+    o = np.array([oracle.e4m3_to_f64(c) for c in range(256)])
+    assert ieee_equal(o, t)
+    # format facts: 0x7E = 448, 0x08 = 2^-6 (smallest normal), 0x01 = 2^-9, NaN only at S.1111.111
+    assert o[0x7E] == 448.0 and o[0x08] == 2.0 ** -6 and o[0x01] == 2.0 ** -9 and o[0x38] == 1.0
+    assert [c for c in range(256) if math.isnan(o[c])] == [0x7F, 0xFF]
+
+
+def test_e4m3_encode_vs_torch(oracle):
+    v = _e4m3_probe_values()
+    o = np.array([oracle.f32_to_e4m3(float(x)) for x in v], np.uint8)
+    assert np.array_equal(o, _torch_e4m3(v))
+
+
+def test_e4m3_encode_ties_to_even_and_overflow(oracle):
+    f = oracle.f32_to_e4m3
+    assert f(1.0625) == 0x38          # tie between 1 and 1.125 -> even mantissa (1.0)
+    assert f(1.1875) == 0x3A          # tie between 1.125 and 1.25 -> 1.25
+    assert f(3 * 2.0 ** -10) == 0x02  # subnormal tie between 1 and 2 (x 2^-9) -> 2
+    assert f(2.0 ** -10) == 0x00 and f(-(2.0 ** -10)) == 0x80
+    assert f(464.0) == 0x7E and f(464.01) == 0x7F and f(-500.0) == 0xFF
+    assert f(float("inf")) == 0x7F and f(float("-inf")) == 0xFF
+
+
+def _f32(x):
+    return float(np.float32(x))
+
+
+def test_quantize_fp8_rowwise_exact(oracle):
+    rng = np.random.default_rng(11)
+    w = (rng.standard_normal((6, 300)) * np.exp2(rng.uniform(-8, 8, (6, 1)))).astype(np.float32)
+    w[1, 17] = -abs(w[1]).max() * 2  # the absmax element negative
+    w[2, :] = 0.0
+    w[3, 5] = np.nan
+    w[4, 9] = np.inf
+    w[5, 0] = -0.0
+    q, s = oracle.quantize_fp8_rowwise(w)
+    dec = _torch_decode(q).astype(np.float64)
+    for r in range(w.shape[0]):
+        row = w[r].astype(np.float64)
+        absmax = np.nanmax(np.abs(row))
+        # scale: f32 of the f64 quotient absmax / 448, floored at 1e-10
+        assert s[r] == np.float32(max(absmax / 448.0, 1e-10))
+        for i, x in enumerate(row):
+            if math.isnan(x) or (math.isinf(x) and math.isinf(s[r])):
+                assert q[r, i] == 0x7F
+                continue
+            qt = _f32(Fraction(x) / Fraction(float(s[r]))) if math.isfinite(s[r]) else 0.0 * x
+            # the code is a nearest e4m3 value of the f32 quotient (clamped to +-448)
+            c = dec[r, i]
+            t = max(-448.0, min(448.0, qt))
+            grid_step = 2.0 ** (max(math.floor(math.log2(abs(t))), -6) - 3) if t != 0 else 2.0 ** -9
+            assert abs(c - t) <= grid_step / 2, (r, i, x, c, t)
+            assert (q[r, i] >> 7) == int(math.copysign(1.0, x) < 0), (r, i, x)  # sign bit of x, zeros too
+    assert q[2].tolist() == [0] * 300 and s[2] == np.float32(1e-10)
+    assert q[5, 0] == 0x80                         # -0 keeps its sign
+    assert np.all(q[4, np.arange(300) != 9] & 0x7F == 0)  # finite / inf -> +-0
+    # the absmax element lands on +-448
+    assert q[1, 17] == 0xFE and np.abs(dec[0]).max() == 448.0
+
+
+def test_quantize_fp8_rowwise_vs_torch_composition(oracle):
+    import torch
+
+    rng = np.random.default_rng(12)
+    w = (rng.standard_normal((16, 512)) * 3).astype(np.float32)
+    q, s = oracle.quantize_fp8_rowwise(w)
+    s_ref = np.maximum(np.abs(w.astype(np.float64)).max(axis=1) / 448.0, 1e-10).astype(np.float32)
+    assert np.array_equal(s, s_ref)
+    t = torch.from_numpy(w) / torch.from_numpy(s_ref)[:, None]
+    ref = t.clamp(-448, 448).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    assert np.array_equal(q, ref)
+
+
+def test_dequantize_fp8_rowwise_vs_numpy(oracle):
+    rng = np.random.default_rng(13)
+    q = rng.integers(0, 256, (5, 64), dtype=np.uint8)
+    s = (rng.uniform(0.5, 2, 5) * np.exp2(rng.integers(-20, 20, 5))).astype(np.float32)
+    out = oracle.dequantize_fp8_rowwise(q, s)
+    ref = _torch_decode(q) * s[:, None]  # f32 product: one rounding
+    assert ieee_equal(out, ref)
+
+
+def test_linear_fp8_vs_numpy(oracle):
+    rng = np.random.default_rng(14)
+    qa = rng.integers(0, 256, (7, 96), dtype=np.uint8)
+    qw = rng.integers(0, 256, (9, 96), dtype=np.uint8)
+    qa[(qa & 0x7F) == 0x7F] = 0x38
+    qw[(qw & 0x7F) == 0x7F] = 0xB8
+    sa = rng.uniform(0.5, 2, 7).astype(np.float32)
+    sw = rng.uniform(0.5, 2, 9).astype(np.float32)
+    b = rng.standard_normal(9).astype(np.float32)
+    a = _torch_decode(qa).astype(np.float64) * sa[:, None].astype(np.float64)
+    w = _torch_decode(qw).astype(np.float64) * sw[:, None].astype(np.float64)
+    ref = a @ w.T + b.astype(np.float64)
+    y = oracle.linear_fp8(qa, sa, qw, sw, b)
+    assert np.allclose(y, ref, rtol=1e-12, atol=1e-9)

@@ -339,6 +339,30 @@ Result<Int8Weight> quantize_per_channel_i8(const Tensor& weight, hipStream_t str
     });
 }
 
+Result<Fp8Weight> quantize_per_channel_fp8(const Tensor& weight, hipStream_t stream) {
+    return capture<Fp8Weight>([&]() -> Result<Fp8Weight> {
+        Fp8Weight w;
+        const std::vector<float> f = as_f32_matrix(weight, "quantize_per_channel_fp8", &w.rows, &w.cols);
+        DeviceBuffer<float> src(f.size());
+        src.upload(f.data(), f.size(), stream);
+        w.codes = DeviceBuffer<uint8_t>(w.rows * w.cols);
+        w.scales = DeviceBuffer<float>(w.rows);
+        const int st = tq_quantize_fp8_rowwise(src.data(), static_cast<int64_t>(w.rows),
+                                               static_cast<int64_t>(w.cols), w.codes.data(), w.scales.data(),
+                                               reinterpret_cast<tq_stream_t>(stream));
+        if (st != TQ_OK) return TheanoError::from_status(st, "quantize_per_channel_fp8");
+        check_hip(hipStreamSynchronize(stream), "quantize_per_channel_fp8");
+        return std::move(w);
+    });
+}
+
+double e4m3_value(uint8_t code) {
+    const double sign = (code & 0x80) ? -1.0 : 1.0;
+    const int e = (code >> 3) & 0xF, m = code & 7;
+    if (e == 15 && m == 7) return std::nan("");
+    return e == 0 ? sign * std::ldexp(m, -9) : sign * std::ldexp(8 + m, e - 10);
+}
+
 void make_tiled(Int4Weight& w, hipStream_t stream);
 
 Result<Int4Weight> quantize_i4_g128(const Tensor& weight, hipStream_t stream) {
@@ -383,6 +407,17 @@ Result<Tensor> dequantize(const Int8Weight& w, hipStream_t stream) {
         const int st = tq_dequantize_i8_rowwise(w.codes.data(), w.scales.data(), static_cast<int64_t>(w.rows),
                                                 static_cast<int64_t>(w.cols), out.data(),
                                                 reinterpret_cast<tq_stream_t>(stream));
+        if (st != TQ_OK) return TheanoError::from_status(st, "dequantize");
+        return to_tensor(out.to_host(stream), {w.rows, w.cols});
+    });
+}
+
+Result<Tensor> dequantize(const Fp8Weight& w, hipStream_t stream) {
+    return capture<Tensor>([&]() -> Result<Tensor> {
+        DeviceBuffer<float> out(w.rows * w.cols);
+        const int st = tq_dequantize_fp8_rowwise(w.codes.data(), w.scales.data(), static_cast<int64_t>(w.rows),
+                                                 static_cast<int64_t>(w.cols), out.data(),
+                                                 reinterpret_cast<tq_stream_t>(stream));
         if (st != TQ_OK) return TheanoError::from_status(st, "dequantize");
         return to_tensor(out.to_host(stream), {w.rows, w.cols});
     });
@@ -493,6 +528,13 @@ Result<QuantizedLinear> QuantizedLinear::from_tensors(const Tensor& weight, cons
             l.w8_ = std::move(r).unwrap();
             l.out_ = l.w8_.rows;
             l.in_ = l.w8_.cols;
+        } else if (qconfig.weight_dtype == QuantDType::FP8) {
+            l.mode_ = Mode::FP8;
+            auto r = quantize::quantize_per_channel_fp8(weight, stream);
+            if (r.is_err()) return r.unwrap_err();
+            l.fp8_ = std::move(r).unwrap();
+            l.out_ = l.fp8_.rows;
+            l.in_ = l.fp8_.cols;
         } else {
             return TheanoError::invalid_argument(std::string("QuantizedLinear: unsupported weight dtype ") +
                                                  qconfig.weight_dtype.name());
@@ -553,6 +595,15 @@ Result<void> QuantizedLinear::forward_device(const void* x, int64_t m, float* y,
                                   ts);
             break;
         }
+        case Mode::FP8: {
+            if (!act_codes || !act_scales)
+                return TheanoError::invalid_argument("QuantizedLinear::forward_device: fp8 needs activation scratch");
+            auto* qa = reinterpret_cast<uint8_t*>(act_codes);
+            st = tq_quantize_fp8_rowwise(static_cast<const float*>(x), m, k, qa, act_scales, ts);
+            if (st == TQ_OK)
+                st = tq_gemm_fp8(qa, act_scales, fp8_.codes.data(), fp8_.scales.data(), b, m, n, k, y, ts);
+            break;
+        }
     }
     if (st != TQ_OK) return TheanoError::from_status(st, "QuantizedLinear::forward");
     return {};
@@ -577,7 +628,7 @@ Result<Tensor> QuantizedLinear::try_forward(const Tensor& input) const {
             const std::vector<float> xf(xv.begin(), xv.end());
             DeviceBuffer<float> xd(xf.size());
             xd.upload(xf.data(), xf.size(), stream_);
-            if (mode_ == Mode::W8A8) {
+            if (mode_ == Mode::W8A8 || mode_ == Mode::FP8) {
                 DeviceBuffer<int8_t> qa(m * in_);
                 DeviceBuffer<float> sa(m);
                 r = forward_device(xd.data(), static_cast<int64_t>(m), y.data(), stream_, qa.data(), sa.data());
@@ -613,6 +664,13 @@ std::vector<std::pair<std::string, Tensor>> QuantizedLinear::named_parameters() 
         }
         out.emplace_back("weight", Tensor::from_slice(std::move(codes), {out_, in_}));
         out.emplace_back("weight_scale", Tensor::from_slice(std::move(sc), {out_, in_ / 128}));
+    } else if (mode_ == Mode::FP8) {
+        const auto q = fp8_.codes.to_host(stream_);
+        const auto s = fp8_.scales.to_host(stream_);
+        std::vector<double> codes(q.size());
+        for (size_t i = 0; i < q.size(); ++i) codes[i] = quantize::e4m3_value(q[i]);
+        out.emplace_back("weight", Tensor::from_slice(std::move(codes), {out_, in_}));
+        out.emplace_back("weight_scale", Tensor::from_slice(std::vector<double>(s.begin(), s.end()), {out_}));
     } else {
         const auto q = w8_.codes.to_host(stream_);
         const auto s = w8_.scales.to_host(stream_);
@@ -778,6 +836,10 @@ Result<void> QuantizedLinear::save(SafeTensorsFile& f, const std::string& name) 
             f.metadata[name + ".quant"] = "int4_g128";
             f.metadata[name + ".group_size"] = "128";
             put_int4(f, name, w4_, stream_);
+        } else if (mode_ == Mode::FP8) {
+            f.metadata[name + ".quant"] = "fp8_e4m3_per_channel";
+            put(f, name + ".weight", "F8_E4M3", {out_, in_}, bytes_of(fp8_.codes, stream_));
+            put(f, name + ".weight_scale", "F32", {out_}, bytes_of(fp8_.scales, stream_));
         } else {
             f.metadata[name + ".quant"] = mode_ == Mode::W8 ? "int8_per_channel" : "int8_per_channel_a8";
             put(f, name + ".weight", "I8", {out_, in_}, bytes_of(w8_.codes, stream_));
@@ -809,6 +871,12 @@ Result<QuantizedLinear> QuantizedLinear::load(const SafeTensorsFile& f, const st
             l.w8_.cols = l.in_;
             l.w8_.codes = device_of<int8_t>(get<int8_t>(f, name + ".weight", "I8", {l.out_, l.in_}), stream);
             l.w8_.scales = device_of<float>(get<float>(f, name + ".weight_scale", "F32", {l.out_}), stream);
+        } else if (q == "fp8_e4m3_per_channel") {
+            l.mode_ = Mode::FP8;
+            l.fp8_.rows = l.out_;
+            l.fp8_.cols = l.in_;
+            l.fp8_.codes = device_of<uint8_t>(get<uint8_t>(f, name + ".weight", "F8_E4M3", {l.out_, l.in_}), stream);
+            l.fp8_.scales = device_of<float>(get<float>(f, name + ".weight_scale", "F32", {l.out_}), stream);
         } else {
             return TheanoError::runtime("checkpoint: '" + name + "' has unknown scheme " + q);
         }

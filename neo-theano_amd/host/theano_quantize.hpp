@@ -275,12 +275,25 @@ struct Int4Weight {
     rocm::DeviceBuffer<uint16_t> scales_tiled;
 };
 
+// Symmetric per-output-channel FP8 (OCP e4m3: bias 7, largest finite 448, the
+// range of QuantDType::FP8) held in HBM: codes u8 [rows, cols] (e4m3 bit
+// patterns), scales f32 [rows] (s = f32(max(absmax / 448, 1e-10))).
+struct Fp8Weight {
+    size_t rows = 0, cols = 0;
+    rocm::DeviceBuffer<uint8_t> codes;
+    rocm::DeviceBuffer<float> scales;
+};
+
 // The weight's f32 values (f64 host values are rounded to f32 first, the
 // element type the device formats are defined on).
 Result<Int8Weight> quantize_per_channel_i8(const Tensor& weight, hipStream_t stream = nullptr);
 Result<Int4Weight> quantize_i4_g128(const Tensor& weight, hipStream_t stream = nullptr);
+Result<Fp8Weight> quantize_per_channel_fp8(const Tensor& weight, hipStream_t stream = nullptr);
 Result<Tensor> dequantize(const Int8Weight& w, hipStream_t stream = nullptr);
 Result<Tensor> dequantize(const Int4Weight& w, hipStream_t stream = nullptr);
+Result<Tensor> dequantize(const Fp8Weight& w, hipStream_t stream = nullptr);
+// value of an e4m3 bit pattern (NaN for S.1111.111)
+double e4m3_value(uint8_t code);
 
 }  // namespace quantize
 
@@ -308,9 +321,10 @@ class Module {
 //   weight Int8, activations not Int8 -> "w8":   INT8 weight-only, f32 activations
 //   weight Int8, activations Int8     -> "w8a8": per-row dynamic INT8 activations
 //   weight Int4                       -> "w4":   INT4 g128 weight-only, bf16 activations
+//   weight FP8                        -> "fp8":  FP8 e4m3 weights, per-row dynamic FP8 activations
 class QuantizedLinear : public Module {
    public:
-    enum class Mode { W8, W8A8, W4 };
+    enum class Mode { W8, W8A8, W4, FP8 };
     static Result<QuantizedLinear> from_tensors(const Tensor& weight, const std::optional<Tensor>& bias,
                                                 const quantize::QConfig& qconfig = quantize::QConfig::default_int8(),
                                                 hipStream_t stream = nullptr);
@@ -318,9 +332,10 @@ class QuantizedLinear : public Module {
     // x [M, in] or [in]; returns [M, out] or [out] (f64 values of the f32 result)
     Tensor forward(const Tensor& input) const override;
     Result<Tensor> try_forward(const Tensor& input) const;
-    // Device-resident forward: x is f32 [m, in] (w8, w8a8) or bf16 bits [m, in] (w4),
-    // y is f32 [m, out]; enqueued on `stream`, no host synchronisation.  w8a8
-    // needs `act_codes` (int8 [m, in]) and `act_scales` (f32 [m]) device scratch;
+    // Device-resident forward: x is f32 [m, in] (w8, w8a8, fp8) or bf16 bits [m, in]
+    // (w4), y is f32 [m, out]; enqueued on `stream`, no host synchronisation.  w8a8
+    // and fp8 need `act_codes` (one byte per element, [m, in]) and `act_scales`
+    // (f32 [m]) device scratch;
     // w4 with m > 16 uses `workspace` (workspace_bytes(m) bytes) when given.
     Result<void> forward_device(const void* x, int64_t m, float* y, hipStream_t stream,
                                 int8_t* act_codes = nullptr, float* act_scales = nullptr,
@@ -347,6 +362,7 @@ class QuantizedLinear : public Module {
     hipStream_t stream_ = nullptr;
     quantize::Int8Weight w8_;
     quantize::Int4Weight w4_;
+    quantize::Fp8Weight fp8_;
     std::optional<rocm::DeviceBuffer<float>> bias_;
 };
 

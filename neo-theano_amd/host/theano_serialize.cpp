@@ -281,6 +281,7 @@ double decode(const std::string& code, const uint8_t* p, size_t i) {
     if (code == "I16") { int16_t v; std::memcpy(&v, p + 2 * i, 2); return v; }
     if (code == "I8") return static_cast<int8_t>(p[i]);
     if (code == "U8") return p[i];
+    if (code == "F8_E4M3") return quantize::e4m3_value(p[i]);
     return p[i] != 0 ? 1.0 : 0.0;  // BOOL
 }
 
@@ -288,7 +289,8 @@ double decode(const std::string& code, const uint8_t* p, size_t i) {
 
 size_t element_size(const std::string& dtype) {
     static const std::map<std::string, size_t> sz = {{"F64", 8}, {"F32", 4}, {"F16", 2}, {"BF16", 2}, {"I64", 8},
-                                                     {"I32", 4}, {"I16", 2}, {"I8", 1},  {"U8", 1},   {"BOOL", 1}};
+                                                     {"I32", 4}, {"I16", 2}, {"I8", 1},  {"U8", 1},   {"BOOL", 1},
+                                                     {"F8_E4M3", 1}};
     const auto it = sz.find(standard_code(dtype));
     return it == sz.end() ? 0 : it->second;
 }

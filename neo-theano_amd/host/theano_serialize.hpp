@@ -9,6 +9,7 @@
 //    (add_tensor :36-54).  A payload of 8 bytes per element is that f64
 //    encoding; a payload of the named type's size is raw.
 //  * standard safetensors: dtype codes F64 F32 F16 BF16 I64 I32 I16 I8 U8 BOOL
+//    F8_E4M3
 //    with payloads of that type and an optional "__metadata__" string map.
 // Written: standard safetensors (tensors in name order, contiguous, header
 // padded with spaces to a multiple of 8 bytes).  add_tensor writes F64, whose
@@ -68,9 +69,11 @@ Result<std::map<std::string, Tensor>> load_safetensors(const std::vector<uint8_t
 
 // Quantized checkpoints (build-defined layout, shared with the Python package):
 //   <name>.weight        I8 [N, K] | U8 [N, K/2] (INT4 g128, low nibble = even k)
-//   <name>.weight_scale  F32 [N]   | F16 [N, K/128]
+//                        | F8_E4M3 [N, K] (FP8 per channel)
+//   <name>.weight_scale  F32 [N]   | F16 [N, K/128] (INT4)
 //   <name>.bias          F32 [N]   (optional)
-//   metadata <name>.quant = int8_per_channel | int8_per_channel_a8 | int4_g128,
+//   metadata <name>.quant = int8_per_channel | int8_per_channel_a8 | int4_g128
+//   | fp8_e4m3_per_channel,
 //   <name>.group_size = 128 (INT4), <name>.in_features, <name>.out_features;
 //   a QuantizedMLP <name>: <name>.{gate,up,down}.{weight,weight_scale},
 //   <name>.quant = mlp_int4_g128, <name>.hidden, <name>.intermediate;

@@ -14,18 +14,21 @@ Read: both dialects of the container.
   of 8 bytes per element is the reference's f64 encoding and decodes to f64; a
   payload of the named type's size decodes as that type.
 * Standard safetensors: dtype codes F64, F32, F16, BF16, I64, I32, I16, I8, U8,
-  BOOL with payloads of that element type, and an optional ``__metadata__``
-  map of strings.
+  BOOL, F8_E4M3 with payloads of that element type, and an optional
+  ``__metadata__`` map of strings.  F8_E4M3 payloads are read as their uint8
+  bit patterns.
 
 Written: standard safetensors (tensors in name order, contiguous, header
 padded with spaces to a multiple of 8 bytes).  A quantized Linear ``<name>``
 becomes
     <name>.weight        I8 [N, K]    per-row INT8 codes
                          U8 [N, K/2]  INT4 g128, two nibbles per byte, low nibble = even k
-    <name>.weight_scale  F32 [N]      | F16 [N, K/128]
+                         F8_E4M3 [N, K]  per-row FP8 (OCP e4m3) codes
+    <name>.weight_scale  F32 [N]      | F16 [N, K/128] (INT4)
     <name>.bias          F32 [N]      (when present)
 with ``__metadata__`` entries ``<name>.quant`` ("int8_per_channel",
-"int8_per_channel_a8" for W8A8, or "int4_g128"), ``<name>.group_size`` ("128",
+"int8_per_channel_a8" for W8A8, "int4_g128", or "fp8_e4m3_per_channel"),
+``<name>.group_size`` ("128",
 INT4), ``<name>.in_features`` and
 ``<name>.out_features``; a ``QuantizedMLP`` ``<name>`` is the three INT4
 Linears ``<name>.gate``, ``<name>.up``, ``<name>.down`` plus ``<name>.quant`` =
@@ -44,7 +47,8 @@ FORMAT = "theano-quantize/1"
 
 # standard safetensors codes -> numpy element type (BF16 kept as its 16-bit pattern)
 _STD = {"F64": np.float64, "F32": np.float32, "F16": np.float16, "BF16": np.uint16, "I64": np.int64,
-        "I32": np.int32, "I16": np.int16, "I8": np.int8, "U8": np.uint8, "BOOL": np.bool_}
+        "I32": np.int32, "I16": np.int16, "I8": np.int8, "U8": np.uint8, "BOOL": np.bool_,
+        "F8_E4M3": np.uint8}
 # the reference's DType names (dtype.rs:79-100) -> numpy element type of a raw payload
 _REF = {"float64": np.float64, "float32": np.float32, "float16": np.float16, "bfloat16": np.uint16,
         "int64": np.int64, "int32": np.int32, "int16": np.int16, "int8": np.int8, "uint8": np.uint8,
@@ -55,7 +59,8 @@ _CODE_OF = {np.dtype(np.float64): "F64", np.dtype(np.float32): "F32", np.dtype(n
 
 
 def _host_array(t):
-    """numpy view of a numpy array or a (device) torch tensor; bfloat16 -> (uint16 bits, "BF16")."""
+    """numpy view of a numpy array or a (device) torch tensor; bfloat16 -> (uint16 bits, "BF16"),
+    float8_e4m3fn -> (uint8 bits, "F8_E4M3")."""
     try:
         import torch
     except ImportError:  # pragma: no cover
@@ -64,6 +69,8 @@ def _host_array(t):
         t = t.detach()
         if t.dtype == torch.bfloat16:
             return t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16), "BF16"
+        if t.dtype == torch.float8_e4m3fn:
+            return t.contiguous().view(torch.uint8).cpu().numpy(), "F8_E4M3"
         t = t.contiguous().cpu().numpy()
     a = np.ascontiguousarray(t)
     code = _CODE_OF.get(a.dtype)
@@ -94,6 +101,12 @@ def save_safetensors(tensors, metadata=None) -> bytes:
 
 def load_safetensors(data: bytes):
     """-> ({name: numpy array}, {metadata}); reads both dialects (module docstring)."""
+    out, meta, _ = _parse(data)
+    return out, meta
+
+
+def _parse(data: bytes):
+    """-> (tensors, metadata, {name: header dtype string})."""
     data = memoryview(data)
     if len(data) < 8:
         raise InvalidArgument("safetensors: too short")
@@ -110,7 +123,7 @@ def load_safetensors(data: bytes):
     meta = header.pop("__metadata__", None) or {}
     if not isinstance(meta, dict):
         raise InvalidArgument("safetensors: __metadata__ is not an object")
-    out = {}
+    out, dtypes = {}, {}
     for name, info in header.items():
         try:
             dtype, shape, (b, e) = info["dtype"], [int(s) for s in info["shape"]], info["data_offsets"]
@@ -132,7 +145,8 @@ def load_safetensors(data: bytes):
             raise InvalidArgument(f"safetensors: '{name}' holds {nbytes} bytes, shape {shape} of {dtype} "
                                   f"needs {n * el.itemsize}")
         out[name] = np.frombuffer(body[b:e], dtype=el.newbyteorder("<")).astype(el, copy=True).reshape(shape)
-    return out, {str(k): str(v) for k, v in meta.items()}
+        dtypes[name] = dtype
+    return out, {str(k): str(v) for k, v in meta.items()}, dtypes
 
 
 # ------------------------------------------------------------ quantized modules
@@ -146,11 +160,15 @@ def _linear_entries(name, lin, tensors, meta):
         meta[f"{name}.group_size"] = "128"
     elif lin.mode in ("w8", "w8a8"):
         meta[f"{name}.quant"] = "int8_per_channel" if lin.mode == "w8" else "int8_per_channel_a8"
+    elif lin.mode == "fp8":
+        meta[f"{name}.quant"] = "fp8_e4m3_per_channel"
     else:
         raise InvalidArgument(f"save_quantized: '{name}' has mode {lin.mode!r}")
     meta[f"{name}.in_features"] = str(lin.in_features)
     meta[f"{name}.out_features"] = str(lin.out_features)
-    tensors[f"{name}.weight"] = lin.qweight
+    import torch
+
+    tensors[f"{name}.weight"] = lin.qweight.view(torch.float8_e4m3fn) if lin.mode == "fp8" else lin.qweight
     tensors[f"{name}.weight_scale"] = lin.scales
     if lin.bias is not None:
         tensors[f"{name}.bias"] = lin.bias
@@ -192,7 +210,7 @@ def load_quantized(data: bytes, device="cuda"):
 
     from .nn import QuantizedLinear, QuantizedMLP
 
-    tensors, meta = load_safetensors(data)
+    tensors, meta, dtypes = _parse(data)
     if meta.get("format") != FORMAT:
         raise InvalidArgument(f"load_quantized: not a {FORMAT} checkpoint (format={meta.get('format')!r})")
 
@@ -221,6 +239,12 @@ def load_quantized(data: bytes, device="cuda"):
             s = dev(_need(tensors, f"{name}.weight_scale", np.float16, (n, k // 128)).view(np.int16))
             s = s.view(torch.float16)
             mode = "w4"
+        elif kind == "fp8_e4m3_per_channel":
+            if dtypes.get(f"{name}.weight") != "F8_E4M3":
+                raise InvalidArgument(f"load_quantized: '{name}.weight' is not F8_E4M3")
+            q = dev(_need(tensors, f"{name}.weight", np.uint8, (n, k)))
+            s = dev(_need(tensors, f"{name}.weight_scale", np.float32, (n,)))
+            mode = "fp8"
         elif kind in ("int8_per_channel", "int8_per_channel_a8"):
             q = dev(_need(tensors, f"{name}.weight", np.int8, (n, k)))
             s = dev(_need(tensors, f"{name}.weight_scale", np.float32, (n,)))

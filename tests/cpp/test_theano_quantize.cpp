@@ -483,6 +483,24 @@ TEST_GPU(test_parity_quantized_linear_w8a8) {
     assert_close(y, ref, "w8a8 linear");
 }
 
+TEST_GPU(test_parity_quantized_linear_fp8) {
+    const size_t n = 272, k = 1024, m = 37;
+    const auto wv = randn(n * k, 0.02, 53), xv = randn(m * k, 1.0, 54), bv = randn(n, 0.1, 55);
+    const QConfig cfg{QuantDType::FP8, QuantDType::FP8, true, true};
+    const QuantizedLinear layer =
+        QuantizedLinear::from_tensors(Tensor::from_slice(wv, {n, k}), Tensor::from_slice(bv, {n}), cfg).unwrap();
+    ASSERT(layer.mode() == QuantizedLinear::Mode::FP8);
+    const auto y = layer.forward(Tensor::from_slice(xv, {m, k})).to_vec_f64().unwrap();
+    const auto w32 = f32(wv), x32 = f32(xv), b32 = f32(bv);
+    std::vector<uint8_t> qw(n * k), qa(m * k);
+    std::vector<float> sw(n), sa(m);
+    tqo_quantize_fp8_rowwise(w32.data(), n, k, qw.data(), sw.data());
+    tqo_quantize_fp8_rowwise(x32.data(), m, k, qa.data(), sa.data());
+    std::vector<double> ref(m * n);
+    tqo_linear_fp8(qa.data(), sa.data(), qw.data(), sw.data(), b32.data(), m, n, k, ref.data());
+    assert_close(y, ref, "fp8 linear");
+}
+
 TEST_GPU(test_parity_quantized_mlp) {
     const size_t d = 256, f = 384, m = 5;
     const auto gv = randn(f * d, 0.02, 61), uv = randn(f * d, 0.02, 62), dv = randn(d * f, 0.02, 63);
@@ -522,6 +540,16 @@ TEST_GPU(test_parity_weight_formats) {
     tqo_quantize_i4_g128(w32.data(), n, k, p.data(), s4.data());
     ASSERT(i4.packed.to_host(nullptr) == p);
     ASSERT(i4.scales.to_host(nullptr) == s4);
+    auto f8 = quantize_per_channel_fp8(w).unwrap();
+    std::vector<uint8_t> q8(n * k);
+    std::vector<float> s8(n);
+    tqo_quantize_fp8_rowwise(w32.data(), n, k, q8.data(), s8.data());
+    ASSERT(f8.codes.to_host(nullptr) == q8);
+    ASSERT(f8.scales.to_host(nullptr) == s8);
+    std::vector<float> wh8(n * k);
+    tqo_dequantize_fp8_rowwise(q8.data(), s8.data(), n, k, wh8.data());
+    const auto got8 = dequantize(f8).unwrap().to_vec_f64().unwrap();
+    for (size_t i = 0; i < wh8.size(); ++i) ASSERT_EQ(got8[i], static_cast<double>(wh8[i]));
     std::vector<float> wh(n * k);
     tqo_dequantize_i4_g128(p.data(), s4.data(), n, k, wh.data());
     const auto got = dequantize(i4).unwrap().to_vec_f64().unwrap();
@@ -597,6 +625,14 @@ TEST_CPU(test_safetensors_raw_payloads) {
     ASSERT(g.get_raw("a", "U8", {2, 2}).is_err());
     ASSERT(g.get_tensor("a").unwrap().to_vec_f64().unwrap() == (std::vector<double>{-128, -1, 0, 127}));
     ASSERT(g.get_tensor("b").unwrap().to_vec_f64().unwrap() == (std::vector<double>{0.5, -1.0}));
+    // F8_E4M3 codes: 1.0, -448, smallest subnormal 2^-9, NaN
+    ser::SafeTensorsFile h;
+    const uint8_t f8[4] = {0x38, 0xFE, 0x01, 0x7F};
+    ASSERT(h.add_raw("e", "F8_E4M3", {4}, f8, 4).is_ok());
+    const auto hb = ser::SafeTensorsFile::from_bytes(h.to_bytes()).unwrap();
+    ASSERT(hb.get_raw("e", "F8_E4M3", {4}).is_ok());
+    const auto ev = hb.get_tensor("e").unwrap().to_vec_f64().unwrap();
+    ASSERT(ev[0] == 1.0 && ev[1] == -448.0 && ev[2] == std::ldexp(1.0, -9) && std::isnan(ev[3]));
 }
 
 TEST_CPU(test_safetensors_malformed) {
@@ -652,8 +688,9 @@ TEST_GPU(test_checkpoint_linear_and_mlp_roundtrip) {
     const size_t n = 256, k = 512;
     const auto wv = randn(n * k, 0.02, 91), bv = randn(n, 0.1, 92);
     const QConfig a8{QuantDType::Int8, QuantDType::Int8, true, true};
+    const QConfig fp8{QuantDType::FP8, QuantDType::FP8, true, true};
     const std::vector<std::pair<std::string, QConfig>> cfgs = {
-        {"l4", QConfig::default_int4()}, {"l8", QConfig::default_int8()}, {"l8a8", a8}};
+        {"l4", QConfig::default_int4()}, {"l8", QConfig::default_int8()}, {"l8a8", a8}, {"lfp8", fp8}};
     ser::SafeTensorsFile file;
     std::vector<QuantizedLinear> layers;
     for (const auto& [name, cfg] : cfgs) {

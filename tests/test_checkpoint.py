@@ -140,3 +140,17 @@ def test_golden_checkpoint_fixture():
     assert np.array_equal(got["proj.weight_scale"].view(np.uint16), ref["s_f16"])
     assert meta["proj.quant"] == "int4_g128" and meta["proj.group_size"] == "128"
     assert got["const.f16"].tolist() == [0.5, -1.0, 65504.0]
+
+
+def test_f8_e4m3_against_the_safetensors_torch_package():
+    """F8_E4M3 tensors (FP8 codes) both ways through safetensors.torch."""
+    torch = pytest.importorskip("torch")
+    st_torch = pytest.importorskip("safetensors.torch")
+    codes = torch.arange(256, dtype=torch.int32).to(torch.uint8).view(16, 16)
+    blob = save_safetensors({"w.weight": codes.view(torch.float8_e4m3fn), "w.weight_scale": np.ones(16, np.float32)},
+                            {"format": "x"})
+    got = st_torch.load(blob)
+    assert got["w.weight"].dtype == torch.float8_e4m3fn
+    assert torch.equal(got["w.weight"].view(torch.uint8), codes)
+    back, _ = load_safetensors(st_torch.save({"w.weight": codes.view(torch.float8_e4m3fn)}))
+    assert back["w.weight"].dtype == np.uint8 and np.array_equal(back["w.weight"], codes.numpy())

@@ -8,7 +8,7 @@ weights rotate over enough copies (> 2x the 256 MB MALL) that every step
 streams them from HBM.  The timed region is a HIP graph of `--steps`
 launches bracketed by events on the launch stream.
 
-Secondary workloads (reported in `secondary`): INT8 GEMV (config 2), INT4
+Secondary workloads (reported in `secondary`): INT8 and FP8 GEMV (config 2), INT4
 GEMV at M=2..16, W8A8 GEMM at M=2048 (config 4) in INT8 and in FP8 e4m3,
 per-row INT8 quantize /
 dequantize round trip (config 1) and the INT4 FFN block (config 5).
@@ -43,7 +43,7 @@ def parse_args():
     p.add_argument("--steps", type=int, default=200)
     p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--only", default=None,
-                   help="run one workload: gemv_w4, gemv_w8, gemv_w4_m, w8a8, fp8, roundtrip, mlp, copy")
+                   help="run one workload: gemv_w4, gemv_w8, gemv_fp8, gemv_w4_m, w8a8, fp8, roundtrip, mlp, copy")
     p.add_argument("--no-secondary", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=12.0, help="bound of the CPU baseline sample (0: skip)")
     p.add_argument("--eager", action="store_true", help="time eager launches instead of a HIP graph")
@@ -195,6 +195,26 @@ def main():
         secondary["gemv_w8_m1"] = {"us": round(ms * 1e3, 3), "GB/s": round(gbs, 1),
                                    "hbm_frac": round(gbs / HBM_PEAK_GBS, 4), "bytes": b2}
         log(f"gemv_w8 M=1: {ms * 1e3:.2f} us/step  {gbs:.0f} GB/s")
+        del copies
+
+    # ------------------------------------------------ FP8 GEMV (C2 shape)
+    if not args.no_secondary and want("gemv_fp8"):
+        n2 = k2 = 4096
+        b2 = n2 * k2 + 4 * n2 + 4 * k2 + 4 * n2
+        w = normal_f32(1, (n2, k2), 0.02)
+        copies = quant_copies(w, tq.quantize_per_channel_fp8, rotation(n2 * k2))
+        x = dt(normal_f32(1, (1, k2), 1.0, stream=1))
+        y = torch.empty((1, n2), dtype=torch.float32, device=dev)
+
+        def launch(i):
+            q, s = copies[i % len(copies)]
+            _abi.call("tq_gemv_fp8", ptr(x), 1, ptr(q), ptr(s), None, n2, k2, ptr(y), stream())
+
+        ms, mode = timer.run(launch, args.steps, args.warmup)
+        gbs = b2 / (ms * 1e-3) / 1e9
+        secondary["gemv_fp8_m1"] = {"us": round(ms * 1e3, 3), "GB/s": round(gbs, 1),
+                                    "hbm_frac": round(gbs / HBM_PEAK_GBS, 4), "bytes": b2}
+        log(f"gemv_fp8 M=1: {ms * 1e3:.2f} us/step  {gbs:.0f} GB/s")
         del copies
 
     # ---------------------------------------------------------- W8A8 (C4)

@@ -192,6 +192,12 @@ int tq_dequantize_i4_g128(const uint8_t* packed, const uint16_t* s_f16, int64_t 
 int tq_gemv_w8(const float* x, int64_t m, const int8_t* q, const float* s,
                const float* bias, int64_t n, int64_t k, float* y, tq_stream_t stream);
 
+/* The same GEMV over per-row FP8 (OCP e4m3) weights (tq_quantize_fp8_rowwise):
+ * y = s[n] * sum_k e4m3(q[n,k]) * x[m,k] (+ bias[n]), f32 accumulation.  Same
+ * shapes, alignment and kernels as tq_gemv_w8. */
+int tq_gemv_fp8(const float* x, int64_t m, const uint8_t* q, const float* s,
+                const float* bias, int64_t n, int64_t k, float* y, tq_stream_t stream);
+
 /* Decode-shaped GEMV, INT4 g128 weights (canonical layout), bf16 activations
  * x [M, K] (bf16 bits), M <= 16, K % 128 == 0 (the format), any N.  The MFMA
  * kernel serves K <= 16384 with x and packed 16-byte aligned; other cases take

@@ -1,7 +1,8 @@
-// tq_gemv.hip -- decode-shaped INT8 weight-only quantized Linear
+// tq_gemv.hip -- decode-shaped 8-bit weight-only quantized Linear
 // (y = x . dequant(W)^T + b) for gfx950, the reference's Linear::forward
 // (crates/theano-nn/src/linear.rs:111-121) over the dequantized weight of
-// quantize.rs:22-27.
+// quantize.rs:22-27.  One kernel body serves per-row INT8 codes and per-row
+// FP8 (OCP e4m3) codes; only the byte -> f32 decode differs.
 //
 // HBM-bound weight stream.  The grid is persistent: every
 // wave owns a contiguous range of output rows, keeps its slice of x in
@@ -22,9 +23,28 @@ __device__ __forceinline__ int64_t uniform(int64_t v) {
 }
 
 
-// ------------------------------------------------------------------- INT8
+// Byte codes -> f32 values: 4 codes of a little-endian word.
+struct CodeI8 {
+    typedef int8_t code_t;
+    __device__ static void decode4(int w, float (&v)[4]) {
+#pragma unroll
+        for (int b = 0; b < 4; ++b) v[b] = static_cast<float>(static_cast<int8_t>((w >> (8 * b)) & 0xFF));
+    }
+};
+
+struct CodeFp8 {
+    typedef uint8_t code_t;
+    __device__ static void decode4(int w, float (&v)[4]) {
+        v[0] = __builtin_amdgcn_cvt_f32_fp8(w, 0);
+        v[1] = __builtin_amdgcn_cvt_f32_fp8(w, 1);
+        v[2] = __builtin_amdgcn_cvt_f32_fp8(w, 2);
+        v[3] = __builtin_amdgcn_cvt_f32_fp8(w, 3);
+    }
+};
+
+// ------------------------------------------------------------------ kernel
 // Chunk c covers k in [1024c, 1024c + 1024): lane l owns the 16 codes at
-// k = 1024c + 16l.  y = s[row] * sum(q * x) + b.
+// k = 1024c + 16l.  y = s[row] * sum(value(q) * x) + b.
 //
 // One 512-thread block per CU (persistent), 8 waves, each owning a contiguous
 // run of rows.  A wave first issues the weight loads of its first kRows rows
@@ -37,9 +57,9 @@ __device__ __forceinline__ int64_t uniform(int64_t v) {
 constexpr int kBlockW8 = 512;
 constexpr int kWavesW8 = kBlockW8 / kWave;
 
-template <int kM, int kChunks, int kRows>
+template <class Code, int kM, int kChunks, int kRows>
 __global__ __launch_bounds__(kBlockW8) void k_gemv_w8(const float* __restrict__ x, int64_t x_stride,
-                                                      const int8_t* __restrict__ q,
+                                                      const typename Code::code_t* __restrict__ q,
                                                       const float* __restrict__ s,
                                                       const float* __restrict__ bias, int64_t n,
                                                       int64_t k, float* __restrict__ y,
@@ -103,13 +123,14 @@ __global__ __launch_bounds__(kBlockW8) void k_gemv_w8(const float* __restrict__ 
             for (int c = 0; c < kChunks; ++c) {
                 const int words[4] = {cur[r][c].x, cur[r][c].y, cur[r][c].z, cur[r][c].w};
 #pragma unroll
-                for (int j = 0; j < 4; ++j)
+                for (int j = 0; j < 4; ++j) {
+                    float wv[4];
+                    Code::decode4(words[j], wv);
 #pragma unroll
-                    for (int b = 0; b < 4; ++b) {
-                        const float wv = static_cast<float>(static_cast<int8_t>((words[j] >> (8 * b)) & 0xFF));
+                    for (int b = 0; b < 4; ++b)
 #pragma unroll
-                        for (int m = 0; m < kM; ++m) acc[m] = fmaf(wv, xr[m][c][4 * j + b], acc[m]);
-                    }
+                        for (int m = 0; m < kM; ++m) acc[m] = fmaf(wv[b], xr[m][c][4 * j + b], acc[m]);
+                }
             }
             const int64_t row = row0 + r;
             const float sc = s[min(row, row_clamp)];
@@ -136,29 +157,59 @@ void grid_for_rows(int64_t n, int64_t* blocks, int64_t* rows_per_wave) {
     *blocks = (waves + kWavesW8 - 1) / kWavesW8;
 }
 
-template <int kM, int kChunks>
-void launch_w8(const float* x, int64_t xs, const int8_t* q, const float* s, const float* b,
+template <class Code, int kM, int kChunks>
+void launch_w8(const float* x, int64_t xs, const typename Code::code_t* q, const float* s, const float* b,
                int64_t n, int64_t k, float* y, int64_t ys, hipStream_t st) {
     constexpr int kRows = 2;
     int64_t blocks, rpw;
     grid_for_rows<kRows>(n, &blocks, &rpw);
-    k_gemv_w8<kM, kChunks, kRows><<<static_cast<unsigned>(blocks), kBlockW8, 0, st>>>(x, xs, q, s, b, n, k, y,
-                                                                                    ys, rpw);
+    k_gemv_w8<Code, kM, kChunks, kRows><<<static_cast<unsigned>(blocks), kBlockW8, 0, st>>>(x, xs, q, s, b, n, k,
+                                                                                          y, ys, rpw);
 }
 
-template <int kM>
-void dispatch_w8(int chunks, const float* x, int64_t xs, const int8_t* q, const float* s,
+template <class Code, int kM>
+void dispatch_w8(int chunks, const float* x, int64_t xs, const typename Code::code_t* q, const float* s,
                  const float* b, int64_t n, int64_t k, float* y, int64_t ys, hipStream_t st) {
     switch (chunks) {
-    case 1: launch_w8<kM, 1>(x, xs, q, s, b, n, k, y, ys, st); break;
-    case 2: launch_w8<kM, 2>(x, xs, q, s, b, n, k, y, ys, st); break;
-    case 3: launch_w8<kM, 3>(x, xs, q, s, b, n, k, y, ys, st); break;
-    case 4: launch_w8<kM, 4>(x, xs, q, s, b, n, k, y, ys, st); break;
-    case 5: launch_w8<kM, 5>(x, xs, q, s, b, n, k, y, ys, st); break;
-    case 6: launch_w8<kM, 6>(x, xs, q, s, b, n, k, y, ys, st); break;
-    case 7: launch_w8<kM, 7>(x, xs, q, s, b, n, k, y, ys, st); break;
-    default: launch_w8<kM, 8>(x, xs, q, s, b, n, k, y, ys, st); break;
+    case 1: launch_w8<Code, kM, 1>(x, xs, q, s, b, n, k, y, ys, st); break;
+    case 2: launch_w8<Code, kM, 2>(x, xs, q, s, b, n, k, y, ys, st); break;
+    case 3: launch_w8<Code, kM, 3>(x, xs, q, s, b, n, k, y, ys, st); break;
+    case 4: launch_w8<Code, kM, 4>(x, xs, q, s, b, n, k, y, ys, st); break;
+    case 5: launch_w8<Code, kM, 5>(x, xs, q, s, b, n, k, y, ys, st); break;
+    case 6: launch_w8<Code, kM, 6>(x, xs, q, s, b, n, k, y, ys, st); break;
+    case 7: launch_w8<Code, kM, 7>(x, xs, q, s, b, n, k, y, ys, st); break;
+    default: launch_w8<Code, kM, 8>(x, xs, q, s, b, n, k, y, ys, st); break;
     }
+}
+
+template <class Code>
+int gemv_8bit(const float* x, int64_t m, const typename Code::code_t* q, const float* s, const float* bias,
+              int64_t n, int64_t k, float* y, hipStream_t st, const char* what) {
+    TQ_REQUIRE(m >= 0 && n >= 0 && k >= 0, "%s: negative shape", what);
+    TQ_REQUIRE(m <= 16, "%s: M=%lld > 16 (decode shapes; run longer inputs in chunks)", what, (long long)m);
+    if (m == 0 || n == 0) return TQ_OK;
+    TQ_REQUIRE(y, "%s: null y", what);
+    TQ_REQUIRE(k == 0 || (x && q), "%s: null pointer", what);
+    TQ_REQUIRE(s, "%s: null scales", what);
+    TQ_REQUIRE(aligned(x, 4) && aligned(s, 4) && (!bias || aligned(bias, 4)) && aligned(y, 4),
+               "%s: misaligned f32 pointer", what);
+    // the tuned kernel streams 16-byte vectors of K-contiguous rows held in registers
+    if (k == 0 || k % 16 != 0 || k > 8 * 1024 || !aligned(x, 16) || !aligned(q, 16))
+        return launch_linear_8bit_generic(x, m, q, s, bias, n, k, y, st);
+    const int chunks = static_cast<int>((k + 1023) / 1024);
+    const int64_t per_pass = chunks <= 2 ? 4 : (chunks <= 4 ? 2 : 1);
+    for (int64_t m0 = 0; m0 < m; m0 += per_pass) {
+        const int64_t mm = (m - m0) < per_pass ? (m - m0) : per_pass;
+        const float* xp = x + m0 * k;
+        float* yp = y + m0 * n;
+        if (mm == 1) dispatch_w8<Code, 1>(chunks, xp, k, q, s, bias, n, k, yp, n, st);
+        else if (mm == 2) dispatch_w8<Code, 2>(chunks, xp, k, q, s, bias, n, k, yp, n, st);
+        else if (mm == 3) dispatch_w8<Code, 3>(chunks, xp, k, q, s, bias, n, k, yp, n, st);
+        else dispatch_w8<Code, 4>(chunks, xp, k, q, s, bias, n, k, yp, n, st);
+        const int rc = check_launch(what);
+        if (rc != TQ_OK) return rc;
+    }
+    return TQ_OK;
 }
 
 }  // namespace
@@ -170,32 +221,12 @@ extern "C" {
 
 int tq_gemv_w8(const float* x, int64_t m, const int8_t* q, const float* s, const float* bias,
                int64_t n, int64_t k, float* y, tq_stream_t stream) {
-    TQ_REQUIRE(m >= 0 && n >= 0 && k >= 0, "tq_gemv_w8: negative shape");
-    TQ_REQUIRE(m <= 16, "tq_gemv_w8: M=%lld > 16 (decode shapes; run longer inputs in chunks)", (long long)m);
-    if (m == 0 || n == 0) return TQ_OK;
-    TQ_REQUIRE(y, "tq_gemv_w8: null y");
-    TQ_REQUIRE(k == 0 || (x && q), "tq_gemv_w8: null pointer");
-    TQ_REQUIRE(s, "tq_gemv_w8: null scales");
-    TQ_REQUIRE(aligned(x, 4) && aligned(s, 4) && (!bias || aligned(bias, 4)) && aligned(y, 4),
-               "tq_gemv_w8: misaligned f32 pointer");
-    // the tuned kernel streams 16-byte vectors of K-contiguous rows held in registers
-    if (k == 0 || k % 16 != 0 || k > 8 * 1024 || !aligned(x, 16) || !aligned(q, 16))
-        return launch_linear_w8_generic(x, m, q, s, bias, n, k, y, as_hip(stream));
-    const int chunks = static_cast<int>((k + 1023) / 1024);
-    const hipStream_t st = as_hip(stream);
-    const int64_t per_pass = chunks <= 2 ? 4 : (chunks <= 4 ? 2 : 1);
-    for (int64_t m0 = 0; m0 < m; m0 += per_pass) {
-        const int64_t mm = (m - m0) < per_pass ? (m - m0) : per_pass;
-        const float* xp = x + m0 * k;
-        float* yp = y + m0 * n;
-        if (mm == 1) dispatch_w8<1>(chunks, xp, k, q, s, bias, n, k, yp, n, st);
-        else if (mm == 2) dispatch_w8<2>(chunks, xp, k, q, s, bias, n, k, yp, n, st);
-        else if (mm == 3) dispatch_w8<3>(chunks, xp, k, q, s, bias, n, k, yp, n, st);
-        else dispatch_w8<4>(chunks, xp, k, q, s, bias, n, k, yp, n, st);
-        const int rc = check_launch("tq_gemv_w8");
-        if (rc != TQ_OK) return rc;
-    }
-    return TQ_OK;
+    return gemv_8bit<CodeI8>(x, m, q, s, bias, n, k, y, as_hip(stream), "tq_gemv_w8");
+}
+
+int tq_gemv_fp8(const float* x, int64_t m, const uint8_t* q, const float* s, const float* bias,
+                int64_t n, int64_t k, float* y, tq_stream_t stream) {
+    return gemv_8bit<CodeFp8>(x, m, q, s, bias, n, k, y, as_hip(stream), "tq_gemv_fp8");
 }
 
 }  // extern "C"

@@ -26,19 +26,24 @@ __device__ __forceinline__ int wave_sum_i32(int v) {
 __device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __uint_as_float(static_cast<uint32_t>(b) << 16); }
 
 // y[i, j] = s[j] * sum_k x[i, k] q[j, k] + b[j]
-__global__ __launch_bounds__(kGenBlock) void k_linear_w8_generic(const float* __restrict__ x, int64_t m,
-                                                                 const int8_t* __restrict__ q,
-                                                                 const float* __restrict__ s,
-                                                                 const float* __restrict__ bias, int64_t n,
-                                                                 int64_t k, float* __restrict__ y) {
+// value of an 8-bit code: int8_t INT8, uint8_t FP8 (OCP e4m3)
+__device__ __forceinline__ float code_value(int8_t c) { return static_cast<float>(c); }
+__device__ __forceinline__ float code_value(uint8_t c) { return __builtin_amdgcn_cvt_f32_fp8(static_cast<int>(c), 0); }
+
+template <class Code>
+__global__ __launch_bounds__(kGenBlock) void k_linear_8bit_generic(const float* __restrict__ x, int64_t m,
+                                                                   const Code* __restrict__ q,
+                                                                   const float* __restrict__ s,
+                                                                   const float* __restrict__ bias, int64_t n,
+                                                                   int64_t k, float* __restrict__ y) {
     const int64_t out = static_cast<int64_t>(blockIdx.x) * kGenWaves + threadIdx.x / kWave;
     if (out >= m * n) return;  // wave-uniform
     const int lane = threadIdx.x & (kWave - 1);
     const int64_t i = out / n, j = out % n;
     const float* xr = x + i * k;
-    const int8_t* qr = q + j * k;
+    const Code* qr = q + j * k;
     float acc = 0.f;
-    for (int64_t p = lane; p < k; p += kWave) acc += xr[p] * static_cast<float>(qr[p]);
+    for (int64_t p = lane; p < k; p += kWave) acc += xr[p] * code_value(qr[p]);
     acc = wave_sum(acc);
     if (lane == 0) y[out] = acc * s[j] + (bias ? bias[j] : 0.f);
 }
@@ -109,8 +114,7 @@ __global__ __launch_bounds__(kGenBlock) void k_gemm_fp8_generic(const uint8_t* _
     const uint8_t* wr = qw + j * k;
     float acc = 0.f;
     for (int64_t p = lane; p < k; p += kWave)
-        acc += __builtin_amdgcn_cvt_f32_fp8(static_cast<int>(ar[p]), 0) *
-               __builtin_amdgcn_cvt_f32_fp8(static_cast<int>(wr[p]), 0);
+        acc += code_value(ar[p]) * code_value(wr[p]);
     acc = wave_sum(acc);
     if (lane == 0) y[out] = acc * sa[i] * sw[j] + (bias ? bias[j] : 0.f);
 }
@@ -119,12 +123,20 @@ unsigned generic_grid(int64_t outputs) { return static_cast<unsigned>((outputs +
 
 }  // namespace
 
-int launch_linear_w8_generic(const float* x, int64_t m, const int8_t* q, const float* s, const float* bias,
-                             int64_t n, int64_t k, float* y, hipStream_t st) {
+int launch_linear_8bit_generic(const float* x, int64_t m, const int8_t* q, const float* s, const float* bias,
+                               int64_t n, int64_t k, float* y, hipStream_t st) {
     if (m == 0 || n == 0) return TQ_OK;
     TQ_REQUIRE(m * n / kGenWaves < (int64_t(1) << 31), "linear (generic): too many outputs");
-    k_linear_w8_generic<<<generic_grid(m * n), kGenBlock, 0, st>>>(x, m, q, s, bias, n, k, y);
+    k_linear_8bit_generic<int8_t><<<generic_grid(m * n), kGenBlock, 0, st>>>(x, m, q, s, bias, n, k, y);
     return check_launch("linear_w8 (generic)");
+}
+
+int launch_linear_8bit_generic(const float* x, int64_t m, const uint8_t* q, const float* s, const float* bias,
+                               int64_t n, int64_t k, float* y, hipStream_t st) {
+    if (m == 0 || n == 0) return TQ_OK;
+    TQ_REQUIRE(m * n / kGenWaves < (int64_t(1) << 31), "linear (generic): too many outputs");
+    k_linear_8bit_generic<uint8_t><<<generic_grid(m * n), kGenBlock, 0, st>>>(x, m, q, s, bias, n, k, y);
+    return check_launch("linear_fp8 (generic)");
 }
 
 int launch_linear_w4_generic(const uint16_t* x, int64_t m, const uint8_t* packed, const uint16_t* s16,

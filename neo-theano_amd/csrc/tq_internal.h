@@ -41,8 +41,10 @@ int device_cu_count();
 
 // Shape-general fallbacks of the matmul entry points (tq_generic.hip); any N,
 // K (K % 128 == 0 for INT4 g128), element-aligned pointers.
-int launch_linear_w8_generic(const float* x, int64_t m, const int8_t* q, const float* s, const float* bias,
-                             int64_t n, int64_t k, float* y, hipStream_t st);
+int launch_linear_8bit_generic(const float* x, int64_t m, const int8_t* q, const float* s, const float* bias,
+                               int64_t n, int64_t k, float* y, hipStream_t st);
+int launch_linear_8bit_generic(const float* x, int64_t m, const uint8_t* q, const float* s, const float* bias,
+                               int64_t n, int64_t k, float* y, hipStream_t st);
 int launch_linear_w4_generic(const uint16_t* x, int64_t m, const uint8_t* packed, const uint16_t* s16,
                              const float* bias, int64_t n, int64_t k, float* y, hipStream_t st);
 int launch_gemm_w8a8_generic(const int8_t* qa, const float* sa, const int8_t* qw, const float* sw,

@@ -529,7 +529,7 @@ Result<QuantizedLinear> QuantizedLinear::from_tensors(const Tensor& weight, cons
             l.out_ = l.w8_.rows;
             l.in_ = l.w8_.cols;
         } else if (qconfig.weight_dtype == QuantDType::FP8) {
-            l.mode_ = Mode::FP8;
+            l.mode_ = qconfig.activation_dtype == QuantDType::FP8 ? Mode::FP8 : Mode::FP8Weight;
             auto r = quantize::quantize_per_channel_fp8(weight, stream);
             if (r.is_err()) return r.unwrap_err();
             l.fp8_ = std::move(r).unwrap();
@@ -553,6 +553,7 @@ Result<QuantizedLinear> QuantizedLinear::from_tensors(const Tensor& weight, cons
 }
 
 size_t QuantizedLinear::workspace_bytes(int64_t m) const {
+    if (mode_ == Mode::FP8 && m <= 16) return static_cast<size_t>(m) * in_ * sizeof(float);
     if (mode_ != Mode::W4 || m <= 16) return 0;
     return static_cast<size_t>(tq_gemm_w4g128_bf16_workspace_bytes(m, static_cast<int64_t>(in_)));
 }
@@ -599,9 +600,27 @@ Result<void> QuantizedLinear::forward_device(const void* x, int64_t m, float* y,
             if (!act_codes || !act_scales)
                 return TheanoError::invalid_argument("QuantizedLinear::forward_device: fp8 needs activation scratch");
             auto* qa = reinterpret_cast<uint8_t*>(act_codes);
-            st = tq_quantize_fp8_rowwise(static_cast<const float*>(x), m, k, qa, act_scales, ts);
-            if (st == TQ_OK)
-                st = tq_gemm_fp8(qa, act_scales, fp8_.codes.data(), fp8_.scales.data(), b, m, n, k, y, ts);
+            if (m > 16) {
+                st = tq_quantize_fp8_rowwise(static_cast<const float*>(x), m, k, qa, act_scales, ts);
+                if (st == TQ_OK)
+                    st = tq_gemm_fp8(qa, act_scales, fp8_.codes.data(), fp8_.scales.data(), b, m, n, k, y, ts);
+                break;
+            }
+            // decode: the GEMV over x_hat = e4m3(qa) * sa, the GEMM's activation values
+            if (!workspace || workspace_bytes < this->workspace_bytes(m))
+                return TheanoError::invalid_argument(
+                    "QuantizedLinear::forward_device: fp8 with m <= 16 needs workspace_bytes(m) of workspace");
+            auto* xq = static_cast<float*>(workspace);
+            st = tq_fake_quantize_fp8_rowwise(static_cast<const float*>(x), m, k, qa, act_scales, xq, ts);
+            if (st == TQ_OK) st = tq_gemv_fp8(xq, m, fp8_.codes.data(), fp8_.scales.data(), b, n, k, y, ts);
+            break;
+        }
+        case Mode::FP8Weight: {
+            const auto* xf = static_cast<const float*>(x);
+            for (int64_t m0 = 0; m0 < m && st == TQ_OK; m0 += 16) {
+                const int64_t mm = std::min<int64_t>(16, m - m0);
+                st = tq_gemv_fp8(xf + m0 * k, mm, fp8_.codes.data(), fp8_.scales.data(), b, n, k, y + m0 * n, ts);
+            }
             break;
         }
     }
@@ -631,7 +650,10 @@ Result<Tensor> QuantizedLinear::try_forward(const Tensor& input) const {
             if (mode_ == Mode::W8A8 || mode_ == Mode::FP8) {
                 DeviceBuffer<int8_t> qa(m * in_);
                 DeviceBuffer<float> sa(m);
-                r = forward_device(xd.data(), static_cast<int64_t>(m), y.data(), stream_, qa.data(), sa.data());
+                const size_t wsb = workspace_bytes(static_cast<int64_t>(m));
+                DeviceBuffer<uint8_t> ws(std::max<size_t>(wsb, 1));
+                r = forward_device(xd.data(), static_cast<int64_t>(m), y.data(), stream_, qa.data(), sa.data(),
+                                   wsb ? ws.data() : nullptr, wsb);
                 if (r.is_ok()) check_hip(hipStreamSynchronize(stream_), "QuantizedLinear::forward");
             } else {
                 r = forward_device(xd.data(), static_cast<int64_t>(m), y.data(), stream_);
@@ -664,7 +686,7 @@ std::vector<std::pair<std::string, Tensor>> QuantizedLinear::named_parameters() 
         }
         out.emplace_back("weight", Tensor::from_slice(std::move(codes), {out_, in_}));
         out.emplace_back("weight_scale", Tensor::from_slice(std::move(sc), {out_, in_ / 128}));
-    } else if (mode_ == Mode::FP8) {
+    } else if (mode_ == Mode::FP8 || mode_ == Mode::FP8Weight) {
         const auto q = fp8_.codes.to_host(stream_);
         const auto s = fp8_.scales.to_host(stream_);
         std::vector<double> codes(q.size());
@@ -836,8 +858,8 @@ Result<void> QuantizedLinear::save(SafeTensorsFile& f, const std::string& name) 
             f.metadata[name + ".quant"] = "int4_g128";
             f.metadata[name + ".group_size"] = "128";
             put_int4(f, name, w4_, stream_);
-        } else if (mode_ == Mode::FP8) {
-            f.metadata[name + ".quant"] = "fp8_e4m3_per_channel";
+        } else if (mode_ == Mode::FP8 || mode_ == Mode::FP8Weight) {
+            f.metadata[name + ".quant"] = mode_ == Mode::FP8 ? "fp8_e4m3_per_channel_a8" : "fp8_e4m3_per_channel";
             put(f, name + ".weight", "F8_E4M3", {out_, in_}, bytes_of(fp8_.codes, stream_));
             put(f, name + ".weight_scale", "F32", {out_}, bytes_of(fp8_.scales, stream_));
         } else {
@@ -871,8 +893,8 @@ Result<QuantizedLinear> QuantizedLinear::load(const SafeTensorsFile& f, const st
             l.w8_.cols = l.in_;
             l.w8_.codes = device_of<int8_t>(get<int8_t>(f, name + ".weight", "I8", {l.out_, l.in_}), stream);
             l.w8_.scales = device_of<float>(get<float>(f, name + ".weight_scale", "F32", {l.out_}), stream);
-        } else if (q == "fp8_e4m3_per_channel") {
-            l.mode_ = Mode::FP8;
+        } else if (q == "fp8_e4m3_per_channel" || q == "fp8_e4m3_per_channel_a8") {
+            l.mode_ = q == "fp8_e4m3_per_channel" ? Mode::FP8Weight : Mode::FP8;
             l.fp8_.rows = l.out_;
             l.fp8_.cols = l.in_;
             l.fp8_.codes = device_of<uint8_t>(get<uint8_t>(f, name + ".weight", "F8_E4M3", {l.out_, l.in_}), stream);

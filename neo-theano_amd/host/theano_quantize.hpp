@@ -321,10 +321,11 @@ class Module {
 //   weight Int8, activations not Int8 -> "w8":   INT8 weight-only, f32 activations
 //   weight Int8, activations Int8     -> "w8a8": per-row dynamic INT8 activations
 //   weight Int4                       -> "w4":   INT4 g128 weight-only, bf16 activations
-//   weight FP8                        -> "fp8":  FP8 e4m3 weights, per-row dynamic FP8 activations
+//   weight FP8, activations FP8       -> "fp8":  FP8 e4m3 weights, per-row dynamic FP8 activations
+//   weight FP8, activations not FP8   -> "fp8_weight": FP8 e4m3 weight-only, f32 activations
 class QuantizedLinear : public Module {
    public:
-    enum class Mode { W8, W8A8, W4, FP8 };
+    enum class Mode { W8, W8A8, W4, FP8, FP8Weight };
     static Result<QuantizedLinear> from_tensors(const Tensor& weight, const std::optional<Tensor>& bias,
                                                 const quantize::QConfig& qconfig = quantize::QConfig::default_int8(),
                                                 hipStream_t stream = nullptr);
@@ -335,12 +336,14 @@ class QuantizedLinear : public Module {
     // Device-resident forward: x is f32 [m, in] (w8, w8a8, fp8) or bf16 bits [m, in]
     // (w4), y is f32 [m, out]; enqueued on `stream`, no host synchronisation.  w8a8
     // and fp8 need `act_codes` (one byte per element, [m, in]) and `act_scales`
-    // (f32 [m]) device scratch;
+    // (f32 [m]) device scratch; fp8 with m <= 16 runs the GEMV on the
+    // fake-quantized activations, held in `workspace` (workspace_bytes(m) bytes);
     // w4 with m > 16 uses `workspace` (workspace_bytes(m) bytes) when given.
     Result<void> forward_device(const void* x, int64_t m, float* y, hipStream_t stream,
                                 int8_t* act_codes = nullptr, float* act_scales = nullptr,
                                 void* workspace = nullptr, size_t workspace_bytes = 0) const;
-    // device scratch of the w4 prefill path for m tokens (0 for other modes / m <= 16)
+    // device scratch for m tokens: the w4 prefill path (m > 16) and the fp8
+    // decode path (m <= 16); 0 otherwise
     size_t workspace_bytes(int64_t m) const;
     // Quantized checkpoint entries under `name` (layout in theano_serialize.hpp):
     // codes and scales as stored on the device, loaded back without re-quantizing.

@@ -73,7 +73,7 @@ Result<std::map<std::string, Tensor>> load_safetensors(const std::vector<uint8_t
 //   <name>.weight_scale  F32 [N]   | F16 [N, K/128] (INT4)
 //   <name>.bias          F32 [N]   (optional)
 //   metadata <name>.quant = int8_per_channel | int8_per_channel_a8 | int4_g128
-//   | fp8_e4m3_per_channel,
+//   | fp8_e4m3_per_channel (FP8 weight-only) | fp8_e4m3_per_channel_a8 (FP8 W8A8),
 //   <name>.group_size = 128 (INT4), <name>.in_features, <name>.out_features;
 //   a QuantizedMLP <name>: <name>.{gate,up,down}.{weight,weight_scale},
 //   <name>.quant = mlp_int4_g128, <name>.hidden, <name>.intermediate;

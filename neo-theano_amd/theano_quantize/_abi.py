@@ -50,6 +50,7 @@ SIGNATURES = {
     "tq_quantize_i4_g128": [_p, _i64, _i64, _p, _p, _p],
     "tq_dequantize_i4_g128": [_p, _p, _i64, _i64, _p, _p],
     "tq_gemv_w8": [_p, _i64, _p, _p, _p, _i64, _i64, _p, _p],
+    "tq_gemv_fp8": [_p, _i64, _p, _p, _p, _i64, _i64, _p, _p],
     "tq_gemv_w4g128": [_p, _i64, _p, _p, _p, _i64, _i64, _p, _p],
     "tq_w4g128_tile_rows": [_i64],
     "tq_repack_w4g128_tiled": [_p, _p, _i64, _i64, _i64, _p, _p, _p],

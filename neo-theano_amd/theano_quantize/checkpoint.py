@@ -27,7 +27,8 @@ becomes
     <name>.weight_scale  F32 [N]      | F16 [N, K/128] (INT4)
     <name>.bias          F32 [N]      (when present)
 with ``__metadata__`` entries ``<name>.quant`` ("int8_per_channel",
-"int8_per_channel_a8" for W8A8, "int4_g128", or "fp8_e4m3_per_channel"),
+"int8_per_channel_a8" for W8A8, "int4_g128", "fp8_e4m3_per_channel" (FP8
+weight-only) or "fp8_e4m3_per_channel_a8" (FP8 weights and activations)),
 ``<name>.group_size`` ("128",
 INT4), ``<name>.in_features`` and
 ``<name>.out_features``; a ``QuantizedMLP`` ``<name>`` is the three INT4
@@ -160,15 +161,16 @@ def _linear_entries(name, lin, tensors, meta):
         meta[f"{name}.group_size"] = "128"
     elif lin.mode in ("w8", "w8a8"):
         meta[f"{name}.quant"] = "int8_per_channel" if lin.mode == "w8" else "int8_per_channel_a8"
-    elif lin.mode == "fp8":
-        meta[f"{name}.quant"] = "fp8_e4m3_per_channel"
+    elif lin.mode in ("fp8", "fp8_weight"):
+        meta[f"{name}.quant"] = "fp8_e4m3_per_channel_a8" if lin.mode == "fp8" else "fp8_e4m3_per_channel"
     else:
         raise InvalidArgument(f"save_quantized: '{name}' has mode {lin.mode!r}")
     meta[f"{name}.in_features"] = str(lin.in_features)
     meta[f"{name}.out_features"] = str(lin.out_features)
     import torch
 
-    tensors[f"{name}.weight"] = lin.qweight.view(torch.float8_e4m3fn) if lin.mode == "fp8" else lin.qweight
+    fp8 = lin.mode in ("fp8", "fp8_weight")
+    tensors[f"{name}.weight"] = lin.qweight.view(torch.float8_e4m3fn) if fp8 else lin.qweight
     tensors[f"{name}.weight_scale"] = lin.scales
     if lin.bias is not None:
         tensors[f"{name}.bias"] = lin.bias
@@ -239,12 +241,12 @@ def load_quantized(data: bytes, device="cuda"):
             s = dev(_need(tensors, f"{name}.weight_scale", np.float16, (n, k // 128)).view(np.int16))
             s = s.view(torch.float16)
             mode = "w4"
-        elif kind == "fp8_e4m3_per_channel":
+        elif kind in ("fp8_e4m3_per_channel", "fp8_e4m3_per_channel_a8"):
             if dtypes.get(f"{name}.weight") != "F8_E4M3":
                 raise InvalidArgument(f"load_quantized: '{name}.weight' is not F8_E4M3")
             q = dev(_need(tensors, f"{name}.weight", np.uint8, (n, k)))
             s = dev(_need(tensors, f"{name}.weight_scale", np.float32, (n,)))
-            mode = "fp8"
+            mode = "fp8" if kind.endswith("_a8") else "fp8_weight"
         elif kind in ("int8_per_channel", "int8_per_channel_a8"):
             q = dev(_need(tensors, f"{name}.weight", np.int8, (n, k)))
             s = dev(_need(tensors, f"{name}.weight_scale", np.float32, (n,)))

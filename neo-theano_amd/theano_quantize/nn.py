@@ -14,9 +14,12 @@ Modes (chosen from the QConfig):
   * "w4"   weight-only INT4 group-128, bf16 activations
            (QConfig.default_int4());
   * "fp8"  FP8 e4m3 weights per output channel and per-row dynamic FP8
-           activations (QConfig with weight_dtype FP8).
-Decode shapes (M <= 16 tokens) run the dequant-GEMV kernels; prefill shapes run
-the i8-MFMA W8A8 GEMM or the bf16-MFMA W4A16 GEMM; FP8 runs the FP8-MFMA GEMM.
+           activations (QConfig with weight_dtype and activation_dtype FP8);
+  * "fp8_weight"  FP8 e4m3 weight-only, f32 activations (weight_dtype FP8,
+           activations not FP8).
+Decode shapes (M <= 16 tokens) run the dequant-GEMV kernels (in "fp8" mode on
+the fake-quantized activations, the same product as the GEMM); prefill shapes
+run the i8-MFMA W8A8 GEMM, the fp8-MFMA GEMM or the bf16-MFMA W4A16 GEMM.
 """
 from __future__ import annotations
 
@@ -60,7 +63,7 @@ def _mode_of(qconfig: QConfig) -> str:
     if qconfig.weight_dtype == QuantDType.Int8:
         return "w8a8" if qconfig.activation_dtype == QuantDType.Int8 else "w8"
     if qconfig.weight_dtype == QuantDType.FP8:
-        return "fp8"
+        return "fp8" if qconfig.activation_dtype == QuantDType.FP8 else "fp8_weight"
     raise InvalidArgument(f"QuantizedLinear: unsupported weight dtype {qconfig.weight_dtype!r}")
 
 
@@ -90,7 +93,7 @@ class QuantizedLinear(Module):
         out_f, in_f = w.shape
         if mode == "w4":
             q, s = quantize_i4_g128(w)
-        elif mode == "fp8":
+        elif mode in ("fp8", "fp8_weight"):
             q, s = quantize_per_channel_fp8(w)
         else:
             q, s = quantize_per_channel_i8(w)
@@ -140,12 +143,23 @@ class QuantizedLinear(Module):
                 mm = min(DECODE_MAX_M, m - m0)
                 _abi.call("tq_gemv_w8", ptr(x[m0:m0 + mm]), mm, ptr(self.qweight), ptr(self.scales),
                           ptr(self.bias), n, k, ptr(y[m0:m0 + mm]), stream())
-        elif self.mode == "fp8":
+        elif self.mode == "fp8" and m > DECODE_MAX_M:
             qa = torch.empty((m, k), dtype=torch.uint8, device=x.device)
             sa = torch.empty(m, dtype=torch.float32, device=x.device)
             _abi.call("tq_quantize_fp8_rowwise", ptr(x), m, k, ptr(qa), ptr(sa), stream())
             _abi.call("tq_gemm_fp8", ptr(qa), ptr(sa), ptr(self.qweight), ptr(self.scales),
                       ptr(self.bias), m, n, k, ptr(y), stream())
+        elif self.mode in ("fp8", "fp8_weight"):
+            if self.mode == "fp8":  # x -> e4m3(qa) * sa, the GEMM's activation values
+                qa = torch.empty((m, k), dtype=torch.uint8, device=x.device)
+                sa = torch.empty(m, dtype=torch.float32, device=x.device)
+                xq = torch.empty_like(x)
+                _abi.call("tq_fake_quantize_fp8_rowwise", ptr(x), m, k, ptr(qa), ptr(sa), ptr(xq), stream())
+                x = xq
+            for m0 in range(0, m, DECODE_MAX_M):
+                mm = min(DECODE_MAX_M, m - m0)
+                _abi.call("tq_gemv_fp8", ptr(x[m0:m0 + mm]), mm, ptr(self.qweight), ptr(self.scales),
+                          ptr(self.bias), n, k, ptr(y[m0:m0 + mm]), stream())
         else:
             qa = torch.empty((m, k), dtype=torch.int8, device=x.device)
             sa = torch.empty(m, dtype=torch.float32, device=x.device)

@@ -484,21 +484,42 @@ TEST_GPU(test_parity_quantized_linear_w8a8) {
 }
 
 TEST_GPU(test_parity_quantized_linear_fp8) {
-    const size_t n = 272, k = 1024, m = 37;
-    const auto wv = randn(n * k, 0.02, 53), xv = randn(m * k, 1.0, 54), bv = randn(n, 0.1, 55);
+    const size_t n = 272, k = 1024;
+    const auto wv = randn(n * k, 0.02, 53), bv = randn(n, 0.1, 55);
     const QConfig cfg{QuantDType::FP8, QuantDType::FP8, true, true};
     const QuantizedLinear layer =
         QuantizedLinear::from_tensors(Tensor::from_slice(wv, {n, k}), Tensor::from_slice(bv, {n}), cfg).unwrap();
     ASSERT(layer.mode() == QuantizedLinear::Mode::FP8);
-    const auto y = layer.forward(Tensor::from_slice(xv, {m, k})).to_vec_f64().unwrap();
-    const auto w32 = f32(wv), x32 = f32(xv), b32 = f32(bv);
-    std::vector<uint8_t> qw(n * k), qa(m * k);
-    std::vector<float> sw(n), sa(m);
+    const auto w32 = f32(wv), b32 = f32(bv);
+    std::vector<uint8_t> qw(n * k);
+    std::vector<float> sw(n);
     tqo_quantize_fp8_rowwise(w32.data(), n, k, qw.data(), sw.data());
-    tqo_quantize_fp8_rowwise(x32.data(), m, k, qa.data(), sa.data());
-    std::vector<double> ref(m * n);
-    tqo_linear_fp8(qa.data(), sa.data(), qw.data(), sw.data(), b32.data(), m, n, k, ref.data());
-    assert_close(y, ref, "fp8 linear");
+    for (size_t m : {3u, 37u}) {  // decode GEMV and prefill GEMM
+        const auto xv = randn(m * k, 1.0, 54 + m);
+        const auto y = layer.forward(Tensor::from_slice(xv, {m, k})).to_vec_f64().unwrap();
+        const auto x32 = f32(xv);
+        std::vector<uint8_t> qa(m * k);
+        std::vector<float> sa(m);
+        tqo_quantize_fp8_rowwise(x32.data(), m, k, qa.data(), sa.data());
+        std::vector<double> ref(m * n);
+        tqo_linear_fp8(qa.data(), sa.data(), qw.data(), sw.data(), b32.data(), m, n, k, ref.data());
+        assert_close(y, ref, "fp8 linear");
+    }
+    // weight-only: f32 activations against Linear over the dequantized weight
+    const QuantizedLinear wo =
+        QuantizedLinear::from_tensors(Tensor::from_slice(wv, {n, k}), std::nullopt,
+                                      QConfig{QuantDType::FP8, QuantDType::UInt8, true, true})
+            .unwrap();
+    ASSERT(wo.mode() == QuantizedLinear::Mode::FP8Weight);
+    const size_t m = 20;
+    const auto xv = randn(m * k, 1.0, 56);
+    const auto y = wo.forward(Tensor::from_slice(xv, {m, k})).to_vec_f64().unwrap();
+    std::vector<float> wh(n * k);
+    tqo_dequantize_fp8_rowwise(qw.data(), sw.data(), n, k, wh.data());
+    std::vector<double> x64(m * k), w64(wh.begin(), wh.end()), ref(m * n);
+    for (size_t i = 0; i < x64.size(); ++i) x64[i] = static_cast<float>(xv[i]);
+    tqo_linear(x64.data(), m, w64.data(), nullptr, n, k, ref.data());
+    assert_close(y, ref, "fp8 weight-only linear");
 }
 
 TEST_GPU(test_parity_quantized_mlp) {
@@ -689,8 +710,12 @@ TEST_GPU(test_checkpoint_linear_and_mlp_roundtrip) {
     const auto wv = randn(n * k, 0.02, 91), bv = randn(n, 0.1, 92);
     const QConfig a8{QuantDType::Int8, QuantDType::Int8, true, true};
     const QConfig fp8{QuantDType::FP8, QuantDType::FP8, true, true};
-    const std::vector<std::pair<std::string, QConfig>> cfgs = {
-        {"l4", QConfig::default_int4()}, {"l8", QConfig::default_int8()}, {"l8a8", a8}, {"lfp8", fp8}};
+    const QConfig fp8w{QuantDType::FP8, QuantDType::Int8, true, true};
+    const std::vector<std::pair<std::string, QConfig>> cfgs = {{"l4", QConfig::default_int4()},
+                                                              {"l8", QConfig::default_int8()},
+                                                              {"l8a8", a8},
+                                                              {"lfp8", fp8},
+                                                              {"lfp8w", fp8w}};
     ser::SafeTensorsFile file;
     std::vector<QuantizedLinear> layers;
     for (const auto& [name, cfg] : cfgs) {

@@ -51,13 +51,15 @@ def test_linear_and_mlp_roundtrip(tq):
                                                                            True, True)),
         "lfp8": tq.QuantizedLinear.from_tensors(dev(w), dev(b), tq.QConfig(tq.QuantDType.FP8, tq.QuantDType.FP8,
                                                                             True, True)),
+        "lfp8w": tq.QuantizedLinear.from_tensors(dev(w), None, tq.QConfig(tq.QuantDType.FP8, tq.QuantDType.UInt8,
+                                                                           True, True)),
         "mlp": tq.QuantizedMLP.from_tensors(dev(normal(82, (512, 256), 0.02)), dev(normal(82, (512, 256), 0.02, 1)),
                                             dev(normal(82, (256, 512), 0.02, 2))),
     }
     blob = tq.save_quantized(mods)
     back = tq.load_quantized(blob)
     assert set(back) == set(mods)
-    for name in ("l4", "l8", "l8a8", "lfp8"):
+    for name in ("l4", "l8", "l8a8", "lfp8", "lfp8w"):
         a, c = mods[name], back[name]
         assert (c.mode, c.in_features, c.out_features) == (a.mode, a.in_features, a.out_features)
         assert torch.equal(a.qweight, c.qweight) and torch.equal(a.scales.view(torch.int16) if a.scales.dtype ==

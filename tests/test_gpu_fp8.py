@@ -181,3 +181,48 @@ def test_quantized_linear_fp8_module(tq, oracle):
     rqa, rsa = oracle.quantize_fp8_rowwise(x)
     rqw, rsw = oracle.quantize_fp8_rowwise(w)
     assert_close(y, oracle.linear_fp8(rqa, rsa, rqw, rsw), RTOL, ATOL, "QuantizedLinear fp8")
+
+
+# ------------------------------------------------------------------- GEMV
+@pytest.mark.parametrize("m,n,k", [(1, 14336, 4096), (4, 4096, 4096), (16, 512, 1024), (3, 300, 8192),
+                                   (2, 64, 2048), (5, 33, 100), (1, 16, 16)])
+def test_gemv_fp8_shapes_bias(tq, oracle, m, n, k):
+    """Weight-only FP8 decode GEMV: y = x . dequant(W)^T + b with f32 x."""
+    import torch
+    from theano_quantize import _abi
+    from theano_quantize._tensor import ptr, stream
+
+    w = normal(78, (n, k), 0.02)
+    x = normal(78, (m, k), 1.0, stream=1)
+    b = normal(78, (n,), 0.1, stream=2)
+    q, s = tq.quantize_per_channel_fp8(dev_tensor(w))
+    y = torch.empty((m, n), dtype=torch.float32, device="cuda")
+    xd, bd = dev_tensor(x), dev_tensor(b)  # held until the kernel has run
+    _abi.call("tq_gemv_fp8", ptr(xd), m, ptr(q), ptr(s), ptr(bd), n, k, ptr(y), stream())
+    rq, rs = oracle.quantize_fp8_rowwise(w)
+    assert np.array_equal(host(q), rq)
+    ref = oracle.linear(x.astype(np.float64), oracle.dequantize_fp8_rowwise(rq, rs).astype(np.float64), b)
+    assert_close(host(y), ref, RTOL, ATOL, f"gemv_fp8 {m}x{n}x{k}")
+
+
+@pytest.mark.parametrize("m", [1, 3, 16, 17, 40])
+def test_quantized_linear_fp8_decode_and_weight_only(tq, oracle, m):
+    """fp8 mode at decode sizes (GEMV on the fake-quantized activations) and above
+    (GEMM) give the FP8 W8A8 product; fp8_weight mode gives Linear over the
+    dequantized weight with f32 activations."""
+    from theano_quantize import QConfig, QuantDType
+
+    n, k = 384, 1024
+    w = normal(79, (n, k), 0.02)
+    x = normal(79, (m, k), 1.0, stream=1)
+    b = normal(79, (n,), 0.1, stream=2)
+    rqw, rsw = oracle.quantize_fp8_rowwise(w)
+    rqa, rsa = oracle.quantize_fp8_rowwise(x)
+    lin = tq.QuantizedLinear.from_tensors(dev_tensor(w), dev_tensor(b), QConfig(QuantDType.FP8, QuantDType.FP8, True,
+                                                                                 True))
+    assert_close(host(lin(dev_tensor(x))), oracle.linear_fp8(rqa, rsa, rqw, rsw, b), RTOL, ATOL, "fp8 mode")
+    wo = tq.QuantizedLinear.from_tensors(dev_tensor(w), dev_tensor(b), QConfig(QuantDType.FP8, QuantDType.UInt8,
+                                                                                True, True))
+    assert wo.mode == "fp8_weight"
+    ref = oracle.linear(x.astype(np.float64), oracle.dequantize_fp8_rowwise(rqw, rsw).astype(np.float64), b)
+    assert_close(host(wo(dev_tensor(x))), ref, RTOL, ATOL, "fp8_weight mode")

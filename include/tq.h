@@ -50,6 +50,21 @@ typedef enum {
     TQ_ENOMEM = 3,  /* device allocation failure (host-side helpers only) */
 } tq_status;
 
+/* DType of a device buffer: crates/theano-types/src/dtype.rs:5-25 (same order;
+ * complex and quantized variants have no element conversion here). */
+typedef enum {
+    TQ_DT_F16 = 0,
+    TQ_DT_BF16 = 1,
+    TQ_DT_F32 = 2,
+    TQ_DT_F64 = 3,
+    TQ_DT_U8 = 4,
+    TQ_DT_I8 = 5,
+    TQ_DT_I16 = 6,
+    TQ_DT_I32 = 7,
+    TQ_DT_I64 = 8,
+    TQ_DT_BOOL = 9,
+} tq_dtype;
+
 /* QuantDType: crates/theano-quantize/src/qconfig.rs:5-10 (same order) */
 typedef enum {
     TQ_QINT8 = 0,
@@ -282,6 +297,20 @@ int tq_mlp_w4g128(const uint16_t* x_bf16, int64_t m, int64_t d, int64_t f,
                   const uint8_t* up_packed, const uint16_t* up_s,
                   const uint8_t* down_packed, const uint16_t* down_s,
                   void* workspace, int64_t workspace_bytes, float* y, tq_stream_t stream);
+
+/* ------------------------------------------------------------------------
+ * Element type conversion of device buffers: the device half of Tensor::to
+ * (crates/theano-core/src/tensor.rs:277-299) and of RocmStorage::from_host_f64
+ * / to_host_f64 (crates/theano-rocm/src/storage.rs:54-99), whose tensors hold
+ * f64 values in a buffer of their DType.
+ * dst[i] = cast(f64(src[i])): F32/F16/BF16 round to nearest even from the f64
+ * value (overflow -> inf, NaN stays NaN); integer types follow Rust's
+ * `f64 as T` (toward zero, saturating, NaN -> 0); Bool is value != 0.
+ * src and dst must not overlap and are aligned to their element sizes.
+ * ------------------------------------------------------------------------ */
+int64_t tq_dtype_size(int dtype); /* bytes per element, 0 if unsupported */
+int tq_convert(const void* src, int src_dtype, void* dst, int dst_dtype, int64_t n,
+               tq_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -9,6 +9,7 @@ quantize_per_channel_fp8 (OCP e4m3),
 QuantizedLinear, QuantizedMLP; quantized checkpoints (save_quantized /
 load_quantized over the safetensors container of crates/theano-serialize).
 """
+from ._tensor import convert
 from .checkpoint import load_quantized, load_safetensors, save_quantized, save_safetensors
 from .errors import InvalidArgument, KernelError, OutOfMemory, TheanoError
 from .formats import (
@@ -35,5 +36,5 @@ __all__ = [
     "quantize_per_channel_i8", "dequantize_per_channel_i8", "fake_quantize_per_channel_i8",
     "quantize_per_channel_fp8", "dequantize_per_channel_fp8", "fake_quantize_per_channel_fp8",
     "quantize_i4_g128", "dequantize_i4_g128", "repack_i4_g128_tiled", "tile_rows_for", "Module", "QuantizedLinear", "QuantizedMLP",
-    "save_safetensors", "load_safetensors", "save_quantized", "load_quantized",
+    "save_safetensors", "load_safetensors", "save_quantized", "load_quantized", "convert",
 ]

@@ -57,6 +57,8 @@ SIGNATURES = {
     "tq_gemv_w4g128_tiled": [_p, _i64, _p, _p, _p, _i64, _i64, _i64, _p, _p],
     "tq_gemm_w8a8": [_p, _p, _p, _p, _p, _i64, _i64, _i64, _p, _p, _p],
     "tq_gemm_fp8": [_p, _p, _p, _p, _p, _i64, _i64, _i64, _p, _p],
+    "tq_dtype_size": [_int],
+    "tq_convert": [_p, _int, _p, _int, _i64, _p],
     "tq_gemm_w4g128_bf16": [_p, _i64, _p, _p, _p, _i64, _i64, _p, _p],
     "tq_gemm_w4g128_bf16_workspace_bytes": [_i64, _i64],
     "tq_gemm_w4g128_bf16_ws": [_p, _i64, _p, _p, _p, _i64, _i64, _p, _i64, _p, _p],
@@ -65,7 +67,7 @@ SIGNATURES = {
 }
 _RESTYPE = {"tq_status_string": ctypes.c_char_p, "tq_last_error": ctypes.c_char_p,
             "tq_w4g128_tile_rows": ctypes.c_int64, "tq_mlp_w4g128_workspace_bytes": ctypes.c_int64,
-            "tq_gemm_w4g128_bf16_workspace_bytes": ctypes.c_int64}
+            "tq_gemm_w4g128_bf16_workspace_bytes": ctypes.c_int64, "tq_dtype_size": ctypes.c_int64}
 
 _lib = None
 

@@ -60,6 +60,9 @@ def lib():
             "tqo_linear_w8a8": ([p, p, p, p, p, i64, i64, i64, p], None),
             "tqo_mlp_w4g128": ([p, i64, i64, i64, p, p, p, p, p, p, p], None),
             "tqo_e4m3_to_f64": ([ctypes.c_uint8], d),
+            "tqo_f64_to_bf16_bits": ([d], ctypes.c_uint16),
+            "tqo_dtype_size": ([ctypes.c_int], i64),
+            "tqo_convert": ([p, ctypes.c_int, p, ctypes.c_int, i64], None),
             "tqo_f32_to_e4m3": ([ctypes.c_float], ctypes.c_uint8),
             "tqo_quantize_fp8_rowwise": ([p, i64, i64, p, p], None),
             "tqo_dequantize_fp8_rowwise": ([p, p, i64, i64, p], None),
@@ -362,3 +365,21 @@ def linear_fp8(qa, sa, qw, sw, bias=None):
     y = np.empty((m, n))
     lib().tqo_linear_fp8(_ptr(qa), _ptr(sa), _ptr(qw), _ptr(sw), _ptr(b), m, n, k, _ptr(y))
     return y
+
+
+# ---- element conversion (DType order) ----
+DTYPES = ["float16", "bfloat16", "float32", "float64", "uint8", "int8", "int16", "int32", "int64", "bool"]
+NP_STORAGE = [np.uint16, np.uint16, np.float32, np.float64, np.uint8, np.int8, np.int16, np.int32, np.int64, np.uint8]
+
+
+def f64_to_bf16_bits(x):
+    return lib().tqo_f64_to_bf16_bits(float(x))
+
+
+def convert(src, src_t, dst_t):
+    """src: numpy array in the storage type of src_t (F16/BF16 as uint16 bits,
+    Bool as uint8) -> numpy array in the storage type of dst_t."""
+    src = _c(src, NP_STORAGE[src_t])
+    out = np.empty(src.shape, NP_STORAGE[dst_t])
+    lib().tqo_convert(_ptr(src), src_t, _ptr(out), dst_t, src.size)
+    return out

@@ -475,3 +475,82 @@ void tqo_linear_fp8(const uint8_t* qa, const float* sa, const uint8_t* qw, const
     free(w);
     free(a);
 }
+
+/* ---- element type conversion (build-defined; the reference keeps f64 values
+ * and a DType, crates/theano-types/src/dtype.rs:5-25, tensor.rs:277-299) ----
+ * Type codes follow DType's order: F16 BF16 F32 F64 U8 I8 I16 I32 I64 Bool. */
+uint16_t tqo_f64_to_bf16_bits(double x) {
+    const uint16_t sign = signbit(x) ? 0x8000u : 0u;
+    if (x != x) return (uint16_t)(sign | 0x7FC0u);
+    const double a = fabs(x);
+    /* largest finite bf16 is (2 - 2^-7) 2^127; half an ulp above rounds to inf */
+    if (a >= ldexp(2.0 - ldexp(1.0, -8), 127)) return (uint16_t)(sign | 0x7F80u);
+    if (a < 0x1p-126) { /* subnormal range, ulp 2^-133 */
+        const double m = nearbyint(ldexp(a, 133));
+        return (uint16_t)(sign | (uint16_t)m); /* m == 128 encodes 2^-126 */
+    }
+    int e2;
+    frexp(a, &e2);
+    int e = e2 - 1;
+    double m = nearbyint(ldexp(a, 7 - e));
+    if (m == 256.0) {
+        m = 128.0;
+        e += 1;
+    }
+    return (uint16_t)(sign | (uint16_t)((e + 127) << 7) | (uint16_t)(m - 128.0));
+}
+
+int64_t tqo_dtype_size(int t) {
+    static const int64_t sz[10] = {2, 2, 4, 8, 1, 1, 2, 4, 8, 1};
+    return (t >= 0 && t < 10) ? sz[t] : 0;
+}
+
+static double conv_get(const void* p, int t, int64_t i) {
+    switch (t) {
+        case 0: return tqo_f16_bits_to_f64(((const uint16_t*)p)[i]);
+        case 1: return tqo_bf16_bits_to_f64(((const uint16_t*)p)[i]);
+        case 2: return (double)((const float*)p)[i];
+        case 3: return ((const double*)p)[i];
+        case 4: return (double)((const uint8_t*)p)[i];
+        case 5: return (double)((const int8_t*)p)[i];
+        case 6: return (double)((const int16_t*)p)[i];
+        case 7: return (double)((const int32_t*)p)[i];
+        case 8: return (double)((const int64_t*)p)[i];
+        default: return ((const uint8_t*)p)[i] ? 1.0 : 0.0;
+    }
+}
+
+/* Rust `f64 as T` for an integer T with range [lo, hi]: toward zero,
+ * saturating, NaN -> 0 */
+static double rust_as(double x, double lo, double hi) {
+    if (x != x) return 0.0;
+    if (x <= lo) return lo;
+    if (x >= hi) return hi;
+    return trunc(x);
+}
+
+static void conv_put(void* p, int t, int64_t i, double v) {
+    switch (t) {
+        case 0: ((uint16_t*)p)[i] = tqo_f64_to_f16_bits(v); break;
+        case 1: ((uint16_t*)p)[i] = tqo_f64_to_bf16_bits(v); break;
+        case 2: ((float*)p)[i] = (float)v; break; /* C double -> float: IEEE RNE */
+        case 3: ((double*)p)[i] = v; break;
+        case 4: ((uint8_t*)p)[i] = (uint8_t)rust_as(v, 0.0, 255.0); break;
+        case 5: ((int8_t*)p)[i] = (int8_t)rust_as(v, -128.0, 127.0); break;
+        case 6: ((int16_t*)p)[i] = (int16_t)rust_as(v, -32768.0, 32767.0); break;
+        case 7: ((int32_t*)p)[i] = (int32_t)rust_as(v, -2147483648.0, 2147483647.0); break;
+        case 8: {
+            /* 2^63 is not an i64; every double below it truncates exactly */
+            if (v != v) ((int64_t*)p)[i] = 0;
+            else if (v >= 0x1p63) ((int64_t*)p)[i] = INT64_MAX;
+            else if (v <= -0x1p63) ((int64_t*)p)[i] = INT64_MIN;
+            else ((int64_t*)p)[i] = (int64_t)trunc(v);
+            break;
+        }
+        default: ((uint8_t*)p)[i] = (v != 0.0) ? 1u : 0u; break; /* NaN != 0 */
+    }
+}
+
+void tqo_convert(const void* src, int src_t, void* dst, int dst_t, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) conv_put(dst, dst_t, i, conv_get(src, src_t, i));
+}

@@ -29,6 +29,8 @@
  *   rowwise / g128 quant   exact-rational rounding (fractions.Fraction),
  *                          numpy float16 RNE, pack/unpack bijection
  *   w8a8 accumulators      numpy int64 matmul
+ *   conversions            numpy astype (f32, f16), exact rationals (bf16),
+ *                          closed forms for Rust `as` (saturation, NaN)
  *   e4m3 encode / decode   torch.float8_e4m3fn on all 256 codes and on every
  *                          midpoint / boundary / special value; rowwise FP8
  *                          quantize: exact-rational checks of the scale and
@@ -119,6 +121,12 @@ void tqo_dequantize_fp8_rowwise(const uint8_t* q, const float* s, int64_t rows, 
                                 float* w_hat);
 void tqo_linear_fp8(const uint8_t* qa, const float* sa, const uint8_t* qw, const float* sw,
                     const float* bias_or_null, int64_t m, int64_t n, int64_t k, double* y);
+
+/* build-defined element conversion (DType order F16 BF16 F32 F64 U8 I8 I16 I32
+ * I64 Bool): dst = cast(f64(src)), RNE for floats, Rust `as` for integers */
+uint16_t tqo_f64_to_bf16_bits(double x);
+int64_t tqo_dtype_size(int dtype);
+void tqo_convert(const void* src, int src_dtype, void* dst, int dst_dtype, int64_t n);
 
 /* build-defined quantized Llama FFN: y = (SiLU(x Wg^T) * (x Wu^T)) Wd^T */
 void tqo_mlp_w4g128(const uint16_t* x_bf16, int64_t m, int64_t d, int64_t f,

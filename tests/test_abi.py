@@ -99,6 +99,12 @@ def test_observer_scale_zp_matches_oracle(abi, oracle):
     ("tq_quantize_tensor", [None, 10, 1.0, 0.0, 7, None, None]),          # bad QuantDType
     ("tq_quantize_per_tensor", [None, 10, 0, None, None, None, None]),
     ("tq_minmax_reset", [None, 0, None]),
+    ("tq_convert", [None, 3, None, 12, 4, None]),                          # unsupported dtype
+    ("tq_convert", [None, 3, None, 2, -1, None]),                          # negative length
+    ("tq_convert", [None, 3, None, 2, 4, None]),                           # null pointers
+    ("tq_quantize_fp8_rowwise", [None, 4, 16, None, None, None]),         # null pointers
+    ("tq_gemm_fp8", [None, None, None, None, None, -1, 16, 128, None, None]),  # negative shape
+    ("tq_gemv_fp8", [None, 17, None, None, None, 16, 128, None, None]),   # M > 16
 ])
 def test_invalid_arguments_are_rejected(abi, call):
     from theano_quantize import InvalidArgument
@@ -121,8 +127,16 @@ def test_mlp_workspace_bytes(abi):
     assert ws(0, 128, 128) == 0
 
 
+def test_dtype_sizes(abi, oracle):
+    # DType::size_in_bytes (crates/theano-types/src/dtype.rs:33-40) in DType order
+    assert [abi.lib().tq_dtype_size(t) for t in range(10)] == [2, 2, 4, 8, 1, 1, 2, 4, 8, 1]
+    assert [abi.lib().tq_dtype_size(t) for t in range(10)] == [oracle.lib().tqo_dtype_size(t) for t in range(10)]
+    assert abi.lib().tq_dtype_size(10) == 0 and abi.lib().tq_dtype_size(-1) == 0
+
+
 def test_zero_sizes_are_noops(abi):
     # empty inputs enqueue nothing and succeed
     assert abi.call("tq_quantize_i8_rowwise", None, 0, 16, None, None, None) == 0
     assert abi.call("tq_gemv_w8", None, 0, None, None, None, 16, 16, None, None) == 0
     assert abi.call("tq_quantize_tensor", None, 0, 1.0, 0.0, 0, None, None) == 0
+    assert abi.call("tq_convert", None, 3, None, 1, 0, None) == 0

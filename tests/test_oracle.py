@@ -484,3 +484,102 @@ def test_linear_fp8_vs_numpy(oracle):
     ref = a @ w.T + b.astype(np.float64)
     y = oracle.linear_fp8(qa, sa, qw, sw, b)
     assert np.allclose(y, ref, rtol=1e-12, atol=1e-9)
+
+
+# ------------------------------------------------------ element conversion
+DT_F16, DT_BF16, DT_F32, DT_F64, DT_U8, DT_I8, DT_I16, DT_I32, DT_I64, DT_BOOL = range(10)
+
+
+def conversion_probe_f64():
+    """f64 values around every rounding case of the narrow float types."""
+    rng = np.random.default_rng(21)
+    wide = rng.standard_normal(3000) * np.exp2(rng.uniform(-160, 130, 3000))
+    f32_ties = (np.float32(rng.standard_normal(500)).astype(np.float64) +
+                np.spacing(np.float32(1)).astype(np.float64) * 0)  # exact f32 values
+    half_ulp = np.spacing(np.abs(f32_ties).astype(np.float32)).astype(np.float64) / 2
+    ties = np.concatenate([f32_ties + half_ulp, f32_ties - half_ulp])
+    near = np.nextafter(ties, np.inf)
+    special = np.array([0.0, -0.0, np.inf, -np.inf, np.nan, 65504.0, 65520.0, 65519.99, 2.0 ** -24, 2.0 ** -25,
+                        3 * 2.0 ** -26, 3.4e38, 3.4028235677973366e38, 3.402823669209385e38, 1e-45, 2.0 ** -149,
+                        2.0 ** -150, 3 * 2.0 ** -151, 2.0 ** -133, 2.0 ** -134, 3 * 2.0 ** -135, 1e-320,
+                        127.5, 128.0, -128.5, -129.0, 255.5, 256.0, -0.7, 2.0 ** 31, -(2.0 ** 31) - 0.5,
+                        2.0 ** 63, -(2.0 ** 63), 9.2e18, -9.2e18, 2.0 ** 53 + 1, 1e300])
+    return np.concatenate([wide, ties, near, special, -special])
+
+
+def test_dtype_sizes_reference_asserts(oracle):
+    # crates/theano-types/src/dtype.rs:107-114
+    sz = {n: oracle.lib().tqo_dtype_size(i) for i, n in enumerate(oracle.DTYPES)}
+    assert sz["float32"] == 4 and sz["float64"] == 8 and sz["float16"] == 2 and sz["bfloat16"] == 2
+    assert sz["int64"] == 8 and sz["bool"] == 1
+    assert [sz[n] for n in ("uint8", "int8", "int16", "int32")] == [1, 1, 2, 4]
+    assert oracle.lib().tqo_dtype_size(10) == 0
+
+
+def test_convert_f64_to_f32_f16_vs_numpy(oracle):
+    v = conversion_probe_f64()
+    got32 = oracle.convert(v, DT_F64, DT_F32)
+    assert ieee_equal(got32, v.astype(np.float32)) and np.array_equal(np.signbit(got32), np.signbit(v))
+    got16 = oracle.convert(v, DT_F64, DT_F16).view(np.float16)
+    ref16 = v.astype(np.float16)
+    assert ieee_equal(got16, ref16) and np.array_equal(np.signbit(got16), np.signbit(ref16))
+
+
+def _bf16_exact(x):
+    """Nearest bf16 (ties to even) of a finite f64 by exact rationals over all bf16 values."""
+    if x != x:
+        return None
+    allv = np.arange(0, 0x7F81, dtype=np.uint32)  # +0 .. +inf
+    vals = (allv << 16).view(np.float32).astype(np.float64)
+    a = abs(x)
+    i = int(np.searchsorted(vals, a))
+    if i < len(vals) and vals[i] == a:
+        code = int(allv[i])
+    else:
+        lo, hi = i - 1, i
+        if hi == len(vals) - 1:  # between max finite and inf: inf past the midpoint to 2^128
+            mid = (Fraction(vals[lo]) + Fraction(2) ** 128) / 2
+            code = 0x7F80 if Fraction(a) >= mid else int(allv[lo])
+        else:
+            dl, dh = Fraction(a) - Fraction(vals[lo]), Fraction(vals[hi]) - Fraction(a)
+            code = int(allv[lo]) if dl < dh or (dl == dh and allv[lo] % 2 == 0) else int(allv[hi])
+    return code | (0x8000 if math.copysign(1.0, x) < 0 else 0)
+
+
+def test_convert_f64_to_bf16_exact(oracle):
+    v = conversion_probe_f64()[::7]
+    got = oracle.convert(v, DT_F64, DT_BF16)
+    for x, g in zip(v, got):
+        ref = _bf16_exact(float(x))
+        if ref is None:
+            assert (g & 0x7F80) == 0x7F80 and (g & 0x7F) != 0
+        else:
+            assert g == ref, (x, hex(g), hex(ref))
+
+
+def test_convert_float_to_int_rust_as(oracle):
+    v = np.array([0.0, -0.0, 0.7, -0.7, 127.9, 128.0, -128.9, -129.0, 255.5, 256.0, -1.0, np.nan, np.inf,
+                  -np.inf, 2.0 ** 31, -(2.0 ** 31) - 0.5, 2.0 ** 63, -(2.0 ** 63), 9.2e18, -9.2e18, 1e300, 3e4,
+                  -4e4])
+    i8 = oracle.convert(v, DT_F64, DT_I8).tolist()
+    assert i8[:12] == [0, 0, 0, 0, 127, 127, -128, -128, 127, 127, -1, 0] and i8[12:14] == [127, -128]
+    u8 = oracle.convert(v, DT_F64, DT_U8).tolist()
+    assert u8[:13] == [0, 0, 0, 0, 127, 128, 0, 0, 255, 255, 0, 0, 255] and u8[13] == 0
+    i32 = oracle.convert(v, DT_F64, DT_I32).tolist()
+    assert i32[14:16] == [2 ** 31 - 1, -(2 ** 31)]
+    i64 = oracle.convert(v, DT_F64, DT_I64).tolist()
+    assert i64[16:20] == [2 ** 63 - 1, -(2 ** 63), 9200000000000000000, -9200000000000000000]
+    assert i64[11] == 0 and i64[12] == 2 ** 63 - 1 and i64[13] == -(2 ** 63)
+    i16 = oracle.convert(v, DT_F64, DT_I16).tolist()
+    assert i16[21:] == [30000, -32768]
+    b = oracle.convert(v, DT_F64, DT_BOOL).tolist()
+    assert b[:4] == [0, 0, 1, 1] and b[11] == 1  # NaN != 0
+
+
+def test_convert_sources_decode_exactly(oracle):
+    h = np.arange(0, 65536, 17, dtype=np.uint16)
+    assert ieee_equal(oracle.convert(h, DT_F16, DT_F64), h.view(np.float16).astype(np.float64))
+    assert ieee_equal(oracle.convert(h, DT_BF16, DT_F64), (h.astype(np.uint32) << 16).view(np.float32).astype(np.float64))
+    big = np.array([2 ** 53 + 1, -(2 ** 63), 2 ** 63 - 1, 12345], dtype=np.int64)
+    assert np.array_equal(oracle.convert(big, DT_I64, DT_F64), big.astype(np.float64))  # RNE above 2^53
+    assert oracle.convert(np.array([0, 1, 7], np.uint8), DT_BOOL, DT_F32).tolist() == [0.0, 1.0, 1.0]

@@ -74,6 +74,7 @@ def build_host(verbose=False):
     tmp = HOSTLIB + ".tmp"
     out = _run([HIPCC, "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall",
                 f"-I{os.path.join(ROOT, 'include')}", f"-I{HOST}", src, os.path.join(HOST, "theano_serialize.cpp"),
+                os.path.join(HOST, "theano_rocm.cpp"),
                 "-o", tmp,
                 f"-L{PKG}", "-ltq", "-Wl,-rpath,$ORIGIN"])
     if verbose and out.strip():

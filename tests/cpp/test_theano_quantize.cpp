@@ -10,6 +10,8 @@
 // Usage: test_theano_quantize [--cpu]   (--cpu: only the tests that need no GPU)
 #include <cmath>
 #include <cstdio>
+#include <cstdlib>
+#include <memory>
 #include <cstring>
 #include <functional>
 #include <random>
@@ -18,6 +20,7 @@
 
 #include "../../oracle/tq_oracle.h"
 #include "theano_quantize.hpp"
+#include "theano_rocm.hpp"
 #include "theano_serialize.hpp"
 
 #include <fstream>
@@ -765,6 +768,267 @@ TEST_GPU(test_checkpoint_independent_writer_forward) {
     std::vector<double> ref(m * n);
     tqo_linear_w4g128_bf16(xb.data(), m, p.data(), s.data(), b.data(), n, k, ref.data());
     assert_close(y, ref, "checkpoint linear");
+}
+
+// ------------------------------------- allocator.rs:249-348 (host-memory backend)
+
+struct HostMem {
+    size_t limit = SIZE_MAX, used = 0;
+    int mallocs = 0, frees = 0;
+    std::map<void*, size_t> live;
+};
+
+rocm::MemoryBackend host_backend(std::shared_ptr<HostMem> h) {
+    rocm::MemoryBackend b;
+    b.malloc = [h](void** p, size_t n) {
+        if (h->used + n > h->limit) return false;
+        *p = std::malloc(n);
+        h->used += n;
+        h->live[*p] = n;
+        ++h->mallocs;
+        return true;
+    };
+    b.free = [h](void* p) {
+        h->used -= h->live.at(p);
+        h->live.erase(p);
+        std::free(p);
+        ++h->frees;
+    };
+    b.synchronize = []() {};
+    return b;
+}
+
+TEST_CPU(test_allocator_basic) {
+    auto h = std::make_shared<HostMem>();
+    rocm::CachingAllocator alloc(0, host_backend(h));
+    const rocm::Block b1 = alloc.allocate(1024).unwrap();
+    ASSERT(b1.ptr != nullptr && b1.size >= 1024);
+    auto st = alloc.stats();
+    ASSERT_EQ(st.num_cache_misses, 1u);
+    ASSERT(st.allocated_bytes > 0);
+    alloc.free(b1);
+    st = alloc.stats();
+    ASSERT_EQ(st.allocated_bytes, 0u);
+    ASSERT(st.cached_bytes > 0);
+}
+
+TEST_CPU(test_allocator_cache_reuse) {
+    auto h = std::make_shared<HostMem>();
+    rocm::CachingAllocator alloc(0, host_backend(h));
+    const rocm::Block b1 = alloc.allocate(1024).unwrap();
+    const size_t size1 = b1.size;
+    alloc.free(b1);
+    const rocm::Block b2 = alloc.allocate(1024).unwrap();
+    ASSERT_EQ(b2.size, size1);
+    ASSERT(b2.ptr == b1.ptr);
+    const auto st = alloc.stats();
+    ASSERT_EQ(st.num_cache_hits, 1u);
+    ASSERT_EQ(st.num_mallocs, 1u);  // only one real malloc
+    alloc.free(b2);
+}
+
+TEST_CPU(test_allocator_empty_cache) {
+    auto h = std::make_shared<HostMem>();
+    rocm::CachingAllocator alloc(0, host_backend(h));
+    const rocm::Block b1 = alloc.allocate(1024).unwrap(), b2 = alloc.allocate(2048).unwrap();
+    alloc.free(b1);
+    alloc.free(b2);
+    ASSERT(alloc.stats().cached_bytes > 0);
+    alloc.empty_cache();
+    ASSERT_EQ(alloc.stats().cached_bytes, 0u);
+    ASSERT_EQ(alloc.stats().num_frees, 2u);
+    ASSERT(h->live.empty() && h->frees == 2);  // the driver got both segments back
+}
+
+TEST_CPU(test_allocator_large_pool) {
+    auto h = std::make_shared<HostMem>();
+    rocm::CachingAllocator alloc(0, host_backend(h));
+    const rocm::Block b = alloc.allocate(2 * 1024 * 1024).unwrap();
+    ASSERT(b.size >= 2u * 1024 * 1024);
+    alloc.free(b);
+    ASSERT(alloc.stats().cached_bytes > 0);
+    ASSERT_EQ(rocm::CachingAllocator::round_size(2 * 1024 * 1024 + 1), 4u * 1024 * 1024);
+    ASSERT_EQ(rocm::CachingAllocator::round_size(1000), 1024u);
+}
+
+TEST_CPU(test_allocator_zero_size) {
+    auto h = std::make_shared<HostMem>();
+    rocm::CachingAllocator alloc(0, host_backend(h));
+    const rocm::Block b = alloc.allocate(0).unwrap();
+    ASSERT_EQ(b.size, 0u);
+    ASSERT(b.ptr == nullptr);
+    alloc.free(b);
+    ASSERT_EQ(h->mallocs, 0);
+}
+
+TEST_CPU(test_allocator_stats) {
+    auto h = std::make_shared<HostMem>();
+    rocm::CachingAllocator alloc(0, host_backend(h));
+    const rocm::Block b1 = alloc.allocate(512).unwrap(), b2 = alloc.allocate(1024).unwrap();
+    const auto st = alloc.stats();
+    ASSERT_EQ(st.num_mallocs, 2u);
+    ASSERT(st.peak_allocated_bytes >= 512 + 1024);
+    alloc.free(b1);
+    alloc.free(b2);
+}
+
+TEST_CPU(test_allocator_device_ordinal) {
+    auto h = std::make_shared<HostMem>();
+    rocm::CachingAllocator alloc(3, host_backend(h));
+    ASSERT_EQ(alloc.device(), 3);
+}
+
+TEST_CPU(test_allocator_split_merge_streams) {
+    auto h = std::make_shared<HostMem>();
+    rocm::CachingAllocator alloc(0, host_backend(h));
+    const size_t MB = 1u << 20;
+    const rocm::Block big = alloc.allocate(2 * MB + 1).unwrap();  // one 4 MB segment
+    ASSERT_EQ(big.size, 4 * MB);
+    alloc.free(big);
+    const rocm::Block a = alloc.allocate(MB + 1).unwrap();  // 2 MB from the 4 MB piece; 2 MB stays cached
+    const rocm::Block b = alloc.allocate(2 * MB).unwrap();  // the remainder
+    ASSERT_EQ(h->mallocs, 1);
+    ASSERT(static_cast<char*>(b.ptr) == static_cast<char*>(a.ptr) + 2 * MB);
+    auto st = alloc.stats();
+    ASSERT_EQ(st.allocated_bytes, 4 * MB);
+    ASSERT_EQ(st.cached_bytes, 0u);
+    alloc.free(a);
+    alloc.free(b);  // merges back into one free 4 MB piece
+    st = alloc.stats();
+    ASSERT_EQ(st.allocated_bytes, 0u);
+    ASSERT_EQ(st.cached_bytes, 4 * MB);
+    alloc.empty_cache();
+    ASSERT_EQ(h->frees, 1);
+    ASSERT(h->live.empty());
+    // stream order: a block freed on one stream is not handed to another
+    hipStream_t s1 = reinterpret_cast<hipStream_t>(0x10), s2 = reinterpret_cast<hipStream_t>(0x20);
+    const rocm::Block c = alloc.allocate(4096, s1).unwrap();
+    alloc.free(c);
+    const rocm::Block d = alloc.allocate(4096, s2).unwrap();
+    ASSERT(d.ptr != c.ptr);
+    const rocm::Block e = alloc.allocate(4096, s1).unwrap();
+    ASSERT(e.ptr == c.ptr);
+    alloc.free(d);
+    alloc.free(e);
+}
+
+TEST_CPU(test_allocator_oom_recovery) {
+    auto h = std::make_shared<HostMem>();
+    const size_t MB = 1u << 20;
+    h->limit = 5 * MB;
+    rocm::CachingAllocator alloc(0, host_backend(h));
+    const rocm::Block a = alloc.allocate(4 * MB, reinterpret_cast<hipStream_t>(0x10)).unwrap();
+    alloc.free(a);  // cached, not usable by the other stream
+    const rocm::Block b = alloc.allocate(4 * MB, reinterpret_cast<hipStream_t>(0x20)).unwrap();  // frees the cache, retries
+    ASSERT_EQ(h->frees, 1);
+    auto r = alloc.allocate(4 * MB, reinterpret_cast<hipStream_t>(0x20));
+    ASSERT(r.is_err() && r.unwrap_err().kind() == TheanoError::Kind::OutOfMemory);
+    alloc.free(b);
+}
+
+// ------------------------------------------- device.rs / storage.rs on the GPU
+
+TEST_GPU(test_rocm_device_properties) {
+    auto dev = rocm::DeviceManager::global().get_device(0).unwrap();
+    ASSERT(dev == rocm::DeviceManager::global().get_device(0).unwrap());  // one handle per ordinal
+    const auto& p = dev->properties();
+    ASSERT_EQ(p.gcn_arch, 950u);
+    ASSERT_EQ(p.warp_size, 64u);
+    ASSERT(p.multiprocessor_count >= 256u);
+    ASSERT(p.total_memory > (200ull << 30));
+    std::printf("[%s gfx%u, %u CUs, %zu GiB, %u threads/block, %zu B LDS/block] ", p.name.c_str(), p.gcn_arch,
+                p.multiprocessor_count, p.total_memory >> 30, p.max_threads_per_block, p.max_shared_memory_per_block);
+    ASSERT(p.max_threads_per_block >= 1024u);
+    ASSERT(p.max_shared_memory_per_block >= 32u * 1024);
+    const auto mi = dev->memory_info().unwrap();
+    ASSERT(mi.second > 0 && mi.first <= mi.second);
+    ASSERT(rocm::DeviceManager::global().get_device(99).is_err());
+    ASSERT(rocm::DeviceManager::global().device_count() >= 1);
+    ASSERT(dev->synchronize().is_ok());
+}
+
+TEST_GPU(test_rocm_storage_roundtrip_dtypes) {
+    auto dev = rocm::DeviceManager::global().get_device(0).unwrap();
+    std::vector<double> v = randn(100000, 1e3, 101);
+    const double special[] = {0.0, -0.0, INFINITY, -INFINITY, NAN, 65520.0, 3.4e38, 1e-40, 127.5, -128.5,
+                              300.0, -3e9, 9.3e18, 2.5, -2.5, 1e-8};
+    for (double x : special) v.push_back(x);
+    for (int t = 0; t < 10; ++t) {
+        const DType dt = static_cast<DType>(t);
+        const auto s = rocm::RocmStorage::from_host_f64(dev, v.data(), v.size(), dt).unwrap();
+        ASSERT_EQ(s.byte_size(), v.size() * dtype_size(dt));
+        const auto back = s.to_host_f64().unwrap();
+        // oracle: the conversion, then its source decode back to f64
+        std::vector<uint8_t> conv(v.size() * dtype_size(dt));
+        tqo_convert(v.data(), 3, conv.data(), t, static_cast<int64_t>(v.size()));
+        std::vector<double> ref(v.size());
+        tqo_convert(conv.data(), t, ref.data(), 3, static_cast<int64_t>(v.size()));
+        ASSERT(same_bits(back, ref));
+    }
+    // more than two staging chunks (f64 and f32 payloads)
+    std::vector<double> big = randn(10u << 20, 1.0, 102);
+    const auto s64 = rocm::RocmStorage::from_host_f64(dev, big.data(), big.size(), DType::F64).unwrap();
+    ASSERT(same_bits(s64.to_host_f64().unwrap(), big));
+    const auto s32 = s64.to_dtype(DType::F32).unwrap();
+    const auto b32 = s32.to_host_f64().unwrap();
+    for (size_t i = 0; i < big.size(); i += 997) ASSERT_EQ(b32[i], static_cast<double>(static_cast<float>(big[i])));
+}
+
+TEST_GPU(test_rocm_storage_returns_blocks_to_the_pool) {
+    auto dev = rocm::DeviceManager::global().get_device(0).unwrap();
+    { auto warm = rocm::RocmStorage::allocate(dev, 12345, DType::F32).unwrap(); }
+    const auto before = dev->allocator().stats();
+    for (int i = 0; i < 5; ++i) {
+        auto s = rocm::RocmStorage::allocate(dev, 12345, DType::F32).unwrap();
+        ASSERT(s.device_ptr() != nullptr);
+    }
+    const auto after = dev->allocator().stats();
+    ASSERT_EQ(after.num_mallocs, before.num_mallocs);
+    ASSERT_EQ(after.num_cache_hits, before.num_cache_hits + 5);
+    ASSERT_EQ(after.allocated_bytes, before.allocated_bytes);
+}
+
+// Tensor::to(Device) round trip and quantized modules chained on the device give
+// the host path's results bit for bit, without driver allocations once warm.
+TEST_GPU(test_device_tensor_chain_matches_host_path) {
+    auto dev = rocm::DeviceManager::global().get_device(0).unwrap();
+    const size_t m = 24, d = 256, f = 384;
+    const QConfig a8{QuantDType::Int8, QuantDType::Int8, true, true};
+    const QConfig fp8{QuantDType::FP8, QuantDType::FP8, true, true};
+    const QuantizedLinear l1 =
+        QuantizedLinear::from_tensors(Tensor::from_slice(randn(f * d, 0.05, 111), {f, d}), std::nullopt, a8).unwrap();
+    const QuantizedLinear l2 = QuantizedLinear::from_tensors(Tensor::from_slice(randn(d * f, 0.05, 112), {d, f}),
+                                                             Tensor::from_slice(randn(d, 0.1, 113), {d}),
+                                                             QConfig::default_int4())
+                                   .unwrap();
+    const QuantizedLinear l3 =
+        QuantizedLinear::from_tensors(Tensor::from_slice(randn(d * d, 0.05, 114), {d, d}), std::nullopt, fp8).unwrap();
+    const QuantizedMLP mlp = QuantizedMLP::from_tensors(Tensor::from_slice(randn(f * d, 0.02, 115), {f, d}),
+                                                        Tensor::from_slice(randn(f * d, 0.02, 116), {f, d}),
+                                                        Tensor::from_slice(randn(d * f, 0.02, 117), {d, f}))
+                                 .unwrap();
+    const Tensor x = Tensor::from_slice(randn(m * d, 1.0, 118), {m, d});
+    const Tensor ref = mlp.forward(l3.forward(l2.forward(l1.forward(x))));
+    const DeviceTensor xd = DeviceTensor::from_host(x, dev, DType::F32).unwrap();
+    ASSERT(same_bits(xd.to_host().unwrap().to_vec_f64().unwrap(),
+                     [&] {
+                         std::vector<double> v = x.to_vec_f64().unwrap();
+                         for (auto& e : v) e = static_cast<float>(e);
+                         return v;
+                     }()));
+    auto run = [&]() {
+        const DeviceTensor h1 = nn::forward(l1, xd).unwrap();
+        const DeviceTensor h2 = nn::forward(l2, h1).unwrap();  // F32 -> BF16 on the device
+        const DeviceTensor h3 = nn::forward(l3, h2).unwrap();
+        return nn::forward(mlp, h3).unwrap();
+    };
+    const DeviceTensor y = run();
+    ASSERT(y.shape() == (std::vector<size_t>{m, d}) && y.dtype() == DType::F32);
+    ASSERT(same_bits(y.to_host().unwrap().to_vec_f64().unwrap(), ref.to_vec_f64().unwrap()));
+    const auto warm = dev->allocator().stats();
+    for (int i = 0; i < 3; ++i) (void)run();
+    ASSERT_EQ(dev->allocator().stats().num_mallocs, warm.num_mallocs);  // served from the pool
+    ASSERT(dev->synchronize().is_ok());
 }
 
 int main(int argc, char** argv) {

@@ -43,7 +43,7 @@ def parse_args():
     p.add_argument("--steps", type=int, default=200)
     p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--only", default=None,
-                   help="run one workload: gemv_w4, gemv_w8, gemv_fp8, gemv_w4_m, w8a8, fp8, roundtrip, mlp, copy")
+                   help="run one workload: gemv_w4, gemv_w8, gemv_fp8, gemv_w4_m, w8a8, fp8, storage, roundtrip, mlp, copy")
     p.add_argument("--no-secondary", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=12.0, help="bound of the CPU baseline sample (0: skip)")
     p.add_argument("--eager", action="store_true", help="time eager launches instead of a HIP graph")
@@ -282,6 +282,19 @@ def main():
             "act_quant_us": round(msq * 1e3, 3), "act_quant_GB/s": round(qbytes / (msq * 1e-3) / 1e9, 1)}
         log(f"fp8 M=2048: {ms * 1e3:.2f} us  {tf:.0f} TFLOP/s; act quant {msq * 1e3:.2f} us")
         del qa, qw, y, xd
+
+    # ------------------------------------- device storage (C++ host layer)
+    if not args.no_secondary and want("storage"):
+        exe = os.path.join(ROOT, "neo-theano_amd", "bench_storage")
+        if os.path.exists(exe):
+            import subprocess
+
+            r = subprocess.run([exe], stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True, timeout=300)
+            if r.returncode == 0:
+                secondary["device_storage"] = json.loads(r.stdout.strip().splitlines()[-1])
+                log(f"device storage: {secondary['device_storage']}")
+            else:
+                log(f"bench_storage failed ({r.returncode}): {r.stderr[-500:]}")
 
     # ------------------------------------------------ round trip (C1)
     if not args.no_secondary and want("roundtrip"):

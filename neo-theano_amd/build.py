@@ -80,6 +80,13 @@ def build_host(verbose=False):
     if verbose and out.strip():
         print(out)
     os.replace(tmp, HOSTLIB)
+    # measurement driver of the storage layer (run by bench.py)
+    bsrc = os.path.join(HOST, "bench_storage.cpp")
+    if os.path.exists(bsrc):
+        bout = os.path.join(PKG, "bench_storage")
+        _run([HIPCC, "-O2", "-std=c++17", "-Wall", f"-I{os.path.join(ROOT, 'include')}", f"-I{HOST}", bsrc,
+              "-o", bout + ".tmp", f"-L{PKG}", "-ltheano_quantize_rocm", "-ltq", "-Wl,-rpath,$ORIGIN"])
+        os.replace(bout + ".tmp", bout)
     return HOSTLIB
 
 

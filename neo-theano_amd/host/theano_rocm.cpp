@@ -45,21 +45,26 @@ double bf16_to_f64(uint16_t h) {
     return f;
 }
 
-// element i of a host buffer of `dtype` as f64
-double widen(const uint8_t* p, DType d, size_t i) {
+// n elements of a host buffer of `dtype` -> f64 (one tight loop per type)
+template <class T, class F>
+void widen_as(const uint8_t* p, size_t n, double* out, F f) {
+    const T* v = reinterpret_cast<const T*>(p);  // staging chunks are page aligned
+    for (size_t i = 0; i < n; ++i) out[i] = f(v[i]);
+}
+
+void widen(const uint8_t* p, DType d, size_t n, double* out) {
     switch (d) {
-        case DType::F16: { uint16_t v; std::memcpy(&v, p + 2 * i, 2); return f16_to_f64(v); }
-        case DType::BF16: { uint16_t v; std::memcpy(&v, p + 2 * i, 2); return bf16_to_f64(v); }
-        case DType::F32: { float v; std::memcpy(&v, p + 4 * i, 4); return v; }
-        case DType::F64: { double v; std::memcpy(&v, p + 8 * i, 8); return v; }
-        case DType::U8: return p[i];
-        case DType::I8: return static_cast<int8_t>(p[i]);
-        case DType::I16: { int16_t v; std::memcpy(&v, p + 2 * i, 2); return v; }
-        case DType::I32: { int32_t v; std::memcpy(&v, p + 4 * i, 4); return v; }
-        case DType::I64: { int64_t v; std::memcpy(&v, p + 8 * i, 8); return static_cast<double>(v); }
-        case DType::Bool: return p[i] ? 1.0 : 0.0;
+        case DType::F16: widen_as<uint16_t>(p, n, out, f16_to_f64); break;
+        case DType::BF16: widen_as<uint16_t>(p, n, out, bf16_to_f64); break;
+        case DType::F32: widen_as<float>(p, n, out, [](float v) { return static_cast<double>(v); }); break;
+        case DType::F64: std::memcpy(out, p, n * 8); break;
+        case DType::U8: widen_as<uint8_t>(p, n, out, [](uint8_t v) { return static_cast<double>(v); }); break;
+        case DType::I8: widen_as<int8_t>(p, n, out, [](int8_t v) { return static_cast<double>(v); }); break;
+        case DType::I16: widen_as<int16_t>(p, n, out, [](int16_t v) { return static_cast<double>(v); }); break;
+        case DType::I32: widen_as<int32_t>(p, n, out, [](int32_t v) { return static_cast<double>(v); }); break;
+        case DType::I64: widen_as<int64_t>(p, n, out, [](int64_t v) { return static_cast<double>(v); }); break;
+        case DType::Bool: widen_as<uint8_t>(p, n, out, [](uint8_t v) { return v ? 1.0 : 0.0; }); break;
     }
-    return 0.0;
 }
 
 constexpr size_t kStagingBytes = size_t(32) << 20;  // per pinned staging buffer
@@ -351,13 +356,20 @@ Result<void> RocmDevice::copy_to_device(void* dst, const void* src, size_t bytes
 }
 
 Result<void> RocmDevice::copy_to_host(void* dst, const void* src, size_t bytes, hipStream_t stream) {
+    return copy_to_host_chunks(src, bytes, stream, [dst](const uint8_t* chunk, size_t off, size_t n) {
+        std::memcpy(static_cast<uint8_t*>(dst) + off, chunk, n);
+    });
+}
+
+Result<void> RocmDevice::copy_to_host_chunks(const void* src, size_t bytes, hipStream_t stream,
+                                             const std::function<void(const uint8_t*, size_t, size_t)>& consume) {
     return capture<void>([&]() -> Result<void> {
         std::lock_guard<std::mutex> lk(staging_mu_);
         for (int i = 0; i < 2; ++i) {
             if (!staging_[i]) check_hip(hipHostMalloc(&staging_[i], kStagingBytes, hipHostMallocDefault), "hipHostMalloc");
             if (!staged_[i]) check_hip(hipEventCreateWithFlags(&staged_[i], hipEventDisableTiming), "hipEventCreate");
         }
-        // DMA chunk c into buffer c % 2 while the host copies chunk c - 1 out
+        // DMA chunk c into buffer c % 2 while the host consumes chunk c - 1
         const size_t chunks = (bytes + kStagingBytes - 1) / kStagingBytes;
         auto issue = [&](size_t c) {
             const size_t off = c * kStagingBytes, n = std::min(kStagingBytes, bytes - off);
@@ -371,7 +383,7 @@ Result<void> RocmDevice::copy_to_host(void* dst, const void* src, size_t bytes, 
             if (c + 1 < chunks) issue(c + 1);
             check_hip(hipEventSynchronize(staged_[c & 1]), "staging wait");
             const size_t off = c * kStagingBytes, n = std::min(kStagingBytes, bytes - off);
-            std::memcpy(static_cast<uint8_t*>(dst) + off, staging_[c & 1], n);
+            consume(static_cast<const uint8_t*>(staging_[c & 1]), off, n);
         }
         return {};
     });
@@ -442,13 +454,19 @@ Result<RocmStorage> RocmStorage::from_host_f64(std::shared_ptr<RocmDevice> devic
 }
 
 Result<std::vector<double>> RocmStorage::to_host_f64() const {
-    std::vector<uint8_t> raw(byte_size());
-    if (!raw.empty()) {
-        auto c = device_->copy_to_host(raw.data(), device_ptr(), raw.size(), stream_);
-        if (c.is_err()) return c.unwrap_err();
-    }
     std::vector<double> out(len_);
-    for (size_t i = 0; i < len_; ++i) out[i] = widen(raw.data(), dtype_, i);
+    if (len_ == 0) return out;
+    if (dtype_ == DType::F64) {  // straight into the result
+        auto c = device_->copy_to_host(out.data(), device_ptr(), byte_size(), stream_);
+        if (c.is_err()) return c.unwrap_err();
+        return out;
+    }
+    const size_t es = dtype_size(dtype_);
+    auto c = device_->copy_to_host_chunks(device_ptr(), byte_size(), stream_,
+                                          [&](const uint8_t* chunk, size_t off, size_t n) {
+                                              widen(chunk, dtype_, n / es, out.data() + off / es);
+                                          });
+    if (c.is_err()) return c.unwrap_err();
     return out;
 }
 

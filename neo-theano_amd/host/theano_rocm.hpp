@@ -155,6 +155,10 @@ class RocmDevice {
     // the host memcpy with the DMA); synchronous with respect to the host
     Result<void> copy_to_device(void* dst, const void* src, size_t bytes, hipStream_t stream);
     Result<void> copy_to_host(void* dst, const void* src, size_t bytes, hipStream_t stream);
+    // D2H in staging-buffer chunks handed to `consume(chunk, offset, bytes)` on
+    // the host while the next chunk's DMA runs (chunks are multiples of 8 bytes)
+    Result<void> copy_to_host_chunks(const void* src, size_t bytes, hipStream_t stream,
+                                     const std::function<void(const uint8_t*, size_t, size_t)>& consume);
 
    private:
     RocmDevice() = default;

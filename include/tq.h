@@ -299,6 +299,23 @@ int tq_mlp_w4g128(const uint16_t* x_bf16, int64_t m, int64_t d, int64_t f,
                   void* workspace, int64_t workspace_bytes, float* y, tq_stream_t stream);
 
 /* ------------------------------------------------------------------------
+ * Attention core of MultiheadAttention::forward_with_mask
+ * (crates/theano-nn/src/transformer.rs:95-142) between the quantized q/k/v and
+ * out projections, f32:
+ *   scores = (Q_h K_h^T) * (1/sqrt(head_dim)) (+ mask);  P = softmax(scores, -1)
+ *   (tensor_ops.rs:574-620);  O_h = P V_h, heads concatenated.
+ * q, k, v: [batch * seq, ld*] row-major, head h in columns [h*D, (h+1)*D)
+ * (the fused QKV projection's [B*S, 3E] output in place: ld = 3E, k = q + E,
+ * v = q + 2E).  mask: NULL (mask_batch = 0) or additive f32 [mask_batch, seq,
+ * seq], mask_batch 1 (broadcast) or batch, shared by the heads.  out: [batch *
+ * seq, ldo].  head_dim <= 128.  A row whose scores are all -inf gives NaN, as
+ * the reference's softmax does.
+ * ------------------------------------------------------------------------ */
+int tq_attention_f32(const float* q, int64_t ldq, const float* k, int64_t ldk, const float* v,
+                     int64_t ldv, const float* mask, int64_t mask_batch, int64_t batch, int64_t seq,
+                     int64_t heads, int64_t head_dim, float* out, int64_t ldo, tq_stream_t stream);
+
+/* ------------------------------------------------------------------------
  * Element type conversion of device buffers: the device half of Tensor::to
  * (crates/theano-core/src/tensor.rs:277-299) and of RocmStorage::from_host_f64
  * / to_host_f64 (crates/theano-rocm/src/storage.rs:54-99), whose tensors hold

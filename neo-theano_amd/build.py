@@ -35,7 +35,7 @@ HIP_FLAGS = [
     f"-I{os.path.join(ROOT, 'include')}",
 ]
 
-SOURCES = ["tq_api.hip", "tq_quant.hip", "tq_gemv.hip", "tq_decode_w4.hip", "tq_decode_tiled.hip", "tq_gemm.hip", "tq_mlp.hip", "tq_ffn.hip", "tq_generic.hip", "tq_convert.hip"]
+SOURCES = ["tq_api.hip", "tq_quant.hip", "tq_gemv.hip", "tq_decode_w4.hip", "tq_decode_tiled.hip", "tq_gemm.hip", "tq_mlp.hip", "tq_ffn.hip", "tq_generic.hip", "tq_convert.hip", "tq_attention.hip"]
 
 
 def _run(cmd):

@@ -24,7 +24,7 @@ from .formats import (
     repack_i4_g128_tiled,
     tile_rows_for,
 )
-from .nn import Module, QuantizedLinear, QuantizedMLP
+from .nn import Module, QuantizedLinear, QuantizedMLP, QuantizedMultiheadAttention
 from .observer import MinMaxObserver, Observer, PerChannelMinMaxObserver
 from .qconfig import QConfig, QuantDType
 from .quantize import dequantize_tensor, fake_quantize, quantize_per_tensor, quantize_tensor
@@ -35,6 +35,6 @@ __all__ = [
     "quantize_tensor", "dequantize_tensor", "quantize_per_tensor", "fake_quantize",
     "quantize_per_channel_i8", "dequantize_per_channel_i8", "fake_quantize_per_channel_i8",
     "quantize_per_channel_fp8", "dequantize_per_channel_fp8", "fake_quantize_per_channel_fp8",
-    "quantize_i4_g128", "dequantize_i4_g128", "repack_i4_g128_tiled", "tile_rows_for", "Module", "QuantizedLinear", "QuantizedMLP",
+    "quantize_i4_g128", "dequantize_i4_g128", "repack_i4_g128_tiled", "tile_rows_for", "Module", "QuantizedLinear", "QuantizedMLP", "QuantizedMultiheadAttention",
     "save_safetensors", "load_safetensors", "save_quantized", "load_quantized", "convert",
 ]

@@ -59,6 +59,7 @@ SIGNATURES = {
     "tq_gemm_fp8": [_p, _p, _p, _p, _p, _i64, _i64, _i64, _p, _p],
     "tq_dtype_size": [_int],
     "tq_convert": [_p, _int, _p, _int, _i64, _p],
+    "tq_attention_f32": [_p, _i64, _p, _i64, _p, _i64, _p, _i64, _i64, _i64, _i64, _i64, _p, _i64, _p],
     "tq_gemm_w4g128_bf16": [_p, _i64, _p, _p, _p, _i64, _i64, _p, _p],
     "tq_gemm_w4g128_bf16_workspace_bytes": [_i64, _i64],
     "tq_gemm_w4g128_bf16_ws": [_p, _i64, _p, _p, _p, _i64, _i64, _p, _i64, _p, _p],

@@ -70,7 +70,7 @@ def _mode_of(qconfig: QConfig) -> str:
 class QuantizedLinear(Module):
     """y = x . dequant(W)^T + b with W quantized on the device."""
 
-    def __init__(self, mode, in_features, out_features, qweight, scales, bias=None):
+    def __init__(self, mode, in_features, out_features, qweight, scales, bias=None, tiled=True):
         self.mode = mode
         self.in_features = int(in_features)
         self.out_features = int(out_features)
@@ -78,7 +78,7 @@ class QuantizedLinear(Module):
         self.scales = scales
         self.bias = bias
         self.tiled = None
-        if mode == "w4" and self.in_features <= 16384:
+        if tiled and mode == "w4" and self.in_features <= 16384:
             # row-tiled copy (a permutation of qweight) for the decode GEMV, M <= 16
             self.tiled = repack_i4_g128_tiled(qweight, scales)
 
@@ -217,3 +217,100 @@ class QuantizedMLP(Module):
                   ptr(self.up[0]), ptr(self.up[1]), ptr(self.down[0]), ptr(self.down[1]),
                   ptr(workspace), workspace.numel() * workspace.element_size(), ptr(y), stream())
         return y
+
+
+class QuantizedMultiheadAttention(Module):
+    """MultiheadAttention (crates/theano-nn/src/transformer.rs:9-162) with its
+    q/k/v/out projections as QuantizedLinear consumers.
+
+    The q, k and v weights are quantized row by row (per channel, or per row
+    group for INT4), so their concatenation [3E, E] quantizes to exactly the
+    three separate codes: self-attention runs the three projections as ONE
+    fused GEMM / GEMV over the concatenated weight; cross-attention
+    (forward_with_mask with distinct query / key / value) runs row slices of it.
+    The attention core (scores, additive mask, softmax, P V) is libtq's
+    tq_attention_f32 reading q, k and v in place in the fused [B*S, 3E] output.
+    Inputs and outputs are f32 [batch, seq, embed_dim] device tensors."""
+
+    def __init__(self, num_heads, qkv: QuantizedLinear, out_proj: QuantizedLinear):
+        e = out_proj.in_features
+        if qkv.out_features != 3 * e or qkv.in_features != e or out_proj.out_features != e or e % num_heads:
+            raise InvalidArgument("QuantizedMultiheadAttention: qkv must be [3E, E], out_proj [E, E], E % heads == 0")
+        self.embed_dim, self.num_heads, self.head_dim = e, int(num_heads), e // int(num_heads)
+        self.qkv, self.out_proj = qkv, out_proj
+        self._parts = []
+        for i in range(3):  # row slices (views) of the fused weight
+            rows = slice(i * e, (i + 1) * e)
+            self._parts.append(QuantizedLinear(qkv.mode, e, e, qkv.qweight[rows], qkv.scales[rows],
+                                               None if qkv.bias is None else qkv.bias[rows], tiled=False))
+
+    @staticmethod
+    def from_tensors(num_heads, wq, wk, wv, wo, bq=None, bk=None, bv=None, bo=None,
+                     qconfig: QConfig | None = None) -> "QuantizedMultiheadAttention":
+        """Quantizes [E, E] f32 weights (cf. MultiheadAttention::from_linears,
+        transformer.rs:49-61); missing q/k/v biases are zeros when any is given."""
+        ws = [on_device(w, torch.float32, "QuantizedMultiheadAttention.from_tensors") for w in (wq, wk, wv)]
+        e = ws[0].shape[0]
+        bias = None
+        if any(b is not None for b in (bq, bk, bv)):
+            bias = torch.cat([torch.zeros(e, dtype=torch.float32, device=ws[0].device) if b is None
+                              else on_device(b, torch.float32, "bias") for b in (bq, bk, bv)])
+        qkv = QuantizedLinear.from_tensors(torch.cat(ws, 0), bias, qconfig)
+        out = QuantizedLinear.from_tensors(wo, bo, qconfig)
+        return QuantizedMultiheadAttention(num_heads, qkv, out)
+
+    def named_parameters(self):
+        out = []
+        for name, part in zip(("q_proj", "k_proj", "v_proj"), self._parts):
+            out += [(f"{name}.{n}", t) for n, t in part.named_parameters()]
+        out += [(f"out_proj.{n}", t) for n, t in self.out_proj.named_parameters()]
+        return out
+
+    def num_parameters(self) -> int:
+        return self.qkv.num_parameters() + self.out_proj.num_parameters()
+
+    def _act(self, x2d):
+        from ._tensor import convert
+
+        return convert(x2d, torch.bfloat16) if self.qkv.mode == "w4" else x2d
+
+    def _attend(self, q, k, v, ldq, ldk, ldv, batch, seq, mask):
+        from . import _abi
+
+        e = self.embed_dim
+        o = torch.empty((batch * seq, e), dtype=torch.float32, device=q.device)
+        mb, mp = 0, None
+        if mask is not None:
+            mp = on_device(mask, torch.float32, "attention mask")
+            if mp.dim() == 4:  # [Bm, 1, S, S]
+                mp = mp.reshape(mp.shape[0], seq, seq)
+            if mp.dim() != 3 or mp.shape[1:] != (seq, seq) or mp.shape[0] not in (1, batch):
+                raise InvalidArgument(f"attention mask: expected [batch or 1, {seq}, {seq}], got {tuple(mask.shape)}")
+            mb = 1 if mp.shape[0] == 1 and batch != 1 else mp.shape[0]
+        _abi.call("tq_attention_f32", ptr(q), ldq, ptr(k), ldk, ptr(v), ldv, ptr(mp), mb, batch, seq,
+                  self.num_heads, self.head_dim, ptr(o), e, stream())
+        return o
+
+    def forward_with_mask(self, query, key, value, mask=None):
+        """query, key, value: [batch, seq, embed_dim]; mask additive [batch or 1,
+        (1,) seq, seq] (transformer.rs:86-142).  Returns [batch, seq, embed_dim]."""
+        xs = [on_device(t, torch.float32, "QuantizedMultiheadAttention.forward") for t in (query, key, value)]
+        if any(t.dim() != 3 or t.shape[2] != self.embed_dim for t in xs) or len({tuple(t.shape) for t in xs}) != 1:
+            raise InvalidArgument("QuantizedMultiheadAttention: query, key, value must be [batch, seq, embed_dim]")
+        batch, seq, e = xs[0].shape
+        flat = [t.reshape(batch * seq, e) for t in xs]
+        if query is key and key is value:  # self-attention: one fused projection
+            qkv = self.qkv(self._act(flat[0]))
+            q, k, v = qkv, qkv[:, e:], qkv[:, 2 * e:]
+            ld = 3 * e
+            o = self._attend(q, k, v, ld, ld, ld, batch, seq, mask)
+        else:
+            q, k, v = (part(self._act(x)) for part, x in zip(self._parts, flat))
+            o = self._attend(q, k, v, e, e, e, batch, seq, mask)
+        return self.out_proj(self._act(o)).reshape(batch, seq, e)
+
+    def forward_qkv(self, query, key, value):
+        return self.forward_with_mask(query, key, value, None)
+
+    def forward(self, x):
+        return self.forward_with_mask(x, x, x, None)

@@ -63,6 +63,7 @@ def lib():
             "tqo_f64_to_bf16_bits": ([d], ctypes.c_uint16),
             "tqo_dtype_size": ([ctypes.c_int], i64),
             "tqo_convert": ([p, ctypes.c_int, p, ctypes.c_int, i64], None),
+            "tqo_attention": ([p, p, p, p, i64, i64, i64, i64, i64, p], None),
             "tqo_f32_to_e4m3": ([ctypes.c_float], ctypes.c_uint8),
             "tqo_quantize_fp8_rowwise": ([p, i64, i64, p, p], None),
             "tqo_dequantize_fp8_rowwise": ([p, p, i64, i64, p], None),
@@ -382,4 +383,19 @@ def convert(src, src_t, dst_t):
     src = _c(src, NP_STORAGE[src_t])
     out = np.empty(src.shape, NP_STORAGE[dst_t])
     lib().tqo_convert(_ptr(src), src_t, _ptr(out), dst_t, src.size)
+    return out
+
+
+# ---- attention core (transformer.rs:95-142) ----
+
+def attention(q, k, v, heads, mask=None):
+    """q, k, v: [B, S, E] f64 -> [B, S, E] f64; mask None or [Bm, S, S] (Bm 1 or B)."""
+    q = _c(q, np.float64)
+    k = _c(k, np.float64)
+    v = _c(v, np.float64)
+    B, S, E = q.shape
+    m = None if mask is None else _c(mask, np.float64)
+    out = np.empty((B, S, E))
+    lib().tqo_attention(_ptr(q), _ptr(k), _ptr(v), _ptr(m), 0 if m is None else m.shape[0], B, S, heads,
+                        E // heads, _ptr(out))
     return out

@@ -554,3 +554,45 @@ static void conv_put(void* p, int t, int64_t i, double v) {
 void tqo_convert(const void* src, int src_t, void* dst, int dst_t, int64_t n) {
     for (int64_t i = 0; i < n; ++i) conv_put(dst, dst_t, i, conv_get(src, src_t, i));
 }
+
+/* ---- attention core of MultiheadAttention::forward_with_mask
+ * (crates/theano-nn/src/transformer.rs:95-142), f64:
+ *   scores = (q_h . k_h^T) * (1 / sqrt(D))  (+ mask[b or 0][i][j])
+ *   P = softmax(scores) per row (tensor_ops.rs:574-620: max with f64::max,
+ *       exp(x - max), sequential sum, divide), O_h = P . v_h.
+ * q, k, v, out: [B*S, E] row-major, head h in columns [h*D, (h+1)*D), E = H*D.
+ * mask: NULL or [mask_batch, S, S] (mask_batch 1 broadcasts over the batch). */
+void tqo_attention(const double* q, const double* k, const double* v, const double* mask,
+                   int64_t mask_batch, int64_t B, int64_t S, int64_t H, int64_t D, double* out) {
+    const int64_t E = H * D;
+    const double inv_scale = 1.0 / sqrt((double)D);
+    double* row = (double*)malloc(sizeof(double) * (size_t)S);
+    for (int64_t b = 0; b < B; ++b)
+        for (int64_t h = 0; h < H; ++h)
+            for (int64_t i = 0; i < S; ++i) {
+                const double* qi = q + (b * S + i) * E + h * D;
+                double mx = -INFINITY;
+                for (int64_t j = 0; j < S; ++j) {
+                    const double* kj = k + (b * S + j) * E + h * D;
+                    double dot = 0.0;
+                    for (int64_t d = 0; d < D; ++d) dot += qi[d] * kj[d];
+                    double sc = dot * inv_scale;
+                    if (mask) sc += mask[((mask_batch == 1 ? 0 : b) * S + i) * S + j];
+                    row[j] = sc;
+                    mx = fmax(mx, sc);
+                }
+                double sum = 0.0;
+                for (int64_t j = 0; j < S; ++j) {
+                    row[j] = exp(row[j] - mx);
+                    sum += row[j];
+                }
+                for (int64_t j = 0; j < S; ++j) row[j] /= sum;
+                double* oi = out + (b * S + i) * E + h * D;
+                for (int64_t d = 0; d < D; ++d) {
+                    double acc = 0.0;
+                    for (int64_t j = 0; j < S; ++j) acc += row[j] * v[(b * S + j) * E + h * D + d];
+                    oi[d] = acc;
+                }
+            }
+    free(row);
+}

@@ -29,6 +29,9 @@
  *   rowwise / g128 quant   exact-rational rounding (fractions.Fraction),
  *                          numpy float16 RNE, pack/unpack bijection
  *   w8a8 accumulators      numpy int64 matmul
+ *   attention              closed forms (uniform keys -> mean of v, one
+ *                          unmasked key -> that v row, all masked -> NaN),
+ *                          numpy f64 softmax / matmul, scale invariance
  *   conversions            numpy astype (f32, f16), exact rationals (bf16),
  *                          closed forms for Rust `as` (saturation, NaN)
  *   e4m3 encode / decode   torch.float8_e4m3fn on all 256 codes and on every
@@ -127,6 +130,10 @@ void tqo_linear_fp8(const uint8_t* qa, const float* sa, const uint8_t* qw, const
 uint16_t tqo_f64_to_bf16_bits(double x);
 int64_t tqo_dtype_size(int dtype);
 void tqo_convert(const void* src, int src_dtype, void* dst, int dst_dtype, int64_t n);
+
+/* attention core of MultiheadAttention::forward_with_mask (transformer.rs:95-142) */
+void tqo_attention(const double* q, const double* k, const double* v, const double* mask_or_null,
+                   int64_t mask_batch, int64_t B, int64_t S, int64_t H, int64_t D, double* out);
 
 /* build-defined quantized Llama FFN: y = (SiLU(x Wg^T) * (x Wu^T)) Wd^T */
 void tqo_mlp_w4g128(const uint16_t* x_bf16, int64_t m, int64_t d, int64_t f,

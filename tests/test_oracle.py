@@ -583,3 +583,50 @@ def test_convert_sources_decode_exactly(oracle):
     big = np.array([2 ** 53 + 1, -(2 ** 63), 2 ** 63 - 1, 12345], dtype=np.int64)
     assert np.array_equal(oracle.convert(big, DT_I64, DT_F64), big.astype(np.float64))  # RNE above 2^53
     assert oracle.convert(np.array([0, 1, 7], np.uint8), DT_BOOL, DT_F32).tolist() == [0.0, 1.0, 1.0]
+
+
+# ------------------------------------------------ attention (transformer.rs)
+def _np_attention(q, k, v, heads, mask=None):
+    B, S, E = q.shape
+    D = E // heads
+    qh = q.reshape(B, S, heads, D).transpose(0, 2, 1, 3)
+    kh = k.reshape(B, S, heads, D).transpose(0, 2, 1, 3)
+    vh = v.reshape(B, S, heads, D).transpose(0, 2, 1, 3)
+    sc = qh @ kh.transpose(0, 1, 3, 2) * (1.0 / math.sqrt(D))
+    if mask is not None:
+        sc = sc + mask.reshape(mask.shape[0], 1, S, S)
+    with np.errstate(invalid="ignore"):
+        e = np.exp(sc - sc.max(axis=-1, keepdims=True))
+        p = e / e.sum(axis=-1, keepdims=True)
+    return (p @ vh).transpose(0, 2, 1, 3).reshape(B, S, E)
+
+
+def test_attention_closed_forms(oracle):
+    rng = np.random.default_rng(31)
+    B, S, H, D = 2, 5, 2, 3
+    q = rng.standard_normal((B, S, H * D))
+    v = rng.standard_normal((B, S, H * D))
+    k = np.repeat(rng.standard_normal((B, 1, H * D)), S, axis=1)  # identical keys: uniform weights
+    out = oracle.attention(q, k, v, H)
+    assert np.allclose(out, np.repeat(v.mean(axis=1, keepdims=True), S, axis=1), rtol=1e-12, atol=1e-14)
+    # causal mask (transformer.rs:238-246): the first query sees only the first key
+    mask = np.triu(np.full((1, S, S), -np.inf), k=1)
+    out = oracle.attention(q, rng.standard_normal((B, S, H * D)), v, H, mask)
+    assert np.array_equal(out[:, 0], v[:, 0])
+    # a row masked everywhere is NaN (softmax of -inf row), others are finite
+    mask = np.zeros((B, S, S))
+    mask[1, 2, :] = -np.inf
+    out = oracle.attention(q, k, v, H, mask)
+    assert np.isnan(out[1, 2]).all() and np.isfinite(np.delete(out[1], 2, axis=0)).all()
+
+
+def test_attention_matches_numpy(oracle):
+    rng = np.random.default_rng(32)
+    B, S, H, D = 2, 9, 4, 8
+    q, k, v = (rng.standard_normal((B, S, H * D)) for _ in range(3))
+    mask = np.where(rng.random((B, S, S)) < 0.3, -np.inf, rng.standard_normal((B, S, S)))
+    mask[:, :, 0] = 0.0  # at least one key per row
+    for m in (None, mask, mask[:1]):
+        assert np.allclose(oracle.attention(q, k, v, H, m), _np_attention(q, k, v, H, m), rtol=1e-12, atol=1e-13)
+    # one head spanning the whole embedding
+    assert np.allclose(oracle.attention(q, k, v, 1), _np_attention(q, k, v, 1), rtol=1e-12, atol=1e-13)

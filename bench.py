@@ -43,7 +43,8 @@ def parse_args():
     p.add_argument("--steps", type=int, default=200)
     p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--only", default=None,
-                   help="run one workload: gemv_w4, gemv_w8, gemv_fp8, gemv_w4_m, w8a8, fp8, storage, roundtrip, mlp, copy")
+                   help="run one workload: gemv_w4, gemv_w8, gemv_fp8, gemv_w4_m, w8a8, fp8, mha, storage, roundtrip, mlp, "
+                        "copy")
     p.add_argument("--no-secondary", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=12.0, help="bound of the CPU baseline sample (0: skip)")
     p.add_argument("--eager", action="store_true", help="time eager launches instead of a HIP graph")
@@ -282,6 +283,30 @@ def main():
             "act_quant_us": round(msq * 1e3, 3), "act_quant_GB/s": round(qbytes / (msq * 1e-3) / 1e9, 1)}
         log(f"fp8 M=2048: {ms * 1e3:.2f} us  {tf:.0f} TFLOP/s; act quant {msq * 1e3:.2f} us")
         del qa, qw, y, xd
+
+    # ------------------------------ MultiheadAttention, INT4 projections
+    if not args.no_secondary and want("mha"):
+        b6, s6, e6, h6 = 1, 2048, 4096, 32
+        ws6 = [dt(normal_f32(6, (e6, e6), 0.02, stream=i)) for i in range(4)]
+        mha = tq.QuantizedMultiheadAttention.from_tensors(h6, *ws6, qconfig=tq.QConfig.default_int4())
+        del ws6
+        x6 = dt(normal_f32(6, (b6, s6, e6), 1.0, stream=9))
+        qkv6 = mha.qkv(tq.convert(x6.reshape(b6 * s6, e6), torch.bfloat16))
+        o6 = torch.empty((b6 * s6, e6), dtype=torch.float32, device=dev)
+
+        def launch_core(i):
+            _abi.call("tq_attention_f32", ptr(qkv6), 3 * e6, ptr(qkv6[:, e6:]), 3 * e6, ptr(qkv6[:, 2 * e6:]), 3 * e6,
+                      None, 0, b6, s6, h6, e6 // h6, ptr(o6), e6, stream())
+
+        ms_core, mode_core = timer.run(launch_core, 5, 1)
+        ms_all, mode_all = timer.run(lambda i: mha(x6), 5, 1)
+        core_tf = 4.0 * b6 * h6 * s6 * s6 * (e6 // h6) / (ms_core * 1e-3) / 1e12
+        secondary["mha_w4_b1_s2048_e4096_h32"] = {
+            "us": round(ms_all * 1e3, 1), "timing": mode_all, "attention_core_us": round(ms_core * 1e3, 1),
+            "attention_core_TFLOP/s": round(core_tf, 1), "tokens/s": round(b6 * s6 / (ms_all * 1e-3), 1)}
+        log(f"mha S=2048 E=4096 H=32 (int4): {ms_all * 1e3:.0f} us, attention core {ms_core * 1e3:.0f} us "
+            f"({core_tf:.1f} TFLOP/s f32)")
+        del mha, x6, qkv6, o6
 
     # ------------------------------------- device storage (C++ host layer)
     if not args.no_secondary and want("storage"):

@@ -213,6 +213,19 @@ int tq_gemv_w8(const float* x, int64_t m, const int8_t* q, const float* s,
 int tq_gemv_fp8(const float* x, int64_t m, const uint8_t* q, const float* s,
                 const float* bias, int64_t n, int64_t k, float* y, tq_stream_t stream);
 
+/* Decode-shaped W8A8 with the activation quantization fused in: x f32 [M, K],
+ * M <= 16, is quantized per row inside the kernel exactly as
+ * tq_quantize_i8_rowwise does, then y = fma(f32(sum_p qa*qw) * sa, sw, bias)
+ * with exact int32 dot products: the same y as tq_quantize_i8_rowwise +
+ * tq_gemm_w8a8, bit for bit, in one launch.  Requires K % 16 == 0, K <= 8192,
+ * x and qw 16-byte aligned (TQ_EINVAL otherwise: run the two-step path). */
+int tq_gemv_w8a8(const float* x, int64_t m, const int8_t* qw, const float* sw,
+                 const float* bias, int64_t n, int64_t k, float* y, tq_stream_t stream);
+/* The FP8 counterpart (tq_quantize_fp8_rowwise + tq_gemm_fp8 in one launch;
+ * f32 accumulation, so equal to the GEMM within the float tolerance). */
+int tq_gemv_fp8a8(const float* x, int64_t m, const uint8_t* qw, const float* sw,
+                  const float* bias, int64_t n, int64_t k, float* y, tq_stream_t stream);
+
 /* Decode-shaped GEMV, INT4 g128 weights (canonical layout), bf16 activations
  * x [M, K] (bf16 bits), M <= 16, K % 128 == 0 (the format), any N.  The MFMA
  * kernel serves K <= 16384 with x and packed 16-byte aligned; other cases take
@@ -241,7 +254,7 @@ int tq_gemv_w4g128_tiled(const uint16_t* x_bf16, int64_t m, const uint8_t* packe
 
 /* Prefill-shaped W8A8: activations already quantized per row (use
  * tq_quantize_i8_rowwise on X).  acc[i,j] = sum_p qa[i,p]*qw[j,p] (int32,
- * bit-exact); y = f32(acc) * sa[i] * sw[j] (+ bias[j]).  acc may be NULL.
+ * bit-exact); y = fma(f32(acc) * sa[i], sw[j], bias[j] or 0).  acc may be NULL.
  * Any M, N, K.  The MFMA kernels serve N % 16 == 0 and K % 16 == 0 (the LDS-DMA
  * kernel K % 128 == 0) with 16-byte aligned qa, qw, sw, bias, y and acc; other
  * cases take a shape-general kernel. */
@@ -250,7 +263,7 @@ int tq_gemm_w8a8(const int8_t* qa, const float* sa, const int8_t* qw, const floa
                  float* y, tq_stream_t stream);
 
 /* Prefill-shaped FP8 W8A8 (both operands per-row E4M3, tq_quantize_fp8_rowwise):
- * y[i,j] = f32(sum_p e4m3(qa[i,p]) * e4m3(qw[j,p])) * sa[i] * sw[j] (+ bias[j]);
+ * y[i,j] = fma(f32(sum_p e4m3(qa[i,p]) * e4m3(qw[j,p])) * sa[i], sw[j], bias[j] or 0);
  * products exact, f32 accumulation.  The reference value is Linear over the
  * dequantized operands (linear.rs:111-121, tensor_ops.rs:379-410).  Any M, N,
  * K.  The FP8 MFMA kernel serves K % 128 == 0 and N % 16 == 0 with 16-byte

@@ -141,10 +141,10 @@ __global__ __launch_bounds__(kBlock, 2) void k_gemm_w8a8(const int8_t* __restric
             if (acc_out) *reinterpret_cast<i32x4*>(acc_out + mm * n + nb) = c;
             const float s_row = sa[mm];
             f32x4 o;
-            o.x = static_cast<float>(c.x) * s_row * swv.x + bv.x;
-            o.y = static_cast<float>(c.y) * s_row * swv.y + bv.y;
-            o.z = static_cast<float>(c.z) * s_row * swv.z + bv.z;
-            o.w = static_cast<float>(c.w) * s_row * swv.w + bv.w;
+            o.x = fmaf(static_cast<float>(c.x) * s_row, swv.x, bv.x);
+            o.y = fmaf(static_cast<float>(c.y) * s_row, swv.y, bv.y);
+            o.z = fmaf(static_cast<float>(c.z) * s_row, swv.z, bv.z);
+            o.w = fmaf(static_cast<float>(c.w) * s_row, swv.w, bv.w);
             *reinterpret_cast<f32x4*>(y + mm * n + nb) = o;
         }
     }
@@ -310,10 +310,10 @@ __device__ __forceinline__ void dma_epilogue(const Acc (&acc)[4][2], const DmaCt
         if (nval && mm < m) {
             if (acc_out) *reinterpret_cast<i32x4*>(acc_out + static_cast<int64_t>(mm) * n + nb) = v;
             f32x4 o;
-            o.x = acc_value(v.x, Acc{}) * s_row * swv.x + bv.x;
-            o.y = acc_value(v.y, Acc{}) * s_row * swv.y + bv.y;
-            o.z = acc_value(v.z, Acc{}) * s_row * swv.z + bv.z;
-            o.w = acc_value(v.w, Acc{}) * s_row * swv.w + bv.w;
+            o.x = fmaf(acc_value(v.x, Acc{}) * s_row, swv.x, bv.x);
+            o.y = fmaf(acc_value(v.y, Acc{}) * s_row, swv.y, bv.y);
+            o.z = fmaf(acc_value(v.z, Acc{}) * s_row, swv.z, bv.z);
+            o.w = fmaf(acc_value(v.w, Acc{}) * s_row, swv.w, bv.w);
             __builtin_nontemporal_store(o, reinterpret_cast<f32x4*>(y + static_cast<int64_t>(mm) * n + nb));
         }
     }

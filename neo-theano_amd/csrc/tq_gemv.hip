@@ -12,6 +12,7 @@
 // 1 KB chunk, so each wave-wide load is 1 KB contiguous; a row's partial dot
 // products meet in one wave64 butterfly.  Up to 4 tokens per pass.
 #include "tq_internal.h"
+#include "tq_rowfmt.h"
 
 namespace tq {
 namespace {
@@ -143,6 +144,156 @@ __global__ __launch_bounds__(kBlockW8) void k_gemv_w8(const float* __restrict__ 
     }
 }
 
+// ------------------------------------------- W8A8 / FP8 with fused activations
+// The decode form of quantize(x) + W8A8 GEMM in one kernel: every block stages
+// the (few) activation rows in LDS, computes their per-row absmax and scale and
+// codes them exactly as tq_quantize_{i8,fp8}_rowwise do, then streams weight
+// rows as k_gemv_w8.  INT8: v_dot4 int32 dot products of the codes (exact, the
+// GEMM's accumulators); FP8: f32 FMAs of the e4m3 values.  Epilogue as the
+// GEMM's: y = (f32(acc) * s_a) * s_w (+ b).
+template <class Fmt>
+struct A8;
+template <>
+struct A8<FmtI8> {
+    typedef int32_t acc_t;
+    typedef uint32_t xreg_t;  // 4 codes
+    __device__ static void encode(const FmtI8::Row& r, f32x4 v, xreg_t* out) { out[0] = r.code4(v); }
+    static constexpr int kRegsPer4 = 1;
+    __device__ static void dot16(const i32x4& w, const xreg_t* x, acc_t& acc) {
+        acc = __builtin_amdgcn_sdot4(w.x, static_cast<int>(x[0]), acc, false);
+        acc = __builtin_amdgcn_sdot4(w.y, static_cast<int>(x[1]), acc, false);
+        acc = __builtin_amdgcn_sdot4(w.z, static_cast<int>(x[2]), acc, false);
+        acc = __builtin_amdgcn_sdot4(w.w, static_cast<int>(x[3]), acc, false);
+    }
+    __device__ static float total(acc_t a) {
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) a += __shfl_xor(a, o, kWave);
+        return static_cast<float>(a);
+    }
+};
+template <>
+struct A8<FmtFp8> {
+    typedef float acc_t;
+    typedef float xreg_t;  // e4m3 values (the codes without the row scale)
+    __device__ static void encode(const FmtFp8::Row& r, f32x4 v, xreg_t* out) {
+        const f32x4 e = FmtFp8::value4(r.code4(v), 1.0f);
+        out[0] = e.x;
+        out[1] = e.y;
+        out[2] = e.z;
+        out[3] = e.w;
+    }
+    static constexpr int kRegsPer4 = 4;
+    __device__ static void dot16(const i32x4& w, const xreg_t* x, acc_t& acc) {
+        const int words[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            float wv[4];
+            CodeFp8::decode4(words[j], wv);
+#pragma unroll
+            for (int b = 0; b < 4; ++b) acc = fmaf(wv[b], x[4 * j + b], acc);
+        }
+    }
+    __device__ static float total(acc_t a) { return wave_sum(a); }
+};
+
+template <class Fmt, int kM, int kChunks, int kRows>
+__global__ __launch_bounds__(kBlockW8) void k_gemv_a8(const float* __restrict__ x, int64_t x_stride,
+                                                      const typename Fmt::code_t* __restrict__ q,
+                                                      const float* __restrict__ s, const float* __restrict__ bias,
+                                                      int64_t n, int64_t k, float* __restrict__ y, int64_t y_stride,
+                                                      int64_t rows_per_wave) {
+    using P = A8<Fmt>;
+    __shared__ f32x4 xs[kM][kChunks * 256];
+    __shared__ float red[kWavesW8][kM];
+    const int lane = threadIdx.x & (kWave - 1), wv = threadIdx.x >> 6;
+    const int64_t wave = uniform(static_cast<int64_t>(blockIdx.x) * kWavesW8 + wv);
+    const int64_t row_begin = wave * rows_per_wave;
+    const int64_t row_end = min(n, row_begin + rows_per_wave);
+    const int64_t row_last = max(row_begin, row_end - 1);
+    const int64_t row_clamp = min(row_last, n - 1);
+
+    auto load_rows = [&](int64_t row0, i32x4 (&wq)[kRows][kChunks]) {
+#pragma unroll
+        for (int r = 0; r < kRows; ++r)
+#pragma unroll
+            for (int c = 0; c < kChunks; ++c) {
+                const int64_t row = min(row0 + r, row_clamp);
+                const int64_t kb = min<int64_t>(1024 * c + 16 * lane, k - 16);
+                wq[r][c] = __builtin_nontemporal_load(reinterpret_cast<const i32x4*>(q + row * k + kb));
+            }
+    };
+    i32x4 wq[kRows][kChunks];
+    load_rows(row_begin, wq);
+
+    // x -> LDS (zero past K) and the NaN-ignoring absmax of each row over its K values
+    const int k4 = static_cast<int>(k >> 2);
+    float mx[kM];
+#pragma unroll
+    for (int m = 0; m < kM; ++m) mx[m] = -INFINITY;
+    for (int i = threadIdx.x; i < kM * kChunks * 256; i += kBlockW8) {
+        const int m = i / (kChunks * 256), j = i - m * (kChunks * 256);
+        const f32x4 v = j < k4 ? *reinterpret_cast<const f32x4*>(x + m * x_stride + 4 * j) : f32x4{0.f, 0.f, 0.f, 0.f};
+        xs[m][j] = v;
+        if (j < k4) {
+            const float a = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+#pragma unroll
+            for (int mm = 0; mm < kM; ++mm)
+                if (mm == m) mx[mm] = fmaxf(mx[mm], a);
+        }
+    }
+#pragma unroll
+    for (int m = 0; m < kM; ++m) {
+        const float w = wave_max(mx[m]);
+        if (lane == 0) red[wv][m] = w;
+    }
+    __syncthreads();
+    float sa[kM];
+#pragma unroll
+    for (int m = 0; m < kM; ++m) {
+        float r = red[0][m];
+#pragma unroll
+        for (int i = 1; i < kWavesW8; ++i) r = fmaxf(r, red[i][m]);
+        sa[m] = row_scale<Fmt>(absmax_finish(r));
+    }
+    // this lane's 16-value slices, coded
+    typename P::xreg_t xr[kM][kChunks][4 * P::kRegsPer4];
+#pragma unroll
+    for (int m = 0; m < kM; ++m) {
+        const typename Fmt::Row coder(sa[m]);
+#pragma unroll
+        for (int c = 0; c < kChunks; ++c)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) P::encode(coder, xs[m][c * 256 + 4 * lane + j], &xr[m][c][j * P::kRegsPer4]);
+    }
+    if (row_begin >= row_end) return;
+
+    for (int64_t row0 = row_begin; row0 < row_end; row0 += kRows) {
+        i32x4 cur[kRows][kChunks];
+#pragma unroll
+        for (int r = 0; r < kRows; ++r)
+#pragma unroll
+            for (int c = 0; c < kChunks; ++c) cur[r][c] = wq[r][c];
+        if (row0 + kRows < row_end) load_rows(row0 + kRows, wq);
+#pragma unroll
+        for (int r = 0; r < kRows; ++r) {
+            typename P::acc_t acc[kM];
+#pragma unroll
+            for (int m = 0; m < kM; ++m) acc[m] = 0;
+#pragma unroll
+            for (int c = 0; c < kChunks; ++c)
+#pragma unroll
+                for (int m = 0; m < kM; ++m) P::dot16(cur[r][c], xr[m][c], acc[m]);
+            const int64_t row = row0 + r;
+            const float sc = s[min(row, row_clamp)];
+#pragma unroll
+            for (int m = 0; m < kM; ++m) {
+                const float v = P::total(acc[m]);
+                if (lane == 0 && row < row_end) y[m * y_stride + row] = fmaf(v * sa[m], sc, bias ? bias[row] : 0.0f);
+            }
+        }
+    }
+}
+
 // Persistent grid: one block per CU (fewer if there are few rows), contiguous
 // row runs per wave, a multiple of kRows each.
 template <int kRows>
@@ -180,6 +331,61 @@ void dispatch_w8(int chunks, const float* x, int64_t xs, const typename Code::co
     case 7: launch_w8<Code, kM, 7>(x, xs, q, s, b, n, k, y, ys, st); break;
     default: launch_w8<Code, kM, 8>(x, xs, q, s, b, n, k, y, ys, st); break;
     }
+}
+
+template <class Fmt, int kM, int kChunks>
+void launch_a8(const float* x, int64_t xs, const typename Fmt::code_t* q, const float* s, const float* b, int64_t n,
+               int64_t k, float* y, int64_t ys, hipStream_t st) {
+    constexpr int kRows = 2;
+    int64_t blocks, rpw;
+    grid_for_rows<kRows>(n, &blocks, &rpw);
+    k_gemv_a8<Fmt, kM, kChunks, kRows><<<static_cast<unsigned>(blocks), kBlockW8, 0, st>>>(x, xs, q, s, b, n, k, y,
+                                                                                         ys, rpw);
+}
+
+template <class Fmt, int kM>
+void dispatch_a8(int chunks, const float* x, int64_t xs, const typename Fmt::code_t* q, const float* s,
+                 const float* b, int64_t n, int64_t k, float* y, int64_t ys, hipStream_t st) {
+    switch (chunks) {
+    case 1: launch_a8<Fmt, kM, 1>(x, xs, q, s, b, n, k, y, ys, st); break;
+    case 2: launch_a8<Fmt, kM, 2>(x, xs, q, s, b, n, k, y, ys, st); break;
+    case 3: launch_a8<Fmt, kM, 3>(x, xs, q, s, b, n, k, y, ys, st); break;
+    case 4: launch_a8<Fmt, kM, 4>(x, xs, q, s, b, n, k, y, ys, st); break;
+    case 5: launch_a8<Fmt, kM, 5>(x, xs, q, s, b, n, k, y, ys, st); break;
+    case 6: launch_a8<Fmt, kM, 6>(x, xs, q, s, b, n, k, y, ys, st); break;
+    case 7: launch_a8<Fmt, kM, 7>(x, xs, q, s, b, n, k, y, ys, st); break;
+    default: launch_a8<Fmt, kM, 8>(x, xs, q, s, b, n, k, y, ys, st); break;
+    }
+}
+
+// Activations quantized in place: K % 16 == 0, K <= 8192, x and q 16-byte
+// aligned.  Other shapes are rejected (TQ_EINVAL); callers run
+// tq_quantize_*_rowwise + tq_gemm_* for them.
+template <class Fmt>
+int gemv_a8(const float* x, int64_t m, const typename Fmt::code_t* q, const float* s, const float* bias, int64_t n,
+            int64_t k, float* y, hipStream_t st, const char* what) {
+    TQ_REQUIRE(m >= 0 && n >= 0 && k >= 0, "%s: negative shape", what);
+    TQ_REQUIRE(m <= 16, "%s: M=%lld > 16 (decode shapes)", what, (long long)m);
+    if (m == 0 || n == 0) return TQ_OK;
+    TQ_REQUIRE(x && q && s && y, "%s: null pointer", what);
+    TQ_REQUIRE(k > 0 && k % 16 == 0 && k <= 8 * 1024, "%s: K=%lld must be a positive multiple of 16 up to 8192", what,
+               (long long)k);
+    TQ_REQUIRE(aligned(x, 16) && aligned(q, 16) && aligned(s, 4) && aligned(y, 4) && (!bias || aligned(bias, 4)),
+               "%s: x and q must be 16-byte aligned, f32 pointers 4-byte aligned", what);
+    const int chunks = static_cast<int>((k + 1023) / 1024);
+    const int64_t per_pass = chunks <= 2 ? 4 : (chunks <= 4 ? 2 : 1);
+    for (int64_t m0 = 0; m0 < m; m0 += per_pass) {
+        const int64_t mm = (m - m0) < per_pass ? (m - m0) : per_pass;
+        const float* xp = x + m0 * k;
+        float* yp = y + m0 * n;
+        if (mm == 1) dispatch_a8<Fmt, 1>(chunks, xp, k, q, s, bias, n, k, yp, n, st);
+        else if (mm == 2) dispatch_a8<Fmt, 2>(chunks, xp, k, q, s, bias, n, k, yp, n, st);
+        else if (mm == 3) dispatch_a8<Fmt, 3>(chunks, xp, k, q, s, bias, n, k, yp, n, st);
+        else dispatch_a8<Fmt, 4>(chunks, xp, k, q, s, bias, n, k, yp, n, st);
+        const int rc = check_launch(what);
+        if (rc != TQ_OK) return rc;
+    }
+    return TQ_OK;
 }
 
 template <class Code>
@@ -227,6 +433,16 @@ int tq_gemv_w8(const float* x, int64_t m, const int8_t* q, const float* s, const
 int tq_gemv_fp8(const float* x, int64_t m, const uint8_t* q, const float* s, const float* bias,
                 int64_t n, int64_t k, float* y, tq_stream_t stream) {
     return gemv_8bit<CodeFp8>(x, m, q, s, bias, n, k, y, as_hip(stream), "tq_gemv_fp8");
+}
+
+int tq_gemv_w8a8(const float* x, int64_t m, const int8_t* qw, const float* sw, const float* bias, int64_t n,
+                 int64_t k, float* y, tq_stream_t stream) {
+    return gemv_a8<FmtI8>(x, m, qw, sw, bias, n, k, y, as_hip(stream), "tq_gemv_w8a8");
+}
+
+int tq_gemv_fp8a8(const float* x, int64_t m, const uint8_t* qw, const float* sw, const float* bias, int64_t n,
+                  int64_t k, float* y, tq_stream_t stream) {
+    return gemv_a8<FmtFp8>(x, m, qw, sw, bias, n, k, y, as_hip(stream), "tq_gemv_fp8a8");
 }
 
 }  // extern "C"

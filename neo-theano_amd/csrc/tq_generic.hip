@@ -75,7 +75,7 @@ __global__ __launch_bounds__(kGenBlock) void k_linear_w4_generic(const uint16_t*
     if (lane == 0) y[out] = total + (bias ? bias[j] : 0.f);
 }
 
-// acc[i, j] = sum_k qa[i, k] qw[j, k] (int32, exact); y = f32(acc) * sa[i] * sw[j] + b[j]
+// acc[i, j] = sum_k qa[i, k] qw[j, k] (int32, exact); y = fma(f32(acc) * sa[i], sw[j], b[j])
 __global__ __launch_bounds__(kGenBlock) void k_gemm_w8a8_generic(const int8_t* __restrict__ qa,
                                                                  const float* __restrict__ sa,
                                                                  const int8_t* __restrict__ qw,
@@ -95,7 +95,7 @@ __global__ __launch_bounds__(kGenBlock) void k_gemm_w8a8_generic(const int8_t* _
     acc = wave_sum_i32(acc);
     if (lane == 0) {
         if (acc_out) acc_out[out] = acc;
-        y[out] = static_cast<float>(acc) * sa[i] * sw[j] + (bias ? bias[j] : 0.f);
+        y[out] = fmaf(static_cast<float>(acc) * sa[i], sw[j], bias ? bias[j] : 0.f);
     }
 }
 
@@ -116,7 +116,7 @@ __global__ __launch_bounds__(kGenBlock) void k_gemm_fp8_generic(const uint8_t* _
     for (int64_t p = lane; p < k; p += kWave)
         acc += code_value(ar[p]) * code_value(wr[p]);
     acc = wave_sum(acc);
-    if (lane == 0) y[out] = acc * sa[i] * sw[j] + (bias ? bias[j] : 0.f);
+    if (lane == 0) y[out] = fmaf(acc * sa[i], sw[j], bias ? bias[j] : 0.f);
 }
 
 unsigned generic_grid(int64_t outputs) { return static_cast<unsigned>((outputs + kGenWaves - 1) / kGenWaves); }

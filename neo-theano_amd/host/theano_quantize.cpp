@@ -509,6 +509,14 @@ std::vector<uint16_t> to_bf16(const std::vector<double>& v) {
 
 }  // namespace
 
+namespace {
+// shapes the fused-activation decode GEMVs take
+bool fused_a8_ok(const void* x, const void* q, int64_t k) {
+    return k > 0 && k <= 8192 && k % 16 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0 &&
+           reinterpret_cast<uintptr_t>(q) % 16 == 0;
+}
+}  // namespace
+
 Result<QuantizedLinear> QuantizedLinear::from_tensors(const Tensor& weight, const std::optional<Tensor>& bias,
                                                       const QConfig& qconfig, hipStream_t stream) {
     return capture<QuantizedLinear>([&]() -> Result<QuantizedLinear> {
@@ -588,6 +596,11 @@ Result<void> QuantizedLinear::forward_device(const void* x, int64_t m, float* y,
             break;
         }
         case Mode::W8A8: {
+            if (m <= 16 && fused_a8_ok(x, w8_.codes.data(), k)) {  // quantize-in-GEMV, one launch
+                st = tq_gemv_w8a8(static_cast<const float*>(x), m, w8_.codes.data(), w8_.scales.data(), b, n, k, y,
+                                  ts);
+                break;
+            }
             if (!act_codes || !act_scales)
                 return TheanoError::invalid_argument("QuantizedLinear::forward_device: w8a8 needs activation scratch");
             st = tq_quantize_i8_rowwise(static_cast<const float*>(x), m, k, act_codes, act_scales, ts);
@@ -597,6 +610,11 @@ Result<void> QuantizedLinear::forward_device(const void* x, int64_t m, float* y,
             break;
         }
         case Mode::FP8: {
+            if (m <= 16 && fused_a8_ok(x, fp8_.codes.data(), k)) {
+                st = tq_gemv_fp8a8(static_cast<const float*>(x), m, fp8_.codes.data(), fp8_.scales.data(), b, n, k,
+                                   y, ts);
+                break;
+            }
             if (!act_codes || !act_scales)
                 return TheanoError::invalid_argument("QuantizedLinear::forward_device: fp8 needs activation scratch");
             auto* qa = reinterpret_cast<uint8_t*>(act_codes);

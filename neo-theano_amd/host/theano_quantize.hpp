@@ -336,9 +336,11 @@ class QuantizedLinear : public Module {
     // Device-resident forward: x is f32 [m, in] (w8, w8a8, fp8) or bf16 bits [m, in]
     // (w4), y is f32 [m, out]; enqueued on `stream`, no host synchronisation.  w8a8
     // and fp8 need `act_codes` (one byte per element, [m, in]) and `act_scales`
-    // (f32 [m]) device scratch; fp8 with m <= 16 runs the GEMV on the
-    // fake-quantized activations, held in `workspace` (workspace_bytes(m) bytes);
-    // w4 with m > 16 uses `workspace` (workspace_bytes(m) bytes) when given.
+    // (f32 [m]) device scratch.  With m <= 16 both quantize x inside the decode
+    // GEMV (tq_gemv_w8a8 / tq_gemv_fp8a8) when K % 16 == 0, K <= 8192 and x is
+    // 16-byte aligned; otherwise fp8 runs the GEMV on the fake-quantized
+    // activations held in `workspace` (workspace_bytes(m) bytes).  w4 with
+    // m > 16 uses `workspace` (workspace_bytes(m) bytes) when given.
     Result<void> forward_device(const void* x, int64_t m, float* y, hipStream_t stream,
                                 int8_t* act_codes = nullptr, float* act_scales = nullptr,
                                 void* workspace = nullptr, size_t workspace_bytes = 0) const;

@@ -51,6 +51,8 @@ SIGNATURES = {
     "tq_dequantize_i4_g128": [_p, _p, _i64, _i64, _p, _p],
     "tq_gemv_w8": [_p, _i64, _p, _p, _p, _i64, _i64, _p, _p],
     "tq_gemv_fp8": [_p, _i64, _p, _p, _p, _i64, _i64, _p, _p],
+    "tq_gemv_w8a8": [_p, _i64, _p, _p, _p, _i64, _i64, _p, _p],
+    "tq_gemv_fp8a8": [_p, _i64, _p, _p, _p, _i64, _i64, _p, _p],
     "tq_gemv_w4g128": [_p, _i64, _p, _p, _p, _i64, _i64, _p, _p],
     "tq_w4g128_tile_rows": [_i64],
     "tq_repack_w4g128_tiled": [_p, _p, _i64, _i64, _i64, _p, _p, _p],

@@ -17,9 +17,10 @@ Modes (chosen from the QConfig):
            activations (QConfig with weight_dtype and activation_dtype FP8);
   * "fp8_weight"  FP8 e4m3 weight-only, f32 activations (weight_dtype FP8,
            activations not FP8).
-Decode shapes (M <= 16 tokens) run the dequant-GEMV kernels (in "fp8" mode on
-the fake-quantized activations, the same product as the GEMM); prefill shapes
-run the i8-MFMA W8A8 GEMM, the fp8-MFMA GEMM or the bf16-MFMA W4A16 GEMM.
+Decode shapes (M <= 16 tokens) run the dequant-GEMV kernels; in "w8a8" and
+"fp8" modes the GEMV quantizes the activation rows itself (the same codes and
+product as quantize + GEMM, one launch).  Prefill shapes run the i8-MFMA W8A8
+GEMM, the fp8-MFMA GEMM or the bf16-MFMA W4A16 GEMM.
 """
 from __future__ import annotations
 
@@ -65,6 +66,11 @@ def _mode_of(qconfig: QConfig) -> str:
     if qconfig.weight_dtype == QuantDType.FP8:
         return "fp8" if qconfig.activation_dtype == QuantDType.FP8 else "fp8_weight"
     raise InvalidArgument(f"QuantizedLinear: unsupported weight dtype {qconfig.weight_dtype!r}")
+
+
+def _fused_a8_ok(x, q, k) -> bool:
+    """Shapes the fused-activation decode GEMVs take (tq_gemv_w8a8 / tq_gemv_fp8a8)."""
+    return 0 < k <= 8192 and k % 16 == 0 and x.data_ptr() % 16 == 0 and q.data_ptr() % 16 == 0
 
 
 class QuantizedLinear(Module):
@@ -143,6 +149,10 @@ class QuantizedLinear(Module):
                 mm = min(DECODE_MAX_M, m - m0)
                 _abi.call("tq_gemv_w8", ptr(x[m0:m0 + mm]), mm, ptr(self.qweight), ptr(self.scales),
                           ptr(self.bias), n, k, ptr(y[m0:m0 + mm]), stream())
+        elif self.mode in ("w8a8", "fp8") and m <= DECODE_MAX_M and _fused_a8_ok(x, self.qweight, k):
+            # activation quantization fused into the decode GEMV (one launch)
+            _abi.call("tq_gemv_w8a8" if self.mode == "w8a8" else "tq_gemv_fp8a8", ptr(x), m, ptr(self.qweight),
+                      ptr(self.scales), ptr(self.bias), n, k, ptr(y), stream())
         elif self.mode == "fp8" and m > DECODE_MAX_M:
             qa = torch.empty((m, k), dtype=torch.uint8, device=x.device)
             sa = torch.empty(m, dtype=torch.float32, device=x.device)

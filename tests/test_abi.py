@@ -105,6 +105,9 @@ def test_observer_scale_zp_matches_oracle(abi, oracle):
     ("tq_quantize_fp8_rowwise", [None, 4, 16, None, None, None]),         # null pointers
     ("tq_gemm_fp8", [None, None, None, None, None, -1, 16, 128, None, None]),  # negative shape
     ("tq_gemv_fp8", [None, 17, None, None, None, 16, 128, None, None]),   # M > 16
+    ("tq_gemv_w8a8", [16, 1, 16, 16, None, 16, 100, 16, None]),           # K % 16 (fused path)
+    ("tq_gemv_fp8a8", [16, 17, 16, 16, None, 16, 128, 16, None]),         # M > 16
+    ("tq_attention_f32", [16, 8, 16, 8, 16, 8, None, 0, 1, 4, 2, 200, 16, 8, None]),  # head_dim > 128
 ])
 def test_invalid_arguments_are_rejected(abi, call):
     from theano_quantize import InvalidArgument

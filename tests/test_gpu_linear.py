@@ -409,3 +409,47 @@ def test_gemm_w4g128_bf16_entry_points_agree(tq, oracle):
     with pytest.raises(InvalidArgument):
         _abi.call("tq_gemm_w4g128_bf16_ws", ptr(x), m, ptr(q), ptr(s), ptr(bias), n, k, ptr(ws), nb - 256,
                   ptr(y1), stream())
+
+
+# ------------------------------------------ decode W8A8 / FP8, fused activations
+@pytest.mark.parametrize("m,n,k", [(1, 4096, 4096), (3, 512, 1024), (16, 272, 8192), (5, 33, 48), (2, 4096, 128)])
+def test_gemv_w8a8_fused_equals_quantize_plus_gemm(tq, oracle, m, n, k):
+    """One launch (activation codes computed in the GEMV) gives the two-step
+    path's y bit for bit: same codes, exact int32 sums, same epilogue."""
+    import torch
+    from theano_quantize import _abi
+    from theano_quantize._tensor import ptr, stream
+
+    x = normal(61, (m, k), 1.0)
+    x[0, :5] = [0.0, -0.0, np.nan, 3e4, -3e4]
+    w = normal(61, (n, k), 0.02, stream=1)
+    b = normal(61, (n,), 0.1, stream=2)
+    xd, bd = dev_tensor(x), dev_tensor(b)
+    qw, sw = tq.quantize_per_channel_i8(dev_tensor(w))
+    y1 = torch.empty((m, n), dtype=torch.float32, device="cuda")
+    _abi.call("tq_gemv_w8a8", ptr(xd), m, ptr(qw), ptr(sw), ptr(bd), n, k, ptr(y1), stream())
+    qa, sa = tq.quantize_per_channel_i8(xd)
+    y2 = torch.empty((m, n), dtype=torch.float32, device="cuda")
+    _abi.call("tq_gemm_w8a8", ptr(qa), ptr(sa), ptr(qw), ptr(sw), ptr(bd), m, n, k, None, ptr(y2), stream())
+    assert np.array_equal(host(y1), host(y2))
+    rqa, rsa = oracle.quantize_i8_rowwise(x)
+    rqw, rsw = oracle.quantize_i8_rowwise(w)
+    assert_close(host(y1), oracle.linear_w8a8(rqa, rsa, rqw, rsw, b), RTOL, ATOL, "fused w8a8 vs oracle")
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 4096, 4096), (4, 512, 1024), (16, 272, 8192), (3, 40, 64)])
+def test_gemv_fp8a8_fused_vs_oracle(tq, oracle, m, n, k):
+    import torch
+    from theano_quantize import _abi
+    from theano_quantize._tensor import ptr, stream
+
+    x = normal(62, (m, k), 1.0)
+    w = normal(62, (n, k), 0.02, stream=1)
+    b = normal(62, (n,), 0.1, stream=2)
+    xd, bd = dev_tensor(x), dev_tensor(b)
+    qw, sw = tq.quantize_per_channel_fp8(dev_tensor(w))
+    y = torch.empty((m, n), dtype=torch.float32, device="cuda")
+    _abi.call("tq_gemv_fp8a8", ptr(xd), m, ptr(qw), ptr(sw), ptr(bd), n, k, ptr(y), stream())
+    rqa, rsa = oracle.quantize_fp8_rowwise(x)
+    rqw, rsw = oracle.quantize_fp8_rowwise(w)
+    assert_close(host(y), oracle.linear_fp8(rqa, rsa, rqw, rsw, b), RTOL, ATOL, "fused fp8 vs oracle")

@@ -43,8 +43,8 @@ def parse_args():
     p.add_argument("--steps", type=int, default=200)
     p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--only", default=None,
-                   help="run one workload: gemv_w4, gemv_w8, gemv_fp8, gemv_w4_m, w8a8, fp8, mha, storage, roundtrip, mlp, "
-                        "copy")
+                   help="run one workload: gemv_w4, gemv_w8, gemv_fp8, gemv_w4_m, w8a8_decode, w8a8, fp8, mha, storage, "
+                        "roundtrip, mlp, copy")
     p.add_argument("--no-secondary", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=12.0, help="bound of the CPU baseline sample (0: skip)")
     p.add_argument("--eager", action="store_true", help="time eager launches instead of a HIP graph")
@@ -209,6 +209,40 @@ def main():
                                    "hbm_frac": round(gbs / HBM_PEAK_GBS, 4), "bytes": b2}
         log(f"gemv_w8 M=1: {ms * 1e3:.2f} us/step  {gbs:.0f} GB/s")
         del copies
+
+    # ------------------------- decode W8A8: fused activation quantization
+    if not args.no_secondary and want("w8a8_decode"):
+        n2 = k2 = 4096
+        w = normal_f32(1, (n2, k2), 0.02)
+        res = {}
+        for kind, qfn, fused, quant, gemm in (
+                ("w8a8", tq.quantize_per_channel_i8, "tq_gemv_w8a8", "tq_quantize_i8_rowwise", "tq_gemm_w8a8"),
+                ("fp8", tq.quantize_per_channel_fp8, "tq_gemv_fp8a8", "tq_quantize_fp8_rowwise", "tq_gemm_fp8")):
+            copies = quant_copies(w, qfn, rotation(n2 * k2))
+            x = dt(normal_f32(1, (1, k2), 1.0, stream=1))
+            y = torch.empty((1, n2), dtype=torch.float32, device=dev)
+            qa = torch.empty((1, k2), dtype=torch.int8 if kind == "w8a8" else torch.uint8, device=dev)
+            sa = torch.empty(1, dtype=torch.float32, device=dev)
+
+            def launch_fused(i, fused=fused, copies=copies, x=x, y=y):
+                q, s = copies[i % len(copies)]
+                _abi.call(fused, ptr(x), 1, ptr(q), ptr(s), None, n2, k2, ptr(y), stream())
+
+            def launch_two(i, quant=quant, gemm=gemm, copies=copies, x=x, y=y, qa=qa, sa=sa, kind=kind):
+                q, s = copies[i % len(copies)]
+                _abi.call(quant, ptr(x), 1, k2, ptr(qa), ptr(sa), stream())
+                if kind == "w8a8":
+                    _abi.call(gemm, ptr(qa), ptr(sa), ptr(q), ptr(s), None, 1, n2, k2, None, ptr(y), stream())
+                else:
+                    _abi.call(gemm, ptr(qa), ptr(sa), ptr(q), ptr(s), None, 1, n2, k2, ptr(y), stream())
+
+            ms_f, mode_f = timer.run(launch_fused, args.steps, args.warmup)
+            ms_t, _ = timer.run(launch_two, args.steps, args.warmup)
+            res[kind] = {"fused_us": round(ms_f * 1e3, 3), "quantize_plus_gemm_us": round(ms_t * 1e3, 3),
+                         "timing": mode_f}
+            log(f"decode {kind} M=1 4096x4096: fused {ms_f * 1e3:.2f} us, quantize + GEMM {ms_t * 1e3:.2f} us")
+            del copies
+        secondary["a8_decode_m1_n4096_k4096"] = res
 
     # ------------------------------------------------ FP8 GEMV (C2 shape)
     if not args.no_secondary and want("gemv_fp8"):

@@ -10,13 +10,17 @@
 // occupies columns [h*D, (h+1)*D) (the fused QKV projection's output is read in
 // place with ld = 3E); O is [B*S, ldo].
 //
-// One block per (16 queries, head, batch): 4 waves of 4 query rows.  Keys run
-// in tiles of 64 staged in LDS (K padded against bank conflicts); lane j
-// scores key j of the tile for the wave's 4 rows (q rows broadcast from LDS),
-// an online softmax keeps the running max / sum per row, and P V accumulates
-// with lanes over the head dimension.  A running max of -inf (every key so far
-// masked) leaves the row untouched; a row masked everywhere ends as 0/0 = NaN,
-// as the reference's softmax gives.
+// One block per (128 queries, head, batch): 4 waves of 32 query rows on the
+// f32 matrix cores (v_mfma_f32_32x32x2_f32).  Keys run in tiles of 32, staged
+// in LDS for the 4 waves (K row-major, V transposed; both padded against bank
+// conflicts), the next tile's loads in flight during the current tile's work.
+// Per tile a wave computes S^T = K Q^T (lane = query, registers = keys, so the
+// softmax of a query row is in-lane plus one partner lane), updates its
+// running max / sum, and accumulates O^T += V^T P^T with the probabilities as
+// they came out of the first product.  The head dimension is padded with zeros
+// to 32, 64 or 128.  A running max of -inf (every key so far masked) leaves the
+// row untouched; a row masked everywhere ends as 0/0 = NaN, as the
+// reference's softmax gives.
 #include <cmath>
 
 #include "tq_internal.h"
@@ -25,118 +29,152 @@ namespace tq {
 namespace {
 
 constexpr int kWaves = 4;
-constexpr int kRowsPerWave = 4;
-constexpr int kQB = kWaves * kRowsPerWave;  // queries per block
-constexpr int kKT = 64;                     // keys per tile
+constexpr int kQW = 32;              // query rows per wave
+constexpr int kQB = kWaves * kQW;    // per block
+constexpr int kKT = 32;              // keys per tile
 constexpr int kMaxD = 128;
 
+__device__ __forceinline__ f32x16 mfma_f32(float a, float b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+}
+
+template <int kDP>
 __global__ __launch_bounds__(kWaves * kWave) void k_attention(const float* __restrict__ q, int64_t ldq,
                                                               const float* __restrict__ k, int64_t ldk,
                                                               const float* __restrict__ v, int64_t ldv,
                                                               const float* __restrict__ mask, int64_t mask_batch,
                                                               int S, int D, float scale, float* __restrict__ o,
                                                               int64_t ldo) {
-    __shared__ float kt[kKT][kMaxD + 1];
-    __shared__ float vt[kKT][kMaxD];
-    __shared__ f32x4 qs[kWaves][kMaxD];          // the wave's 4 rows, element d of each in one f32x4
-    __shared__ f32x4 ps[kWaves][kKT];            // probabilities of the tile for the 4 rows
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    constexpr int kHalf = kDP / 2;     // d positions per lane group in S^T = K Q^T
+    constexpr int kKRow = kDP + 4;     // K tile row (floats), padded
+    constexpr int kVRow = kKT + 4;     // transposed V tile row, padded
+    constexpr int kBlocks = kDP / 32;  // 32-wide d blocks of O^T
+    constexpr int kElems = kKT * kDP / (kWaves * kWave);  // tile elements per thread (K and V each)
+    __shared__ __attribute__((aligned(16))) float ks[2][kKT * kKRow];
+    __shared__ __attribute__((aligned(16))) float vs[2][kDP * kVRow];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 5, lr = lane & 31;
     const int h = blockIdx.y, b = blockIdx.z;
-    const int i0 = blockIdx.x * kQB + wave * kRowsPerWave;  // first query row of this wave
-    const int64_t rowbase = static_cast<int64_t>(b) * S;
+    const int qrow = blockIdx.x * kQB + wave * kQW + lr;  // this lane's query row
+    const int64_t base = static_cast<int64_t>(b) * S;
     const int col = h * D;
 
-    // q rows of this wave (rows past S read row S-1; never stored)
-    for (int d = lane; d < D; d += kWave) {
-        f32x4 t;
-        t.x = q[(rowbase + min(i0 + 0, S - 1)) * ldq + col + d];
-        t.y = q[(rowbase + min(i0 + 1, S - 1)) * ldq + col + d];
-        t.z = q[(rowbase + min(i0 + 2, S - 1)) * ldq + col + d];
-        t.w = q[(rowbase + min(i0 + 3, S - 1)) * ldq + col + d];
-        qs[wave][d] = t;
-    }
-    const float* mrow[kRowsPerWave];
+    // Q fragment: d = g * kHalf + t (rows past S read row S-1; never stored)
+    float qf[kHalf];
+    {
+        const float* qr = q + (base + min(qrow, S - 1)) * ldq + col;
 #pragma unroll
-    for (int r = 0; r < kRowsPerWave; ++r)
-        mrow[r] = mask ? mask + ((mask_batch == 1 ? 0 : static_cast<int64_t>(b)) * S + min(i0 + r, S - 1)) *
-                                    static_cast<int64_t>(S)
-                       : nullptr;
-
-    float m[kRowsPerWave], l[kRowsPerWave], acc[kRowsPerWave][2];
-#pragma unroll
-    for (int r = 0; r < kRowsPerWave; ++r) {
-        m[r] = -INFINITY;
-        l[r] = 0.f;
-        acc[r][0] = acc[r][1] = 0.f;
+        for (int t = 0; t < kHalf; ++t) {
+            const int d = g * kHalf + t;
+            qf[t] = d < D ? qr[d] : 0.f;
+        }
     }
+    const float* mrow =
+        mask ? mask + ((mask_batch == 1 ? 0 : static_cast<int64_t>(b)) * S + min(qrow, S - 1)) * static_cast<int64_t>(S)
+             : nullptr;
 
+    // tile loads: element e = tid + 256 i -> key e / kDP, d e % kDP (coalesced along d)
+    float kreg[kElems], vreg[kElems];
+    auto load_tile = [&](int j0) {
+#pragma unroll
+        for (int i = 0; i < kElems; ++i) {
+            const int e = tid + i * kWaves * kWave, key = e / kDP, d = e % kDP;
+            const bool ok = j0 + key < S && d < D;
+            const int64_t row = base + (ok ? j0 + key : 0);
+            kreg[i] = ok ? k[row * ldk + col + d] : 0.f;
+            vreg[i] = ok ? v[row * ldv + col + d] : 0.f;
+        }
+    };
+    auto store_tile = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < kElems; ++i) {
+            const int e = tid + i * kWaves * kWave, key = e / kDP, d = e % kDP;
+            ks[buf][key * kKRow + d] = kreg[i];
+            vs[buf][d * kVRow + key] = vreg[i];
+        }
+    };
+
+    f32x16 ot[kBlocks];
+#pragma unroll
+    for (int c = 0; c < kBlocks; ++c) ot[c] = f32x16{};
+    float m = -INFINITY, l = 0.f;
+
+    load_tile(0);
+    store_tile(0);
+    __syncthreads();
+    int buf = 0;
     for (int j0 = 0; j0 < S; j0 += kKT) {
-        __syncthreads();  // previous tile fully consumed
-        for (int e = tid; e < kKT * D; e += kWaves * kWave) {
-            const int j = e / D, d = e - j * D;
-            const bool ok = j0 + j < S;
-            const int64_t row = rowbase + (ok ? j0 + j : 0);
-            kt[j][d] = ok ? k[row * ldk + col + d] : 0.f;
-            vt[j][d] = ok ? v[row * ldv + col + d] : 0.f;
-        }
-        __syncthreads();
-        // scores of key j0 + lane for the 4 rows
-        float s[kRowsPerWave] = {0.f, 0.f, 0.f, 0.f};
-        for (int d = 0; d < D; ++d) {
-            const float kv = kt[lane][d];
-            const f32x4 qv = qs[wave][d];
-            s[0] = fmaf(qv.x, kv, s[0]);
-            s[1] = fmaf(qv.y, kv, s[1]);
-            s[2] = fmaf(qv.z, kv, s[2]);
-            s[3] = fmaf(qv.w, kv, s[3]);
-        }
-        const bool kval = j0 + lane < S;
-        float p[kRowsPerWave];
+        const bool more = j0 + kKT < S;
+        if (more) load_tile(j0 + kKT);  // in flight during this tile
+
+        // S^T[key][q] = sum_d K[key][d] Q[q][d]: lane holds keys 8(r/4) + 4g + r%4 of query lr
+        f32x16 st = f32x16{};
+        const float* kr = &ks[buf][lr * kKRow + g * kHalf];
 #pragma unroll
-        for (int r = 0; r < kRowsPerWave; ++r) {
-            float sc = s[r] * scale;
-            if (mrow[r] && kval) sc += mrow[r][j0 + lane];
-            sc = kval ? sc : -INFINITY;
-            const float mt = wave_max(sc);
-            const float mn = fmaxf(m[r], mt);
-            const float base = mn == -INFINITY ? 0.f : mn;  // all masked so far: nothing to add
-            p[r] = expf(sc - base);
-            const float alpha = expf(m[r] - base);
-            l[r] = l[r] * alpha + wave_sum(p[r]);
-            acc[r][0] *= alpha;
-            acc[r][1] *= alpha;
-            m[r] = mn;
+        for (int t = 0; t < kHalf; t += 4) {
+            const f32x4 kv = *reinterpret_cast<const f32x4*>(kr + t);
+            st = mfma_f32(kv.x, qf[t], st);
+            st = mfma_f32(kv.y, qf[t + 1], st);
+            st = mfma_f32(kv.z, qf[t + 2], st);
+            st = mfma_f32(kv.w, qf[t + 3], st);
         }
-        // the wave's lanes exchange p through LDS (in order within a wave)
-        ps[wave][lane] = f32x4{p[0], p[1], p[2], p[3]};
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        const int jn = min(kKT, S - j0);
-        for (int j = 0; j < jn; ++j) {
-            const f32x4 pj = ps[wave][j];
+        float p[16];
+        float mt = -INFINITY;
 #pragma unroll
-            for (int c = 0; c < 2; ++c) {
-                const int d = lane + c * kWave;
-                if (d < D) {
-                    const float vv = vt[j][d];
-                    acc[0][c] = fmaf(pj.x, vv, acc[0][c]);
-                    acc[1][c] = fmaf(pj.y, vv, acc[1][c]);
-                    acc[2][c] = fmaf(pj.z, vv, acc[2][c]);
-                    acc[3][c] = fmaf(pj.w, vv, acc[3][c]);
-                }
+        for (int r = 0; r < 16; ++r) {
+            const int key = j0 + 8 * (r >> 2) + 4 * g + (r & 3);
+            float sc = st[r] * scale;
+            if (key < S) {
+                if (mrow) sc += mrow[key];
+            } else {
+                sc = -INFINITY;
+            }
+            p[r] = sc;
+            mt = fmaxf(mt, sc);
+        }
+        mt = fmaxf(mt, __shfl_xor(mt, 32, kWave));  // the partner lane holds the other 16 keys
+        const float mn = fmaxf(m, mt);
+        const float base_m = mn == -INFINITY ? 0.f : mn;  // all masked so far: nothing to add
+        float ls = 0.f;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            p[r] = expf(p[r] - base_m);
+            ls += p[r];
+        }
+        ls += __shfl_xor(ls, 32, kWave);
+        const float alpha = expf(m - base_m);
+        l = l * alpha + ls;
+        m = mn;
+        // O^T[d][q] += sum_key V[key][d] P[q][key]; step t of a 4-key run uses key 8a + 4g + b
+#pragma unroll
+        for (int c = 0; c < kBlocks; ++c) {
+            ot[c] *= alpha;
+            const float* vr = &vs[buf][(32 * c + lr) * kVRow + 4 * g];
+#pragma unroll
+            for (int a = 0; a < 4; ++a) {
+                const f32x4 vv = *reinterpret_cast<const f32x4*>(vr + 8 * a);
+                ot[c] = mfma_f32(vv.x, p[4 * a + 0], ot[c]);
+                ot[c] = mfma_f32(vv.y, p[4 * a + 1], ot[c]);
+                ot[c] = mfma_f32(vv.z, p[4 * a + 2], ot[c]);
+                ot[c] = mfma_f32(vv.w, p[4 * a + 3], ot[c]);
             }
         }
-    }
-#pragma unroll
-    for (int r = 0; r < kRowsPerWave; ++r) {
-        const int i = i0 + r;
-        if (i >= S) continue;
-#pragma unroll
-        for (int c = 0; c < 2; ++c) {
-            const int d = lane + c * kWave;
-            if (d < D) o[(rowbase + i) * ldo + col + d] = acc[r][c] / l[r];
+        if (more) {
+            store_tile(buf ^ 1);  // the other buffer: last read before the previous barrier
+            __syncthreads();
+            buf ^= 1;
         }
+    }
+    // lane holds O^T[d = 32c + 8(r/4) + 4g + r%4][q = lr]
+    if (qrow < S) {
+        float* orow = o + (base + qrow) * ldo + col;
+        const float inv = 1.0f / l;
+#pragma unroll
+        for (int c = 0; c < kBlocks; ++c)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int d = 32 * c + 8 * (r >> 2) + 4 * g + (r & 3);
+                if (d < D) orow[d] = ot[c][r] * inv;
+            }
     }
 }
 
@@ -164,8 +202,16 @@ extern "C" int tq_attention_f32(const float* q, int64_t ldq, const float* k, int
     const dim3 grid(static_cast<unsigned>((seq + kQB - 1) / kQB), static_cast<unsigned>(heads),
                     static_cast<unsigned>(batch));
     const float scale = static_cast<float>(1.0 / std::sqrt(static_cast<double>(head_dim)));
-    k_attention<<<grid, kWaves * kWave, 0, as_hip(stream)>>>(q, ldq, k, ldk, v, ldv, mask_batch ? mask : nullptr,
-                                                             mask_batch, static_cast<int>(seq),
-                                                             static_cast<int>(head_dim), scale, out, ldo);
+    const float* mk = mask_batch ? mask : nullptr;
+    const int S = static_cast<int>(seq), D = static_cast<int>(head_dim);
+    if (head_dim <= 32)
+        k_attention<32><<<grid, kWaves * kWave, 0, as_hip(stream)>>>(q, ldq, k, ldk, v, ldv, mk, mask_batch, S, D,
+                                                                      scale, out, ldo);
+    else if (head_dim <= 64)
+        k_attention<64><<<grid, kWaves * kWave, 0, as_hip(stream)>>>(q, ldq, k, ldk, v, ldv, mk, mask_batch, S, D,
+                                                                      scale, out, ldo);
+    else
+        k_attention<128><<<grid, kWaves * kWave, 0, as_hip(stream)>>>(q, ldq, k, ldk, v, ldv, mk, mask_batch, S, D,
+                                                                       scale, out, ldo);
     return check_launch("tq_attention_f32");
 }

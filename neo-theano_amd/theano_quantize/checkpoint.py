@@ -33,7 +33,10 @@ weight-only) or "fp8_e4m3_per_channel_a8" (FP8 weights and activations)),
 INT4), ``<name>.in_features`` and
 ``<name>.out_features``; a ``QuantizedMLP`` ``<name>`` is the three INT4
 Linears ``<name>.gate``, ``<name>.up``, ``<name>.down`` plus ``<name>.quant`` =
-"mlp_int4_g128".  ``format`` = "theano-quantize/1".
+"mlp_int4_g128".  A ``QuantizedMultiheadAttention`` ``<name>`` is the Linears
+``<name>.qkv`` (the fused [3E, E] projection) and ``<name>.out_proj`` plus
+``<name>.attention`` = "multihead" and ``<name>.num_heads``.  ``format`` =
+"theano-quantize/1".
 """
 from __future__ import annotations
 
@@ -177,12 +180,18 @@ def _linear_entries(name, lin, tensors, meta):
 
 
 def save_quantized(modules) -> bytes:
-    """{name: QuantizedLinear | QuantizedMLP} -> safetensors bytes (layout in the module docstring)."""
-    from .nn import QuantizedMLP
+    """{name: QuantizedLinear | QuantizedMLP | QuantizedMultiheadAttention} ->
+    safetensors bytes (layout in the module docstring)."""
+    from .nn import QuantizedMLP, QuantizedMultiheadAttention
 
     tensors, meta = {}, {"format": FORMAT}
     for name, mod in modules.items():
-        if isinstance(mod, QuantizedMLP):
+        if isinstance(mod, QuantizedMultiheadAttention):
+            meta[f"{name}.attention"] = "multihead"
+            meta[f"{name}.num_heads"] = str(mod.num_heads)
+            _linear_entries(f"{name}.qkv", mod.qkv, tensors, meta)
+            _linear_entries(f"{name}.out_proj", mod.out_proj, tensors, meta)
+        elif isinstance(mod, QuantizedMLP):
             meta[f"{name}.quant"] = "mlp_int4_g128"
             meta[f"{name}.group_size"] = "128"
             meta[f"{name}.hidden"] = str(mod.d)
@@ -206,15 +215,19 @@ def _need(tensors, key, dtype, shape):
 
 
 def load_quantized(data: bytes, device="cuda"):
-    """safetensors bytes -> {name: QuantizedLinear | QuantizedMLP} with the codes and
-    scales copied into device buffers as stored (no re-quantization)."""
-    import torch
-
-    from .nn import QuantizedLinear, QuantizedMLP
-
+    """safetensors bytes -> {name: QuantizedLinear | QuantizedMLP |
+    QuantizedMultiheadAttention} with the codes and scales copied into device
+    buffers as stored (no re-quantization)."""
     tensors, meta, dtypes = _parse(data)
     if meta.get("format") != FORMAT:
         raise InvalidArgument(f"load_quantized: not a {FORMAT} checkpoint (format={meta.get('format')!r})")
+    return _load(tensors, meta, dtypes, device)
+
+
+def _load(tensors, meta, dtypes, device):
+    import torch
+
+    from .nn import QuantizedLinear, QuantizedMLP, QuantizedMultiheadAttention
 
     def dev(a):
         return torch.from_numpy(np.ascontiguousarray(a)).to(device)
@@ -224,6 +237,9 @@ def load_quantized(data: bytes, device="cuda"):
         if not key.endswith(".quant"):
             continue
         name = key[:-len(".quant")]
+        owner = name.rsplit(".", 1)[0] if "." in name else None
+        if owner is not None and meta.get(f"{owner}.attention") == "multihead":
+            continue  # the projections of an attention module, assembled below
         if kind == "mlp_int4_g128":
             d, f = int(meta[f"{name}.hidden"]), int(meta[f"{name}.intermediate"])
             parts = []
@@ -256,4 +272,12 @@ def load_quantized(data: bytes, device="cuda"):
         b = tensors.get(f"{name}.bias")
         bias = None if b is None else dev(_need(tensors, f"{name}.bias", np.float32, (n,)))
         out[name] = QuantizedLinear(mode, k, n, q, s, bias)
+    for key, kind in meta.items():
+        if key.endswith(".attention") and kind == "multihead":
+            name = key[:-len(".attention")]
+            pre = name + "."
+            sub = _load({k[len(pre):]: v for k, v in tensors.items() if k.startswith(pre)},
+                        {k[len(pre):]: v for k, v in meta.items() if k.startswith(pre)},
+                        {k[len(pre):]: v for k, v in dtypes.items() if k.startswith(pre)}, device)
+            out[name] = QuantizedMultiheadAttention(int(meta[f"{name}.num_heads"]), sub["qkv"], sub["out_proj"])
     return out

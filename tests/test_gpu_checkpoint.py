@@ -90,3 +90,18 @@ def test_checkpoint_from_the_safetensors_package(tq, oracle):
     xb = f32_to_bf16_bits(normal(86, (m, k), 1.0))
     y = host(lin(bf16(normal(86, (m, k), 1.0))))
     assert_close(y, oracle.linear_w4g128_bf16(xb, p, s, b), RTOL, ATOL, "checkpoint w4")
+
+
+def test_attention_roundtrip(tq):
+    import torch
+
+    E, H = 128, 4
+    ws = [dev(normal(87, (E, E), 0.05, stream=i)) for i in range(4)]
+    bs = [dev(normal(87, (E,), 0.1, stream=10 + i)) for i in range(4)]
+    for cfg in (tq.QConfig.default_int4(), tq.QConfig(tq.QuantDType.FP8, tq.QuantDType.FP8, True, True)):
+        mha = tq.QuantizedMultiheadAttention.from_tensors(H, *ws, *bs, qconfig=cfg)
+        back = tq.load_quantized(tq.save_quantized({"layers.0.attn": mha}))["layers.0.attn"]
+        assert isinstance(back, tq.QuantizedMultiheadAttention) and back.num_heads == H
+        assert torch.equal(back.qkv.qweight, mha.qkv.qweight) and back.qkv.mode == mha.qkv.mode
+        x = dev(normal(88, (2, 9, E), 1.0))
+        assert np.array_equal(host(mha(x)), host(back(x)))

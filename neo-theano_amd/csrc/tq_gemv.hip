@@ -158,6 +158,8 @@ struct A8<FmtI8> {
     typedef int32_t acc_t;
     typedef uint32_t xreg_t;  // 4 codes
     __device__ static void encode(const FmtI8::Row& r, f32x4 v, xreg_t* out) { out[0] = r.code4(v); }
+    __device__ static f32x4 pack(const xreg_t* e) { return f32x4{__uint_as_float(e[0]), 0.f, 0.f, 0.f}; }
+    __device__ static void unpack(const f32x4& v, xreg_t* e) { e[0] = __float_as_uint(v.x); }
     static constexpr int kRegsPer4 = 1;
     __device__ static void dot16(const i32x4& w, const xreg_t* x, acc_t& acc) {
         acc = __builtin_amdgcn_sdot4(w.x, static_cast<int>(x[0]), acc, false);
@@ -181,6 +183,13 @@ struct A8<FmtFp8> {
         out[1] = e.y;
         out[2] = e.z;
         out[3] = e.w;
+    }
+    __device__ static f32x4 pack(const xreg_t* e) { return f32x4{e[0], e[1], e[2], e[3]}; }
+    __device__ static void unpack(const f32x4& v, xreg_t* e) {
+        e[0] = v.x;
+        e[1] = v.y;
+        e[2] = v.z;
+        e[3] = v.w;
     }
     static constexpr int kRegsPer4 = 4;
     __device__ static void dot16(const i32x4& w, const xreg_t* x, acc_t& acc) {
@@ -255,16 +264,25 @@ __global__ __launch_bounds__(kBlockW8) void k_gemv_a8(const float* __restrict__ 
         for (int i = 1; i < kWavesW8; ++i) r = fmaxf(r, red[i][m]);
         sa[m] = row_scale<Fmt>(absmax_finish(r));
     }
-    // this lane's 16-value slices, coded
+    // the block codes each 4-value entry once (in place in LDS), then every lane
+    // copies its 16-value slices into registers
+    for (int i = threadIdx.x; i < kM * kChunks * 256; i += kBlockW8) {
+        const int m = i / (kChunks * 256), j = i - m * (kChunks * 256);
+        typename P::xreg_t e[P::kRegsPer4];
+        float sm = sa[0];
+#pragma unroll
+        for (int mm = 1; mm < kM; ++mm) sm = mm == m ? sa[mm] : sm;
+        P::encode(typename Fmt::Row(sm), xs[m][j], e);
+        xs[m][j] = P::pack(e);
+    }
+    __syncthreads();
     typename P::xreg_t xr[kM][kChunks][4 * P::kRegsPer4];
 #pragma unroll
-    for (int m = 0; m < kM; ++m) {
-        const typename Fmt::Row coder(sa[m]);
+    for (int m = 0; m < kM; ++m)
 #pragma unroll
         for (int c = 0; c < kChunks; ++c)
 #pragma unroll
-            for (int j = 0; j < 4; ++j) P::encode(coder, xs[m][c * 256 + 4 * lane + j], &xr[m][c][j * P::kRegsPer4]);
-    }
+            for (int j = 0; j < 4; ++j) P::unpack(xs[m][c * 256 + 4 * lane + j], &xr[m][c][j * P::kRegsPer4]);
     if (row_begin >= row_end) return;
 
     for (int64_t row0 = row_begin; row0 < row_end; row0 += kRows) {

@@ -793,6 +793,155 @@ std::vector<Tensor> QuantizedMLP::parameters() const {
     return out;
 }
 
+// ------------------------------------------------- QuantizedMultiheadAttention
+
+namespace {
+
+// rows [r0, r0 + n) of a [rows, ...] tensor
+Tensor row_slice(const Tensor& t, size_t r0, size_t n) {
+    const size_t cols = t.ndim() == 2 ? t.shape()[1] : 1;
+    std::vector<double> v(t.data() + r0 * cols, t.data() + (r0 + n) * cols);
+    return t.ndim() == 2 ? Tensor::from_slice(std::move(v), {n, cols}) : Tensor::from_slice(std::move(v), {n});
+}
+
+// y [m, n] f32 = layer(x [m, in] f32) on the device, with the mode's activation
+// type and scratch (device buffers owned here, released after the stream syncs)
+void run_projection(const QuantizedLinear& l, const float* x, int64_t m, float* y, hipStream_t st) {
+    const auto ts = reinterpret_cast<tq_stream_t>(st);
+    const size_t k = l.in_features();
+    DeviceBuffer<uint16_t> xb;
+    const void* xin = x;
+    if (l.mode() == QuantizedLinear::Mode::W4) {
+        xb = DeviceBuffer<uint16_t>(static_cast<size_t>(m) * k);
+        check(tq_convert(x, TQ_DT_F32, xb.data(), TQ_DT_BF16, m * static_cast<int64_t>(k), ts), "bf16 activations");
+        xin = xb.data();
+    }
+    DeviceBuffer<int8_t> codes(static_cast<size_t>(m) * k);
+    DeviceBuffer<float> scales(static_cast<size_t>(m));
+    const size_t wsb = l.workspace_bytes(m);
+    DeviceBuffer<uint8_t> ws(std::max<size_t>(wsb, 1));
+    l.forward_device(xin, m, y, st, codes.data(), scales.data(), wsb ? ws.data() : nullptr, wsb).unwrap();
+    check_hip(hipStreamSynchronize(st), "QuantizedMultiheadAttention projection");
+}
+
+}  // namespace
+
+Result<QuantizedMultiheadAttention> QuantizedMultiheadAttention::from_tensors(
+    size_t num_heads, const Tensor& wq, const Tensor& wk, const Tensor& wv, const Tensor& wo,
+    const std::optional<Tensor>& bq, const std::optional<Tensor>& bk, const std::optional<Tensor>& bv,
+    const std::optional<Tensor>& bo, const QConfig& qconfig, hipStream_t stream) {
+    return capture<QuantizedMultiheadAttention>([&]() -> Result<QuantizedMultiheadAttention> {
+        if (wq.ndim() != 2 || wq.shape()[0] != wq.shape()[1] || wk.shape() != wq.shape() || wv.shape() != wq.shape() ||
+            wo.shape() != wq.shape())
+            return TheanoError::shape_mismatch("QuantizedMultiheadAttention: the four weights must be [E, E]");
+        const size_t e = wq.shape()[0];
+        if (num_heads == 0 || e % num_heads)
+            return TheanoError::invalid_argument("QuantizedMultiheadAttention: embed_dim % num_heads != 0");
+        std::vector<double> cat;
+        cat.reserve(3 * e * e);
+        for (const Tensor* w : {&wq, &wk, &wv}) cat.insert(cat.end(), w->data(), w->data() + e * e);
+        std::optional<Tensor> bcat;
+        if (bq || bk || bv) {
+            std::vector<double> b(3 * e, 0.0);
+            const std::optional<Tensor>* bs[3] = {&bq, &bk, &bv};
+            for (size_t i = 0; i < 3; ++i)
+                if (*bs[i]) {
+                    if ((*bs[i])->numel() != e)
+                        return TheanoError::shape_mismatch("QuantizedMultiheadAttention: bias must be [E]");
+                    std::copy((*bs[i])->data(), (*bs[i])->data() + e, b.begin() + i * e);
+                }
+            bcat = Tensor::from_slice(std::move(b), {3 * e});
+        }
+        QuantizedMultiheadAttention a;
+        a.e_ = e;
+        a.h_ = num_heads;
+        a.stream_ = stream;
+        auto qkv = QuantizedLinear::from_tensors(Tensor::from_slice(std::move(cat), {3 * e, e}), bcat, qconfig, stream);
+        if (qkv.is_err()) return qkv.unwrap_err();
+        auto out = QuantizedLinear::from_tensors(wo, bo, qconfig, stream);
+        if (out.is_err()) return out.unwrap_err();
+        a.qkv_ = std::move(qkv).unwrap();
+        a.out_ = std::move(out).unwrap();
+        return std::move(a);
+    });
+}
+
+Result<Tensor> QuantizedMultiheadAttention::forward_with_mask(const Tensor& query, const Tensor& key,
+                                                              const Tensor& value,
+                                                              const std::optional<Tensor>& mask) const {
+    return capture<Tensor>([&]() -> Result<Tensor> {
+        const auto& sh = query.shape();
+        if (query.ndim() != 3 || sh[2] != e_ || key.shape() != sh || value.shape() != sh)
+            return TheanoError::shape_mismatch("QuantizedMultiheadAttention: query, key, value must be [batch, seq, " +
+                                               std::to_string(e_) + "], got " + shape_str(sh));
+        const size_t b = sh[0], s = sh[1], m = b * s;
+        int64_t mb = 0;
+        if (mask) {
+            const auto& ms = mask->shape();
+            const bool ok3 = ms.size() == 3 && ms[1] == s && ms[2] == s;
+            const bool ok4 = ms.size() == 4 && ms[1] == 1 && ms[2] == s && ms[3] == s;
+            if (!(ok3 || ok4) || (ms[0] != 1 && ms[0] != b))
+                return TheanoError::shape_mismatch("QuantizedMultiheadAttention: mask must be [batch or 1, (1,) seq, seq]");
+            mb = static_cast<int64_t>(ms[0]);
+        }
+        const hipStream_t st = stream_;
+        const bool self = &query == &key && &key == &value;
+        // fused projections: [m, 3E] per distinct input
+        std::vector<DeviceBuffer<float>> proj;
+        for (const Tensor* in : self ? std::vector<const Tensor*>{&query} : std::vector<const Tensor*>{&query, &key, &value}) {
+            std::vector<float> xf(in->data(), in->data() + m * e_);
+            DeviceBuffer<float> xd(xf.size());
+            xd.upload(xf.data(), xf.size(), st);
+            proj.emplace_back(m * 3 * e_);
+            run_projection(qkv_, xd.data(), static_cast<int64_t>(m), proj.back().data(), st);
+        }
+        const float* qp = proj[0].data();
+        const float* kp = (self ? proj[0].data() : proj[1].data()) + e_;
+        const float* vp = (self ? proj[0].data() : proj[2].data()) + 2 * e_;
+        DeviceBuffer<float> md;
+        if (mask) {
+            std::vector<float> mf(mask->data(), mask->data() + mask->numel());
+            md = DeviceBuffer<float>(mf.size());
+            md.upload(mf.data(), mf.size(), st);
+        }
+        DeviceBuffer<float> att(m * e_), y(m * e_);
+        const int64_t ld = static_cast<int64_t>(3 * e_);
+        check(tq_attention_f32(qp, ld, kp, ld, vp, ld, mask ? md.data() : nullptr, mb, static_cast<int64_t>(b),
+                               static_cast<int64_t>(s), static_cast<int64_t>(h_), static_cast<int64_t>(e_ / h_),
+                               att.data(), static_cast<int64_t>(e_), reinterpret_cast<tq_stream_t>(st)),
+              "QuantizedMultiheadAttention attention");
+        run_projection(out_, att.data(), static_cast<int64_t>(m), y.data(), st);
+        const auto yv = y.to_host(st);
+        return Tensor::from_slice(std::vector<double>(yv.begin(), yv.end()), sh);
+    });
+}
+
+Tensor QuantizedMultiheadAttention::forward(const Tensor& input) const {
+    return forward_with_mask(input, input, input, std::nullopt).unwrap();
+}
+
+Tensor QuantizedMultiheadAttention::forward_qkv(const Tensor& query, const Tensor& key, const Tensor& value) const {
+    return forward_with_mask(query, key, value, std::nullopt).unwrap();
+}
+
+std::vector<std::pair<std::string, Tensor>> QuantizedMultiheadAttention::named_parameters() const {
+    std::vector<std::pair<std::string, Tensor>> out;
+    const auto fused = qkv_.named_parameters();
+    const char* names[3] = {"q_proj", "k_proj", "v_proj"};
+    for (size_t i = 0; i < 3; ++i)
+        for (const auto& kv : fused) out.emplace_back(std::string(names[i]) + "." + kv.first, row_slice(kv.second, i * e_, e_));
+    for (const auto& kv : out_.named_parameters()) out.emplace_back("out_proj." + kv.first, kv.second);
+    return out;
+}
+
+std::vector<Tensor> QuantizedMultiheadAttention::parameters() const {
+    std::vector<Tensor> out;
+    for (auto& kv : named_parameters()) out.push_back(kv.second);
+    return out;
+}
+
+size_t QuantizedMultiheadAttention::num_parameters() const { return qkv_.num_parameters() + out_.num_parameters(); }
+
 }  // namespace nn
 }  // namespace theano
 

@@ -404,5 +404,44 @@ class QuantizedMLP : public Module {
 uint16_t f32_to_bf16(float x);
 float bf16_to_f32(uint16_t b);
 
+// MultiheadAttention (crates/theano-nn/src/transformer.rs:9-162) with its q/k/v
+// and out projections as QuantizedLinear consumers.  q, k and v are quantized
+// row by row, so their concatenation [3E, E] has exactly the three codes: the
+// module holds one fused q/k/v QuantizedLinear (one GEMM / GEMV for
+// self-attention) and the out projection; the attention core (scores, additive
+// mask, softmax, P V) is tq_attention_f32 on the f32 projections.  Inputs and
+// outputs are [batch, seq, E].  Cross-attention (distinct query / key / value)
+// runs the fused projection on each input and keeps its third.
+class QuantizedMultiheadAttention : public Module {
+   public:
+    static Result<QuantizedMultiheadAttention> from_tensors(
+        size_t num_heads, const Tensor& wq, const Tensor& wk, const Tensor& wv, const Tensor& wo,
+        const std::optional<Tensor>& bq = std::nullopt, const std::optional<Tensor>& bk = std::nullopt,
+        const std::optional<Tensor>& bv = std::nullopt, const std::optional<Tensor>& bo = std::nullopt,
+        const quantize::QConfig& qconfig = quantize::QConfig::default_int8(), hipStream_t stream = nullptr);
+
+    // self-attention (Module::forward, transformer.rs:145-150)
+    Tensor forward(const Tensor& input) const override;
+    // transformer.rs:86-142; mask additive [batch or 1, (1,) seq, seq]
+    Result<Tensor> forward_with_mask(const Tensor& query, const Tensor& key, const Tensor& value,
+                                     const std::optional<Tensor>& mask) const;
+    Tensor forward_qkv(const Tensor& query, const Tensor& key, const Tensor& value) const;
+
+    std::vector<Tensor> parameters() const override;
+    // q_proj.*, k_proj.*, v_proj.*, out_proj.* (weight, weight_scale, bias)
+    std::vector<std::pair<std::string, Tensor>> named_parameters() const override;
+    size_t num_parameters() const override;
+    size_t embed_dim() const { return e_; }
+    size_t num_heads() const { return h_; }
+    size_t head_dim() const { return e_ / h_; }
+    const QuantizedLinear& qkv() const { return qkv_; }
+    const QuantizedLinear& out_proj() const { return out_; }
+
+   private:
+    size_t e_ = 0, h_ = 1;
+    hipStream_t stream_ = nullptr;
+    QuantizedLinear qkv_, out_;
+};
+
 }  // namespace nn
 }  // namespace theano

@@ -586,5 +586,62 @@ Result<DeviceTensor> forward(const QuantizedMLP& mlp, const DeviceTensor& x) {
     return y;
 }
 
+Result<DeviceTensor> forward_with_mask(const QuantizedMultiheadAttention& mha, const DeviceTensor& query,
+                                       const DeviceTensor& key, const DeviceTensor& value,
+                                       const std::optional<DeviceTensor>& mask) {
+    const size_t e = mha.embed_dim();
+    const auto& sh = query.shape();
+    if (sh.size() != 3 || sh[2] != e || key.shape() != sh || value.shape() != sh)
+        return TheanoError::shape_mismatch("QuantizedMultiheadAttention::forward: query, key, value must be [batch, seq, " +
+                                           std::to_string(e) + "]");
+    if (!query.storage().device_handle() || !key.storage().device_handle() || !value.storage().device_handle())
+        return TheanoError::invalid_argument("QuantizedMultiheadAttention::forward: empty tensor");
+    const size_t b = sh[0], s = sh[1], m = b * s;
+    int64_t mb = 0;
+    std::optional<DeviceTensor> mf;
+    if (mask) {
+        const auto& ms = mask->shape();
+        const bool ok3 = ms.size() == 3 && ms[1] == s && ms[2] == s;
+        const bool ok4 = ms.size() == 4 && ms[1] == 1 && ms[2] == s && ms[3] == s;
+        if (!(ok3 || ok4) || (ms[0] != 1 && ms[0] != b))
+            return TheanoError::shape_mismatch("QuantizedMultiheadAttention::forward: mask must be [batch or 1, (1,) seq, seq]");
+        auto c = mask->to_dtype(DType::F32);
+        if (c.is_err()) return c.unwrap_err();
+        mf = std::move(c).unwrap();
+        mb = static_cast<int64_t>(ms[0]);
+    }
+    const auto dev = query.storage().device_handle();
+    const hipStream_t st = query.stream();
+    // the fused projection once for self-attention, per input otherwise; each [m, 3E]
+    const bool self = query.data() == key.data() && key.data() == value.data() && query.dtype() == key.dtype() &&
+                      key.dtype() == value.dtype();
+    std::vector<DeviceTensor> proj;
+    for (const DeviceTensor* in : self ? std::vector<const DeviceTensor*>{&query}
+                                       : std::vector<const DeviceTensor*>{&query, &key, &value}) {
+        auto y = forward(mha.qkv(), DeviceTensor(in->storage(), {m, e}));
+        if (y.is_err()) return y.unwrap_err();
+        proj.push_back(std::move(y).unwrap());
+    }
+    const float* qp = static_cast<const float*>(proj[0].data());
+    const float* kp = static_cast<const float*>(proj[self ? 0 : 1].data()) + e;
+    const float* vp = static_cast<const float*>(proj[self ? 0 : 2].data()) + 2 * e;
+    auto att = DeviceTensor::empty(dev, {m, e}, DType::F32, st);
+    if (att.is_err()) return att.unwrap_err();
+    const int64_t ld = static_cast<int64_t>(3 * e);
+    const int rc = tq_attention_f32(qp, ld, kp, ld, vp, ld, mf ? static_cast<const float*>(mf->data()) : nullptr, mb,
+                                    static_cast<int64_t>(b), static_cast<int64_t>(s),
+                                    static_cast<int64_t>(mha.num_heads()), static_cast<int64_t>(mha.head_dim()),
+                                    static_cast<float*>(att.unwrap().data()), static_cast<int64_t>(e),
+                                    reinterpret_cast<tq_stream_t>(st));
+    if (rc != TQ_OK) return TheanoError::from_status(rc, "QuantizedMultiheadAttention attention");
+    auto y = forward(mha.out_proj(), att.unwrap());
+    if (y.is_err()) return y.unwrap_err();
+    return DeviceTensor(y.unwrap().storage(), sh);
+}
+
+Result<DeviceTensor> forward(const QuantizedMultiheadAttention& mha, const DeviceTensor& x) {
+    return forward_with_mask(mha, x, x, x, std::nullopt);
+}
+
 }  // namespace nn
 }  // namespace theano

@@ -250,6 +250,13 @@ namespace nn {
 // F32, scratch from the device's caching allocator, everything on x's stream.
 Result<DeviceTensor> forward(const QuantizedLinear& layer, const DeviceTensor& x);
 Result<DeviceTensor> forward(const QuantizedMLP& mlp, const DeviceTensor& x);
+// MultiheadAttention::forward_with_mask (transformer.rs:95-142): query, key,
+// value [B, S, E] (one projection pass when the three share storage), mask
+// [B or 1, (1,) S, S] additive; y [B, S, E] F32.
+Result<DeviceTensor> forward_with_mask(const QuantizedMultiheadAttention& mha, const DeviceTensor& query,
+                                       const DeviceTensor& key, const DeviceTensor& value,
+                                       const std::optional<DeviceTensor>& mask);
+Result<DeviceTensor> forward(const QuantizedMultiheadAttention& mha, const DeviceTensor& x);
 
 }  // namespace nn
 }  // namespace theano

@@ -31,6 +31,7 @@ using namespace theano;
 using namespace theano::quantize;
 using theano::nn::QuantizedLinear;
 using theano::nn::QuantizedMLP;
+using theano::nn::QuantizedMultiheadAttention;
 namespace ser = theano::serialize;
 
 namespace {
@@ -1028,6 +1029,135 @@ TEST_GPU(test_device_tensor_chain_matches_host_path) {
     const auto warm = dev->allocator().stats();
     for (int i = 0; i < 3; ++i) (void)run();
     ASSERT_EQ(dev->allocator().stats().num_mallocs, warm.num_mallocs);  // served from the pool
+    ASSERT(dev->synchronize().is_ok());
+}
+
+// ------------------------------------------------------------ multi-head attention (transformer.rs)
+
+namespace {
+
+struct MhaWeights {
+    std::vector<std::vector<double>> w, b;  // q, k, v, out: [E, E] and [E]
+};
+
+MhaWeights mha_weights(size_t e, uint64_t seed) {
+    MhaWeights r;
+    for (uint64_t i = 0; i < 4; ++i) {
+        r.w.push_back(randn(e * e, 0.05, seed + i));
+        r.b.push_back(randn(e, 0.1, seed + 10 + i));
+    }
+    return r;
+}
+
+QuantizedMultiheadAttention make_mha(const MhaWeights& p, size_t e, size_t h, const QConfig& cfg) {
+    auto t = [&](size_t i) { return Tensor::from_slice(p.w[i], {e, e}); };
+    auto b = [&](size_t i) { return std::optional<Tensor>(Tensor::from_slice(p.b[i], {e})); };
+    return QuantizedMultiheadAttention::from_tensors(h, t(0), t(1), t(2), t(3), b(0), b(1), b(2), b(3), cfg).unwrap();
+}
+
+std::vector<double> causal_mask(size_t s) {
+    std::vector<double> m(s * s, 0.0);
+    for (size_t i = 0; i < s; ++i)
+        for (size_t j = i + 1; j < s; ++j) m[i * s + j] = -INFINITY;
+    return m;
+}
+
+}  // namespace
+
+TEST_CPU(test_mha_construction_errors) {
+    // embed_dim % num_heads != 0 and non-square weights fail before any device work
+    const Tensor w10 = Tensor::ones({10, 10});
+    auto r = QuantizedMultiheadAttention::from_tensors(3, w10, w10, w10, w10);
+    ASSERT(r.is_err() && r.unwrap_err().kind() == TheanoError::Kind::InvalidArgument);
+    const Tensor w = Tensor::ones({8, 4});
+    auto r2 = QuantizedMultiheadAttention::from_tensors(2, w, w, w, w);
+    ASSERT(r2.is_err() && r2.unwrap_err().kind() == TheanoError::Kind::ShapeMismatch);
+    auto r3 = QuantizedMultiheadAttention::from_tensors(0, w10, w10, w10, w10);
+    ASSERT(r3.is_err() && r3.unwrap_err().kind() == TheanoError::Kind::InvalidArgument);
+}
+
+TEST_GPU(test_mha_reference_shapes_and_names) {
+    // transformer.rs:188-268: output shape, parameter names and counts, masked forward
+    const QuantizedMultiheadAttention mha = make_mha(mha_weights(64, 200), 64, 8, QConfig::default_int8());
+    ASSERT(mha.embed_dim() == 64 && mha.num_heads() == 8 && mha.head_dim() == 8);
+    ASSERT(mha.forward(Tensor::ones({2, 10, 64})).shape() == (std::vector<size_t>{2, 10, 64}));
+    const auto named = mha.named_parameters();
+    ASSERT_EQ(named.size(), size_t{12});
+    ASSERT(named[0].first == "q_proj.weight" && named[1].first == "q_proj.weight_scale" && named[2].first == "q_proj.bias");
+    ASSERT(named[3].first == "k_proj.weight" && named[6].first == "v_proj.weight" && named[11].first == "out_proj.bias");
+    ASSERT(named[0].second.shape() == (std::vector<size_t>{64, 64}) && named[2].second.shape() == (std::vector<size_t>{64}));
+    ASSERT_EQ(mha.parameters().size(), size_t{12});
+    const QuantizedMultiheadAttention m16 = make_mha(mha_weights(16, 210), 16, 4, QConfig::default_int8());
+    const Tensor x = Tensor::ones({1, 4, 16});
+    const Tensor mask = Tensor::from_slice(causal_mask(4), {1, 4, 4});
+    ASSERT(m16.forward_with_mask(x, x, x, mask).unwrap().shape() == (std::vector<size_t>{1, 4, 16}));
+    ASSERT(m16.forward_qkv(x, x, x).shape() == (std::vector<size_t>{1, 4, 16}));
+    ASSERT_EQ(m16.num_parameters(), size_t{4 * (16 * 16 + 16)});
+    auto bad = m16.forward_with_mask(x, x, x, Tensor::ones({1, 3, 4}));
+    ASSERT(bad.is_err() && bad.unwrap_err().kind() == TheanoError::Kind::ShapeMismatch);
+    auto bad2 = m16.forward_with_mask(Tensor::ones({1, 4, 8}), Tensor::ones({1, 4, 8}), Tensor::ones({1, 4, 8}),
+                                      std::nullopt);
+    ASSERT(bad2.is_err() && bad2.unwrap_err().kind() == TheanoError::Kind::ShapeMismatch);
+}
+
+TEST_GPU(test_parity_mha_w8) {
+    // INT8 weight-only projections + attention against the oracle chain in f64
+    const size_t b = 2, s = 40, e = 256, h = 4, m = b * s;
+    const MhaWeights p = mha_weights(e, 220);
+    const QuantizedMultiheadAttention mha = make_mha(p, e, h, QConfig::default_int8());
+    const auto xv = randn(m * e, 1.0, 230), kv = randn(m * e, 1.0, 231), vv = randn(m * e, 1.0, 232);
+    const auto mask = causal_mask(s);
+    auto proj = [&](size_t i, const std::vector<double>& x) {
+        const auto w32 = f32(p.w[i]), b32 = f32(p.b[i]), x32 = f32(x);
+        std::vector<int8_t> q(e * e);
+        std::vector<float> sc(e);
+        tqo_quantize_i8_rowwise(w32.data(), e, e, q.data(), sc.data());
+        std::vector<double> y(x.size() / e * e);
+        tqo_linear_w8(x32.data(), static_cast<int64_t>(x.size() / e), q.data(), sc.data(), b32.data(), e, e, y.data());
+        return y;
+    };
+    auto chain = [&](const std::vector<double>& xq, const std::vector<double>& xk, const std::vector<double>& xw,
+                     const double* mk) {
+        const auto q = proj(0, xq), k = proj(1, xk), v = proj(2, xw);
+        std::vector<double> att(m * e);
+        tqo_attention(q.data(), k.data(), v.data(), mk, mk ? 1 : 0, b, s, h, e / h, att.data());
+        return proj(3, att);
+    };
+    const Tensor x = Tensor::from_slice(xv, {b, s, e});
+    assert_close(mha.forward_with_mask(x, x, x, Tensor::from_slice(mask, {1, s, s})).unwrap().to_vec_f64().unwrap(),
+                 chain(xv, xv, xv, mask.data()), "mha w8 self, causal");
+    assert_close(mha.forward(x).to_vec_f64().unwrap(), chain(xv, xv, xv, nullptr), "mha w8 self");
+    assert_close(mha.forward_qkv(x, Tensor::from_slice(kv, {b, s, e}), Tensor::from_slice(vv, {b, s, e}))
+                     .to_vec_f64()
+                     .unwrap(),
+                 chain(xv, kv, vv, nullptr), "mha w8 cross");
+}
+
+TEST_GPU(test_mha_device_tensor_matches_host_path) {
+    // the device-resident forward gives the host API's bits, for each activation format
+    auto dev = rocm::DeviceManager::global().get_device(0).unwrap();
+    const size_t b = 2, s = 33, e = 256, h = 8;
+    const MhaWeights p = mha_weights(e, 240);
+    const QConfig a8{QuantDType::Int8, QuantDType::Int8, true, true};
+    const QConfig fp8{QuantDType::FP8, QuantDType::FP8, true, true};
+    const Tensor x = Tensor::from_slice(randn(b * s * e, 1.0, 250), {b, s, e});
+    const Tensor xk = Tensor::from_slice(randn(b * s * e, 1.0, 251), {b, s, e});
+    const Tensor mask = Tensor::from_slice(causal_mask(s), {1, 1, s, s});
+    const DeviceTensor xd = DeviceTensor::from_host(x, dev, DType::F32).unwrap();
+    const DeviceTensor xkd = DeviceTensor::from_host(xk, dev, DType::F32).unwrap();
+    const DeviceTensor md = DeviceTensor::from_host(mask, dev, DType::F32).unwrap();
+    for (const QConfig& cfg : {QConfig::default_int8(), QConfig::default_int4(), a8, fp8}) {
+        const QuantizedMultiheadAttention mha = make_mha(p, e, h, cfg);
+        const Tensor ref = mha.forward_with_mask(x, x, x, mask).unwrap();
+        const DeviceTensor y = nn::forward_with_mask(mha, xd, xd, xd, md).unwrap();
+        ASSERT(y.shape() == (std::vector<size_t>{b, s, e}) && y.dtype() == DType::F32);
+        ASSERT(same_bits(y.to_host().unwrap().to_vec_f64().unwrap(), ref.to_vec_f64().unwrap()));
+        const Tensor ref2 = mha.forward_qkv(x, xk, xk);
+        ASSERT(same_bits(nn::forward_with_mask(mha, xd, xkd, xkd, std::nullopt).unwrap().to_host().unwrap().to_vec_f64().unwrap(),
+                         ref2.to_vec_f64().unwrap()));
+        ASSERT(same_bits(nn::forward(mha, xd).unwrap().to_host().unwrap().to_vec_f64().unwrap(),
+                         mha.forward(x).to_vec_f64().unwrap()));
+    }
     ASSERT(dev->synchronize().is_ok());
 }
 

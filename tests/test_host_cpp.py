@@ -19,7 +19,7 @@ def run(*args, timeout=300):
 
 def test_cpp_host_layer_cpu_cases():
     out = run("--cpu")
-    assert "25 of 25 tests passed" in out
+    assert "26 of 26 tests passed" in out
 
 
 @pytest.mark.gpu

@@ -11,9 +11,18 @@
 //   s_t[(t*G + g)*T + r]               = s[t*T + r][g]
 // so the 16-byte chunk c of the T rows of a tile is one contiguous T*16-byte run.
 //
-// Two kernels read this layout:
-//  * k_decode_tiled (1-2 tokens): one block (16 waves) per tile, lane = row, waves
-//    split the chunks.
+// Three kernels read this layout:
+//  * k_decode_diag (1-4 tokens, T = 16, 32 or 64; the decode path): one block of
+//    16 waves per tile, waves split K by groups.  Every packed dword of a lane is
+//    the A operand of one v_mfma_f32_16x16x32_bf16; the 4 k-groups of the MFMA
+//    are kR = T/16 row groups times 4/kR consecutive chunks, and the B operand
+//    carries token j's x only in the k-groups of row group c % kR for column
+//    c = j kR + (row group), zeros elsewhere, so the product's columns are the
+//    (token, row group) dot products (details at the kernel).  The vector ALU
+//    only unpacks nibbles (7 instructions per dword); x is staged once per wave
+//    in LDS.
+//  * k_decode_tiled (fallback for other tile heights and long K at 3-4 tokens):
+//    one block (16 waves) per tile, lane = row, waves split the chunks.
 // x is wave-uniform, so each wave permutes its slice of x once into a private
 // LDS strip and reads it back with broadcast ds_read_b128; no cross-lane
 // reduction is needed per row.  Nibbles become bf16 with bit operations
@@ -306,6 +315,201 @@ __global__ __launch_bounds__(kBlock) void k_decode_tiled_mfma(const uint16_t* __
     }
 }
 
+// Packed dword (nibbles k..k+7, two's complement) -> bf16 136 + q in the slot
+// order (k, k+4), (k+1, k+5), (k+2, k+6), (k+3, k+7): nibble pair s of the dword
+// sits at bits 4s and 16 + 4s, so a shift, a mask and an xor (which turns the
+// nibble into q + 8 and sets the exponent of 128) make each slot pair.
+__device__ __forceinline__ u32x4 unpack_w4_136(uint32_t w) {
+    u32x4 a;
+    a.x = (w & 0x000F000Fu) ^ 0x43084308u;
+    a.y = ((w >> 4) & 0x000F000Fu) ^ 0x43084308u;
+    a.z = ((w >> 8) & 0x000F000Fu) ^ 0x43084308u;
+    a.w = ((w >> 12) & 0x000F000Fu) ^ 0x43084308u;
+    return a;
+}
+
+// Decode kernel for 1..kM tokens (kM * kR <= 16), T = 16 kR rows per tile.
+//
+// Lane l (i = l % 16, kg = l / 16) loads, per step, the 16 bytes of row
+// 16 (kg % kR) + i at chunk kS step + kg / kR (kS = 4 / kR chunks per step, kR
+// steps per 128-element group), and feeds each of their 4 dwords to one MFMA as
+// row i of k-group kg.  B lane (kg, c) holds the matching 8 values of token
+// c / kR when c % kR == kg % kR and c / kR < kM, zeros otherwise.  Then
+//   D[i][c] = sum over the kS chunks of the step of
+//             row 16 (c % kR) + i  .  x_{c / kR}
+// and a lane of the output holds D[4 (l / 16) + e][l % 16], e = 0..3: four
+// consecutive tile rows of one token.  The accumulators restart per group; the
+// group's f16 scale and 136 * sum(x) of the group are applied as
+// y += s * (acc - 136 X_g).
+//
+// Each wave stages its K slice of every token's x in a private LDS strip (slot
+// order as above; a zero strip of the same size serves the other B lanes) and
+// keeps 136 X_g per (token, group) in registers.  Loads are issued x first,
+// then scales, then kWin steps of weights ahead of the arithmetic (in-order
+// vmcnt), and every wave runs all its groups (groups past K read clamped
+// addresses with a zero scale) so the refills are not moved behind a branch.
+// The 16 waves' partial sums meet in LDS in a fixed order.
+template <int kR, int kM, int kGPW, int kWinD>
+__global__ __launch_bounds__(kBlock) void k_decode_diag(const uint16_t* __restrict__ x, int m,
+                                                        const uint8_t* __restrict__ pt,
+                                                        const uint16_t* __restrict__ st,
+                                                        const float* __restrict__ bias, int64_t n, int64_t k,
+                                                        float* __restrict__ y) {
+    static_assert(kM * kR <= 16, "columns are (token, row group) pairs");
+    constexpr int T = 16 * kR;
+    constexpr int kS = 4 / kR;                  // chunks per step
+    constexpr int kCPW = 4 * kGPW;              // chunks per wave
+    constexpr int kSteps = kCPW / kS;           // weight loads per lane
+    constexpr int kStrip = kCPW * 64;           // bytes of one token's slice (bf16)
+    constexpr int kItems = kM * kCPW * 8;       // 4-element items of the slices
+    constexpr int kIPL = (kItems + kWave - 1) / kWave;
+    constexpr int kW = kWinD < kSteps ? kWinD : kSteps;
+    __shared__ __attribute__((aligned(16))) uint8_t xs[kWaves][kM + 1][kStrip];  // [kM]: zeros
+    __shared__ __attribute__((aligned(16))) float part[kWaves][kM][T];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int64_t tile = blockIdx.x;
+    const int64_t C = k >> 5, G = k >> 7;
+    const int64_t g0 = static_cast<int64_t>(wave) * kGPW, c0 = 4 * g0;
+    const int col = lane & 15, kg = lane >> 4;
+    const int rg = kg % kR, cs = kg / kR;  // this lane's row group and chunk slot (loads)
+    const int tok = col / kR;              // token of this lane's output column
+    const int row0 = 16 * (col % kR) + 4 * kg;  // first of its four output rows
+
+    // x items: item it -> token it / (8 kCPW), elements 4 (it % (8 kCPW)) .. + 3 of
+    // the wave's slice (clamped past K; zero past m)
+    uint2 xv[kIPL];
+#pragma unroll
+    for (int q = 0; q < kIPL; ++q) {
+        const int it = min(lane + kWave * q, kItems - 1);
+        const int j = it / (kCPW * 8), r = it - j * (kCPW * 8);
+        const int64_t kx = min<int64_t>(c0 * 32 + 4 * r, k - 4);
+        xv[q] = j < m ? *reinterpret_cast<const uint2*>(x + j * k + kx) : make_uint2(0u, 0u);
+    }
+    uint2 sc[kGPW];
+#pragma unroll
+    for (int g = 0; g < kGPW; ++g)
+        sc[g] = *reinterpret_cast<const uint2*>(st + (tile * G + min<int64_t>(g0 + g, G - 1)) * T + row0);
+    const uint8_t* wb = pt + (tile * C * T + 16 * rg + (lane & 15)) * 16;
+    u32x4 w[kW];
+#pragma unroll
+    for (int i = 0; i < kW; ++i)
+        w[i] = __builtin_nontemporal_load(
+            reinterpret_cast<const u32x4*>(wb + min<int64_t>(c0 + i * kS + cs, C - 1) * T * 16));
+
+    for (int b = lane * 16; b < kStrip; b += kWave * 16)
+        *reinterpret_cast<u32x4*>(&xs[wave][kM][b]) = u32x4{0u, 0u, 0u, 0u};
+    // stage: lanes 2b, 2b+1 hold an 8-block's (x0..x3) and (x4..x7); the even lane
+    // writes slots (x0,x4)(x1,x5), the odd lane (x2,x6)(x3,x7)
+    float gsum[kIPL];
+#pragma unroll
+    for (int q = 0; q < kIPL; ++q) {
+        const int it = lane + kWave * q;
+        const int itc = min(it, kItems - 1);
+        const int j = itc / (kCPW * 8), r = itc - j * (kCPW * 8);
+        const uint2 v = xv[q];
+        const uint2 p = make_uint2(__shfl_xor(v.x, 1, kWave), __shfl_xor(v.y, 1, kWave));
+        const bool odd = r & 1;
+        const uint32_t hi = odd ? v.y : p.x, lo = odd ? p.y : v.x;
+        if (it < kItems)
+            *reinterpret_cast<uint2*>(&xs[wave][j][(r >> 1) * 16 + (odd ? 8 : 0)]) =
+                make_uint2(__builtin_amdgcn_perm(hi, lo, 0x05040100u), __builtin_amdgcn_perm(hi, lo, 0x07060302u));
+        // group sums: a group is 32 consecutive items, i.e. one half of the wave
+        float s = bf16_lo(v.x) + bf16_hi(v.x) + bf16_lo(v.y) + bf16_hi(v.y);
+        s += __shfl_xor(s, 1, kWave);
+        s += __shfl_xor(s, 2, kWave);
+        s += __shfl_xor(s, 4, kWave);
+        s += __shfl_xor(s, 8, kWave);
+        s += __shfl_xor(s, 16, kWave);
+        gsum[q] = s;
+    }
+    float corr[kGPW];
+#pragma unroll
+    for (int g = 0; g < kGPW; ++g) {
+        float c = 0.0f;
+#pragma unroll
+        for (int j = 0; j < kM; ++j) {
+            const int it = j * kCPW * 8 + 32 * g;  // first item of (token j, group g)
+            const float v = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(gsum[it / kWave]), it % kWave));
+            c = tok == j ? v : c;
+        }
+        corr[g] = 136.0f * c;
+    }
+    const bool diag = col % kR == rg && tok < kM;
+    const uint8_t* bsrc = diag ? &xs[wave][tok][cs * 64] : &xs[wave][kM][0];
+    // the strips are private to the wave: its LDS accesses complete in order
+
+    f32x4 tot = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int g = 0; g < kGPW; ++g) {
+        const bool live = g0 + g < G;
+        f32x4 a0 = f32x4{0.f, 0.f, 0.f, 0.f}, a1 = a0;
+#pragma unroll
+        for (int ss = 0; ss < kR; ++ss) {
+            const int i = kR * g + ss;  // step
+            const int slot = i % kW;
+            const uint32_t ws[4] = {w[slot].x, w[slot].y, w[slot].z, w[slot].w};
+#pragma unroll
+            for (int d = 0; d < 4; ++d) {
+                const u32x4 b = *reinterpret_cast<const u32x4*>(bsrc + (i * kS * 4 + d) * 16);
+                if (d & 1)
+                    a1 = mfma16_bf16(unpack_w4_136(ws[d]), b, a1);
+                else
+                    a0 = mfma16_bf16(unpack_w4_136(ws[d]), b, a0);
+            }
+            if (i + kW < kSteps) {
+                w[slot] = __builtin_nontemporal_load(
+                    reinterpret_cast<const u32x4*>(wb + min<int64_t>(c0 + (i + kW) * kS + cs, C - 1) * T * 16));
+                __builtin_amdgcn_sched_barrier(0);  // the refill is issued here, not after the group
+            }
+        }
+        const uint32_t s01 = live ? sc[g].x : 0u, s23 = live ? sc[g].y : 0u;
+        tot.x = fmaf(__half2float(__ushort_as_half(static_cast<uint16_t>(s01))), (a0.x + a1.x) - corr[g], tot.x);
+        tot.y = fmaf(__half2float(__ushort_as_half(static_cast<uint16_t>(s01 >> 16))), (a0.y + a1.y) - corr[g], tot.y);
+        tot.z = fmaf(__half2float(__ushort_as_half(static_cast<uint16_t>(s23))), (a0.z + a1.z) - corr[g], tot.z);
+        tot.w = fmaf(__half2float(__ushort_as_half(static_cast<uint16_t>(s23 >> 16))), (a0.w + a1.w) - corr[g], tot.w);
+    }
+    if (tok < kM) *reinterpret_cast<f32x4*>(&part[wave][tok][row0]) = tot;
+    __syncthreads();
+    for (int i = threadIdx.x; i < m * T; i += kBlock) {
+        const int j = i / T, r = i - j * T;
+        const int64_t row = tile * T + r;
+        if (row >= n) continue;
+        float s = 0.0f;
+#pragma unroll
+        for (int v = 0; v < kWaves; ++v) s += part[v][j][r];
+        y[j * n + row] = s + (bias ? bias[row] : 0.0f);
+    }
+}
+
+// kR in {1, 2, 4}; kM in {1, 2, 4} (3 tokens run as 4 with a zero token); groups per
+// wave in {1, 2, 4, 8} (8 only for kM <= 2: the strips of 4 tokens would not fit)
+template <int kR, int kM>
+int launch_diag(int64_t gpw, int64_t tiles, hipStream_t s, const uint16_t* x, int m, const uint8_t* pt,
+                const uint16_t* st, const float* b, int64_t n, int64_t k, float* y) {
+    constexpr int kWinD = kR == 1 ? 2 : 3;  // measured: steps of 4 chunks want a shorter window
+    const unsigned grid = static_cast<unsigned>(tiles);
+    if (gpw <= 1)
+        k_decode_diag<kR, kM, 1, kWinD><<<grid, kBlock, 0, s>>>(x, m, pt, st, b, n, k, y);
+    else if (gpw <= 2)
+        k_decode_diag<kR, kM, 2, kWinD><<<grid, kBlock, 0, s>>>(x, m, pt, st, b, n, k, y);
+    else if (gpw <= 4)
+        k_decode_diag<kR, kM, 4, kWinD><<<grid, kBlock, 0, s>>>(x, m, pt, st, b, n, k, y);
+    else if constexpr (kM <= 2)
+        k_decode_diag<kR, kM, 8, kWinD><<<grid, kBlock, 0, s>>>(x, m, pt, st, b, n, k, y);
+    else
+        return fail(TQ_EINVAL, "tq_gemv_w4g128_tiled: 3-4 tokens with K > 8192 on the diagonal kernel");
+    return check_launch("tq_gemv_w4g128_tiled");
+}
+
+template <int kR>
+int launch_diag_m(int64_t gpw, int64_t tiles, hipStream_t s, const uint16_t* x, int m, const uint8_t* pt,
+                  const uint16_t* st, const float* b, int64_t n, int64_t k, float* y) {
+    if (m == 1) return launch_diag<kR, 1>(gpw, tiles, s, x, m, pt, st, b, n, k, y);
+    if (m == 2) return launch_diag<kR, 2>(gpw, tiles, s, x, m, pt, st, b, n, k, y);
+    return launch_diag<kR, 4>(gpw, tiles, s, x, m, pt, st, b, n, k, y);
+}
+
 template <int kR>
 int launch_mfma(int64_t gpw, int64_t tiles, hipStream_t s, const uint16_t* x, int m, const uint8_t* pt,
                 const uint16_t* st, const float* b, int64_t n, int64_t k, float* y) {
@@ -414,10 +618,17 @@ int tq_gemv_w4g128_tiled(const uint16_t* x_bf16, int64_t m, const uint8_t* packe
     const int64_t tiles = (n + tile_rows - 1) / tile_rows;
     const int T = static_cast<int>(tile_rows);
     const hipStream_t st = as_hip(stream);
-    // 3..16 tokens: the MFMA kernel where the tile is 16, 32 or 64 rows, the 16 waves'
-    // K runs are at most 4 groups (K <= 8192) and x rows are 16-byte aligned
     const int kr = T == 16 ? 1 : (T == 32 ? 2 : (T == 64 ? 4 : 0));
     const int64_t gpw = ((k >> 7) + kWaves - 1) / kWaves;
+    // 1-2 tokens (and 3-4 on 16- and 32-row tiles, K <= 8192): the diagonal MFMA kernel
+    if (kr && aligned(x_bf16, 8) && aligned(s_t, 8) && (m <= 2 || (m <= 4 && kr < 4 && gpw <= 4))) {
+        const int mi = static_cast<int>(m);
+        if (kr == 1) return launch_diag_m<1>(gpw, tiles, st, x_bf16, mi, packed_t, s_t, bias, n, k, y);
+        if (kr == 2) return launch_diag_m<2>(gpw, tiles, st, x_bf16, mi, packed_t, s_t, bias, n, k, y);
+        return launch_diag_m<4>(gpw, tiles, st, x_bf16, mi, packed_t, s_t, bias, n, k, y);
+    }
+    // 3..16 tokens: the MFMA kernel where the tile is 16, 32 or 64 rows, the 16 waves'
+    // K runs are at most 4 groups (K <= 8192) and x rows are 16-byte aligned
     if (m >= 3 && kr && gpw <= 4 && aligned(x_bf16, 16) && aligned(s_t, 8)) {
         const int mi = static_cast<int>(m);
         if (kr == 1) return launch_mfma<1>(gpw, tiles, st, x_bf16, mi, packed_t, s_t, bias, n, k, y);

@@ -144,13 +144,17 @@ def test_gemv_w4g128_tiled_config3(tq, c3, m):
     assert_close(host(y), ref[:m], RTOL, ATOL, f"gemv_w4g128_tiled M={m} T={t}")
 
 
-# 1-2 tokens (and tiles that are not 16, 32 or 64 rows, or K ranges past the MFMA
-# kernel's budget) run the dot2 kernel; 3-16 tokens the MFMA kernel (token passes,
-# tail tiles, K up to 8192 with the two-position x staging)
+# Tiles of 16, 32 or 64 rows: 1-2 tokens (3-4 on 16- and 32-row tiles, K <= 8192) run
+# the diagonal MFMA kernel (one to eight groups per wave, waves past K, tail tiles),
+# 3-16 tokens otherwise the MFMA kernel with x from L2 (token passes, K <= 8192);
+# other tile heights and 3-4 tokens at K > 8192 on small tiles run the dot2 kernel.
 @pytest.mark.parametrize("n,k,m,t", [(100, 128, 1, 8), (7, 2176, 2, 8), (256, 14336, 1, 16), (48, 16384, 3, 24),
                                      (1000, 4096, 4, 64), (333, 640, 2, 40),
                                      (1000, 4096, 5, 64), (70, 1024, 16, 16), (200, 6144, 7, 32),
-                                     (130, 8192, 9, 16), (77, 384, 13, 64), (64, 8192, 3, 64)])
+                                     (130, 8192, 9, 16), (77, 384, 13, 64), (64, 8192, 3, 64),
+                                     (100, 128, 1, 16), (200, 6144, 2, 32), (40, 16384, 2, 32), (333, 4224, 2, 64),
+                                     (1000, 4096, 1, 64), (130, 8192, 4, 16), (70, 1152, 3, 16), (100, 2048, 3, 32),
+                                     (48, 16384, 3, 16), (4100, 14336, 2, 16), (90, 16384, 1, 64)])
 def test_gemv_w4g128_tiled_shapes(tq, oracle, n, k, m, t):
     from theano_quantize import _abi
     from theano_quantize._tensor import ptr, stream

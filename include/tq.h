@@ -311,6 +311,29 @@ int tq_mlp_w4g128(const uint16_t* x_bf16, int64_t m, int64_t d, int64_t f,
                   const uint8_t* down_packed, const uint16_t* down_s,
                   void* workspace, int64_t workspace_bytes, float* y, tq_stream_t stream);
 
+/* The same FFN for decode shapes (M <= 16; faster than tq_mlp_w4g128 up to
+ * M = 8) on row-tiled copies of the weights (permutations of the packed bytes):
+ *   gate and up:  tq_repack_w4g128_gate_up_tiled -> 64-row tiles, tile t holding
+ *                 gate rows 32t..32t+31 then up rows 32t..32t+31, padded to F
+ *                 rounded up to 32 with zeros ((F+31)/32 * 64 * D/2 bytes and
+ *                 (F+31)/32 * 64 * D/128 scales);
+ *   down:         tq_repack_w4g128_tiled with tile_rows 16, 32 or 64
+ *                 (tq_w4g128_tile_rows(D) by default).
+ * h = SiLU(x Wg^T) * (x Wu^T) is formed in f32 per token and handed to the down
+ * projection as bf16 hi + lo (lo = bf16(h - hi)).  D, F multiples of 128 and at
+ * most 16384.  `workspace`: tq_mlp_w4g128_decode_workspace_bytes(M, D, F)
+ * bytes, 16-byte aligned; x and the scales 8-byte aligned, packed weights
+ * 16-byte aligned.  These three have no counterpart in the reference: they
+ * serve its FFN composition (Linear, SiLU, Tensor::mul) at decode batch sizes. */
+int64_t tq_mlp_w4g128_decode_workspace_bytes(int64_t m, int64_t d, int64_t f);
+int tq_repack_w4g128_gate_up_tiled(const uint8_t* gate_packed, const uint16_t* gate_s,
+                                   const uint8_t* up_packed, const uint16_t* up_s, int64_t f, int64_t d,
+                                   uint8_t* packed_t, uint16_t* s_t, tq_stream_t stream);
+int tq_mlp_w4g128_decode(const uint16_t* x_bf16, int64_t m, int64_t d, int64_t f,
+                         const uint8_t* gate_up_t, const uint16_t* gate_up_s_t,
+                         const uint8_t* down_t, const uint16_t* down_s_t, int64_t down_tile_rows,
+                         void* workspace, int64_t workspace_bytes, float* y, tq_stream_t stream);
+
 /* ------------------------------------------------------------------------
  * Attention core of MultiheadAttention::forward_with_mask
  * (crates/theano-nn/src/transformer.rs:95-142) between the quantized q/k/v and

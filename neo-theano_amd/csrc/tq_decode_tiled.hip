@@ -21,8 +21,11 @@
 //    (token, row group) dot products (details at the kernel).  The vector ALU
 //    only unpacks nibbles (7 instructions per dword); x is staged once per wave
 //    in LDS.
-//  * k_decode_tiled (fallback for other tile heights and long K at 3-4 tokens):
-//    one block (16 waves) per tile, lane = row, waves split the chunks.
+//    The same kernel runs the decode FFN: gate and up rows share 64-row tiles and
+//    the block applies SiLU(g) * u, then the down projection takes h as bf16
+//    hi + lo rows and adds the two halves per token.
+//  * k_decode_tiled (fallback for other tile heights): one block (16 waves) per
+//    tile, lane = row, waves split the chunks.
 // x is wave-uniform, so each wave permutes its slice of x once into a private
 // LDS strip and reads it back with broadcast ds_read_b128; no cross-lane
 // reduction is needed per row.  Nibbles become bf16 with bit operations
@@ -349,13 +352,37 @@ __device__ __forceinline__ u32x4 unpack_w4_136(uint32_t w) {
 // vmcnt), and every wave runs all its groups (groups past K read clamped
 // addresses with a zero scale) so the refills are not moved behind a branch.
 // The 16 waves' partial sums meet in LDS in a fixed order.
-template <int kR, int kM, int kGPW, int kWinD>
+// What the block does with its rows' dot products (16 waves summed in order):
+//  kEpiPlain:  y[j][row] = sum + bias[row] for the m tokens.
+//  kEpiFold:   the m = 2t tokens are t rows and their t low parts (an f32 input
+//              split into bf16 hi + lo); y[j][row] = sum_j + sum_{t+j} + bias[row].
+//  kEpiGateUp: the 64-row tile holds gate rows 32 tile .. + 31 (rows 0-31) and
+//              the up rows of the same indices (rows 32-63) of a Llama FFN;
+//              h = g / (1 + exp(-g)) * u goes out as bf16 hi = bf16(h) and lo =
+//              bf16(h - hi) into the down projection's input rows (see MlpRows).
+enum DiagEpi { kEpiPlain = 0, kEpiFold = 1, kEpiGateUp = 2 };
+
+// Rows of the down projection's bf16 input for token J of an m-token FFN: tokens
+// go in pairs, pair c = J / 2 with t = min(2, m - 2c) tokens occupies rows
+// 4c .. 4c + 2t - 1 as (hi of its tokens, lo of its tokens), so each pair is one
+// kEpiFold launch of 2t contiguous rows.
+struct MlpRows {
+    __host__ __device__ static int64_t hi(int64_t j, int64_t m) { return 4 * (j / 2) + (j % 2); }
+    __host__ __device__ static int64_t lo(int64_t j, int64_t m) {
+        const int64_t c = j / 2, t = m - 2 * c < 2 ? m - 2 * c : 2;
+        return 4 * c + t + (j % 2);
+    }
+};
+
+template <int kR, int kM, int kGPW, int kWinD, int kEpi>
 __global__ __launch_bounds__(kBlock) void k_decode_diag(const uint16_t* __restrict__ x, int m,
                                                         const uint8_t* __restrict__ pt,
                                                         const uint16_t* __restrict__ st,
                                                         const float* __restrict__ bias, int64_t n, int64_t k,
-                                                        float* __restrict__ y) {
+                                                        float* __restrict__ y, uint16_t* __restrict__ hout,
+                                                        int tok0, int mtot) {
     static_assert(kM * kR <= 16, "columns are (token, row group) pairs");
+    static_assert(kEpi != kEpiGateUp || kR == 4, "gate/up tiles are 64 rows");
     constexpr int T = 16 * kR;
     constexpr int kS = 4 / kR;                  // chunks per step
     constexpr int kCPW = 4 * kGPW;              // chunks per wave
@@ -364,7 +391,8 @@ __global__ __launch_bounds__(kBlock) void k_decode_diag(const uint16_t* __restri
     constexpr int kItems = kM * kCPW * 8;       // 4-element items of the slices
     constexpr int kIPL = (kItems + kWave - 1) / kWave;
     constexpr int kW = kWinD < kSteps ? kWinD : kSteps;
-    __shared__ __attribute__((aligned(16))) uint8_t xs[kWaves][kM + 1][kStrip];  // [kM]: zeros
+    __shared__ __attribute__((aligned(16))) uint8_t xs[kWaves][kM][kStrip];
+    __shared__ __attribute__((aligned(16))) uint8_t zs[kStrip];  // zeros, written by every wave
     __shared__ __attribute__((aligned(16))) float part[kWaves][kM][T];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -397,8 +425,9 @@ __global__ __launch_bounds__(kBlock) void k_decode_diag(const uint16_t* __restri
         w[i] = __builtin_nontemporal_load(
             reinterpret_cast<const u32x4*>(wb + min<int64_t>(c0 + i * kS + cs, C - 1) * T * 16));
 
-    for (int b = lane * 16; b < kStrip; b += kWave * 16)
-        *reinterpret_cast<u32x4*>(&xs[wave][kM][b]) = u32x4{0u, 0u, 0u, 0u};
+    // every wave zeroes the shared zero strip (the same value from every writer, so
+    // no barrier is needed before a wave reads what it wrote itself)
+    for (int b = lane * 16; b < kStrip; b += kWave * 16) *reinterpret_cast<u32x4*>(&zs[b]) = u32x4{0u, 0u, 0u, 0u};
     // stage: lanes 2b, 2b+1 hold an 8-block's (x0..x3) and (x4..x7); the even lane
     // writes slots (x0,x4)(x1,x5), the odd lane (x2,x6)(x3,x7)
     float gsum[kIPL];
@@ -436,7 +465,7 @@ __global__ __launch_bounds__(kBlock) void k_decode_diag(const uint16_t* __restri
         corr[g] = 136.0f * c;
     }
     const bool diag = col % kR == rg && tok < kM;
-    const uint8_t* bsrc = diag ? &xs[wave][tok][cs * 64] : &xs[wave][kM][0];
+    const uint8_t* bsrc = diag ? &xs[wave][tok][cs * 64] : &zs[0];
     // the strips are private to the wave: its LDS accesses complete in order
 
     f32x4 tot = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -471,43 +500,89 @@ __global__ __launch_bounds__(kBlock) void k_decode_diag(const uint16_t* __restri
     }
     if (tok < kM) *reinterpret_cast<f32x4*>(&part[wave][tok][row0]) = tot;
     __syncthreads();
-    for (int i = threadIdx.x; i < m * T; i += kBlock) {
-        const int j = i / T, r = i - j * T;
-        const int64_t row = tile * T + r;
-        if (row >= n) continue;
+    auto wsum = [&](int j, int r) {
         float s = 0.0f;
 #pragma unroll
         for (int v = 0; v < kWaves; ++v) s += part[v][j][r];
-        y[j * n + row] = s + (bias ? bias[row] : 0.0f);
+        return s;
+    };
+    if constexpr (kEpi == kEpiPlain) {
+        for (int i = threadIdx.x; i < m * T; i += kBlock) {
+            const int j = i / T, r = i - j * T;
+            const int64_t row = tile * T + r;
+            if (row >= n) continue;
+            y[j * n + row] = wsum(j, r) + (bias ? bias[row] : 0.0f);
+        }
+    } else if constexpr (kEpi == kEpiFold) {
+        const int t = m >> 1;
+        for (int i = threadIdx.x; i < t * T; i += kBlock) {
+            const int j = i / T, r = i - j * T;
+            const int64_t row = tile * T + r;
+            if (row >= n) continue;
+            y[j * n + row] = (wsum(j, r) + wsum(t + j, r)) + (bias ? bias[row] : 0.0f);
+        }
+    } else {
+        const int64_t f = n >> 1;  // h columns: the stacked weight has 2f rows
+        for (int i = threadIdx.x; i < m * 32; i += kBlock) {
+            const int j = i >> 5, r = i & 31;
+            const int64_t hc = tile * 32 + r;
+            if (hc >= f) continue;
+            const float g = wsum(j, r), u = wsum(j, 32 + r);
+            const float h = g * (1.0f / (1.0f + __expf(-g))) * u;
+            const __bf16 hi = static_cast<__bf16>(h);
+            const __bf16 lo = static_cast<__bf16>(h - static_cast<float>(hi));
+            const int64_t J = tok0 + j;
+            hout[MlpRows::hi(J, mtot) * f + hc] = __builtin_bit_cast(uint16_t, hi);
+            hout[MlpRows::lo(J, mtot) * f + hc] = __builtin_bit_cast(uint16_t, lo);
+        }
     }
 }
 
 // kR in {1, 2, 4}; kM in {1, 2, 4} (3 tokens run as 4 with a zero token); groups per
-// wave in {1, 2, 4, 8} (8 only for kM <= 2: the strips of 4 tokens would not fit)
-template <int kR, int kM>
-int launch_diag(int64_t gpw, int64_t tiles, hipStream_t s, const uint16_t* x, int m, const uint8_t* pt,
-                const uint16_t* st, const float* b, int64_t n, int64_t k, float* y) {
+// wave in {1, 2, 4, 8} (K <= 16384)
+struct DiagArgs {
+    const uint16_t* x;
+    int m;
+    const uint8_t* pt;
+    const uint16_t* st;
+    const float* b;
+    int64_t n, k;
+    float* y;
+    uint16_t* hout;  // kEpiGateUp
+    int tok0, mtot;  // kEpiGateUp
+};
+
+template <int kR, int kM, int kEpi>
+int launch_diag(int64_t gpw, int64_t tiles, hipStream_t s, const DiagArgs& a) {
     constexpr int kWinD = kR == 1 ? 2 : 3;  // measured: steps of 4 chunks want a shorter window
     const unsigned grid = static_cast<unsigned>(tiles);
+#define TQ_DIAG(G)                                                                                      \
+    k_decode_diag<kR, kM, G, kWinD, kEpi><<<grid, kBlock, 0, s>>>(a.x, a.m, a.pt, a.st, a.b, a.n, a.k, a.y, \
+                                                                  a.hout, a.tok0, a.mtot)
     if (gpw <= 1)
-        k_decode_diag<kR, kM, 1, kWinD><<<grid, kBlock, 0, s>>>(x, m, pt, st, b, n, k, y);
+        TQ_DIAG(1);
     else if (gpw <= 2)
-        k_decode_diag<kR, kM, 2, kWinD><<<grid, kBlock, 0, s>>>(x, m, pt, st, b, n, k, y);
+        TQ_DIAG(2);
     else if (gpw <= 4)
-        k_decode_diag<kR, kM, 4, kWinD><<<grid, kBlock, 0, s>>>(x, m, pt, st, b, n, k, y);
-    else if constexpr (kM <= 2)
-        k_decode_diag<kR, kM, 8, kWinD><<<grid, kBlock, 0, s>>>(x, m, pt, st, b, n, k, y);
+        TQ_DIAG(4);
     else
-        return fail(TQ_EINVAL, "tq_gemv_w4g128_tiled: 3-4 tokens with K > 8192 on the diagonal kernel");
+        TQ_DIAG(8);
+#undef TQ_DIAG
     return check_launch("tq_gemv_w4g128_tiled");
 }
 
-template <int kR>
-int launch_diag_m(int64_t gpw, int64_t tiles, hipStream_t s, const uint16_t* x, int m, const uint8_t* pt,
-                  const uint16_t* st, const float* b, int64_t n, int64_t k, float* y) {
-    if (m == 1) return launch_diag<kR, 1>(gpw, tiles, s, x, m, pt, st, b, n, k, y);
-    if (m == 2) return launch_diag<kR, 2>(gpw, tiles, s, x, m, pt, st, b, n, k, y);
-    return launch_diag<kR, 4>(gpw, tiles, s, x, m, pt, st, b, n, k, y);
+template <int kR, int kEpi>
+int launch_diag_m(int64_t gpw, int64_t tiles, hipStream_t s, const DiagArgs& a) {
+    if (a.m == 1) return launch_diag<kR, 1, kEpi>(gpw, tiles, s, a);
+    if (a.m == 2) return launch_diag<kR, 2, kEpi>(gpw, tiles, s, a);
+    return launch_diag<kR, 4, kEpi>(gpw, tiles, s, a);
+}
+
+template <int kEpi>
+int launch_diag_r(int kr, int64_t gpw, int64_t tiles, hipStream_t s, const DiagArgs& a) {
+    if (kr == 1) return launch_diag_m<1, kEpi>(gpw, tiles, s, a);
+    if (kr == 2) return launch_diag_m<2, kEpi>(gpw, tiles, s, a);
+    return launch_diag_m<4, kEpi>(gpw, tiles, s, a);
 }
 
 template <int kR>
@@ -542,6 +617,32 @@ __global__ __launch_bounds__(256) void k_repack_tiled(const uint8_t* __restrict_
         const int64_t r = o % T, tg = o / T, g = tg % G, t = tg / G;
         const int64_t row = t * T + r;
         st[o] = row < n ? s16[row * G + g] : uint16_t(0);
+    }
+}
+
+// Gate and up projections of an FFN as one tiled weight of 64-row tiles: tile t
+// holds gate rows 32t .. 32t + 31 (tile rows 0-31) and up rows 32t .. 32t + 31
+// (tile rows 32-63), in the layout above with T = 64; rows past f are zero.
+__global__ __launch_bounds__(256) void k_repack_gate_up(const uint8_t* __restrict__ gp, const uint16_t* __restrict__ gs,
+                                                        const uint8_t* __restrict__ up, const uint16_t* __restrict__ us,
+                                                        int64_t f, int64_t d, int64_t tiles, uint8_t* __restrict__ pt,
+                                                        uint16_t* __restrict__ st) {
+    const int64_t C = d >> 5, G = d >> 7;
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * 256;
+    const int64_t total = tiles * C * 64;
+    for (int64_t o = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; o < total; o += stride) {
+        const int64_t r = o % 64, tc = o / 64, c = tc % C, t = tc / C;
+        const int64_t row = 32 * t + (r & 31);
+        const uint8_t* src = r < 32 ? gp : up;
+        u32x4 v = u32x4{0u, 0u, 0u, 0u};
+        if (row < f) v = *reinterpret_cast<const u32x4*>(src + row * (d >> 1) + c * 16);
+        reinterpret_cast<u32x4*>(pt)[o] = v;
+    }
+    const int64_t stotal = tiles * G * 64;
+    for (int64_t o = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; o < stotal; o += stride) {
+        const int64_t r = o % 64, tg = o / 64, g = tg % G, t = tg / G;
+        const int64_t row = 32 * t + (r & 31);
+        st[o] = row < f ? (r < 32 ? gs : us)[row * G + g] : uint16_t(0);
     }
 }
 
@@ -620,12 +721,10 @@ int tq_gemv_w4g128_tiled(const uint16_t* x_bf16, int64_t m, const uint8_t* packe
     const hipStream_t st = as_hip(stream);
     const int kr = T == 16 ? 1 : (T == 32 ? 2 : (T == 64 ? 4 : 0));
     const int64_t gpw = ((k >> 7) + kWaves - 1) / kWaves;
-    // 1-2 tokens (and 3-4 on 16- and 32-row tiles, K <= 8192): the diagonal MFMA kernel
-    if (kr && aligned(x_bf16, 8) && aligned(s_t, 8) && (m <= 2 || (m <= 4 && kr < 4 && gpw <= 4))) {
-        const int mi = static_cast<int>(m);
-        if (kr == 1) return launch_diag_m<1>(gpw, tiles, st, x_bf16, mi, packed_t, s_t, bias, n, k, y);
-        if (kr == 2) return launch_diag_m<2>(gpw, tiles, st, x_bf16, mi, packed_t, s_t, bias, n, k, y);
-        return launch_diag_m<4>(gpw, tiles, st, x_bf16, mi, packed_t, s_t, bias, n, k, y);
+    // 1-2 tokens (and 3-4 on 16- and 32-row tiles): the diagonal MFMA kernel
+    if (kr && aligned(x_bf16, 8) && aligned(s_t, 8) && (m <= 2 || (m <= 4 && (kr < 4 || gpw > 4)))) {
+        const DiagArgs a{x_bf16, static_cast<int>(m), packed_t, s_t, bias, n, k, y, nullptr, 0, 0};
+        return launch_diag_r<kEpiPlain>(kr, gpw, tiles, st, a);
     }
     // 3..16 tokens: the MFMA kernel where the tile is 16, 32 or 64 rows, the 16 waves'
     // K runs are at most 4 groups (K <= 8192) and x rows are 16-byte aligned
@@ -644,6 +743,75 @@ int tq_gemv_w4g128_tiled(const uint16_t* x_bf16, int64_t m, const uint8_t* packe
         else if (mm == 3) dispatch_tiled<3>(cpw, tiles, st, xp, packed_t, s_t, bias, n, k, T, yp);
         else dispatch_tiled<4>(cpw, tiles, st, xp, packed_t, s_t, bias, n, k, T, yp);
         const int rc = check_launch("tq_gemv_w4g128_tiled");
+        if (rc != TQ_OK) return rc;
+    }
+    return TQ_OK;
+}
+
+int64_t tq_mlp_w4g128_decode_workspace_bytes(int64_t m, int64_t d, int64_t f) {
+    if (m < 0 || d < 0 || f < 0) return -1;
+    return ((2 * m * f * 2 + 255) / 256) * 256;  // bf16 hi and lo rows of h
+}
+
+int tq_repack_w4g128_gate_up_tiled(const uint8_t* gate_packed, const uint16_t* gate_s, const uint8_t* up_packed,
+                                   const uint16_t* up_s, int64_t f, int64_t d, uint8_t* packed_t, uint16_t* s_t,
+                                   tq_stream_t stream) {
+    TQ_REQUIRE(f >= 0 && d >= 0, "tq_repack_w4g128_gate_up_tiled: negative shape");
+    TQ_REQUIRE(d % 128 == 0, "tq_repack_w4g128_gate_up_tiled: D=%lld is not a multiple of 128", (long long)d);
+    if (f == 0 || d == 0) return TQ_OK;
+    TQ_REQUIRE(gate_packed && gate_s && up_packed && up_s && packed_t && s_t,
+               "tq_repack_w4g128_gate_up_tiled: null pointer");
+    TQ_REQUIRE(aligned(gate_packed, 16) && aligned(up_packed, 16) && aligned(packed_t, 16) && aligned(gate_s, 2) &&
+                   aligned(up_s, 2) && aligned(s_t, 2),
+               "tq_repack_w4g128_gate_up_tiled: misaligned pointer (packed buffers need 16 B)");
+    const int64_t tiles = (f + 31) / 32;
+    int64_t blocks = (tiles * (d >> 5) * 64 + 255) / 256;
+    if (blocks > 65536) blocks = 65536;
+    k_repack_gate_up<<<static_cast<unsigned>(blocks), 256, 0, as_hip(stream)>>>(gate_packed, gate_s, up_packed, up_s,
+                                                                                f, d, tiles, packed_t, s_t);
+    return check_launch("tq_repack_w4g128_gate_up_tiled");
+}
+
+int tq_mlp_w4g128_decode(const uint16_t* x_bf16, int64_t m, int64_t d, int64_t f, const uint8_t* gate_up_t,
+                         const uint16_t* gate_up_s_t, const uint8_t* down_t, const uint16_t* down_s_t,
+                         int64_t down_tile_rows, void* workspace, int64_t workspace_bytes, float* y,
+                         tq_stream_t stream) {
+    TQ_REQUIRE(m >= 0 && d >= 0 && f >= 0, "tq_mlp_w4g128_decode: negative shape");
+    TQ_REQUIRE(m <= 16, "tq_mlp_w4g128_decode: M=%lld > 16", (long long)m);
+    TQ_REQUIRE(d % 128 == 0 && f % 128 == 0, "tq_mlp_w4g128_decode: D=%lld and F=%lld must be multiples of 128",
+               (long long)d, (long long)f);
+    TQ_REQUIRE(d <= kMaxCPW * kWaves * 32 && f <= kMaxCPW * kWaves * 32,
+               "tq_mlp_w4g128_decode: D=%lld or F=%lld > %d", (long long)d, (long long)f, kMaxCPW * kWaves * 32);
+    TQ_REQUIRE(down_tile_rows == 16 || down_tile_rows == 32 || down_tile_rows == 64,
+               "tq_mlp_w4g128_decode: down tile_rows=%lld must be 16, 32 or 64", (long long)down_tile_rows);
+    if (m == 0 || d == 0) return TQ_OK;
+    TQ_REQUIRE(f > 0, "tq_mlp_w4g128_decode: F=0");
+    TQ_REQUIRE(x_bf16 && gate_up_t && gate_up_s_t && down_t && down_s_t && workspace && y,
+               "tq_mlp_w4g128_decode: null pointer");
+    const int64_t need = tq_mlp_w4g128_decode_workspace_bytes(m, d, f);
+    TQ_REQUIRE(workspace_bytes >= need, "tq_mlp_w4g128_decode: workspace of %lld bytes, %lld needed",
+               (long long)workspace_bytes, (long long)need);
+    TQ_REQUIRE(aligned(x_bf16, 8) && aligned(gate_up_t, 16) && aligned(down_t, 16) && aligned(gate_up_s_t, 8) &&
+                   aligned(down_s_t, 8) && aligned(workspace, 16) && aligned(y, 4),
+               "tq_mlp_w4g128_decode: misaligned pointer");
+    const hipStream_t st = as_hip(stream);
+    uint16_t* h = static_cast<uint16_t*>(workspace);
+    const int mi = static_cast<int>(m);
+    // gate + up with SiLU * up, 4 tokens per launch, into the hi/lo rows of h
+    const int64_t gu_tiles = (f + 31) / 32, gu_gpw = ((d >> 7) + kWaves - 1) / kWaves;
+    for (int j0 = 0; j0 < mi; j0 += 4) {
+        const int mm = mi - j0 < 4 ? mi - j0 : 4;
+        const DiagArgs a{x_bf16 + j0 * d, mm, gate_up_t, gate_up_s_t, nullptr, 2 * f, d, nullptr, h, j0, mi};
+        const int rc = launch_diag_m<4, kEpiGateUp>(gu_gpw, gu_tiles, st, a);
+        if (rc != TQ_OK) return rc;
+    }
+    // down, one launch per token pair: its hi and lo rows in, their sum out
+    const int kr = down_tile_rows == 16 ? 1 : (down_tile_rows == 32 ? 2 : 4);
+    const int64_t dn_tiles = (d + down_tile_rows - 1) / down_tile_rows, dn_gpw = ((f >> 7) + kWaves - 1) / kWaves;
+    for (int c = 0; 2 * c < mi; ++c) {
+        const int t = mi - 2 * c < 2 ? mi - 2 * c : 2;
+        const DiagArgs a{h + 4 * c * f, 2 * t, down_t, down_s_t, nullptr, d, f, y + 2 * c * d, nullptr, 0, 0};
+        const int rc = launch_diag_r<kEpiFold>(kr, dn_gpw, dn_tiles, st, a);
         if (rc != TQ_OK) return rc;
     }
     return TQ_OK;

@@ -21,6 +21,7 @@ from .formats import (
     quantize_i4_g128,
     quantize_per_channel_fp8,
     quantize_per_channel_i8,
+    repack_i4_g128_gate_up_tiled,
     repack_i4_g128_tiled,
     tile_rows_for,
 )
@@ -35,6 +36,6 @@ __all__ = [
     "quantize_tensor", "dequantize_tensor", "quantize_per_tensor", "fake_quantize",
     "quantize_per_channel_i8", "dequantize_per_channel_i8", "fake_quantize_per_channel_i8",
     "quantize_per_channel_fp8", "dequantize_per_channel_fp8", "fake_quantize_per_channel_fp8",
-    "quantize_i4_g128", "dequantize_i4_g128", "repack_i4_g128_tiled", "tile_rows_for", "Module", "QuantizedLinear", "QuantizedMLP", "QuantizedMultiheadAttention",
+    "quantize_i4_g128", "dequantize_i4_g128", "repack_i4_g128_tiled", "repack_i4_g128_gate_up_tiled", "tile_rows_for", "Module", "QuantizedLinear", "QuantizedMLP", "QuantizedMultiheadAttention",
     "save_safetensors", "load_safetensors", "save_quantized", "load_quantized", "convert",
 ]

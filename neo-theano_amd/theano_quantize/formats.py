@@ -116,6 +116,25 @@ def tile_rows_for(n: int) -> int:
     return int(_abi.lib().tq_w4g128_tile_rows(int(n)))
 
 
+def repack_i4_g128_gate_up_tiled(gate, up):
+    """Gate and up projections of an FFN (canonical INT4 g128 (packed, scales) pairs
+    of [F, D]) as one row-tiled weight of 64-row tiles: tile t holds gate rows
+    32t..32t+31 then up rows 32t..32t+31.  Returns (packed_t, s_t)."""
+    gp = on_device(gate[0], torch.uint8, "repack_i4_g128_gate_up_tiled")
+    gs = on_device(gate[1], torch.float16, "repack_i4_g128_gate_up_tiled")
+    upk = on_device(up[0], torch.uint8, "repack_i4_g128_gate_up_tiled")
+    us = on_device(up[1], torch.float16, "repack_i4_g128_gate_up_tiled")
+    f, kh = gp.shape
+    if tuple(upk.shape) != (f, kh):
+        raise InvalidArgument("repack_i4_g128_gate_up_tiled: gate and up must have the same shape")
+    d = 2 * kh
+    tiles = (f + 31) // 32
+    pt = torch.empty(tiles * 64 * kh, dtype=torch.uint8, device=gp.device)
+    st = torch.empty(tiles * 64 * (d // GROUP), dtype=torch.float16, device=gp.device)
+    _abi.call("tq_repack_w4g128_gate_up_tiled", ptr(gp), ptr(gs), ptr(upk), ptr(us), f, d, ptr(pt), ptr(st), stream())
+    return pt, st
+
+
 def repack_i4_g128_tiled(packed, scales, tile_rows=None):
     """Row-tiled kernel layout of a canonical INT4 g128 weight (a pure permutation,
     rows padded to a multiple of tile_rows).  Returns (packed_t, s_t, tile_rows)."""

@@ -29,11 +29,13 @@ import torch
 from . import _abi
 from ._tensor import on_device, ptr, stream
 from .errors import InvalidArgument
-from .formats import quantize_i4_g128, quantize_per_channel_fp8, quantize_per_channel_i8, repack_i4_g128_tiled
+from .formats import (quantize_i4_g128, quantize_per_channel_fp8, quantize_per_channel_i8, repack_i4_g128_gate_up_tiled,
+                      repack_i4_g128_tiled)
 from .qconfig import QConfig, QuantDType
 
 DECODE_MAX_M = 16
 TILED_MAX_M = 16  # decode shapes run on the row-tiled copy of an INT4 weight
+DECODE_MLP_MAX_M = 8  # QuantizedMLP runs the decode GEMV kernels up to here, the prefill FFN beyond
 
 
 class Module:
@@ -186,9 +188,16 @@ class QuantizedMLP(Module):
     (crates/theano-nn/src/activation.rs:66-79) and Tensor::mul; the
     SiLU(gate)*up intermediate is kept in f32."""
 
-    def __init__(self, d, f, gate, up, down):
+    def __init__(self, d, f, gate, up, down, tiled=True):
         self.d, self.f = int(d), int(f)
         self.gate, self.up, self.down = gate, up, down  # (packed, scales) pairs
+        self.decode = None
+        if tiled and self.d <= 16384 and self.f <= 16384:
+            # row-tiled copies (permutations of the weights) for decode shapes, M <= 8:
+            # gate and up interleaved in 64-row tiles, down on its own tile height
+            gu = repack_i4_g128_gate_up_tiled(gate, up)
+            dn = repack_i4_g128_tiled(down[0], down[1])
+            self.decode = (gu[0], gu[1], dn[0], dn[1], dn[2])
 
     @staticmethod
     def from_tensors(gate_w, up_w, down_w) -> "QuantizedMLP":
@@ -208,8 +217,13 @@ class QuantizedMLP(Module):
     def num_parameters(self) -> int:
         return 3 * self.d * self.f
 
+    def _decode_path(self, m: int) -> bool:
+        return self.decode is not None and 1 <= m <= DECODE_MLP_MAX_M
+
     def workspace_bytes(self, m: int) -> int:
         """Device bytes of intermediates forward() needs for m tokens."""
+        if self._decode_path(m):
+            return int(_abi.lib().tq_mlp_w4g128_decode_workspace_bytes(m, self.d, self.f))
         return int(_abi.lib().tq_mlp_w4g128_workspace_bytes(m, self.d, self.f))
 
     def forward(self, x, workspace=None):
@@ -223,9 +237,15 @@ class QuantizedMLP(Module):
         if workspace is None:
             workspace = torch.empty((max(need, 1),), dtype=torch.uint8, device=x.device)
         y = torch.empty((m, self.d), dtype=torch.float32, device=x.device)
+        wsb = workspace.numel() * workspace.element_size()
+        if self._decode_path(m):
+            gu_t, gu_st, dn_t, dn_st, dn_rows = self.decode
+            _abi.call("tq_mlp_w4g128_decode", ptr(x), m, self.d, self.f, ptr(gu_t), ptr(gu_st), ptr(dn_t),
+                      ptr(dn_st), dn_rows, ptr(workspace), wsb, ptr(y), stream())
+            return y
         _abi.call("tq_mlp_w4g128", ptr(x), m, self.d, self.f, ptr(self.gate[0]), ptr(self.gate[1]),
                   ptr(self.up[0]), ptr(self.up[1]), ptr(self.down[0]), ptr(self.down[1]),
-                  ptr(workspace), workspace.numel() * workspace.element_size(), ptr(y), stream())
+                  ptr(workspace), wsb, ptr(y), stream())
         return y
 
 

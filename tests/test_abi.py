@@ -96,6 +96,14 @@ def test_observer_scale_zp_matches_oracle(abi, oracle):
     ("tq_mlp_w4g128", [None, 4, 100, 128, None, None, None, None, None, None, None, 0, None, None]),  # D % 128
     ("tq_mlp_w4g128", [None, 4, 256, 256, None, None, None, None, None, None, None, 0, None, None]),  # nulls
     ("tq_mlp_w4g128", [256, 4, 256, 256, 256, 256, 256, 256, 256, 256, 256, 16, 256, None]),  # workspace
+    ("tq_mlp_w4g128_decode", [None, 17, 256, 256, None, None, None, None, 16, None, 0, None, None]),  # M > 16
+    ("tq_mlp_w4g128_decode", [None, 2, 100, 256, None, None, None, None, 16, None, 0, None, None]),  # D % 128
+    ("tq_mlp_w4g128_decode", [None, 2, 256, 32768, None, None, None, None, 16, None, 0, None, None]),  # F > 16384
+    ("tq_mlp_w4g128_decode", [None, 2, 256, 256, None, None, None, None, 24, None, 0, None, None]),  # tile rows
+    ("tq_mlp_w4g128_decode", [None, 2, 256, 256, None, None, None, None, 16, None, 0, None, None]),  # nulls
+    ("tq_mlp_w4g128_decode", [256, 2, 256, 256, 256, 256, 256, 256, 16, 256, 16, 256, None]),  # workspace
+    ("tq_repack_w4g128_gate_up_tiled", [None, None, None, None, 128, 100, None, None, None]),  # D % 128
+    ("tq_repack_w4g128_gate_up_tiled", [None, None, None, None, 128, 128, None, None, None]),  # nulls
     ("tq_quantize_tensor", [None, 10, 1.0, 0.0, 7, None, None]),          # bad QuantDType
     ("tq_quantize_per_tensor", [None, 10, 0, None, None, None, None]),
     ("tq_minmax_reset", [None, 0, None]),
@@ -128,6 +136,15 @@ def test_mlp_workspace_bytes(abi):
     assert ws(m, d, f) == sum((p + 255) // 256 * 256 for p in parts)
     assert ws(1, 128, 128) >= 4 * 1 * 128  # covers the f32 h [M, F] of the shape-general path
     assert ws(0, 128, 128) == 0
+
+
+def test_mlp_decode_workspace_bytes(abi):
+    ws = abi.lib().tq_mlp_w4g128_decode_workspace_bytes
+    # bf16 hi and lo rows of h for each token, rounded up to 256 bytes
+    assert ws(1, 4096, 14336) == 2 * 14336 * 2
+    assert ws(3, 256, 384) == 2 * 3 * 384 * 2
+    assert ws(1, 128, 128) == 512
+    assert ws(0, 128, 128) == 0 and ws(-1, 128, 128) == -1
 
 
 def test_dtype_sizes(abi, oracle):

@@ -144,17 +144,18 @@ def test_gemv_w4g128_tiled_config3(tq, c3, m):
     assert_close(host(y), ref[:m], RTOL, ATOL, f"gemv_w4g128_tiled M={m} T={t}")
 
 
-# Tiles of 16, 32 or 64 rows: 1-2 tokens (3-4 on 16- and 32-row tiles, K <= 8192) run
-# the diagonal MFMA kernel (one to eight groups per wave, waves past K, tail tiles),
-# 3-16 tokens otherwise the MFMA kernel with x from L2 (token passes, K <= 8192);
-# other tile heights and 3-4 tokens at K > 8192 on small tiles run the dot2 kernel.
+# Tiles of 16, 32 or 64 rows: 1-2 tokens (3-4 on 16- and 32-row tiles, and on 64-row
+# tiles at K > 8192) run the diagonal MFMA kernel (one to eight groups per wave,
+# waves past K, tail tiles); 3-16 tokens otherwise the MFMA kernel with x from L2
+# (token passes, K <= 8192); other tile heights run the dot2 kernel.
 @pytest.mark.parametrize("n,k,m,t", [(100, 128, 1, 8), (7, 2176, 2, 8), (256, 14336, 1, 16), (48, 16384, 3, 24),
                                      (1000, 4096, 4, 64), (333, 640, 2, 40),
                                      (1000, 4096, 5, 64), (70, 1024, 16, 16), (200, 6144, 7, 32),
                                      (130, 8192, 9, 16), (77, 384, 13, 64), (64, 8192, 3, 64),
                                      (100, 128, 1, 16), (200, 6144, 2, 32), (40, 16384, 2, 32), (333, 4224, 2, 64),
                                      (1000, 4096, 1, 64), (130, 8192, 4, 16), (70, 1152, 3, 16), (100, 2048, 3, 32),
-                                     (48, 16384, 3, 16), (4100, 14336, 2, 16), (90, 16384, 1, 64)])
+                                     (48, 16384, 3, 16), (4100, 14336, 2, 16), (90, 16384, 1, 64),
+                                     (90, 16384, 4, 64), (50, 9000 // 128 * 128, 3, 64)])
 def test_gemv_w4g128_tiled_shapes(tq, oracle, n, k, m, t):
     from theano_quantize import _abi
     from theano_quantize._tensor import ptr, stream
@@ -314,8 +315,13 @@ def test_gemm_w4g128_bf16_shapes(tq, oracle, m, n, k):
 
 
 # ------------------------------------------------------------------- MLP
-# (5, 256, 384) and (1, 128, 128) have an odd number of groups: shape-general
-# path; the others take the pipelined kernels (row tails at 64 / 128).
+def _prefill_only(tq, mlp):
+    """The same weights without the decode copies: every M runs the prefill kernels."""
+    return tq.QuantizedMLP(mlp.d, mlp.f, mlp.gate, mlp.up, mlp.down, tiled=False)
+
+
+# Prefill kernels: (5, 256, 384) and (1, 128, 128) have an odd number of groups:
+# shape-general path; the others take the pipelined kernels (row tails at 64 / 128).
 @pytest.mark.parametrize("m,d,f", [(5, 256, 384), (1, 128, 128), (70, 512, 1024), (1, 256, 512),
                                    (129, 768, 1536), (300, 1024, 2048), (64, 256, 256), (200, 512, 768)])
 def test_mlp_small(tq, oracle, m, d, f):
@@ -323,7 +329,7 @@ def test_mlp_small(tq, oracle, m, d, f):
     wu = normal(56, (f, d), 0.02, stream=1)
     wd = normal(56, (d, f), 0.02, stream=2)
     xb = to_bf16_bits(normal(56, (m, d), 1.0, stream=3))
-    mlp = tq.QuantizedMLP.from_tensors(dev_tensor(wg), dev_tensor(wu), dev_tensor(wd))
+    mlp = _prefill_only(tq, tq.QuantizedMLP.from_tensors(dev_tensor(wg), dev_tensor(wu), dev_tensor(wd)))
     y = host(mlp(bf16_dev(xb)))
     args = [a for t in (mlp.gate, mlp.up, mlp.down) for a in (host(t[0]), host(t[1]).view(np.uint16))]
     assert_close(y, oracle.mlp_w4g128(xb, *args), RTOL, ATOL, f"mlp {m}x{d}x{f}")
@@ -349,6 +355,64 @@ def _mlp_case(tq, m, d, f, seed=57):
     xb = to_bf16_bits(normal(seed, (m, d), 1.0, stream=3))
     mlp = tq.QuantizedMLP.from_tensors(dev_tensor(wg), dev_tensor(wu), dev_tensor(wd))
     return mlp, xb
+
+
+# Decode path (M <= 8): gate and up interleaved in 64-row tiles with SiLU * up in
+# the epilogue (4 tokens per launch), down on h as bf16 hi + lo rows (a token
+# pair per launch, the halves added per token); one to eight groups per wave,
+# odd M (a last pair of one token), F not a multiple of 64, the Llama shape.
+@pytest.mark.parametrize("m,d,f", [(1, 128, 128), (2, 256, 384), (3, 512, 1024), (4, 1024, 640), (5, 256, 512),
+                                   (7, 384, 1152), (8, 2048, 256), (1, 4096, 14336), (2, 14336, 4096),
+                                   (6, 16384, 128)])
+def test_mlp_decode_path(tq, oracle, m, d, f):
+    wg = normal(60, (f, d), 0.02)
+    wu = normal(60, (f, d), 0.02, stream=1)
+    wd = normal(60, (d, f), 0.02, stream=2)
+    xb = to_bf16_bits(normal(60, (m, d), 1.0, stream=3))
+    mlp = tq.QuantizedMLP.from_tensors(dev_tensor(wg), dev_tensor(wu), dev_tensor(wd))
+    assert mlp._decode_path(m)
+    y = host(mlp(bf16_dev(xb)))
+    args = [a for t in (mlp.gate, mlp.up, mlp.down) for a in (host(t[0]), host(t[1]).view(np.uint16))]
+    assert_close(y, oracle.mlp_w4g128(xb, *args), RTOL, ATOL, f"mlp decode {m}x{d}x{f}")
+
+
+def test_mlp_decode_and_prefill_agree_and_reuse_workspace(tq, oracle):
+    """Both paths meet the tolerance on the same weights; one decode workspace
+    serves calls of decreasing M; a short one is rejected."""
+    import torch
+    from theano_quantize import InvalidArgument
+
+    d, f = 512, 1536
+    mlp, xb = _mlp_case(tq, 8, d, f, seed=61)
+    args = [a for t in (mlp.gate, mlp.up, mlp.down) for a in (host(t[0]), host(t[1]).view(np.uint16))]
+    ws = torch.empty((mlp.workspace_bytes(8),), dtype=torch.uint8, device="cuda")
+    pre = _prefill_only(tq, mlp)
+    for m in (8, 5, 2, 1):
+        ref = oracle.mlp_w4g128(xb[:m], *args)
+        assert_close(host(mlp.forward(bf16_dev(xb[:m]), ws)), ref, RTOL, ATOL, f"decode M={m}")
+        assert_close(host(pre.forward(bf16_dev(xb[:m]))), ref, RTOL, ATOL, f"prefill M={m}")
+    with pytest.raises(InvalidArgument):
+        mlp.forward(bf16_dev(xb), ws[:mlp.workspace_bytes(8) - 256])
+
+
+def test_repack_gate_up_is_a_permutation(tq):
+    """Tile t of the gate/up copy: gate rows 32t..32t+31, then the same up rows, in
+    the row-tiled layout with 64-row tiles; rows past F are zero."""
+    f, d = 96, 384
+    p_g, s_g = tq.quantize_i4_g128(dev_tensor(normal(62, (f, d), 0.02)))
+    p_u, s_u = tq.quantize_i4_g128(dev_tensor(normal(62, (f, d), 0.02, stream=1)))
+    pt, st = tq.repack_i4_g128_gate_up_tiled((p_g, s_g), (p_u, s_u))
+    tiles = (f + 31) // 32
+    up, us = untile(host(pt), host(st).view(np.uint16), tiles * 64, d, 64)
+    pg, pu = np.zeros((tiles * 32, d // 2), np.uint8), np.zeros((tiles * 32, d // 2), np.uint8)
+    sg, su = np.zeros((tiles * 32, d // 128), np.uint16), np.zeros((tiles * 32, d // 128), np.uint16)
+    pg[:f], pu[:f] = host(p_g), host(p_u)
+    sg[:f], su[:f] = host(s_g).view(np.uint16), host(s_u).view(np.uint16)
+    for t in range(tiles):
+        assert np.array_equal(up[64 * t:64 * t + 32], pg[32 * t:32 * t + 32])
+        assert np.array_equal(up[64 * t + 32:64 * t + 64], pu[32 * t:32 * t + 32])
+        assert np.array_equal(us[64 * t:64 * t + 32], sg[32 * t:32 * t + 32])
+        assert np.array_equal(us[64 * t + 32:64 * t + 64], su[32 * t:32 * t + 32])
 
 
 def test_mlp_paths_agree(tq, oracle):
@@ -377,6 +441,7 @@ def test_mlp_workspace_reuse_and_size_check(tq, oracle):
 
     d, f = 256, 512
     mlp, xb = _mlp_case(tq, 300, d, f, seed=58)
+    mlp = _prefill_only(tq, mlp)
     ws = torch.empty((mlp.workspace_bytes(300),), dtype=torch.uint8, device="cuda")
     args = [a for t in (mlp.gate, mlp.up, mlp.down) for a in (host(t[0]), host(t[1]).view(np.uint16))]
     for m in (300, 130, 7):

@@ -44,7 +44,7 @@ def parse_args():
     p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--only", default=None,
                    help="run one workload: gemv_w4, gemv_w8, gemv_fp8, gemv_w4_m, w8a8_decode, w8a8, fp8, mha, storage, "
-                        "roundtrip, mlp, copy")
+                        "roundtrip, mlp, mlp_decode, copy")
     p.add_argument("--no-secondary", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=12.0, help="bound of the CPU baseline sample (0: skip)")
     p.add_argument("--eager", action="store_true", help="time eager launches instead of a HIP graph")
@@ -421,6 +421,33 @@ def main():
                                                        "bf16_mfma_frac": round(tf / BF16_PEAK_TFLOPS, 4)}
         log(f"w4a16 linear M=512 N=14336 K=4096: {ms * 1e3:.1f} us  {tf:.0f} TFLOP/s")
         del mlp, wsl, yl
+
+    # ------------------------------------ decode FFN (C5 weights, M = 1, 4)
+    if not args.no_secondary and want("mlp_decode"):
+        d5, f5 = 4096, 14336
+        base = tq.QuantizedMLP.from_tensors(dt(normal_f32(4, (f5, d5), 0.02)), dt(normal_f32(4, (f5, d5), 0.02, 1)),
+                                            dt(normal_f32(4, (d5, f5), 0.02, 2)))
+        wbytes = 3 * f5 * d5 // 2 + 3 * f5 * d5 // 128 * 2  # packed nibbles + f16 scales of the three weights
+        copies = [base.decode] + [tuple(t.clone() if hasattr(t, "clone") else t for t in base.decode)
+                                  for _ in range(rotation(wbytes) - 1)]
+        res = {}
+        for md in (1, 4):
+            x = bf16(normal_f32(4, (md, d5), 1.0, stream=3))
+            ws = torch.empty((base.workspace_bytes(md),), dtype=torch.uint8, device=dev)
+            y = torch.empty((md, d5), dtype=torch.float32, device=dev)
+
+            def launch_dec(i, md=md, x=x, ws=ws, y=y):
+                gu_t, gu_st, dn_t, dn_st, rows = copies[i % len(copies)]
+                _abi.call("tq_mlp_w4g128_decode", ptr(x), md, d5, f5, ptr(gu_t), ptr(gu_st), ptr(dn_t), ptr(dn_st),
+                          rows, ptr(ws), ws.numel(), ptr(y), stream())
+
+            ms, mode = timer.run(launch_dec, args.steps, args.warmup)
+            gbs = (wbytes + md * d5 * 2 + md * d5 * 4) / (ms * 1e-3) / 1e9
+            res[f"m{md}"] = {"us": round(ms * 1e3, 2), "timing": mode, "GB/s": round(gbs, 1),
+                             "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
+            log(f"mlp decode M={md}: {ms * 1e3:.1f} us  {gbs:.0f} GB/s ({mode})")
+        secondary["mlp_w4g128_decode"] = res
+        del base, copies
 
     # ------------------------------------------ copy (PMC calibration)
     if only == "copy":

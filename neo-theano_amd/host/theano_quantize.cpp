@@ -747,17 +747,51 @@ Result<QuantizedMLP> QuantizedMLP::from_tensors(const Tensor& gate, const Tensor
             if (r.is_err()) return r.unwrap_err();
             *dst = std::move(r).unwrap();
         }
+        mlp.make_decode_copies();
         return std::move(mlp);
     });
 }
 
+void QuantizedMLP::make_decode_copies() {
+    // down keeps the tiled copy every INT4 weight gets; gate and up run from one
+    // interleaved copy instead of their own
+    gate_.packed_tiled = DeviceBuffer<uint8_t>();
+    gate_.scales_tiled = DeviceBuffer<uint16_t>();
+    gate_.tile_rows = 0;
+    up_.packed_tiled = DeviceBuffer<uint8_t>();
+    up_.scales_tiled = DeviceBuffer<uint16_t>();
+    up_.tile_rows = 0;
+    if (d_ == 0 || f_ == 0 || d_ > 16384 || f_ > 16384 || down_.tile_rows == 0) return;
+    const size_t tiles = (f_ + 31) / 32;
+    gu_tiled_ = DeviceBuffer<uint8_t>(tiles * 64 * d_ / 2);
+    gu_scales_tiled_ = DeviceBuffer<uint16_t>(tiles * 64 * d_ / 128);
+    check(tq_repack_w4g128_gate_up_tiled(gate_.packed.data(), gate_.scales.data(), up_.packed.data(),
+                                         up_.scales.data(), static_cast<int64_t>(f_), static_cast<int64_t>(d_),
+                                         gu_tiled_.data(), gu_scales_tiled_.data(),
+                                         reinterpret_cast<tq_stream_t>(stream_)),
+          "QuantizedMLP: tiled gate/up copy");
+    check_hip(hipStreamSynchronize(stream_), "QuantizedMLP: tiled gate/up copy");
+}
+
 size_t QuantizedMLP::workspace_bytes(int64_t m) const {
+    if (decode_path(m))
+        return static_cast<size_t>(
+            tq_mlp_w4g128_decode_workspace_bytes(m, static_cast<int64_t>(d_), static_cast<int64_t>(f_)));
     return static_cast<size_t>(
         tq_mlp_w4g128_workspace_bytes(m, static_cast<int64_t>(d_), static_cast<int64_t>(f_)));
 }
 
 Result<void> QuantizedMLP::forward_device(const uint16_t* x, int64_t m, void* workspace, size_t workspace_bytes,
                                           float* y, hipStream_t stream) const {
+    if (decode_path(m)) {
+        const int st = tq_mlp_w4g128_decode(x, m, static_cast<int64_t>(d_), static_cast<int64_t>(f_), gu_tiled_.data(),
+                                            gu_scales_tiled_.data(), down_.packed_tiled.data(),
+                                            down_.scales_tiled.data(), down_.tile_rows, workspace,
+                                            static_cast<int64_t>(workspace_bytes), y,
+                                            reinterpret_cast<tq_stream_t>(stream));
+        if (st != TQ_OK) return TheanoError::from_status(st, "QuantizedMLP::forward");
+        return {};
+    }
     const int st = tq_mlp_w4g128(x, m, static_cast<int64_t>(d_), static_cast<int64_t>(f_), gate_.packed.data(),
                                  gate_.scales.data(), up_.packed.data(), up_.scales.data(), down_.packed.data(),
                                  down_.scales.data(), workspace, static_cast<int64_t>(workspace_bytes), y,
@@ -1102,6 +1136,7 @@ Result<QuantizedMLP> QuantizedMLP::load(const SafeTensorsFile& f, const std::str
         m.gate_ = get_int4(f, name + ".gate", m.f_, m.d_, stream);
         m.up_ = get_int4(f, name + ".up", m.f_, m.d_, stream);
         m.down_ = get_int4(f, name + ".down", m.d_, m.f_, stream);
+        m.make_decode_copies();
         return std::move(m);
     });
 }

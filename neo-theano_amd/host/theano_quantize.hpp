@@ -380,7 +380,8 @@ class QuantizedMLP : public Module {
                                              hipStream_t stream = nullptr);
     Tensor forward(const Tensor& input) const override;
     Result<Tensor> try_forward(const Tensor& input) const;
-    // device bytes of intermediates for m tokens (tq_mlp_w4g128_workspace_bytes)
+    // device bytes of intermediates for m tokens (tq_mlp_w4g128_decode_workspace_bytes
+    // on the decode path, tq_mlp_w4g128_workspace_bytes otherwise)
     size_t workspace_bytes(int64_t m) const;
     // x bf16 bits [m, d], workspace of workspace_bytes(m) bytes, y f32 [m, d]
     Result<void> forward_device(const uint16_t* x, int64_t m, void* workspace, size_t workspace_bytes, float* y,
@@ -393,11 +394,18 @@ class QuantizedMLP : public Module {
                                      hipStream_t stream = nullptr);
     size_t hidden() const { return d_; }
     size_t intermediate() const { return f_; }
+    // decode shapes (1 <= m <= kDecodeMaxM, D and F at most 16384) run
+    // tq_mlp_w4g128_decode on row-tiled copies of the weights, others tq_mlp_w4g128
+    static constexpr int64_t kDecodeMaxM = 8;
+    bool decode_path(int64_t m) const { return gu_tiled_.size() > 0 && m >= 1 && m <= kDecodeMaxM; }
 
    private:
+    void make_decode_copies();
     size_t d_ = 0, f_ = 0;
     hipStream_t stream_ = nullptr;
     quantize::Int4Weight gate_, up_, down_;
+    rocm::DeviceBuffer<uint8_t> gu_tiled_;  // gate and up interleaved in 64-row tiles
+    rocm::DeviceBuffer<uint16_t> gu_scales_tiled_;
 };
 
 // f32 -> bf16 bits, round to nearest even (NaN stays NaN)

@@ -527,24 +527,29 @@ TEST_GPU(test_parity_quantized_linear_fp8) {
 }
 
 TEST_GPU(test_parity_quantized_mlp) {
-    const size_t d = 256, f = 384, m = 5;
+    // M = 1, 2, 5 run the decode kernels, M = 9 the prefill FFN
+    const size_t d = 256, f = 384;
     const auto gv = randn(f * d, 0.02, 61), uv = randn(f * d, 0.02, 62), dv = randn(d * f, 0.02, 63);
-    const auto xv = randn(m * d, 1.0, 64);
     const QuantizedMLP mlp = QuantizedMLP::from_tensors(Tensor::from_slice(gv, {f, d}), Tensor::from_slice(uv, {f, d}),
                                                         Tensor::from_slice(dv, {d, f}))
                                  .unwrap();
-    const auto y = mlp.forward(Tensor::from_slice(xv, {m, d})).to_vec_f64().unwrap();
     std::vector<uint8_t> pg(f * d / 2), pu(f * d / 2), pd(d * f / 2);
     std::vector<uint16_t> sg(f * d / 128), su(f * d / 128), sd(d * f / 128);
     const auto g32 = f32(gv), u32 = f32(uv), d32 = f32(dv);
     tqo_quantize_i4_g128(g32.data(), f, d, pg.data(), sg.data());
     tqo_quantize_i4_g128(u32.data(), f, d, pu.data(), su.data());
     tqo_quantize_i4_g128(d32.data(), d, f, pd.data(), sd.data());
-    std::vector<uint16_t> xb(m * d);
-    for (size_t i = 0; i < xb.size(); ++i) xb[i] = tqo_f32_to_bf16_bits(static_cast<float>(xv[i]));
-    std::vector<double> ref(m * d);
-    tqo_mlp_w4g128(xb.data(), m, d, f, pg.data(), sg.data(), pu.data(), su.data(), pd.data(), sd.data(), ref.data());
-    assert_close(y, ref, "mlp");
+    for (size_t m : {1, 2, 5, 9}) {
+        ASSERT(mlp.decode_path(static_cast<int64_t>(m)) == (m <= 8));
+        const auto xv = randn(m * d, 1.0, 64 + m);
+        const auto y = mlp.forward(Tensor::from_slice(xv, {m, d})).to_vec_f64().unwrap();
+        std::vector<uint16_t> xb(m * d);
+        for (size_t i = 0; i < xb.size(); ++i) xb[i] = tqo_f32_to_bf16_bits(static_cast<float>(xv[i]));
+        std::vector<double> ref(m * d);
+        tqo_mlp_w4g128(xb.data(), m, d, f, pg.data(), sg.data(), pu.data(), su.data(), pd.data(), sd.data(),
+                       ref.data());
+        assert_close(y, ref, m <= 8 ? "mlp decode" : "mlp prefill");
+    }
 }
 
 TEST_GPU(test_parity_weight_formats) {

@@ -83,14 +83,26 @@ __global__ __launch_bounds__(kBlockW8) void k_gemv_w8(const float* __restrict__ 
                 wq[r][c] = __builtin_nontemporal_load(reinterpret_cast<const i32x4*>(q + row * k + kb));
             }
     };
+    // x first (vmcnt completes in order: staging x then waits for x alone, not for
+    // the weight rows issued after it), then the first rows, then x -> LDS (zero
+    // past K) and each lane's 16-value slices -> registers
+    const int k4 = static_cast<int>(k >> 2);
+    constexpr int kXItems = kM * kChunks * 256, kXPer = (kXItems + kBlockW8 - 1) / kBlockW8;
+    f32x4 xv[kXPer];
+#pragma unroll
+    for (int qi = 0; qi < kXPer; ++qi) {
+        const int i = threadIdx.x + qi * kBlockW8;
+        const int m = i / (kChunks * 256), j = i - m * (kChunks * 256);
+        xv[qi] = i < kXItems && j < k4 ? *reinterpret_cast<const f32x4*>(x + m * x_stride + 4 * j)
+                                       : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
     i32x4 wq[kRows][kChunks];
     load_rows(row_begin, wq);
-
-    // x -> LDS (zero past K), then each lane's 16-value slices -> registers
-    const int k4 = static_cast<int>(k >> 2);
-    for (int i = threadIdx.x; i < kM * kChunks * 256; i += kBlockW8) {
+#pragma unroll
+    for (int qi = 0; qi < kXPer; ++qi) {
+        const int i = threadIdx.x + qi * kBlockW8;
         const int m = i / (kChunks * 256), j = i - m * (kChunks * 256);
-        xs[m][j] = j < k4 ? *reinterpret_cast<const f32x4*>(x + m * x_stride + 4 * j) : f32x4{0.f, 0.f, 0.f, 0.f};
+        if (i < kXItems) xs[m][j] = xv[qi];
     }
     __syncthreads();
     float xr[kM][kChunks][16];
@@ -231,17 +243,31 @@ __global__ __launch_bounds__(kBlockW8) void k_gemv_a8(const float* __restrict__ 
                 wq[r][c] = __builtin_nontemporal_load(reinterpret_cast<const i32x4*>(q + row * k + kb));
             }
     };
+    // x first (vmcnt completes in order: the absmax and coding of x then wait for x
+    // alone, not for the weight rows issued after it), then the first rows
+    const int k4 = static_cast<int>(k >> 2);
+    constexpr int kXItems = kM * kChunks * 256, kXPer = (kXItems + kBlockW8 - 1) / kBlockW8;
+    f32x4 xv[kXPer];
+#pragma unroll
+    for (int qi = 0; qi < kXPer; ++qi) {
+        const int i = threadIdx.x + qi * kBlockW8;
+        const int m = i / (kChunks * 256), j = i - m * (kChunks * 256);
+        xv[qi] = i < kXItems && j < k4 ? *reinterpret_cast<const f32x4*>(x + m * x_stride + 4 * j)
+                                       : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
     i32x4 wq[kRows][kChunks];
     load_rows(row_begin, wq);
 
     // x -> LDS (zero past K) and the NaN-ignoring absmax of each row over its K values
-    const int k4 = static_cast<int>(k >> 2);
     float mx[kM];
 #pragma unroll
     for (int m = 0; m < kM; ++m) mx[m] = -INFINITY;
-    for (int i = threadIdx.x; i < kM * kChunks * 256; i += kBlockW8) {
+#pragma unroll
+    for (int qi = 0; qi < kXPer; ++qi) {
+        const int i = threadIdx.x + qi * kBlockW8;
+        if (i >= kXItems) continue;
         const int m = i / (kChunks * 256), j = i - m * (kChunks * 256);
-        const f32x4 v = j < k4 ? *reinterpret_cast<const f32x4*>(x + m * x_stride + 4 * j) : f32x4{0.f, 0.f, 0.f, 0.f};
+        const f32x4 v = xv[qi];
         xs[m][j] = v;
         if (j < k4) {
             const float a = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));

@@ -92,6 +92,32 @@ __global__ __launch_bounds__(kBlock) void k_decode_w4g128(const uint16_t* __rest
     const uint8_t* wrow = packed + rowc * (k >> 1) + 16 * q;
     const uint16_t* srow = s16 + rowc * G;
 
+    // This wave's x slice: 8-block b (of kGPW*16) of token t, 16 lanes per group.
+    // The first items are loaded before the weights (vmcnt completes in order:
+    // staging them then waits for x alone), any further ones (many tokens) after.
+    const int items = m * kGPW * 16;
+    auto x_at = [&](int idx) {
+        const int t = idx / (kGPW * 16), b = idx - t * (kGPW * 16);
+        const int64_t gk = min<int64_t>(g0 * 16 + b, G * 16 - 1);  // clamp for trailing waves
+        return *reinterpret_cast<const u32x4*>(x + t * k + gk * 8);
+    };
+    auto stage = [&](int idx, const u32x4& v) {
+        const int t = idx / (kGPW * 16), b = idx - t * (kGPW * 16);
+        *reinterpret_cast<u32x4*>(strip_x + t * kTStride + b * 16) = slot_order(v);
+        float sum = bf16_lo(v.x) + bf16_hi(v.x) + bf16_lo(v.y) + bf16_hi(v.y) + bf16_lo(v.z) + bf16_hi(v.z) +
+                    bf16_lo(v.w) + bf16_hi(v.w);
+#pragma unroll
+        for (int o = 8; o > 0; o >>= 1) sum += __shfl_xor(sum, o, kWave);  // a group's 16 lanes are all active
+        if ((b & 15) == 0) strip_sum[(b >> 4) * 16 + t] = 136.0f * sum;
+    };
+    constexpr int kPre = 4 * kGPW < 8 ? 4 * kGPW : 8;  // items per lane loaded up front
+    u32x4 xp[kPre];
+#pragma unroll
+    for (int i = 0; i < kPre; ++i) {
+        const int idx = lane + i * kWave;
+        xp[i] = idx < items ? x_at(idx) : u32x4{0u, 0u, 0u, 0u};
+    }
+
     // first window of weight and scale loads
     u32x4 wq[kWin];
     uint16_t sq[kWin];
@@ -102,18 +128,12 @@ __global__ __launch_bounds__(kBlock) void k_decode_w4g128(const uint16_t* __rest
         sq[i] = srow[g];
     }
 
-    // stage this wave's x slice: 8-block b (of kGPW*16) of token t; 16 lanes per group
-    for (int idx = lane; idx < m * kGPW * 16; idx += kWave) {
-        const int t = idx / (kGPW * 16), b = idx - t * (kGPW * 16);
-        const int64_t gk = min<int64_t>(g0 * 16 + b, G * 16 - 1);  // clamp for trailing waves
-        const u32x4 v = *reinterpret_cast<const u32x4*>(x + t * k + gk * 8);
-        *reinterpret_cast<u32x4*>(strip_x + t * kTStride + b * 16) = slot_order(v);
-        float sum = bf16_lo(v.x) + bf16_hi(v.x) + bf16_lo(v.y) + bf16_hi(v.y) + bf16_lo(v.z) + bf16_hi(v.z) +
-                    bf16_lo(v.w) + bf16_hi(v.w);
 #pragma unroll
-        for (int o = 8; o > 0; o >>= 1) sum += __shfl_xor(sum, o, kWave);
-        if ((b & 15) == 0) strip_sum[(b >> 4) * 16 + t] = 136.0f * sum;
+    for (int i = 0; i < kPre; ++i) {
+        const int idx = lane + i * kWave;
+        if (idx < items) stage(idx, xp[i]);
     }
+    for (int idx = lane + kPre * kWave; idx < items; idx += kWave) stage(idx, x_at(idx));
     // the strip is private to this wave: LDS accesses of one wave complete in order
 
     // dummy token rows (>= m) read token m-1; their results are never stored

@@ -539,7 +539,7 @@ __global__ __launch_bounds__(kBlock) void k_decode_diag(const uint16_t* __restri
 }
 
 // kR in {1, 2, 4}; kM in {1, 2, 4} (3 tokens run as 4 with a zero token); groups per
-// wave in {1, 2, 4, 8} (K <= 16384)
+// wave 1..8 (K <= 16384)
 struct DiagArgs {
     const uint16_t* x;
     int m;
@@ -559,14 +559,18 @@ int launch_diag(int64_t gpw, int64_t tiles, hipStream_t s, const DiagArgs& a) {
 #define TQ_DIAG(G)                                                                                      \
     k_decode_diag<kR, kM, G, kWinD, kEpi><<<grid, kBlock, 0, s>>>(a.x, a.m, a.pt, a.st, a.b, a.n, a.k, a.y, \
                                                                   a.hout, a.tok0, a.mtot)
-    if (gpw <= 1)
-        TQ_DIAG(1);
-    else if (gpw <= 2)
-        TQ_DIAG(2);
-    else if (gpw <= 4)
-        TQ_DIAG(4);
-    else
-        TQ_DIAG(8);
+    // the exact groups per wave, so that no wave of the block runs dead groups (K =
+    // 14336, the Llama FFN's intermediate size, is 7 per wave)
+    switch (gpw) {
+        case 1: TQ_DIAG(1); break;
+        case 2: TQ_DIAG(2); break;
+        case 3: TQ_DIAG(3); break;
+        case 4: TQ_DIAG(4); break;
+        case 5: TQ_DIAG(5); break;
+        case 6: TQ_DIAG(6); break;
+        case 7: TQ_DIAG(7); break;
+        default: TQ_DIAG(8); break;
+    }
 #undef TQ_DIAG
     return check_launch("tq_gemv_w4g128_tiled");
 }

@@ -6,21 +6,27 @@
 //   P      = softmax(scores, -1)                       (tensor_ops.rs:574-620)
 //   O_h    = P V_h,   heads concatenated along the embedding
 //
-// f32 throughout.  Q, K and V are row-major [B*S, ld] matrices whose head h
+// f32 inputs, outputs, softmax and accumulators.  Q, K and V are row-major [B*S, ld] matrices whose head h
 // occupies columns [h*D, (h+1)*D) (the fused QKV projection's output is read in
 // place with ld = 3E); O is [B*S, ldo].
 //
 // One block per (128 queries, head, batch): 4 waves of 32 query rows on the
-// f32 matrix cores (v_mfma_f32_32x32x2_f32).  Keys run in tiles of 32, staged
-// in LDS for the 4 waves (K row-major, V transposed; both padded against bank
-// conflicts), the next tile's loads in flight during the current tile's work.
-// Per tile a wave computes S^T = K Q^T (lane = query, registers = keys, so the
-// softmax of a query row is in-lane plus one partner lane), updates its
-// running max / sum, and accumulates O^T += V^T P^T with the probabilities as
-// they came out of the first product.  The head dimension is padded with zeros
-// to 32, 64 or 128.  A running max of -inf (every key so far masked) leaves the
-// row untouched; a row masked everywhere ends as 0/0 = NaN, as the
-// reference's softmax gives.
+// bf16 matrix cores (v_mfma_f32_32x32x16_bf16).  Every f32 operand is split
+// exactly into bf16 hi = bf16(v) and lo = bf16(v - hi) (|v - hi - lo| <=
+// 2^-18 |v|), and each product runs as hi*hi + hi*lo + lo*hi, all bf16 products
+// exact in the f32 accumulators; the dropped lo*lo term is below 2^-16 of the
+// product.  Keys run in tiles of 32, staged in LDS for the 4 waves as hi and lo
+// planes (K row-major, V transposed, both padded against bank conflicts), the
+// next tile's loads in flight during the current tile's work.  Per tile a wave
+// computes S^T = K Q^T (lane = query, registers = keys, so the softmax of a
+// query row is in-lane plus one partner lane), updates its running max / sum,
+// and accumulates O^T += V^T P^T with the probabilities as they came out of the
+// first product: lane half g holds keys 8a + 4g + b (a, b < 4), and the
+// transposed V tile stores key k at column k with bits 2 and 3 swapped, so the
+// 8 keys of a 16-key MFMA step are one contiguous 16-byte read.  The head
+// dimension is padded with zeros to 32, 64 or 128.  A running max of -inf
+// (every key so far masked) leaves the row untouched; a row masked everywhere
+// ends as 0/0 = NaN, as the reference's softmax gives.
 #include <cmath>
 
 #include "tq_internal.h"
@@ -28,15 +34,44 @@
 namespace tq {
 namespace {
 
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
 constexpr int kWaves = 4;
 constexpr int kQW = 32;              // query rows per wave
 constexpr int kQB = kWaves * kQW;    // per block
 constexpr int kKT = 32;              // keys per tile
 constexpr int kMaxD = 128;
 
-__device__ __forceinline__ f32x16 mfma_f32(float a, float b, f32x16 c) {
-    return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+__device__ __forceinline__ f32x16 mfma_bf16(u32x4 a, u32x4 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
+                                                   0, 0, 0);
 }
+
+__device__ __forceinline__ uint16_t bf16_bits(float v) { return __builtin_bit_cast(uint16_t, static_cast<__bf16>(v)); }
+__device__ __forceinline__ float bf16_value(uint16_t b) { return __uint_as_float(static_cast<uint32_t>(b) << 16); }
+
+// v = hi + lo (+ < 2^-18 |v|): hi = bf16(v), lo = bf16(v - hi)
+__device__ __forceinline__ void split(float v, uint16_t& hi, uint16_t& lo) {
+    hi = bf16_bits(v);
+    lo = bf16_bits(v - bf16_value(hi));
+}
+
+// 8 f32 -> packed bf16 hi and lo
+__device__ __forceinline__ void split8(const float* v, u32x4& hi, u32x4& lo) {
+    uint32_t h[4], l[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        uint16_t h0, l0, h1, l1;
+        split(v[2 * i], h0, l0);
+        split(v[2 * i + 1], h1, l1);
+        h[i] = h0 | static_cast<uint32_t>(h1) << 16;
+        l[i] = l0 | static_cast<uint32_t>(l1) << 16;
+    }
+    hi = u32x4{h[0], h[1], h[2], h[3]};
+    lo = u32x4{l[0], l[1], l[2], l[3]};
+}
+
+__device__ __forceinline__ int vcol(int key) { return (key & ~12) | ((key & 4) << 1) | ((key & 8) >> 1); }
 
 template <int kDP>
 __global__ __launch_bounds__(kWaves * kWave) void k_attention(const float* __restrict__ q, int64_t ldq,
@@ -45,27 +80,32 @@ __global__ __launch_bounds__(kWaves * kWave) void k_attention(const float* __res
                                                               const float* __restrict__ mask, int64_t mask_batch,
                                                               int S, int D, float scale, float* __restrict__ o,
                                                               int64_t ldo) {
-    constexpr int kHalf = kDP / 2;     // d positions per lane group in S^T = K Q^T
-    constexpr int kKRow = kDP + 4;     // K tile row (floats), padded
-    constexpr int kVRow = kKT + 4;     // transposed V tile row, padded
+    constexpr int kSteps = kDP / 16;   // 16-wide d steps of S^T = K Q^T
+    constexpr int kKRow = kDP + 8;     // K plane row (bf16), padded
+    constexpr int kVRow = kKT + 8;     // transposed V plane row (bf16), padded
     constexpr int kBlocks = kDP / 32;  // 32-wide d blocks of O^T
     constexpr int kElems = kKT * kDP / (kWaves * kWave);  // tile elements per thread (K and V each)
-    __shared__ __attribute__((aligned(16))) float ks[2][kKT * kKRow];
-    __shared__ __attribute__((aligned(16))) float vs[2][kDP * kVRow];
+    __shared__ __attribute__((aligned(16))) uint16_t ksh[2][kKT * kKRow], ksl[2][kKT * kKRow];
+    __shared__ __attribute__((aligned(16))) uint16_t vsh[2][kDP * kVRow], vsl[2][kDP * kVRow];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 5, lr = lane & 31;
     const int h = blockIdx.y, b = blockIdx.z;
     const int qrow = blockIdx.x * kQB + wave * kQW + lr;  // this lane's query row
     const int64_t base = static_cast<int64_t>(b) * S;
     const int col = h * D;
 
-    // Q fragment: d = g * kHalf + t (rows past S read row S-1; never stored)
-    float qf[kHalf];
+    // Q operand: step s covers d = 16 s + 8 g + j (rows past S read row S-1; never stored)
+    u32x4 qh[kSteps], ql[kSteps];
     {
         const float* qr = q + (base + min(qrow, S - 1)) * ldq + col;
 #pragma unroll
-        for (int t = 0; t < kHalf; ++t) {
-            const int d = g * kHalf + t;
-            qf[t] = d < D ? qr[d] : 0.f;
+        for (int st = 0; st < kSteps; ++st) {
+            float qv[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int d = 16 * st + 8 * g + j;
+                qv[j] = d < D ? qr[d] : 0.f;
+            }
+            split8(qv, qh[st], ql[st]);
         }
     }
     const float* mrow =
@@ -88,8 +128,13 @@ __global__ __launch_bounds__(kWaves * kWave) void k_attention(const float* __res
 #pragma unroll
         for (int i = 0; i < kElems; ++i) {
             const int e = tid + i * kWaves * kWave, key = e / kDP, d = e % kDP;
-            ks[buf][key * kKRow + d] = kreg[i];
-            vs[buf][d * kVRow + key] = vreg[i];
+            uint16_t hi, lo;
+            split(kreg[i], hi, lo);
+            ksh[buf][key * kKRow + d] = hi;
+            ksl[buf][key * kKRow + d] = lo;
+            split(vreg[i], hi, lo);
+            vsh[buf][d * kVRow + vcol(key)] = hi;
+            vsl[buf][d * kVRow + vcol(key)] = lo;
         }
     };
 
@@ -108,14 +153,17 @@ __global__ __launch_bounds__(kWaves * kWave) void k_attention(const float* __res
 
         // S^T[key][q] = sum_d K[key][d] Q[q][d]: lane holds keys 8(r/4) + 4g + r%4 of query lr
         f32x16 st = f32x16{};
-        const float* kr = &ks[buf][lr * kKRow + g * kHalf];
+        {
+            const uint16_t* kh = &ksh[buf][lr * kKRow + 8 * g];
+            const uint16_t* kl = &ksl[buf][lr * kKRow + 8 * g];
 #pragma unroll
-        for (int t = 0; t < kHalf; t += 4) {
-            const f32x4 kv = *reinterpret_cast<const f32x4*>(kr + t);
-            st = mfma_f32(kv.x, qf[t], st);
-            st = mfma_f32(kv.y, qf[t + 1], st);
-            st = mfma_f32(kv.z, qf[t + 2], st);
-            st = mfma_f32(kv.w, qf[t + 3], st);
+            for (int s2 = 0; s2 < kSteps; ++s2) {
+                const u32x4 a_h = *reinterpret_cast<const u32x4*>(kh + 16 * s2);
+                const u32x4 a_l = *reinterpret_cast<const u32x4*>(kl + 16 * s2);
+                st = mfma_bf16(a_h, qh[s2], st);
+                st = mfma_bf16(a_h, ql[s2], st);
+                st = mfma_bf16(a_l, qh[s2], st);
+            }
         }
         float p[16];
         float mt = -INFINITY;
@@ -144,18 +192,24 @@ __global__ __launch_bounds__(kWaves * kWave) void k_attention(const float* __res
         const float alpha = expf(m - base_m);
         l = l * alpha + ls;
         m = mn;
-        // O^T[d][q] += sum_key V[key][d] P[q][key]; step t of a 4-key run uses key 8a + 4g + b
+        // P^T operand: step t of 16 keys takes registers 8t .. 8t+7 (keys 16t + 8h + 4g + b,
+        // slot 4h + b), the order of the transposed V tile's columns
+        u32x4 ph[2], pl[2];
+        split8(p, ph[0], pl[0]);
+        split8(p + 8, ph[1], pl[1]);
+        // O^T[d][q] += sum_key V[key][d] P[q][key]
 #pragma unroll
         for (int c = 0; c < kBlocks; ++c) {
             ot[c] *= alpha;
-            const float* vr = &vs[buf][(32 * c + lr) * kVRow + 4 * g];
+            const uint16_t* vh = &vsh[buf][(32 * c + lr) * kVRow + 8 * g];
+            const uint16_t* vl = &vsl[buf][(32 * c + lr) * kVRow + 8 * g];
 #pragma unroll
-            for (int a = 0; a < 4; ++a) {
-                const f32x4 vv = *reinterpret_cast<const f32x4*>(vr + 8 * a);
-                ot[c] = mfma_f32(vv.x, p[4 * a + 0], ot[c]);
-                ot[c] = mfma_f32(vv.y, p[4 * a + 1], ot[c]);
-                ot[c] = mfma_f32(vv.z, p[4 * a + 2], ot[c]);
-                ot[c] = mfma_f32(vv.w, p[4 * a + 3], ot[c]);
+            for (int t = 0; t < 2; ++t) {
+                const u32x4 a_h = *reinterpret_cast<const u32x4*>(vh + 16 * t);
+                const u32x4 a_l = *reinterpret_cast<const u32x4*>(vl + 16 * t);
+                ot[c] = mfma_bf16(a_h, ph[t], ot[c]);
+                ot[c] = mfma_bf16(a_h, pl[t], ot[c]);
+                ot[c] = mfma_bf16(a_l, ph[t], ot[c]);
             }
         }
         if (more) {

@@ -17,8 +17,9 @@
 // exact in the f32 accumulators; the dropped lo*lo term is below 2^-16 of the
 // product.  Keys run in tiles of 32, staged in LDS for the 4 waves as hi and lo
 // planes (K row-major, V transposed, both padded against bank conflicts), the
-// next tile's loads in flight during the current tile's work.  Per tile a wave
-// computes S^T = K Q^T (lane = query, registers = keys, so the softmax of a
+// next tile's loads in flight during the current tile's work.  Scores are kept
+// in log2 units (scale * log2(e), the mask likewise), so each probability is
+// one v_exp_f32 (2^x).  Per tile a wave computes S^T = K Q^T (lane = query, registers = keys, so the softmax of a
 // query row is in-lane plus one partner lane), updates its running max / sum,
 // and accumulates O^T += V^T P^T with the probabilities as they came out of the
 // first product: lane half g holds keys 8a + 4g + b (a, b < 4), and the
@@ -92,6 +93,8 @@ __global__ __launch_bounds__(kWaves * kWave) void k_attention(const float* __res
     const int qrow = blockIdx.x * kQB + wave * kQW + lr;  // this lane's query row
     const int64_t base = static_cast<int64_t>(b) * S;
     const int col = h * D;
+    constexpr float kLog2e = 1.4426950408889634f;
+    const float scale2 = scale * kLog2e;
 
     // Q operand: step s covers d = 16 s + 8 g + j (rows past S read row S-1; never stored)
     u32x4 qh[kSteps], ql[kSteps];
@@ -165,17 +168,16 @@ __global__ __launch_bounds__(kWaves * kWave) void k_attention(const float* __res
                 st = mfma_bf16(a_l, qh[s2], st);
             }
         }
+        // scores in log2 units: s * scale * log2(e) (+ mask * log2(e)), so that the
+        // probabilities are one v_exp_f32 (2^x) each
         float p[16];
         float mt = -INFINITY;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
             const int key = j0 + 8 * (r >> 2) + 4 * g + (r & 3);
-            float sc = st[r] * scale;
-            if (key < S) {
-                if (mrow) sc += mrow[key];
-            } else {
-                sc = -INFINITY;
-            }
+            float sc = st[r] * scale2;
+            if (mrow) sc = fmaf(mrow[min(key, S - 1)], kLog2e, sc);  // clamped: no divergent branch
+            sc = key < S ? sc : -INFINITY;
             p[r] = sc;
             mt = fmaxf(mt, sc);
         }
@@ -185,11 +187,11 @@ __global__ __launch_bounds__(kWaves * kWave) void k_attention(const float* __res
         float ls = 0.f;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-            p[r] = expf(p[r] - base_m);
+            p[r] = __builtin_amdgcn_exp2f(p[r] - base_m);
             ls += p[r];
         }
         ls += __shfl_xor(ls, 32, kWave);
-        const float alpha = expf(m - base_m);
+        const float alpha = __builtin_amdgcn_exp2f(m - base_m);
         l = l * alpha + ls;
         m = mn;
         // P^T operand: step t of 16 keys takes registers 8t .. 8t+7 (keys 16t + 8h + 4g + b,

@@ -602,52 +602,57 @@ int launch_mfma(int64_t gpw, int64_t tiles, hipStream_t s, const uint16_t* x, in
     return check_launch("tq_gemv_w4g128_tiled");
 }
 
-__global__ __launch_bounds__(256) void k_repack_tiled(const uint8_t* __restrict__ packed,
-                                                      const uint16_t* __restrict__ s16, int64_t n,
-                                                      int64_t k, int tile_rows, int64_t tiles,
-                                                      uint8_t* __restrict__ pt, uint16_t* __restrict__ st) {
-    const int64_t C = k >> 5, G = k >> 7, T = tile_rows;
-    const int64_t total = tiles * C * T;
-    const int64_t stride = static_cast<int64_t>(gridDim.x) * 256;
-    for (int64_t o = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; o < total; o += stride) {
-        const int64_t r = o % T, tc = o / T, c = tc % C, t = tc / C;
-        const int64_t row = t * T + r;
-        u32x4 v = u32x4{0u, 0u, 0u, 0u};
-        if (row < n) v = *reinterpret_cast<const u32x4*>(packed + row * (k >> 1) + c * 16);
-        reinterpret_cast<u32x4*>(pt)[o] = v;
+// Repack into the tiled layout through LDS: a block takes 2048 / T chunks (rounded
+// down to whole groups of 4; about 32 KB in all) of each of one tile's T rows, reading the rows contiguously (consecutive
+// threads, consecutive chunks of a row), and writes them back in tile order
+// (consecutive threads, consecutive rows of a chunk).  The source of tile row r
+// of tile t is row t*half + r % half of `pa` (r < half) or `pb`: half = T for a
+// single weight, 32 for the FFN's gate (pa) / up (pb) interleave in 64-row tiles.
+// The block also copies the f16 scales of its chunks' groups.  Rows at or past
+// `nrows` are zero.
+constexpr int kRepackItems = 2048;  // 16-byte chunks per block
+
+__global__ __launch_bounds__(256) void k_repack_lds(const uint8_t* __restrict__ pa, const uint16_t* __restrict__ sa,
+                                                    const uint8_t* __restrict__ pb, const uint16_t* __restrict__ sb,
+                                                    int64_t nrows, int64_t k, int tile_rows, int half,
+                                                    int64_t cblocks, uint8_t* __restrict__ pt,
+                                                    uint16_t* __restrict__ st) {
+    __shared__ __attribute__((aligned(16))) uint8_t buf[kRepackItems * 16 + 64 * 16];
+    const int T = tile_rows, cpb = (kRepackItems / T) & ~3;  // whole groups of 4 chunks
+    const int row_b = cpb * 16 + 16;  // padded LDS row: consecutive rows 4 banks apart
+    const int64_t C = k >> 5, G = k >> 7;
+    const int64_t t = blockIdx.x / cblocks, c0 = (blockIdx.x % cblocks) * cpb;
+    const int nc = static_cast<int>(min<int64_t>(cpb, C - c0));
+    // the f16 scales of the block's groups (4 chunks each): s_t[(t*G + g)*T + r]
+    for (int it = threadIdx.x; it < (nc >> 2) * T; it += 256) {
+        const int gg = it / T, r = it - gg * T;
+        const int64_t g = (c0 >> 2) + gg, row = t * half + r % half;
+        st[(t * G + g) * T + r] = row < nrows ? (r < half ? sa : sb)[row * G + g] : uint16_t(0);
     }
-    const int64_t stotal = tiles * G * T;
-    for (int64_t o = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; o < stotal; o += stride) {
-        const int64_t r = o % T, tg = o / T, g = tg % G, t = tg / G;
-        const int64_t row = t * T + r;
-        st[o] = row < n ? s16[row * G + g] : uint16_t(0);
+    for (int it = threadIdx.x; it < T * cpb; it += 256) {
+        const int r = it / cpb, cc = it - r * cpb;
+        const int64_t row = t * half + r % half;
+        const uint8_t* src = r < half ? pa : pb;
+        u32x4 v = u32x4{0u, 0u, 0u, 0u};
+        if (cc < nc && row < nrows) v = *reinterpret_cast<const u32x4*>(src + row * (k >> 1) + (c0 + cc) * 16);
+        *reinterpret_cast<u32x4*>(buf + r * row_b + cc * 16) = v;
+    }
+    __syncthreads();
+    for (int it = threadIdx.x; it < nc * T; it += 256) {
+        const int cc = it / T, r = it - cc * T;
+        reinterpret_cast<u32x4*>(pt)[(t * C + c0 + cc) * T + r] =
+            *reinterpret_cast<const u32x4*>(buf + r * row_b + cc * 16);
     }
 }
 
-// Gate and up projections of an FFN as one tiled weight of 64-row tiles: tile t
-// holds gate rows 32t .. 32t + 31 (tile rows 0-31) and up rows 32t .. 32t + 31
-// (tile rows 32-63), in the layout above with T = 64; rows past f are zero.
-__global__ __launch_bounds__(256) void k_repack_gate_up(const uint8_t* __restrict__ gp, const uint16_t* __restrict__ gs,
-                                                        const uint8_t* __restrict__ up, const uint16_t* __restrict__ us,
-                                                        int64_t f, int64_t d, int64_t tiles, uint8_t* __restrict__ pt,
-                                                        uint16_t* __restrict__ st) {
-    const int64_t C = d >> 5, G = d >> 7;
-    const int64_t stride = static_cast<int64_t>(gridDim.x) * 256;
-    const int64_t total = tiles * C * 64;
-    for (int64_t o = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; o < total; o += stride) {
-        const int64_t r = o % 64, tc = o / 64, c = tc % C, t = tc / C;
-        const int64_t row = 32 * t + (r & 31);
-        const uint8_t* src = r < 32 ? gp : up;
-        u32x4 v = u32x4{0u, 0u, 0u, 0u};
-        if (row < f) v = *reinterpret_cast<const u32x4*>(src + row * (d >> 1) + c * 16);
-        reinterpret_cast<u32x4*>(pt)[o] = v;
-    }
-    const int64_t stotal = tiles * G * 64;
-    for (int64_t o = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; o < stotal; o += stride) {
-        const int64_t r = o % 64, tg = o / 64, g = tg % G, t = tg / G;
-        const int64_t row = 32 * t + (r & 31);
-        st[o] = row < f ? (r < 32 ? gs : us)[row * G + g] : uint16_t(0);
-    }
+int launch_repack(const uint8_t* pa, const uint16_t* sa, const uint8_t* pb, const uint16_t* sb, int64_t nrows,
+                  int64_t k, int tile_rows, int half, int64_t tiles, uint8_t* pt, uint16_t* st, hipStream_t s,
+                  const char* what) {
+    const int64_t C = k >> 5, cpb = (kRepackItems / tile_rows) & ~3, cblocks = (C + cpb - 1) / cpb;
+    if (tiles * cblocks >= (int64_t(1) << 31)) return fail(TQ_EINVAL, "%s: problem too large", what);
+    k_repack_lds<<<static_cast<unsigned>(tiles * cblocks), 256, 0, s>>>(pa, sa, pb, sb, nrows, k, tile_rows, half,
+                                                                        cblocks, pt, st);
+    return check_launch(what);
 }
 
 template <int kM, int kCPW>
@@ -695,13 +700,8 @@ int tq_repack_w4g128_tiled(const uint8_t* packed, const uint16_t* s_f16, int64_t
     TQ_REQUIRE(aligned(packed, 16) && aligned(packed_t, 16) && aligned(s_f16, 2) && aligned(s_t, 2),
                "tq_repack_w4g128_tiled: misaligned pointer (packed buffers need 16 B)");
     const int64_t tiles = (n + tile_rows - 1) / tile_rows;
-    const int64_t total = tiles * (k >> 5) * tile_rows;
-    int64_t blocks = (total + 255) / 256;
-    if (blocks > 65536) blocks = 65536;
-    k_repack_tiled<<<static_cast<unsigned>(blocks), 256, 0, as_hip(stream)>>>(packed, s_f16, n, k,
-                                                                             static_cast<int>(tile_rows), tiles,
-                                                                             packed_t, s_t);
-    return check_launch("tq_repack_w4g128_tiled");
+    return launch_repack(packed, s_f16, packed, s_f16, n, k, static_cast<int>(tile_rows), static_cast<int>(tile_rows),
+                         tiles, packed_t, s_t, as_hip(stream), "tq_repack_w4g128_tiled");
 }
 
 int tq_gemv_w4g128_tiled(const uint16_t* x_bf16, int64_t m, const uint8_t* packed_t, const uint16_t* s_t,
@@ -769,11 +769,8 @@ int tq_repack_w4g128_gate_up_tiled(const uint8_t* gate_packed, const uint16_t* g
                    aligned(up_s, 2) && aligned(s_t, 2),
                "tq_repack_w4g128_gate_up_tiled: misaligned pointer (packed buffers need 16 B)");
     const int64_t tiles = (f + 31) / 32;
-    int64_t blocks = (tiles * (d >> 5) * 64 + 255) / 256;
-    if (blocks > 65536) blocks = 65536;
-    k_repack_gate_up<<<static_cast<unsigned>(blocks), 256, 0, as_hip(stream)>>>(gate_packed, gate_s, up_packed, up_s,
-                                                                                f, d, tiles, packed_t, s_t);
-    return check_launch("tq_repack_w4g128_gate_up_tiled");
+    return launch_repack(gate_packed, gate_s, up_packed, up_s, f, d, 64, 32, tiles, packed_t, s_t, as_hip(stream),
+                         "tq_repack_w4g128_gate_up_tiled");
 }
 
 int tq_mlp_w4g128_decode(const uint16_t* x_bf16, int64_t m, int64_t d, int64_t f, const uint8_t* gate_up_t,

@@ -366,9 +366,14 @@ enum DiagEpi { kEpiPlain = 0, kEpiFold = 1, kEpiGateUp = 2 };
 // go in pairs, pair c = J / 2 with t = min(2, m - 2c) tokens occupies rows
 // 4c .. 4c + 2t - 1 as (hi of its tokens, lo of its tokens), so each pair is one
 // kEpiFold launch of 2t contiguous rows.
+// With `block` set (one down launch for all m tokens) the rows are instead the m
+// hi rows, then the m lo rows.
 struct MlpRows {
-    __host__ __device__ static int64_t hi(int64_t j, int64_t m) { return 4 * (j / 2) + (j % 2); }
-    __host__ __device__ static int64_t lo(int64_t j, int64_t m) {
+    __host__ __device__ static int64_t hi(int64_t j, int64_t m, bool block) {
+        return block ? j : 4 * (j / 2) + (j % 2);
+    }
+    __host__ __device__ static int64_t lo(int64_t j, int64_t m, bool block) {
+        if (block) return m + j;
         const int64_t c = j / 2, t = m - 2 * c < 2 ? m - 2 * c : 2;
         return 4 * c + t + (j % 2);
     }
@@ -380,7 +385,8 @@ __global__ __launch_bounds__(kBlock) void k_decode_diag(const uint16_t* __restri
                                                         const uint16_t* __restrict__ st,
                                                         const float* __restrict__ bias, int64_t n, int64_t k,
                                                         float* __restrict__ y, uint16_t* __restrict__ hout,
-                                                        int tok0, int mtot) {
+                                                        int tok0, int mtot, int rows_block,
+                                                        float* __restrict__ yz, int64_t yz_n) {
     static_assert(kM * kR <= 16, "columns are (token, row group) pairs");
     static_assert(kEpi != kEpiGateUp || kR == 4, "gate/up tiles are 64 rows");
     constexpr int T = 16 * kR;
@@ -398,7 +404,9 @@ __global__ __launch_bounds__(kBlock) void k_decode_diag(const uint16_t* __restri
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int64_t tile = blockIdx.x;
     const int64_t C = k >> 5, G = k >> 7;
-    const int64_t g0 = static_cast<int64_t>(wave) * kGPW, c0 = 4 * g0;
+    // K split over gridDim.y blocks per tile: this block takes groups [gb, ge)
+    const int64_t gh = (G + gridDim.y - 1) / gridDim.y, gb = blockIdx.y * gh, ge = min(G, gb + gh);
+    const int64_t g0 = gb + static_cast<int64_t>(wave) * kGPW, c0 = 4 * g0;
     const int col = lane & 15, kg = lane >> 4;
     const int rg = kg % kR, cs = kg / kR;  // this lane's row group and chunk slot (loads)
     const int tok = col / kR;              // token of this lane's output column
@@ -411,19 +419,19 @@ __global__ __launch_bounds__(kBlock) void k_decode_diag(const uint16_t* __restri
     for (int q = 0; q < kIPL; ++q) {
         const int it = min(lane + kWave * q, kItems - 1);
         const int j = it / (kCPW * 8), r = it - j * (kCPW * 8);
-        const int64_t kx = min<int64_t>(c0 * 32 + 4 * r, k - 4);
+        const int64_t kx = min<int64_t>(c0 * 32 + 4 * r, ge * 128 - 4);
         xv[q] = j < m ? *reinterpret_cast<const uint2*>(x + j * k + kx) : make_uint2(0u, 0u);
     }
     uint2 sc[kGPW];
 #pragma unroll
     for (int g = 0; g < kGPW; ++g)
-        sc[g] = *reinterpret_cast<const uint2*>(st + (tile * G + min<int64_t>(g0 + g, G - 1)) * T + row0);
+        sc[g] = *reinterpret_cast<const uint2*>(st + (tile * G + min<int64_t>(g0 + g, ge - 1)) * T + row0);
     const uint8_t* wb = pt + (tile * C * T + 16 * rg + (lane & 15)) * 16;
     u32x4 w[kW];
 #pragma unroll
     for (int i = 0; i < kW; ++i)
         w[i] = __builtin_nontemporal_load(
-            reinterpret_cast<const u32x4*>(wb + min<int64_t>(c0 + i * kS + cs, C - 1) * T * 16));
+            reinterpret_cast<const u32x4*>(wb + min<int64_t>(c0 + i * kS + cs, 4 * ge - 1) * T * 16));
 
     // every wave zeroes the shared zero strip (the same value from every writer, so
     // no barrier is needed before a wave reads what it wrote itself)
@@ -471,7 +479,7 @@ __global__ __launch_bounds__(kBlock) void k_decode_diag(const uint16_t* __restri
     f32x4 tot = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int g = 0; g < kGPW; ++g) {
-        const bool live = g0 + g < G;
+        const bool live = g0 + g < ge;
         f32x4 a0 = f32x4{0.f, 0.f, 0.f, 0.f}, a1 = a0;
 #pragma unroll
         for (int ss = 0; ss < kR; ++ss) {
@@ -488,7 +496,7 @@ __global__ __launch_bounds__(kBlock) void k_decode_diag(const uint16_t* __restri
             }
             if (i + kW < kSteps) {
                 w[slot] = __builtin_nontemporal_load(
-                    reinterpret_cast<const u32x4*>(wb + min<int64_t>(c0 + (i + kW) * kS + cs, C - 1) * T * 16));
+                    reinterpret_cast<const u32x4*>(wb + min<int64_t>(c0 + (i + kW) * kS + cs, 4 * ge - 1) * T * 16));
                 __builtin_amdgcn_sched_barrier(0);  // the refill is issued here, not after the group
             }
         }
@@ -519,7 +527,11 @@ __global__ __launch_bounds__(kBlock) void k_decode_diag(const uint16_t* __restri
             const int j = i / T, r = i - j * T;
             const int64_t row = tile * T + r;
             if (row >= n) continue;
-            y[j * n + row] = (wsum(j, r) + wsum(t + j, r)) + (bias ? bias[row] : 0.0f);
+            const float v = (wsum(j, r) + wsum(t + j, r)) + (bias && blockIdx.y == 0 ? bias[row] : 0.0f);
+            if (gridDim.y == 1)
+                y[j * n + row] = v;
+            else  // K halves onto a zeroed y: two addends onto zero, the same sum in either order
+                atomicAdd(&y[j * n + row], v);
         }
     } else {
         const int64_t f = n >> 1;  // h columns: the stacked weight has 2f rows
@@ -532,9 +544,13 @@ __global__ __launch_bounds__(kBlock) void k_decode_diag(const uint16_t* __restri
             const __bf16 hi = static_cast<__bf16>(h);
             const __bf16 lo = static_cast<__bf16>(h - static_cast<float>(hi));
             const int64_t J = tok0 + j;
-            hout[MlpRows::hi(J, mtot) * f + hc] = __builtin_bit_cast(uint16_t, hi);
-            hout[MlpRows::lo(J, mtot) * f + hc] = __builtin_bit_cast(uint16_t, lo);
+            hout[MlpRows::hi(J, mtot, rows_block) * f + hc] = __builtin_bit_cast(uint16_t, hi);
+            hout[MlpRows::lo(J, mtot, rows_block) * f + hc] = __builtin_bit_cast(uint16_t, lo);
         }
+        // the output a K-split down projection accumulates into
+        for (int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; i < yz_n;
+             i += static_cast<int64_t>(gridDim.x) * kBlock)
+            yz[i] = 0.0f;
     }
 }
 
@@ -550,15 +566,20 @@ struct DiagArgs {
     float* y;
     uint16_t* hout;  // kEpiGateUp
     int tok0, mtot;  // kEpiGateUp
+    int rows_block = 0;      // kEpiGateUp: MlpRows layout
+    float* yz = nullptr;     // kEpiGateUp: zeroed (yz_n floats)
+    int64_t yz_n = 0;
+    int ksplit = 1;          // kEpiFold: blocks per tile along K
 };
 
 template <int kR, int kM, int kEpi>
 int launch_diag(int64_t gpw, int64_t tiles, hipStream_t s, const DiagArgs& a) {
     constexpr int kWinD = kR == 1 ? 2 : 3;  // measured: steps of 4 chunks want a shorter window
-    const unsigned grid = static_cast<unsigned>(tiles);
+    const dim3 grid(static_cast<unsigned>(tiles), static_cast<unsigned>(a.ksplit));
 #define TQ_DIAG(G)                                                                                      \
     k_decode_diag<kR, kM, G, kWinD, kEpi><<<grid, kBlock, 0, s>>>(a.x, a.m, a.pt, a.st, a.b, a.n, a.k, a.y, \
-                                                                  a.hout, a.tok0, a.mtot)
+                                                                  a.hout, a.tok0, a.mtot, a.rows_block,      \
+                                                                  a.yz, a.yz_n)
     // the exact groups per wave, so that no wave of the block runs dead groups (K =
     // 14336, the Llama FFN's intermediate size, is 7 per wave)
     switch (gpw) {
@@ -566,10 +587,18 @@ int launch_diag(int64_t gpw, int64_t tiles, hipStream_t s, const DiagArgs& a) {
         case 2: TQ_DIAG(2); break;
         case 3: TQ_DIAG(3); break;
         case 4: TQ_DIAG(4); break;
-        case 5: TQ_DIAG(5); break;
-        case 6: TQ_DIAG(6); break;
-        case 7: TQ_DIAG(7); break;
-        default: TQ_DIAG(8); break;
+        default:
+            // 8 x rows fit the LDS at up to 4 groups per wave only
+            if constexpr (kM <= 4) {
+                switch (gpw) {
+                    case 5: TQ_DIAG(5); break;
+                    case 6: TQ_DIAG(6); break;
+                    case 7: TQ_DIAG(7); break;
+                    default: TQ_DIAG(8); break;
+                }
+            } else {
+                return fail(TQ_EINVAL, "tq_mlp_w4g128_decode: %lld groups per wave for 8 rows", (long long)gpw);
+            }
     }
 #undef TQ_DIAG
     return check_launch("tq_gemv_w4g128_tiled");
@@ -579,6 +608,8 @@ template <int kR, int kEpi>
 int launch_diag_m(int64_t gpw, int64_t tiles, hipStream_t s, const DiagArgs& a) {
     if (a.m == 1) return launch_diag<kR, 1, kEpi>(gpw, tiles, s, a);
     if (a.m == 2) return launch_diag<kR, 2, kEpi>(gpw, tiles, s, a);
+    if constexpr (kR == 1 && kEpi == kEpiFold)
+        if (a.m > 4) return launch_diag<kR, 8, kEpi>(gpw, tiles, s, a);  // 3-4 tokens' hi and lo rows
     return launch_diag<kR, 4, kEpi>(gpw, tiles, s, a);
 }
 
@@ -799,16 +830,31 @@ int tq_mlp_w4g128_decode(const uint16_t* x_bf16, int64_t m, int64_t d, int64_t f
     uint16_t* h = static_cast<uint16_t*>(workspace);
     const int mi = static_cast<int>(m);
     // gate + up with SiLU * up, 4 tokens per launch, into the hi/lo rows of h
+    const int kr = down_tile_rows == 16 ? 1 : (down_tile_rows == 32 ? 2 : 4);
+    // 3 or 4 tokens on 16-row down tiles: one down launch for all of them (the
+    // 2m hi/lo rows as 16 MFMA columns), K split over two blocks per tile so that
+    // the x rows fit the LDS; the gate/up launch zeroes y for it
+    const bool block = kr == 1 && (mi == 3 || mi == 4);
     const int64_t gu_tiles = (f + 31) / 32, gu_gpw = ((d >> 7) + kWaves - 1) / kWaves;
     for (int j0 = 0; j0 < mi; j0 += 4) {
         const int mm = mi - j0 < 4 ? mi - j0 : 4;
-        const DiagArgs a{x_bf16 + j0 * d, mm, gate_up_t, gate_up_s_t, nullptr, 2 * f, d, nullptr, h, j0, mi};
+        DiagArgs a{x_bf16 + j0 * d, mm, gate_up_t, gate_up_s_t, nullptr, 2 * f, d, nullptr, h, j0, mi};
+        a.rows_block = block;
+        if (block) {
+            a.yz = y;
+            a.yz_n = m * d;
+        }
         const int rc = launch_diag_m<4, kEpiGateUp>(gu_gpw, gu_tiles, st, a);
         if (rc != TQ_OK) return rc;
     }
-    // down, one launch per token pair: its hi and lo rows in, their sum out
-    const int kr = down_tile_rows == 16 ? 1 : (down_tile_rows == 32 ? 2 : 4);
     const int64_t dn_tiles = (d + down_tile_rows - 1) / down_tile_rows, dn_gpw = ((f >> 7) + kWaves - 1) / kWaves;
+    if (block) {
+        DiagArgs a{h, 2 * mi, down_t, down_s_t, nullptr, d, f, y, nullptr, 0, 0};
+        a.ksplit = 2;
+        const int64_t gpw2 = (((f >> 7) + 1) / 2 + kWaves - 1) / kWaves;
+        return launch_diag_r<kEpiFold>(kr, gpw2, dn_tiles, st, a);
+    }
+    // down, one launch per token pair: its hi and lo rows in, their sum out
     for (int c = 0; 2 * c < mi; ++c) {
         const int t = mi - 2 * c < 2 ? mi - 2 * c : 2;
         const DiagArgs a{h + 4 * c * f, 2 * t, down_t, down_s_t, nullptr, d, f, y + 2 * c * d, nullptr, 0, 0};

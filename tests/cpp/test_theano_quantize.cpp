@@ -527,7 +527,8 @@ TEST_GPU(test_parity_quantized_linear_fp8) {
 }
 
 TEST_GPU(test_parity_quantized_mlp) {
-    // M = 1, 2, 5 run the decode kernels, M = 9 the prefill FFN
+    // M = 1, 2, 4, 5 run the decode kernels (M = 4: one K-split down launch), M = 9
+    // the prefill FFN
     const size_t d = 256, f = 384;
     const auto gv = randn(f * d, 0.02, 61), uv = randn(f * d, 0.02, 62), dv = randn(d * f, 0.02, 63);
     const QuantizedMLP mlp = QuantizedMLP::from_tensors(Tensor::from_slice(gv, {f, d}), Tensor::from_slice(uv, {f, d}),
@@ -539,7 +540,7 @@ TEST_GPU(test_parity_quantized_mlp) {
     tqo_quantize_i4_g128(g32.data(), f, d, pg.data(), sg.data());
     tqo_quantize_i4_g128(u32.data(), f, d, pu.data(), su.data());
     tqo_quantize_i4_g128(d32.data(), d, f, pd.data(), sd.data());
-    for (size_t m : {1, 2, 5, 9}) {
+    for (size_t m : {1, 2, 4, 5, 9}) {
         ASSERT(mlp.decode_path(static_cast<int64_t>(m)) == (m <= 8));
         const auto xv = randn(m * d, 1.0, 64 + m);
         const auto y = mlp.forward(Tensor::from_slice(xv, {m, d})).to_vec_f64().unwrap();

@@ -28,17 +28,30 @@ int check_launch(const char* what) {
 }
 
 int device_cu_count() {
-    static int cached[64] = {0};
+    // one slot per device; concurrent first calls store the same value
+    static std::atomic<int> cached[64];
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-    if (cached[dev] == 0) {
-        int cus = 0;
+    int cus = cached[dev].load(std::memory_order_relaxed);
+    if (cus == 0) {
         if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
             cus <= 0)
             cus = 256;
-        cached[dev] = cus;
+        cached[dev].store(cus, std::memory_order_relaxed);
     }
-    return cached[dev];
+    return cus;
+}
+
+int allow_dynamic_lds(const void* kernel, int bytes, std::atomic<uint64_t>& done_devices) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return fail(TQ_EHIP, "hipGetDevice failed");
+    const uint64_t bit = uint64_t{1} << dev;
+    if (done_devices.load(std::memory_order_acquire) & bit) return TQ_OK;
+    // idempotent: threads racing here all set the same attribute
+    if (hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, bytes) != hipSuccess)
+        return fail(TQ_EHIP, "hipFuncSetAttribute(MaxDynamicSharedMemorySize, %d) failed", bytes);
+    done_devices.fetch_or(bit, std::memory_order_acq_rel);
+    return TQ_OK;
 }
 
 }  // namespace tq

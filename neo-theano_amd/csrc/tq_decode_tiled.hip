@@ -569,12 +569,17 @@ struct DiagArgs {
     int rows_block = 0;      // kEpiGateUp: MlpRows layout
     float* yz = nullptr;     // kEpiGateUp: zeroed (yz_n floats)
     int64_t yz_n = 0;
-    int ksplit = 1;          // kEpiFold: blocks per tile along K
+    int ksplit = 1;          // kEpiFold only: blocks per tile along K; their sums are
+                             // added into y atomically, so the caller zeroes y first
+                             // (the gate/up launch of the same FFN does, through yz)
 };
 
 template <int kR, int kM, int kEpi>
 int launch_diag(int64_t gpw, int64_t tiles, hipStream_t s, const DiagArgs& a) {
     constexpr int kWinD = kR == 1 ? 2 : 3;  // measured: steps of 4 chunks want a shorter window
+    // only the fold epilogue adds K parts; the others would store one part over another
+    if (a.ksplit < 1 || (a.ksplit > 1 && kEpi != kEpiFold))
+        return fail(TQ_EINVAL, "tq_gemv_w4g128_tiled: K split %d needs the accumulating epilogue", a.ksplit);
     const dim3 grid(static_cast<unsigned>(tiles), static_cast<unsigned>(a.ksplit));
 #define TQ_DIAG(G)                                                                                      \
     k_decode_diag<kR, kM, G, kWinD, kEpi><<<grid, kBlock, 0, s>>>(a.x, a.m, a.pt, a.st, a.b, a.n, a.k, a.y, \

@@ -180,13 +180,9 @@ __global__ __launch_bounds__(kBlock) void k_decode_w4g128(const uint16_t* __rest
 template <int kGPW>
 int launch_one(int64_t blocks, int m, hipStream_t st, const uint16_t* x, const uint8_t* p, const uint16_t* s,
                const float* b, int64_t n, int64_t k, float* y) {
-    static bool attr_set = false;  // allow the full 160 KB of LDS per block
-    if (!attr_set) {
-        if (hipFuncSetAttribute(reinterpret_cast<const void*>(k_decode_w4g128<kGPW>),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess)
-            return fail(TQ_EHIP, "tq_gemv_w4g128: hipFuncSetAttribute failed");
-        attr_set = true;
-    }
+    static std::atomic<uint64_t> lds_set{0};  // allow the full 160 KB of LDS per block, per device
+    if (int rc = allow_dynamic_lds(reinterpret_cast<const void*>(k_decode_w4g128<kGPW>), 160 * 1024, lds_set))
+        return rc;
     k_decode_w4g128<kGPW><<<static_cast<unsigned>(blocks), kBlock, lds_bytes(m, kGPW), st>>>(x, m, p, s, b, n, k, y);
     return TQ_OK;
 }

@@ -46,22 +46,14 @@ namespace tq {
 namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef __attribute__((address_space(3))) int8_t lds_i8;
 
 constexpr float kOffset = 192.0f;  // 8 * 24: weight operand 8 * (24 + q)
 constexpr float kUnit = 0.125f;    // 1 / 8
 
-__device__ __forceinline__ uint32_t lds_addr(const int8_t* l) {
-    return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_i8*)l));
-}
 // 64 lanes x 16 bytes -> LDS [la, la + 1024)
-__device__ __forceinline__ void dma16(const int8_t* g, uint32_t la) {
-    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(la), "v"(g) : "memory");
-}
+__device__ __forceinline__ void dma16(const int8_t* g, uint32_t la) { lds_dma16(g, la); }
 // active lanes x 4 bytes -> LDS la + 4 * lane
-__device__ __forceinline__ void dma4(const int8_t* g, uint32_t la) {
-    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, off" ::"s"(la), "v"(g) : "memory");
-}
+__device__ __forceinline__ void dma4(const int8_t* g, uint32_t la) { lds_dma4(g, la); }
 #define TQ_FENCE() __builtin_amdgcn_sched_barrier(0)
 
 // Makes a value opaque to the optimizer: keeps the prologue's LDS reads of the

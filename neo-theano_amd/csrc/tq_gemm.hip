@@ -159,20 +159,10 @@ constexpr int kDmaStage = kDmaW + kDmaBM * kDmaBK;
 constexpr int kDmaEpiRow = 128 * 4 + 16;       // int32 row of a wave's 64 x 128 tile, padded
 constexpr int kDmaGroupM = 8;                  // m tiles per tile group (XCD locality)
 
-typedef __attribute__((address_space(3))) int8_t lds_i8;
-
-// 16 bytes per lane from `g` into LDS at (l + 16 * lane).  Issued as inline asm:
-// the compiler cannot tell which ring buffer a pending LDS DMA targets and would
-// otherwise wait for all of them before every LDS read.  The kernel tracks
+// 16 bytes per lane from `g` into LDS at (l + 16 * lane).  The kernel tracks
 // completion itself with explicit vmcnt waits (vmcnt retires in order, so any
-// wait the compiler adds for its own loads stays conservative).  M0 is written
-// here; nothing else in these kernels uses M0.
-__device__ __forceinline__ void dma16(const int8_t* g, int8_t* l) {
-    // generic -> LDS address space (an address-space cast, so C style); the LDS
-    // address is the low 32 bits
-    const uint32_t la = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_i8*)l));
-    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(la), "v"(g) : "memory");
-}
+// wait the compiler adds for its own loads stays conservative).
+__device__ __forceinline__ void dma16(const int8_t* g, int8_t* l) { lds_dma16(g, lds_addr(l)); }
 
 // XOR swizzle of the 16-byte chunk index of a 128-byte LDS row
 __device__ __forceinline__ int dma_swz(int row) { return (row >> 1) & 7; }

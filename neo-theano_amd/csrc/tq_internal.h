@@ -4,6 +4,7 @@
 #include <hip/hip_runtime.h>
 #include <hip/hip_fp16.h>
 
+#include <atomic>
 #include <cstdarg>
 #include <cstdint>
 #include <cstdio>
@@ -36,8 +37,12 @@ inline bool aligned(const void* p, uintptr_t a) {
     return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0;
 }
 
-// Compute-unit count of the current device (cached per device).
+// Compute-unit count of the current device (cached per device, thread-safe).
 int device_cu_count();
+
+// Raises `kernel`'s dynamic LDS limit to `bytes` once per device (bit d of
+// `done_devices` records device d); thread-safe.
+int allow_dynamic_lds(const void* kernel, int bytes, std::atomic<uint64_t>& done_devices);
 
 // Shape-general fallbacks of the matmul entry points (tq_generic.hip); any N,
 // K (K % 128 == 0 for INT4 g128), element-aligned pointers.
@@ -69,6 +74,31 @@ int launch_mlp_w4g128_general(const uint16_t* x_bf16, int64_t m, int64_t d, int6
 // -------------------------------------------------------------- device side
 
 constexpr int kWave = 64;
+
+typedef __attribute__((address_space(3))) int8_t lds_i8;
+
+// LDS byte address (the low 32 bits of an LDS pointer; an address-space cast).
+__device__ __forceinline__ uint32_t lds_addr(const int8_t* l) {
+    return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_i8*)l));
+}
+
+// Direct global -> LDS loads: each active lane's bytes at `g` land at
+// la + lane * size (M0 holds the wave's LDS base).  These are the only writers
+// of M0 in the library.  Issued as inline asm because the compiler cannot tell
+// which LDS buffer a pending LDS DMA targets and would otherwise wait for all of
+// them before every LDS read; callers track completion with explicit vmcnt
+// waits.  M0 is listed as clobbered so that the compiler never assumes a value
+// of its own survives the statement (clang warns that M0 is reserved, i.e. not
+// saved for the statement, which is the intent: nothing is to be preserved).
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void lds_dma16(const void* g, uint32_t la) {
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(la), "v"(g) : "memory", "m0");
+}
+__device__ __forceinline__ void lds_dma4(const void* g, uint32_t la) {
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, off" ::"s"(la), "v"(g) : "memory", "m0");
+}
+#pragma clang diagnostic pop
 
 // Wave64 butterfly reductions (DPP / ds_swizzle via __shfl_xor).
 __device__ __forceinline__ float wave_max(float v) {

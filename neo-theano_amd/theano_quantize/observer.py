@@ -1,8 +1,10 @@
 """MinMaxObserver / PerChannelMinMaxObserver (crates/theano-quantize/src/observer.rs:6-136).
 
-The running min/max live on the device (f32 is exact for f32 data); the
-scale/zero-point arithmetic is the reference's scalar f64 code, run on the host
-by libtq.so (tq_observer_scale_zp).
+The running min/max live on the device; the scale/zero-point arithmetic is the
+reference's scalar f64 code, run on the host by libtq.so (tq_observer_scale_zp).
+The state starts as float32 (exact for f32 data).  The first float64 input
+widens it to float64 (exact) and from then on every input is folded in f64
+(f32 inputs widen exactly), so f64 data get the reference's f64 min/max.
 """
 from __future__ import annotations
 
@@ -12,6 +14,7 @@ import torch
 
 from . import _abi
 from ._tensor import device, on_device, ptr, stream
+from .errors import InvalidArgument
 from .qconfig import QuantDType
 
 
@@ -20,6 +23,19 @@ def _scale_zp(mn: float, mx: float, initialized: bool, dtype: QuantDType):
     _abi.call("tq_observer_scale_zp", float(mn), float(mx), int(initialized), int(dtype),
               ctypes.byref(s), ctypes.byref(z))
     return s.value, z.value
+
+
+def _observe_input(obs, values, name):
+    """Device input in the state's element type; widens the state to float64
+    on the first float64 input.  Returns (tensor, libtq suffix)."""
+    t = values if isinstance(values, torch.Tensor) else torch.as_tensor(values)
+    if t.dtype not in (torch.float32, torch.float64):
+        raise InvalidArgument(f"{name}: expected float32 or float64, got {t.dtype}")
+    if t.dtype == torch.float64 and obs._state.dtype == torch.float32:
+        obs._state = obs._state.double()
+    if obs._state.dtype == torch.float64:
+        return on_device(t, t.dtype, name).double(), "_f64"
+    return on_device(t, torch.float32, name), ""
 
 
 class Observer:
@@ -43,8 +59,8 @@ class MinMaxObserver(Observer):
         self.reset()
 
     def observe(self, values) -> None:
-        x = on_device(values, torch.float32, "MinMaxObserver.observe")
-        _abi.call("tq_minmax_observe", ptr(x), x.numel(), ptr(self._state), stream())
+        x, f64 = _observe_input(self, values, "MinMaxObserver.observe")
+        _abi.call("tq_minmax_observe" + f64, ptr(x), x.numel(), ptr(self._state), stream())
         self._initialized = True
 
     def min_val(self) -> float:
@@ -58,7 +74,8 @@ class MinMaxObserver(Observer):
         return _scale_zp(mn, mx, self._initialized, dtype)
 
     def reset(self) -> None:
-        _abi.call("tq_minmax_reset", ptr(self._state), 1, stream())
+        f64 = "_f64" if self._state.dtype == torch.float64 else ""
+        _abi.call("tq_minmax_reset" + f64, ptr(self._state), 1, stream())
         self._initialized = False
 
 
@@ -71,8 +88,8 @@ class PerChannelMinMaxObserver(Observer):
         self.reset()
 
     def observe(self, values) -> None:
-        x = on_device(values, torch.float32, "PerChannelMinMaxObserver.observe")
-        _abi.call("tq_minmax_observe_per_channel", ptr(x), x.numel(), self.num_channels,
+        x, f64 = _observe_input(self, values, "PerChannelMinMaxObserver.observe")
+        _abi.call("tq_minmax_observe_per_channel" + f64, ptr(x), x.numel(), self.num_channels,
                   ptr(self._state), stream())
         self._initialized = True
 
@@ -99,5 +116,6 @@ class PerChannelMinMaxObserver(Observer):
         return s / len(sz), z / len(sz)
 
     def reset(self) -> None:
-        _abi.call("tq_minmax_reset", ptr(self._state), self.num_channels, stream())
+        f64 = "_f64" if self._state.dtype == torch.float64 else ""
+        _abi.call("tq_minmax_reset" + f64, ptr(self._state), self.num_channels, stream())
         self._initialized = False

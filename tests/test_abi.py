@@ -160,3 +160,55 @@ def test_zero_sizes_are_noops(abi):
     assert abi.call("tq_gemv_w8", None, 0, None, None, None, 16, 16, None, None) == 0
     assert abi.call("tq_quantize_tensor", None, 0, 1.0, 0.0, 0, None, None) == 0
     assert abi.call("tq_convert", None, 3, None, 1, 0, None) == 0
+
+
+def test_host_paths_from_many_threads(abi):
+    """Entry points called concurrently from 16 threads: each thread's status
+    and tq_last_error message are its own (the message is thread-local), and
+    the cached per-device queries agree across threads."""
+    import threading
+
+    L = abi.lib()
+    cases = [
+        ("tq_quantize_i4_g128", [None, 4, 100, None, None, None], b"tq_quantize_i4_g128: K=100"),
+        ("tq_gemv_w4g128", [None, 17, None, None, None, 16, 128, None, None], b"tq_gemv_w4g128: M=17"),
+        ("tq_convert", [None, 3, None, 12, 4, None], b"tq_convert: unsupported dtype"),
+        ("tq_quantize_tensor", [None, 10, 1.0, 0.0, 7, None, None], b"unknown QuantDType 7"),
+    ]
+    errors, tiles = [], []
+
+    def worker(i):
+        name, args, word = cases[i % len(cases)]
+        for _ in range(200):
+            st = getattr(L, name)(*args)
+            msg = L.tq_last_error()
+            if st != 1 or not msg.startswith(word):
+                errors.append((i, name, st, msg))
+                return
+            tiles.append(L.tq_w4g128_tile_rows(14336))
+            s, z = ctypes.c_double(), ctypes.c_double()
+            if L.tq_observer_scale_zp(-1.0, 3.0, 1, 0, ctypes.byref(s), ctypes.byref(z)) != 0:
+                errors.append((i, "scale_zp"))
+                return
+
+    threads = [threading.Thread(target=worker, args=(i,)) for i in range(16)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    assert not errors, errors[:4]
+    assert len(set(tiles)) == 1
+
+
+def test_python_api_rejects_non_float_data():
+    import numpy as np
+
+    import theano_quantize as tq
+    from theano_quantize import InvalidArgument
+
+    for f in (lambda x: tq.quantize_tensor(x, 1.0, 0.0, tq.QuantDType.Int8),
+              lambda x: tq.dequantize_tensor(x, 1.0, 0.0),
+              lambda x: tq.fake_quantize(x, 1.0, 0.0, tq.QuantDType.Int8),
+              lambda x: tq.quantize_per_tensor(x, tq.QuantDType.Int8)):
+        with pytest.raises(InvalidArgument):
+            f(np.arange(4, dtype=np.int32))

@@ -3,9 +3,14 @@ quantized FFN vs the oracle's f64 reference (Linear::forward over the
 dequantized weight).  Integer accumulators are bit-exact; float outputs are
 checked at |got - ref| <= 1e-4 + 1e-3 * |ref|.
 
-At full W8A8 size (M=2048) the oracle runs on sampled rows and every row is
-checked by exact int64 checksums: row sums, column sums and a random
-projection of the int32 accumulators."""
+At the two heaviest configs every output is compared.  W8A8 at M=2048: all
+int32 accumulators equal an f64 GEMM of the integer codes (exact, since every
+partial sum is an integer below 2^26 < 2^53, whatever the summation order),
+all of y is within tolerance of acc * s_row * s_col in f64 (the product of the
+dequantized operands), and the oracle's sequential restatement anchors sampled
+rows.  The FFN at M=512: all rows against an f64 composition over the
+dequantized weights (SiLU as g * 1/(1+exp(-g)), activation.rs:66-79), with the
+oracle's rows as the anchor."""
 import numpy as np
 import pytest
 
@@ -222,9 +227,15 @@ def test_w8a8_config4_full(tq, oracle):
     assert np.array_equal(qa, rqa) and np.array_equal(sa, rsa)
     assert np.array_equal(qw, rqw) and np.array_equal(sw, rsw)
     assert checksums_ok(acc, qa, qw)
+    acc_ref = qa.astype(np.float64) @ qw.astype(np.float64).T
+    assert np.abs(acc_ref).max() < 2.0 ** 26
+    bad = acc.astype(np.float64) != acc_ref
+    assert not bad.any(), f"{int(bad.sum())} of {acc.size} int32 accumulators differ, first at {np.argwhere(bad)[0]}"
+    y_ref = acc_ref * sa.astype(np.float64)[:, None] * sw.astype(np.float64)[None, :]
+    assert_close(y, y_ref, RTOL, ATOL, "w8a8 y (all rows)")
     rows = np.array([0, 1, 127, 128, 1000, 2047])
     assert np.array_equal(acc[rows], oracle.gemm_w8a8_acc(qa[rows], qw))
-    assert_close(y[rows], oracle.linear_w8a8(qa[rows], sa[rows], qw, sw), RTOL, ATOL, "w8a8 y")
+    assert_close(y[rows], oracle.linear_w8a8(qa[rows], sa[rows], qw, sw), RTOL, ATOL, "w8a8 y vs oracle")
 
 
 # K % 128 == 0 takes the LDS-DMA kernel (1, 2, 3 and more stages; M, N tails; tile
@@ -335,7 +346,18 @@ def test_mlp_small(tq, oracle, m, d, f):
     assert_close(y, oracle.mlp_w4g128(xb, *args), RTOL, ATOL, f"mlp {m}x{d}x{f}")
 
 
-def test_mlp_config5_sampled_rows(tq, oracle):
+def mlp_f64(xb, pg, sg, pu, su, pd, sd, oracle):
+    """The FFN in f64 over the dequantized weights (exact in f32: q * s), as
+    numpy matmuls: h = g * 1/(1+exp(-g)) * u, y = h Wd^T."""
+    x = (xb.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+    g = x @ oracle.dequantize_i4_g128(pg, sg).astype(np.float64).T
+    u = x @ oracle.dequantize_i4_g128(pu, su).astype(np.float64).T
+    h = g * (1.0 / (1.0 + np.exp(-g))) * u
+    del g, u
+    return h @ oracle.dequantize_i4_g128(pd, sd).astype(np.float64).T
+
+
+def test_mlp_config5_all_rows(tq, oracle):
     d, f, m = 4096, 14336, 512
     wg = normal(4, (f, d), 0.02)
     wu = normal(4, (f, d), 0.02, stream=1)
@@ -343,9 +365,15 @@ def test_mlp_config5_sampled_rows(tq, oracle):
     xb = to_bf16_bits(normal(4, (m, d), 1.0, stream=3))
     mlp = tq.QuantizedMLP.from_tensors(dev_tensor(wg), dev_tensor(wu), dev_tensor(wd))
     y = host(mlp(bf16_dev(xb)))
-    rows = np.array([0, 129, 511])
     args = [a for t in (mlp.gate, mlp.up, mlp.down) for a in (host(t[0]), host(t[1]).view(np.uint16))]
-    assert_close(y[rows], oracle.mlp_w4g128(xb[rows], *args), RTOL, ATOL, "mlp config 5")
+    # one row in each 128-row M tile of the prefill kernels, plus the last row
+    rows = np.array([0, 129, 300, 400, 511])
+    ref_rows = oracle.mlp_w4g128(xb[rows], *args)
+    assert_close(y[rows], ref_rows, RTOL, ATOL, "mlp config 5 vs oracle")
+    ref = mlp_f64(xb, *args, oracle)
+    # the f64 composition itself agrees with the oracle's sequential restatement
+    assert_close(ref[rows], ref_rows, 1e-9, 1e-9, "f64 composition vs oracle")
+    assert_close(y, ref, RTOL, ATOL, "mlp config 5 (all rows)")
 
 
 def _mlp_case(tq, m, d, f, seed=57):

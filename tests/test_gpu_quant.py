@@ -217,3 +217,56 @@ def test_observers_match_reference(tq, oracle):
     rs, rz = rpc.scales_and_zero_points(0)
     assert pc.scales_and_zero_points(tq.QuantDType.Int8) == list(zip(rs.tolist(), rz.tolist()))
     assert pc.compute_scale_zero_point(tq.QuantDType.Int8) == rpc.compute_scale_zero_point(0)
+
+
+# ---------------------------------------- f64 data through the Python API
+@pytest.mark.parametrize("dtype", [0, 1, 2, 3])
+@pytest.mark.parametrize("scale,zp", [(0.01, 0.0), (1.0 / 3.0, -2.0), (0.0123, 3.0), (1e-300, 0.0)])
+def test_python_api_f64_matches_reference(tq, oracle, dtype, scale, zp):
+    """float64 tensors run the _f64 entry points: the reference's own element
+    type, values that f32 cannot hold (x/scale within 2^-40 of a tie)."""
+    import torch
+
+    rng = np.random.default_rng(70 + dtype)
+    x = rng.standard_normal(4000) * 3.0
+    x[:8] = [2.5 * scale, -2.5 * scale, 0.5 * scale * (1 + 2.0 ** -40), -0.3 * scale, 0.0, -0.0, np.nan, -np.inf]
+    xd = torch.from_numpy(x).cuda()
+    q = tq.quantize_tensor(xd, scale, zp, tq.QuantDType(dtype))
+    assert q.dtype == torch.float64
+    ref = oracle.quantize_tensor(x, scale, zp, dtype)
+    assert same_codes(host(q), ref)
+    d = tq.dequantize_tensor(q, scale, zp)
+    assert d.dtype == torch.float64 and ieee_equal(host(d), oracle.dequantize_tensor(ref, scale, zp))
+    f = tq.fake_quantize(xd, scale, zp, tq.QuantDType(dtype))
+    assert f.dtype == torch.float64 and ieee_equal(host(f), oracle.fake_quantize(x, scale, zp, dtype))
+    q2, s2, z2 = tq.quantize_per_tensor(xd[8:], tq.QuantDType(dtype))
+    rq2, rs2, rz2 = oracle.quantize_per_tensor(x[8:], dtype)
+    assert (s2, z2) == (rs2, rz2) and same_codes(host(q2), rq2)
+
+
+def test_observers_widen_to_f64(tq, oracle):
+    """An f32 input, then f64 inputs whose extremes f32 cannot hold: the state
+    widens exactly and keeps the reference's f64 min/max."""
+    import torch
+
+    o = tq.MinMaxObserver()
+    ro = oracle.MinMaxObserver()
+    x32 = weights(71, (1000,), 1.0)
+    o.observe(dev_tensor(x32))
+    ro.observe(x32.astype(np.float64))
+    x64 = np.random.default_rng(72).standard_normal(3000) * 2.0
+    x64[7] = 1.0 + 2.0 ** -40 + 9.0
+    x64[8] = np.nan
+    o.observe(torch.from_numpy(x64).cuda())
+    ro.observe(x64)
+    o.observe(dev_tensor(x32 * 0.5))
+    ro.observe((x32 * 0.5).astype(np.float64))
+    assert (o.min_val(), o.max_val()) == (ro.min_val, ro.max_val)
+    for dt in range(4):
+        assert o.compute_scale_zero_point(tq.QuantDType(dt)) == ro.compute_scale_zero_point(dt)
+    pc = tq.PerChannelMinMaxObserver(11)
+    rpc = oracle.PerChannelMinMaxObserver(11)
+    x = np.random.default_rng(73).standard_normal(11 * 40) / 3.0
+    pc.observe(torch.from_numpy(x).cuda())
+    rpc.observe(x)
+    assert pc.min_vals() == rpc.mins.tolist() and pc.max_vals() == rpc.maxs.tolist()

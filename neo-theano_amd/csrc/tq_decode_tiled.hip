@@ -40,6 +40,8 @@
 //    tile and a run of groups, reads its tokens' x straight from L2 (no LDS
 //    staging, no barrier before the arithmetic) and consumes its loads in
 //    order; the runs meet in LDS (details at the kernel).
+#include <mutex>
+
 #include "tq_internal.h"
 
 namespace tq {
@@ -809,28 +811,73 @@ int tq_repack_w4g128_gate_up_tiled(const uint8_t* gate_packed, const uint16_t* g
                          "tq_repack_w4g128_gate_up_tiled");
 }
 
-int tq_mlp_w4g128_decode(const uint16_t* x_bf16, int64_t m, int64_t d, int64_t f, const uint8_t* gate_up_t,
-                         const uint16_t* gate_up_s_t, const uint8_t* down_t, const uint16_t* down_s_t,
-                         int64_t down_tile_rows, void* workspace, int64_t workspace_bytes, float* y,
-                         tq_stream_t stream) {
-    TQ_REQUIRE(m >= 0 && d >= 0 && f >= 0, "tq_mlp_w4g128_decode: negative shape");
-    TQ_REQUIRE(m <= 16, "tq_mlp_w4g128_decode: M=%lld > 16", (long long)m);
-    TQ_REQUIRE(d % 128 == 0 && f % 128 == 0, "tq_mlp_w4g128_decode: D=%lld and F=%lld must be multiples of 128",
+}  // extern "C"
+
+namespace tq {
+namespace {
+
+// Scratch of the allocation-free decode FFN: the bf16 hi and lo rows of h for
+// 16 tokens at F = 16384 (the largest decode shape).  One copy per device, held
+// until the process ends; host code reaches it only through the address that
+// hipGetSymbolAddress returns for the current device.
+constexpr int64_t kMlpDecodeScratch = 2 * 16 * 16384 * 2;
+static_assert(kMlpDecodeScratch == TQ_MLP_DECODE_SCRATCH_BYTES, "tq.h states the scratch size");
+__device__ __align__(256) uint8_t scratch[kMlpDecodeScratch];
+
+std::atomic<void*> g_scratch_ptr[64];
+std::mutex g_scratch_mu;
+
+// Device address of `scratch` on the current device (resolved once per device).
+int scratch_address(const char* fn, void** out) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return fail(TQ_EHIP, "%s: hipGetDevice failed", fn);
+    void* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+    if (!p) {
+        std::lock_guard<std::mutex> lock(g_scratch_mu);
+        p = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+        if (!p) {
+            const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+            if (e != hipSuccess || !p)
+                return fail(TQ_EHIP, "%s: hipGetSymbolAddress(scratch) on device %d: %s", fn, dev,
+                            hipGetErrorString(e));
+            g_scratch_ptr[dev].store(p, std::memory_order_release);
+        }
+    }
+    *out = p;
+    return TQ_OK;
+}
+
+// Checks and launches of the decode FFN.  With `use_scratch` set, h goes to the
+// current device's scratch array (resolved after the arguments are checked)
+// and `workspace` is ignored.
+int mlp_decode(const char* fn, const uint16_t* x_bf16, int64_t m, int64_t d, int64_t f, const uint8_t* gate_up_t,
+               const uint16_t* gate_up_s_t, const uint8_t* down_t, const uint16_t* down_s_t,
+               int64_t down_tile_rows, void* workspace, int64_t workspace_bytes, bool use_scratch, float* y,
+               tq_stream_t stream) {
+    TQ_REQUIRE(m >= 0 && d >= 0 && f >= 0, "%s: negative shape", fn);
+    TQ_REQUIRE(m <= 16, "%s: M=%lld > 16", fn, (long long)m);
+    TQ_REQUIRE(d % 128 == 0 && f % 128 == 0, "%s: D=%lld and F=%lld must be multiples of 128", fn,
                (long long)d, (long long)f);
     TQ_REQUIRE(d <= kMaxCPW * kWaves * 32 && f <= kMaxCPW * kWaves * 32,
-               "tq_mlp_w4g128_decode: D=%lld or F=%lld > %d", (long long)d, (long long)f, kMaxCPW * kWaves * 32);
+               "%s: D=%lld or F=%lld > %d", fn, (long long)d, (long long)f, kMaxCPW * kWaves * 32);
     TQ_REQUIRE(down_tile_rows == 16 || down_tile_rows == 32 || down_tile_rows == 64,
-               "tq_mlp_w4g128_decode: down tile_rows=%lld must be 16, 32 or 64", (long long)down_tile_rows);
+               "%s: down tile_rows=%lld must be 16, 32 or 64", fn, (long long)down_tile_rows);
     if (m == 0 || d == 0) return TQ_OK;
-    TQ_REQUIRE(f > 0, "tq_mlp_w4g128_decode: F=0");
-    TQ_REQUIRE(x_bf16 && gate_up_t && gate_up_s_t && down_t && down_s_t && workspace && y,
-               "tq_mlp_w4g128_decode: null pointer");
+    TQ_REQUIRE(f > 0, "%s: F=0", fn);
+    TQ_REQUIRE(x_bf16 && gate_up_t && gate_up_s_t && down_t && down_s_t && (workspace || use_scratch) && y,
+               "%s: null pointer", fn);
     const int64_t need = tq_mlp_w4g128_decode_workspace_bytes(m, d, f);
-    TQ_REQUIRE(workspace_bytes >= need, "tq_mlp_w4g128_decode: workspace of %lld bytes, %lld needed",
+    if (use_scratch) {
+        TQ_REQUIRE(need <= kMlpDecodeScratch, "%s: M=%lld, F=%lld need %lld bytes of scratch, more than its %lld",
+                   fn, (long long)m, (long long)f, (long long)need, (long long)kMlpDecodeScratch);
+        if (int rc = scratch_address(fn, &workspace)) return rc;
+        workspace_bytes = kMlpDecodeScratch;
+    }
+    TQ_REQUIRE(workspace_bytes >= need, "%s: workspace of %lld bytes, %lld needed", fn,
                (long long)workspace_bytes, (long long)need);
     TQ_REQUIRE(aligned(x_bf16, 8) && aligned(gate_up_t, 16) && aligned(down_t, 16) && aligned(gate_up_s_t, 8) &&
                    aligned(down_s_t, 8) && aligned(workspace, 16) && aligned(y, 4),
-               "tq_mlp_w4g128_decode: misaligned pointer");
+               "%s: misaligned pointer", fn);
     const hipStream_t st = as_hip(stream);
     uint16_t* h = static_cast<uint16_t*>(workspace);
     const int mi = static_cast<int>(m);
@@ -867,6 +914,27 @@ int tq_mlp_w4g128_decode(const uint16_t* x_bf16, int64_t m, int64_t d, int64_t f
         if (rc != TQ_OK) return rc;
     }
     return TQ_OK;
+}
+
+}  // namespace
+}  // namespace tq
+
+extern "C" {
+
+int tq_mlp_w4g128_decode(const uint16_t* x_bf16, int64_t m, int64_t d, int64_t f, const uint8_t* gate_up_t,
+                         const uint16_t* gate_up_s_t, const uint8_t* down_t, const uint16_t* down_s_t,
+                         int64_t down_tile_rows, void* workspace, int64_t workspace_bytes, float* y,
+                         tq_stream_t stream) {
+    return mlp_decode("tq_mlp_w4g128_decode", x_bf16, m, d, f, gate_up_t, gate_up_s_t, down_t, down_s_t,
+                      down_tile_rows, workspace, workspace_bytes, false, y, stream);
+}
+
+int tq_mlp_w4g128_decode_noalloc(const uint16_t* x_bf16, int64_t m, int64_t d, int64_t f,
+                                 const uint8_t* gate_up_t, const uint16_t* gate_up_s_t, const uint8_t* down_t,
+                                 const uint16_t* down_s_t, int64_t down_tile_rows, float* y, tq_stream_t stream) {
+    // nothing is allocated: h goes to this device's scratch array
+    return mlp_decode("tq_mlp_w4g128_decode_noalloc", x_bf16, m, d, f, gate_up_t, gate_up_s_t, down_t, down_s_t,
+                      down_tile_rows, nullptr, 0, true, y, stream);
 }
 
 }  // extern "C"

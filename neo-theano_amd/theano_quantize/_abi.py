@@ -70,6 +70,7 @@ SIGNATURES = {
     "tq_mlp_w4g128_decode_workspace_bytes": [_i64, _i64, _i64],
     "tq_repack_w4g128_gate_up_tiled": [_p, _p, _p, _p, _i64, _i64, _p, _p, _p],
     "tq_mlp_w4g128_decode": [_p, _i64, _i64, _i64, _p, _p, _p, _p, _i64, _p, _i64, _p, _p],
+    "tq_mlp_w4g128_decode_noalloc": [_p, _i64, _i64, _i64, _p, _p, _p, _p, _i64, _p, _p],
 }
 _RESTYPE = {"tq_status_string": ctypes.c_char_p, "tq_last_error": ctypes.c_char_p,
             "tq_w4g128_tile_rows": ctypes.c_int64, "tq_mlp_w4g128_workspace_bytes": ctypes.c_int64,

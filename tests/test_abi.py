@@ -102,6 +102,9 @@ def test_observer_scale_zp_matches_oracle(abi, oracle):
     ("tq_mlp_w4g128_decode", [None, 2, 256, 256, None, None, None, None, 24, None, 0, None, None]),  # tile rows
     ("tq_mlp_w4g128_decode", [None, 2, 256, 256, None, None, None, None, 16, None, 0, None, None]),  # nulls
     ("tq_mlp_w4g128_decode", [256, 2, 256, 256, 256, 256, 256, 256, 16, 256, 16, 256, None]),  # workspace
+    ("tq_mlp_w4g128_decode_noalloc", [256, 17, 256, 16384, 256, 256, 256, 256, 16, 256, None]),  # scratch
+    ("tq_mlp_w4g128_decode_noalloc", [256, 16, 256, 16512, 256, 256, 256, 256, 16, 256, None]),  # scratch
+    ("tq_mlp_w4g128_decode_noalloc", [256, 2, 256, 256, 256, 256, 256, 256, 16, None, None]),  # null y
     ("tq_repack_w4g128_gate_up_tiled", [None, None, None, None, 128, 100, None, None, None]),  # D % 128
     ("tq_repack_w4g128_gate_up_tiled", [None, None, None, None, 128, 128, None, None, None]),  # nulls
     ("tq_quantize_tensor", [None, 10, 1.0, 0.0, 7, None, None]),          # bad QuantDType

@@ -13,9 +13,14 @@ GEMV at M=2..16, W8A8 GEMM at M=2048 (config 4) in INT8 and in FP8 e4m3,
 per-row INT8 quantize /
 dequantize round trip (config 1) and the INT4 FFN block (config 5).
 
-`cpu_baseline` times the C restatement of the reference CPU path
-(oracle/, f64 dequantize + Linear::forward) on a bounded sample of the
-headline workload, single-threaded.
+`cpu_baseline` times the C restatement of the reference CPU path (oracle/,
+f64 Linear::forward over the dequantized weight, which Linear::from_tensors
+holds) on the headline workload, single-threaded; each secondary config carries
+its own `cpu_baseline` timed the same way (configs 4 and 5 from row subsets,
+extrapolated as gather + rows).  `measured_peaks` re-measures the roofline
+denominators on the device (HBM stream over 4 GiB, i8 / bf16 MFMA loops) and
+`read_ceiling_30mb` times a plain streaming read of the headline's bytes with
+the headline's harness.
 """
 from __future__ import annotations
 
@@ -48,6 +53,7 @@ def parse_args():
     p.add_argument("--no-secondary", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=12.0, help="bound of the CPU baseline sample (0: skip)")
     p.add_argument("--eager", action="store_true", help="time eager launches instead of a HIP graph")
+    p.add_argument("--reps", type=int, default=5, help="timed replays of the K launches (median reported)")
     return p.parse_args()
 
 
@@ -63,9 +69,10 @@ class Timer:
     takes longer than the kernel); long ones run back to back either way, and
     graph replay adds a few microseconds per node on this stack."""
 
-    def __init__(self, torch, eager=False):
+    def __init__(self, torch, eager=False, reps=1):
         self.torch = torch
         self.eager = eager
+        self.reps = reps  # timed replays of the `steps` launches; the median is returned
 
     def run(self, launch, steps, warmup):
         best = self._run(launch, steps, warmup, graph=not self.eager)
@@ -94,20 +101,217 @@ class Timer:
             except Exception as e:  # capture unsupported: fall back to eager launches
                 log(f"graph capture failed ({e}); timing eager launches")
                 g = None
-        start = torch.cuda.Event(enable_timing=True)
-        end = torch.cuda.Event(enable_timing=True)
-        torch.cuda.synchronize()
-        start.record()
-        if g is not None:
-            g.replay()
+        times = []
+        for _ in range(self.reps):
+            start = torch.cuda.Event(enable_timing=True)
+            end = torch.cuda.Event(enable_timing=True)
+            torch.cuda.synchronize()
+            start.record()
+            if g is not None:
+                g.replay()
+            else:
+                for i in range(steps):
+                    launch(i)
+            end.record()
+            end.synchronize()
+            torch.cuda.synchronize()
+            times.append(start.elapsed_time(end))
+        times.sort()
+        return times[len(times) // 2] / steps, mode
+
+
+def _peaks_lib():
+    import ctypes
+
+    path = os.path.join(ROOT, "neo-theano_amd", "libtq_peaks.so")
+    if not os.path.exists(path):
+        raise RuntimeError(f"{path} is not built; run `python neo-theano_amd/build.py`")
+    L = ctypes.CDLL(path)
+    vp, i64, i32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int
+    L.tqp_hbm_read.argtypes = [vp, i64, vp, i32, vp]
+    L.tqp_hbm_read_chunks.argtypes = [vp, i64, vp, i32, vp]
+    L.tqp_mfma_i8.argtypes = [i32, i32, vp, vp]
+    L.tqp_mfma_bf16.argtypes = [i32, i32, vp, vp]
+    return L
+
+
+def measured_peaks(torch, timer, dev, log):
+    """HBM read rate over a 4 GiB buffer (16x the MALL) and the dense i8 / bf16
+    MFMA rates of register-only loops, one 4-wave block per CU (the layout of
+    the GEMM kernels) and four, on this device."""
+    import ctypes
+
+    L = _peaks_lib()
+    st = lambda: ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    nb = 4 << 30
+    buf = torch.empty(nb, dtype=torch.uint8, device=dev).fill_(1)
+    out = torch.empty(1 << 20, dtype=torch.int32, device=dev)
+    best = None
+    for blocks in (4 * cus, 8 * cus, 16 * cus):
+        ms, _ = timer.run(lambda i, b=blocks: L.tqp_hbm_read(buf.data_ptr(), nb, out.data_ptr(), b, st()), 5, 1)
+        gbs = nb / (ms * 1e-3) / 1e9
+        if best is None or gbs > best[0]:
+            best = (gbs, blocks)
+    del buf
+    res = {"hbm_read_GB/s": round(best[0], 1), "hbm_read_blocks": best[1], "hbm_read_bytes": nb,
+           "hbm_spec_GB/s": HBM_PEAK_GBS}
+    iters = 400
+    for name, fn, per, spec in (("i8_mfma_TOPS", L.tqp_mfma_i8, 65536, I8_PEAK_TOPS),
+                                ("bf16_mfma_TFLOPS", L.tqp_mfma_bf16, 32768, BF16_PEAK_TFLOPS)):
+        vals = {}
+        for bpc in (1, 4):
+            blocks = bpc * cus
+            ms, _ = timer.run(lambda i, b=blocks, f=fn: f(b, iters, out.data_ptr(), st()), 5, 1)
+            vals[bpc] = blocks * 4 * 8 * iters * per / (ms * 1e-3) / 1e12
+        res[name] = round(max(vals.values()), 1)
+        res[name + "_1_block_per_cu"] = round(vals[1], 1)
+        res[name.replace("_T", "_spec_T")] = spec
+    log(f"measured peaks: {res}")
+    return res
+
+
+def read_ceiling(torch, timer, dev, nbytes, args, log):
+    """A plain streaming read of `nbytes` per launch (16-byte nontemporal loads,
+    no arithmetic), over copies rotating past the MALL, timed by the headline's
+    harness: the rate one launch of this size reaches on this device."""
+    import ctypes
+
+    L = _peaks_lib()
+    st = lambda: ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    n16 = nbytes // 16 * 16
+    copies = [torch.empty(n16, dtype=torch.uint8, device=dev).fill_(1) for _ in range(rotation(n16))]
+    out = torch.empty(1 << 16, dtype=torch.int32, device=dev)
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    res = {"bytes": n16, "variants": {}}
+    best = None
+    shapes = [("grid-stride", b) for b in (2 * cus, 4 * cus, 8 * cus, 16 * cus, 32 * cus)]
+    shapes += [("one-pass", u) for u in (4, 8, 16)]
+    for kind, a in shapes:
+        if kind == "grid-stride":
+            fn = lambda i, b=a: L.tqp_hbm_read(copies[i % len(copies)].data_ptr(), n16, out.data_ptr(), b, st())
+            label = f"grid-stride, {a} blocks"
         else:
-            for i in range(steps):
-                launch(i)
-        end.record()
-        end.synchronize()
-        torch.cuda.synchronize()
-        ms = start.elapsed_time(end)
-        return ms / steps, mode
+            fn = lambda i, u=a: L.tqp_hbm_read_chunks(copies[i % len(copies)].data_ptr(), n16, out.data_ptr(), u,
+                                                      st())
+            label = f"one-pass, {(n16 // 16 + 256 * a - 1) // (256 * a)} blocks of {4096 * a} B"
+        ms, mode = timer.run(fn, args.steps, args.warmup)
+        gbs = n16 / (ms * 1e-3) / 1e9
+        res["variants"][label] = {"us": round(ms * 1e3, 3), "GB/s": round(gbs, 1)}
+        log(f"  read {n16} B, {label}: {ms * 1e3:.2f} us  {gbs:.0f} GB/s")
+        if best is None or gbs > best[1]:
+            best = (ms, gbs, label, mode)
+    res.update({"us": round(best[0] * 1e3, 3), "GB/s": round(best[1], 1), "best": best[2], "timing": best[3],
+                "hbm_frac": round(best[1] / HBM_PEAK_GBS, 4)})
+    log(f"read ceiling {n16} B per launch: {best[0] * 1e3:.2f} us  {best[1]:.0f} GB/s ({best[2]})")
+    del copies
+    return res
+
+
+def cpu_baselines(args, secondary, n3, k3, headline_bytes, log):
+    """The reference CPU path restated in C (oracle/, f64, one thread), timed on
+    the host beside the GPU legs.  A quantized Linear in the reference is
+    Linear::from_tensors over the dequantized weight (linear.rs:65-75), so a
+    forward is Linear::forward (linear.rs:111-121): Tensor::mm gathers the
+    transposed weight and runs the i-p-j loop (tensor_ops.rs:379-410); the
+    dequantization happens once at load and is not timed.  Configs 4 and 5 are
+    timed at M=1 and on a row subset and extrapolated as t(M) = t(1) + (M - 1) *
+    (t(M') - t(1)) / (M' - 1) (the gather is paid once per forward, the loop per
+    row).  Each secondary config gets its own `cpu_baseline`; the headline's is
+    returned."""
+    import numpy as np
+
+    import oracle as O  # the CPU restatement of the reference path, timed as the baseline
+    from theano_quantize.synth import f32_to_bf16_bits, normal_f32
+
+    O.lib()
+    ncpu = os.cpu_count()
+
+    def timed(fn, budget):
+        reps, t0 = 0, time.perf_counter()
+        while True:
+            fn()
+            reps += 1
+            el = time.perf_counter() - t0
+            if el >= budget or reps >= 50:
+                return el / reps, reps
+
+    def bf16_f64(bits):
+        return (bits.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+
+    def entry(value, unit, sample):
+        return {"value": value, "unit": unit, "cores": 1, "kind": "port", "sample": sample + f"; 1 thread on {ncpu} host CPUs"}
+
+    # C3, the headline: INT4 g128 weight [14336, 4096] dequantized once, one token
+    w = normal_f32(2, (n3, k3), 0.02)
+    p, s = O.quantize_i4_g128(w)
+    wh = O.dequantize_i4_g128(p, s).astype(np.float64)
+    del w, p, s
+    x = bf16_f64(f32_to_bf16_bits(normal_f32(2, (1, k3), 1.0, stream=1)))
+    per, reps = timed(lambda: O.linear(x, wh), args.cpu_seconds)
+    head = entry(round(headline_bytes / per / 1e9, 4), "GB/s",
+                 f"config 3 at M=1: Linear::forward over the dequantized [14336, 4096] weight, {reps} calls, "
+                 f"{per * 1e3:.0f} ms per call")
+    log(f"cpu baseline C3: {per * 1e3:.1f} ms/call")
+    del wh
+
+    budget = max(1.0, args.cpu_seconds / 6)
+    # C1: per-row INT8 quantize and dequantize of W [4096, 4096]
+    w = normal_f32(0, (4096, 4096), 0.02)
+    tq_, _ = timed(lambda: O.quantize_i8_rowwise(w), budget)
+    q, sc = O.quantize_i8_rowwise(w)
+    td, _ = timed(lambda: O.dequantize_i8_rowwise(q, sc), budget)
+    b1 = 5 * 4096 * 4096 + 4 * 4096
+    if "roundtrip_i8_4096x4096" in secondary:
+        secondary["roundtrip_i8_4096x4096"]["cpu_baseline"] = entry(
+            {"quantize_GB/s": round(b1 / tq_ / 1e9, 4), "dequantize_GB/s": round(b1 / td / 1e9, 4)}, "GB/s",
+            f"config 1 in full: quantize_tensor per row (f64) {tq_ * 1e3:.0f} ms, dequantize_tensor {td * 1e3:.0f} ms")
+    # C2: INT8 weight [4096, 4096] dequantized once, one f32 token
+    wh = O.dequantize_i8_rowwise(q, sc).astype(np.float64)
+    x = normal_f32(1, (1, 4096), 1.0, stream=1).astype(np.float64)
+    t2, _ = timed(lambda: O.linear(x, wh), budget)
+    if "gemv_w8_m1" in secondary:
+        secondary["gemv_w8_m1"]["cpu_baseline"] = entry(
+            round(secondary["gemv_w8_m1"]["bytes"] / t2 / 1e9, 4), "GB/s",
+            f"config 2 in full: Linear::forward over the dequantized weight, {t2 * 1e3:.0f} ms per call")
+    # C4: activations [M, 4096] quantized per row then dequantized, Linear over the dequantized weight
+    xa = normal_f32(3, (32, 4096), 1.0)
+
+    def c4(m):
+        qa, sa = O.quantize_i8_rowwise(xa[:m])
+        O.linear(O.dequantize_i8_rowwise(qa, sa).astype(np.float64), wh)
+
+    t41, _ = timed(lambda: c4(1), 0)
+    t432, _ = timed(lambda: c4(32), 0)
+    t4 = t41 + (2048 - 1) * (t432 - t41) / 31
+    if "w8a8_gemm_m2048" in secondary:
+        secondary["w8a8_gemm_m2048"]["cpu_baseline"] = entry(
+            round(2.0 * 2048 * 4096 * 4096 / t4 / 1e12, 6), "TOPS",
+            f"config 4: per-row quantize + dequantize + Linear::forward at M=1 ({t41 * 1e3:.0f} ms) and "
+            f"M'=32 ({t432 * 1e3:.0f} ms), extrapolated to M=2048: {t4:.1f} s")
+    del wh, w, q, sc
+    # C5: gate / up [14336, 4096] and down [4096, 14336], each dequantized once
+    if "mlp_w4g128_m512" in secondary:
+        d5, f5, m5, mp = 4096, 14336, 512, 8
+        tot = 0.0
+        parts = []
+        for name, shape, count in (("gate/up", (f5, d5), 2), ("down", (d5, f5), 1)):
+            p5, s5 = O.quantize_i4_g128(normal_f32(4, shape, 0.02))
+            wh5 = O.dequantize_i4_g128(p5, s5).astype(np.float64)
+            del p5, s5
+            x5 = normal_f32(4, (mp, shape[1]), 1.0, stream=3).astype(np.float64)
+            ta, _ = timed(lambda: O.linear(x5[:1], wh5), 0)
+            tb, _ = timed(lambda: O.linear(x5, wh5), 0)
+            tm = ta + (m5 - 1) * (tb - ta) / (mp - 1)
+            tot += count * tm
+            parts.append(f"{name} {ta * 1e3:.0f} ms at M=1, {tb * 1e3:.0f} ms at M'={mp}")
+            del wh5
+        secondary["mlp_w4g128_m512"]["cpu_baseline"] = entry(
+            round(m5 / tot, 4), "tokens/s",
+            f"config 5: Linear::forward (" + "; ".join(parts) + f"), extrapolated to M=512 and summed over "
+            f"gate, up and down (SiLU * up not timed): {tot:.1f} s")
+    log("cpu baselines done")
+    return head
 
 
 def rotation(bytes_per_copy):
@@ -134,7 +338,7 @@ def main():
 
     tq._abi.lib()
     dev = torch.device("cuda", 0)
-    timer = Timer(torch, eager=args.eager)
+    timer = Timer(torch, eager=args.eager, reps=max(1, args.reps))
     secondary = {}
 
     def dt(a):
@@ -189,6 +393,34 @@ def main():
                                                   "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
                 log(f"gemv_w4 M={m}: {ms * 1e3:.2f} us/step  {gbs:.0f} GB/s")
         del copies
+
+    # ------------------------------------- roofline denominators, measured
+    peaks = None
+    if not args.no_secondary and (only is None or only == "peaks"):
+        peaks = measured_peaks(torch, timer, dev, log)
+        secondary["measured_peaks"] = peaks
+
+    # ----------------- plain streaming read of the headline's bytes per launch
+    if not args.no_secondary and (only is None or only == "read_ceiling"):
+        secondary["read_ceiling_30mb"] = read_ceiling(torch, timer, dev, w4_bytes_m(1), args, log)
+
+    # ------------------------------------- INT4 g128 quantize + pack (C3 weight)
+    if not args.no_secondary and want("quant_i4"):
+        nq = rotation(4 * n3 * k3)
+        ins = [dt(normal_f32(2, (n3, k3), 0.02, stream=10 + i)) for i in range(nq)]
+        pq = torch.empty((n3, k3 // 2), dtype=torch.uint8, device=dev)
+        sq = torch.empty((n3, k3 // 128), dtype=torch.float16, device=dev)
+
+        def launch_q4(i):
+            _abi.call("tq_quantize_i4_g128", ptr(ins[i % nq]), n3, k3, ptr(pq), ptr(sq), stream())
+
+        ms, mode = timer.run(launch_q4, args.steps // 4, 5)
+        qb = 4 * n3 * k3 + n3 * k3 // 2 + 2 * n3 * (k3 // 128)
+        gbs = qb / (ms * 1e-3) / 1e9
+        secondary["quantize_i4_g128_14336x4096"] = {"us": round(ms * 1e3, 3), "GB/s": round(gbs, 1), "timing": mode,
+                                                    "hbm_frac": round(gbs / HBM_PEAK_GBS, 4), "bytes": qb}
+        log(f"quantize_i4_g128 14336x4096: {ms * 1e3:.2f} us  {gbs:.0f} GB/s")
+        del ins
 
     # ------------------------------------------------------ INT8 GEMV (C2)
     if not args.no_secondary and want("gemv_w8"):
@@ -461,29 +693,10 @@ def main():
     if headline is None:
         return
 
-    # ------------------------------------------------------ CPU baseline
+    # ------------------------------------------------------ CPU baselines
     cpu = None
     if args.cpu_seconds > 0:
-        import oracle as O  # the CPU restatement of the reference path, timed as the baseline
-
-        O.lib()
-        w = normal_f32(2, (n3, k3), 0.02)
-        p, s = O.quantize_i4_g128(w)
-        del w
-        xb = f32_to_bf16_bits(normal_f32(2, (1, k3), 1.0, stream=1))
-        reps, t0 = 0, time.perf_counter()
-        while True:
-            O.linear_w4g128_bf16(xb, p, s)
-            reps += 1
-            el = time.perf_counter() - t0
-            if el >= args.cpu_seconds or reps >= 50:
-                break
-        per = el / reps
-        cpu = {"value": round(w4_bytes_m(1) / per / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
-               "sample": f"config 3 at M=1 (full [14336, 4096] INT4 g128 weight), {reps} calls of the "
-                         f"f64 dequantize + Linear::forward restatement, {per * 1e3:.0f} ms per call, "
-                         f"1 thread on {os.cpu_count()} host CPUs"}
-        log(f"cpu baseline: {per * 1e3:.1f} ms/call")
+        cpu = cpu_baselines(args, secondary, n3, k3, w4_bytes_m(1), log)
 
     traffic = None
     tfile = os.path.join(ROOT, "profiles", "pmc_traffic.json")
@@ -506,10 +719,13 @@ def main():
         "dtype": "int4xbf16",
         "data": "synthetic (numpy PCG64 normals, seeded; weights rotate over copies > 2x MALL)",
         "config": {"workload": "int4_g128_dequant_gemv", "baseline_config": 3, "n": n3, "k": k3, "m": 1,
-                   "group": 128, "weight_layout": "row-tiled", "timing": headline["mode"]},
+                   "group": 128, "weight_layout": "row-tiled",
+                   "timing": f"{headline['mode']}, median of {max(1, args.reps)} timed replays of {args.steps} launches"},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "algorithmic_bytes_per_launch": w4_bytes_m(1)},
+                     "algorithmic_bytes_per_launch": w4_bytes_m(1),
+                     "peak_measured": peaks["hbm_read_GB/s"] if peaks else None,
+                     "frac_of_measured": round(gbs / peaks["hbm_read_GB/s"], 4) if peaks else None},
         "cpu_baseline": cpu,
         "secondary": secondary,
     }

@@ -118,10 +118,19 @@ def build_oracle():
     return out
 
 
+def build_peaks():
+    """Measurement kernels of bench.py (libtq_peaks.so): HBM stream and MFMA peak loops."""
+    src = os.path.join(CSRC, "bench", "tq_peaks.hip")
+    out = os.path.join(PKG, "libtq_peaks.so")
+    _run([HIPCC, *HIP_FLAGS, "-shared", src, "-o", out + ".tmp"])
+    os.replace(out + ".tmp", out)
+    return out
+
+
 def build_all(verbose=False):
     if shutil.which(HIPCC) is None and not os.path.exists(HIPCC):
         raise RuntimeError(f"hipcc not found at {HIPCC}")
-    libs = [build_oracle(), build_lib(verbose=verbose)]
+    libs = [build_oracle(), build_lib(verbose=verbose), build_peaks()]
     h = build_host(verbose=verbose)
     if h:
         libs.append(h)

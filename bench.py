@@ -663,7 +663,7 @@ def main():
         copies = [base.decode] + [tuple(t.clone() if hasattr(t, "clone") else t for t in base.decode)
                                   for _ in range(rotation(wbytes) - 1)]
         res = {}
-        for md in (1, 4):
+        for md in (1, 2, 4, 8):
             x = bf16(normal_f32(4, (md, d5), 1.0, stream=3))
             ws = torch.empty((base.workspace_bytes(md),), dtype=torch.uint8, device=dev)
             y = torch.empty((md, d5), dtype=torch.float32, device=dev)

@@ -364,20 +364,21 @@ __device__ __forceinline__ u32x4 unpack_w4_136(uint32_t w) {
 //              bf16(h - hi) into the down projection's input rows (see MlpRows).
 enum DiagEpi { kEpiPlain = 0, kEpiFold = 1, kEpiGateUp = 2 };
 
-// Rows of the down projection's bf16 input for token J of an m-token FFN: tokens
-// go in pairs, pair c = J / 2 with t = min(2, m - 2c) tokens occupies rows
-// 4c .. 4c + 2t - 1 as (hi of its tokens, lo of its tokens), so each pair is one
-// kEpiFold launch of 2t contiguous rows.
-// With `block` set (one down launch for all m tokens) the rows are instead the m
-// hi rows, then the m lo rows.
+// Rows of the down projection's bf16 input for token J of an m-token FFN.
+// Pairs (`block` unset): pair c = J / 2 with t = min(2, m - 2c) tokens occupies
+// rows 4c .. 4c + 2t - 1 as (hi of its tokens, lo of its tokens), so each pair
+// is one kEpiFold launch of 2t contiguous rows.
+// Quads (`block` set): the same with blocks of up to four tokens, block c = J / 4
+// with t = min(4, m - 4c) tokens at rows 8c .. 8c + 2t - 1; for m <= 4 that is
+// the m hi rows, then the m lo rows.
 struct MlpRows {
     __host__ __device__ static int64_t hi(int64_t j, int64_t m, bool block) {
-        return block ? j : 4 * (j / 2) + (j % 2);
+        return block ? 8 * (j / 4) + (j % 4) : 4 * (j / 2) + (j % 2);
     }
     __host__ __device__ static int64_t lo(int64_t j, int64_t m, bool block) {
-        if (block) return m + j;
-        const int64_t c = j / 2, t = m - 2 * c < 2 ? m - 2 * c : 2;
-        return 4 * c + t + (j % 2);
+        const int64_t q = block ? 4 : 2;
+        const int64_t c = j / q, t = m - q * c < q ? m - q * c : q;
+        return 2 * q * c + t + (j % q);
     }
 };
 
@@ -615,7 +616,7 @@ template <int kR, int kEpi>
 int launch_diag_m(int64_t gpw, int64_t tiles, hipStream_t s, const DiagArgs& a) {
     if (a.m == 1) return launch_diag<kR, 1, kEpi>(gpw, tiles, s, a);
     if (a.m == 2) return launch_diag<kR, 2, kEpi>(gpw, tiles, s, a);
-    if constexpr (kR == 1 && kEpi == kEpiFold)
+    if constexpr (kR <= 2 && kEpi == kEpiFold)
         if (a.m > 4) return launch_diag<kR, 8, kEpi>(gpw, tiles, s, a);  // 3-4 tokens' hi and lo rows
     return launch_diag<kR, 4, kEpi>(gpw, tiles, s, a);
 }
@@ -883,16 +884,18 @@ int mlp_decode(const char* fn, const uint16_t* x_bf16, int64_t m, int64_t d, int
     const int mi = static_cast<int>(m);
     // gate + up with SiLU * up, 4 tokens per launch, into the hi/lo rows of h
     const int kr = down_tile_rows == 16 ? 1 : (down_tile_rows == 32 ? 2 : 4);
-    // 3 or 4 tokens on 16-row down tiles: one down launch for all of them (the
-    // 2m hi/lo rows as 16 MFMA columns), K split over two blocks per tile so that
-    // the x rows fit the LDS; the gate/up launch zeroes y for it
-    const bool block = kr == 1 && (mi == 3 || mi == 4);
+    // Quads: one down launch per four tokens (their 2t hi/lo rows as MFMA
+    // columns), K split over two blocks per tile so that the x rows fit the LDS;
+    // the gate/up launch zeroes y for the two halves.  Taken for 3-4 tokens on
+    // 16-row down tiles and for every M on 32-row tiles, whose 128 tiles x 2 K
+    // halves fill 256 CUs in one round at D = 4096.
+    const bool block = (kr == 1 && (mi == 3 || mi == 4)) || kr == 2;
     const int64_t gu_tiles = (f + 31) / 32, gu_gpw = ((d >> 7) + kWaves - 1) / kWaves;
     for (int j0 = 0; j0 < mi; j0 += 4) {
         const int mm = mi - j0 < 4 ? mi - j0 : 4;
         DiagArgs a{x_bf16 + j0 * d, mm, gate_up_t, gate_up_s_t, nullptr, 2 * f, d, nullptr, h, j0, mi};
         a.rows_block = block;
-        if (block) {
+        if (block && j0 == 0) {
             a.yz = y;
             a.yz_n = m * d;
         }
@@ -901,10 +904,15 @@ int mlp_decode(const char* fn, const uint16_t* x_bf16, int64_t m, int64_t d, int
     }
     const int64_t dn_tiles = (d + down_tile_rows - 1) / down_tile_rows, dn_gpw = ((f >> 7) + kWaves - 1) / kWaves;
     if (block) {
-        DiagArgs a{h, 2 * mi, down_t, down_s_t, nullptr, d, f, y, nullptr, 0, 0};
-        a.ksplit = 2;
         const int64_t gpw2 = (((f >> 7) + 1) / 2 + kWaves - 1) / kWaves;
-        return launch_diag_r<kEpiFold>(kr, gpw2, dn_tiles, st, a);
+        for (int c = 0; 4 * c < mi; ++c) {
+            const int t = mi - 4 * c < 4 ? mi - 4 * c : 4;
+            DiagArgs a{h + 8 * c * f, 2 * t, down_t, down_s_t, nullptr, d, f, y + 4 * c * d, nullptr, 0, 0};
+            a.ksplit = 2;
+            const int rc = launch_diag_r<kEpiFold>(kr, gpw2, dn_tiles, st, a);
+            if (rc != TQ_OK) return rc;
+        }
+        return TQ_OK;
     }
     // down, one launch per token pair: its hi and lo rows in, their sum out
     for (int c = 0; 2 * c < mi; ++c) {

@@ -363,7 +363,8 @@ double e4m3_value(uint8_t code) {
     return e == 0 ? sign * std::ldexp(m, -9) : sign * std::ldexp(8 + m, e - 10);
 }
 
-void make_tiled(Int4Weight& w, hipStream_t stream);
+// Row-tiled copy of w for the decode GEMV; tile_rows 0 picks tq_w4g128_tile_rows(rows).
+void make_tiled(Int4Weight& w, hipStream_t stream, int64_t tile_rows = 0);
 
 Result<Int4Weight> quantize_i4_g128(const Tensor& weight, hipStream_t stream) {
     return capture<Int4Weight>([&]() -> Result<Int4Weight> {
@@ -386,10 +387,10 @@ Result<Int4Weight> quantize_i4_g128(const Tensor& weight, hipStream_t stream) {
     });
 }
 
-void make_tiled(Int4Weight& w, hipStream_t stream) {
+void make_tiled(Int4Weight& w, hipStream_t stream, int64_t tile_rows) {
     if (w.cols > 16384 || w.rows == 0) return;
     // row-tiled copy for the decode GEMV (a permutation of the packed bytes)
-    const int64_t t = tq_w4g128_tile_rows(static_cast<int64_t>(w.rows));
+    const int64_t t = tile_rows > 0 ? tile_rows : tq_w4g128_tile_rows(static_cast<int64_t>(w.rows));
     if (t <= 0) throw TheanoError::runtime("tiled INT4 copy: tile size query failed");
     const size_t padded = (w.rows + t - 1) / t * t;
     w.packed_tiled = DeviceBuffer<uint8_t>(padded * w.cols / 2);
@@ -762,6 +763,9 @@ void QuantizedMLP::make_decode_copies() {
     up_.scales_tiled = DeviceBuffer<uint16_t>();
     up_.tile_rows = 0;
     if (d_ == 0 || f_ == 0 || d_ > 16384 || f_ > 16384 || down_.tile_rows == 0) return;
+    // down in 32-row tiles: two K halves per tile give 2 D / 32 blocks, one
+    // round on 256 CUs at D = 4096
+    if (down_.tile_rows != 32) quantize::make_tiled(down_, stream_, 32);
     const size_t tiles = (f_ + 31) / 32;
     gu_tiled_ = DeviceBuffer<uint8_t>(tiles * 64 * d_ / 2);
     gu_scales_tiled_ = DeviceBuffer<uint16_t>(tiles * 64 * d_ / 128);

@@ -36,6 +36,7 @@ from .qconfig import QConfig, QuantDType
 DECODE_MAX_M = 16
 TILED_MAX_M = 16  # decode shapes run on the row-tiled copy of an INT4 weight
 DECODE_MLP_MAX_M = 8  # QuantizedMLP runs the decode GEMV kernels up to here, the prefill FFN beyond
+MLP_DOWN_TILE_ROWS = 32  # tile height of the FFN's decode copy of down
 
 
 class Module:
@@ -194,9 +195,10 @@ class QuantizedMLP(Module):
         self.decode = None
         if tiled and self.d <= 16384 and self.f <= 16384:
             # row-tiled copies (permutations of the weights) for decode shapes, M <= 8:
-            # gate and up interleaved in 64-row tiles, down on its own tile height
+            # gate and up interleaved in 64-row tiles, down in 32-row tiles (two K
+            # halves per tile: 2 * D / 32 blocks, one round at D = 4096)
             gu = repack_i4_g128_gate_up_tiled(gate, up)
-            dn = repack_i4_g128_tiled(down[0], down[1])
+            dn = repack_i4_g128_tiled(down[0], down[1], MLP_DOWN_TILE_ROWS)
             self.decode = (gu[0], gu[1], dn[0], dn[1], dn[2])
 
     @staticmethod

@@ -386,15 +386,14 @@ def _mlp_case(tq, m, d, f, seed=57):
 
 
 # Decode path (M <= 8): gate and up interleaved in 64-row tiles with SiLU * up in
-# the epilogue (4 tokens per launch), down on h as bf16 hi + lo rows (a token
-# pair per launch, the halves added per token; 3-4 tokens on 16-row down tiles
-# in one launch with K split over two blocks per tile, including F = 128 where
-# the second block has no groups); one to eight groups per wave, odd M (a last
-# pair of one token), F not a multiple of 64, the Llama shape.
+# the epilogue (4 tokens per launch), down on h as bf16 hi + lo rows in 32-row
+# tiles, one launch per four tokens with K split over two blocks per tile
+# (including F = 128 where the second block has no groups, and two launches for
+# M > 4); one to eight groups per wave, F not a multiple of 64, the Llama shape.
 @pytest.mark.parametrize("m,d,f", [(1, 128, 128), (2, 256, 384), (3, 512, 1024), (4, 1024, 640), (5, 256, 512),
                                    (7, 384, 1152), (8, 2048, 256), (1, 4096, 14336), (2, 14336, 4096),
                                    (6, 16384, 128), (3, 4096, 14336), (4, 4096, 14336), (4, 256, 128),
-                                   (3, 640, 16384)])
+                                   (3, 640, 16384), (6, 4096, 14336), (8, 4096, 14336), (2, 4096, 14336)])
 def test_mlp_decode_path(tq, oracle, m, d, f):
     wg = normal(60, (f, d), 0.02)
     wu = normal(60, (f, d), 0.02, stream=1)

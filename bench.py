@@ -440,7 +440,23 @@ def main():
         secondary["gemv_w8_m1"] = {"us": round(ms * 1e3, 3), "GB/s": round(gbs, 1), "timing": mode,
                                    "hbm_frac": round(gbs / HBM_PEAK_GBS, 4), "bytes": b2}
         log(f"gemv_w8 M=1: {ms * 1e3:.2f} us/step  {gbs:.0f} GB/s")
+        for mw in (2, 4):
+            xm = dt(normal_f32(1, (mw, k2), 1.0, stream=1))
+            ym = torch.empty((mw, n2), dtype=torch.float32, device=dev)
+
+            def launch_m(i, mw=mw, xm=xm, ym=ym):
+                q, s = copies[i % len(copies)]
+                _abi.call("tq_gemv_w8", ptr(xm), mw, ptr(q), ptr(s), None, n2, k2, ptr(ym), stream())
+
+            ms, mode = timer.run(launch_m, args.steps, args.warmup)
+            bm = n2 * k2 + 4 * n2 + 4 * mw * k2 + 4 * mw * n2
+            gbs = bm / (ms * 1e-3) / 1e9
+            secondary[f"gemv_w8_m{mw}"] = {"us": round(ms * 1e3, 3), "GB/s": round(gbs, 1), "timing": mode,
+                                           "hbm_frac": round(gbs / HBM_PEAK_GBS, 4), "bytes": bm}
+            log(f"gemv_w8 M={mw}: {ms * 1e3:.2f} us/step  {gbs:.0f} GB/s")
         del copies
+        if only is None or only == "gemv_w8":
+            secondary["gemv_w8_m1"]["read_ceiling"] = read_ceiling(torch, timer, dev, b2, args, log)
 
     # ------------------------- decode W8A8: fused activation quantization
     if not args.no_secondary and want("w8a8_decode"):

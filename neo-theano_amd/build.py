@@ -47,13 +47,35 @@ def _run(cmd):
     return out
 
 
+def scratch_kernels(remarks):
+    """Kernels whose resource-usage remarks report per-lane scratch (register
+    spills or stack): [(kernel, bytes)]."""
+    bad, cur = [], None
+    for line in remarks.splitlines():
+        if "Function Name:" in line:
+            cur = line.split("Function Name:")[1].split()[0]
+        elif "ScratchSize [bytes/lane]:" in line and cur:
+            nbytes = int(line.split("ScratchSize [bytes/lane]:")[1].split()[0])
+            if nbytes:
+                bad.append((cur, nbytes))
+    return bad
+
+
 def build_lib(verbose=False, jobs=8):
     os.makedirs(OBJ, exist_ok=True)
     srcs = [s for s in SOURCES if os.path.exists(os.path.join(CSRC, s))]
 
     def compile_one(src):
         obj = os.path.join(OBJ, src.replace(".hip", ".o"))
-        out = _run([HIPCC, *HIP_FLAGS, "-c", os.path.join(CSRC, src), "-o", obj])
+        out = _run([HIPCC, *HIP_FLAGS, "-Rpass-analysis=kernel-resource-usage", "-c", os.path.join(CSRC, src),
+                    "-o", obj])
+        # every kernel keeps its working set in registers: a spill to scratch
+        # memory fails the build
+        bad = scratch_kernels(out)
+        if bad:
+            raise RuntimeError(f"{src}: kernels spill to scratch: " +
+                               ", ".join(f"{k} ({b} B/lane)" for k, b in bad))
+        out = "\n".join(l for l in out.splitlines() if "kernel-resource-usage" not in l)
         if verbose and out.strip():
             print(out)
         return obj

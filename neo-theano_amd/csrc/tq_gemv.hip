@@ -352,54 +352,51 @@ void grid_for_rows(int64_t n, int64_t* blocks, int64_t* rows_per_wave) {
     *blocks = (waves + kWavesW8 - 1) / kWavesW8;
 }
 
+// Rows in flight per wave: two, unless the x slices held in registers (16 values
+// per token and chunk) would leave no room for two double-buffered groups of
+// weight rows (the compiler then spills): one at kM * kChunks > 4.
+constexpr int rows_in_flight(int x_regs) { return x_regs <= 64 ? 2 : 1; }
+
+// Token counts and K chunks a pass runs together: 4 tokens up to K = 2048, 2 up
+// to 4096, 1 beyond (the dispatch below never asks for more).
+constexpr bool pass_shape(int m, int chunks) { return m * chunks <= 8 && (m <= 2 || chunks <= 2); }
+
 template <class Code, int kM, int kChunks>
 void launch_w8(const float* x, int64_t xs, const typename Code::code_t* q, const float* s, const float* b,
                int64_t n, int64_t k, float* y, int64_t ys, hipStream_t st) {
-    constexpr int kRows = 2;
+    constexpr int kRows = rows_in_flight(kM * kChunks * 16);
     int64_t blocks, rpw;
     grid_for_rows<kRows>(n, &blocks, &rpw);
     k_gemv_w8<Code, kM, kChunks, kRows><<<static_cast<unsigned>(blocks), kBlockW8, 0, st>>>(x, xs, q, s, b, n, k,
                                                                                           y, ys, rpw);
 }
 
-template <class Code, int kM>
+template <class Code, int kM, int kChunks = 1>
 void dispatch_w8(int chunks, const float* x, int64_t xs, const typename Code::code_t* q, const float* s,
                  const float* b, int64_t n, int64_t k, float* y, int64_t ys, hipStream_t st) {
-    switch (chunks) {
-    case 1: launch_w8<Code, kM, 1>(x, xs, q, s, b, n, k, y, ys, st); break;
-    case 2: launch_w8<Code, kM, 2>(x, xs, q, s, b, n, k, y, ys, st); break;
-    case 3: launch_w8<Code, kM, 3>(x, xs, q, s, b, n, k, y, ys, st); break;
-    case 4: launch_w8<Code, kM, 4>(x, xs, q, s, b, n, k, y, ys, st); break;
-    case 5: launch_w8<Code, kM, 5>(x, xs, q, s, b, n, k, y, ys, st); break;
-    case 6: launch_w8<Code, kM, 6>(x, xs, q, s, b, n, k, y, ys, st); break;
-    case 7: launch_w8<Code, kM, 7>(x, xs, q, s, b, n, k, y, ys, st); break;
-    default: launch_w8<Code, kM, 8>(x, xs, q, s, b, n, k, y, ys, st); break;
+    if constexpr (kChunks < 8 && pass_shape(kM, kChunks + 1)) {
+        if (chunks > kChunks) return dispatch_w8<Code, kM, kChunks + 1>(chunks, x, xs, q, s, b, n, k, y, ys, st);
     }
+    launch_w8<Code, kM, kChunks>(x, xs, q, s, b, n, k, y, ys, st);
 }
 
 template <class Fmt, int kM, int kChunks>
 void launch_a8(const float* x, int64_t xs, const typename Fmt::code_t* q, const float* s, const float* b, int64_t n,
                int64_t k, float* y, int64_t ys, hipStream_t st) {
-    constexpr int kRows = 2;
+    constexpr int kRows = rows_in_flight(kM * kChunks * 4 * A8<Fmt>::kRegsPer4);
     int64_t blocks, rpw;
     grid_for_rows<kRows>(n, &blocks, &rpw);
     k_gemv_a8<Fmt, kM, kChunks, kRows><<<static_cast<unsigned>(blocks), kBlockW8, 0, st>>>(x, xs, q, s, b, n, k, y,
                                                                                          ys, rpw);
 }
 
-template <class Fmt, int kM>
+template <class Fmt, int kM, int kChunks = 1>
 void dispatch_a8(int chunks, const float* x, int64_t xs, const typename Fmt::code_t* q, const float* s,
                  const float* b, int64_t n, int64_t k, float* y, int64_t ys, hipStream_t st) {
-    switch (chunks) {
-    case 1: launch_a8<Fmt, kM, 1>(x, xs, q, s, b, n, k, y, ys, st); break;
-    case 2: launch_a8<Fmt, kM, 2>(x, xs, q, s, b, n, k, y, ys, st); break;
-    case 3: launch_a8<Fmt, kM, 3>(x, xs, q, s, b, n, k, y, ys, st); break;
-    case 4: launch_a8<Fmt, kM, 4>(x, xs, q, s, b, n, k, y, ys, st); break;
-    case 5: launch_a8<Fmt, kM, 5>(x, xs, q, s, b, n, k, y, ys, st); break;
-    case 6: launch_a8<Fmt, kM, 6>(x, xs, q, s, b, n, k, y, ys, st); break;
-    case 7: launch_a8<Fmt, kM, 7>(x, xs, q, s, b, n, k, y, ys, st); break;
-    default: launch_a8<Fmt, kM, 8>(x, xs, q, s, b, n, k, y, ys, st); break;
+    if constexpr (kChunks < 8 && pass_shape(kM, kChunks + 1)) {
+        if (chunks > kChunks) return dispatch_a8<Fmt, kM, kChunks + 1>(chunks, x, xs, q, s, b, n, k, y, ys, st);
     }
+    launch_a8<Fmt, kM, kChunks>(x, xs, q, s, b, n, k, y, ys, st);
 }
 
 // Activations quantized in place: K % 16 == 0, K <= 8192, x and q 16-byte

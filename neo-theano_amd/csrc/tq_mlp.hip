@@ -77,7 +77,7 @@ __device__ __forceinline__ float row16_sum(float v) {
 // Gate/up mode: rows 0..63 of the tile are gate rows f0..f0+63, rows 64..127
 // the up rows of the same f; the epilogue writes h = SiLU(gate) * up.
 template <int kAct, bool kGateUp, int kBM>
-__global__ __launch_bounds__(kBlock, 2) void k_gemm_w4(const void* __restrict__ act,
+__global__ __launch_bounds__(kBlock, kBM == 128 ? 1 : 2) void k_gemm_w4(const void* __restrict__ act,
                                                        const uint8_t* __restrict__ p0,
                                                        const uint16_t* __restrict__ s0,
                                                        const uint8_t* __restrict__ p1,

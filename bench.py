@@ -721,6 +721,7 @@ def main():
             traffic = json.load(f).get("gemv_w4g128_m1", {}).get("hbm_bytes_per_launch")
 
     gbs = headline["gbs"]
+    rc30 = secondary.get("read_ceiling_30mb")
     out = {
         "metric": METRIC,
         "value": round(gbs, 1),
@@ -741,7 +742,9 @@ def main():
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "algorithmic_bytes_per_launch": w4_bytes_m(1),
                      "peak_measured": peaks["hbm_read_GB/s"] if peaks else None,
-                     "frac_of_measured": round(gbs / peaks["hbm_read_GB/s"], 4) if peaks else None},
+                     "frac_of_measured": round(gbs / peaks["hbm_read_GB/s"], 4) if peaks else None,
+                     "read_ceiling_GB/s": rc30["GB/s"] if rc30 else None,
+                     "frac_of_read_ceiling": round(gbs / rc30["GB/s"], 4) if rc30 else None},
         "cpu_baseline": cpu,
         "secondary": secondary,
     }

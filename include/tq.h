@@ -318,8 +318,9 @@ int tq_mlp_w4g128(const uint16_t* x_bf16, int64_t m, int64_t d, int64_t f,
  *                 gate rows 32t..32t+31 then up rows 32t..32t+31, padded to F
  *                 rounded up to 32 with zeros ((F+31)/32 * 64 * D/2 bytes and
  *                 (F+31)/32 * 64 * D/128 scales);
- *   down:         tq_repack_w4g128_tiled with tile_rows 16, 32 or 64
- *                 (tq_w4g128_tile_rows(D) by default).
+ *   down:         tq_repack_w4g128_tiled with tile_rows 16, 32 or 64; 32 (the
+ *                 host layers' choice) runs one launch per four tokens with
+ *                 K split over two blocks per tile, 2 * D / 32 blocks.
  * h = SiLU(x Wg^T) * (x Wu^T) is formed in f32 per token and handed to the down
  * projection as bf16 hi + lo (lo = bf16(h - hi)).  D, F multiples of 128 and at
  * most 16384.  `workspace`: tq_mlp_w4g128_decode_workspace_bytes(M, D, F)

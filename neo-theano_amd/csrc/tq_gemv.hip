@@ -47,39 +47,52 @@ struct CodeFp8 {
 // Chunk c covers k in [1024c, 1024c + 1024): lane l owns the 16 codes at
 // k = 1024c + 16l.  y = s[row] * sum(value(q) * x) + b.
 //
-// One 512-thread block per CU (persistent), 8 waves, each owning a contiguous
-// run of rows.  A wave first issues the weight loads of its first kRows rows
+// One 512-thread block per CU (persistent), 8 waves.  With kKS = 1 every wave
+// owns a contiguous run of rows and all of K; with kKS = 2 the waves pair up:
+// both waves of a pair own the same run of rows, the first takes chunks
+// 0 .. kC0 - 1 and the second the rest, so each holds half of x in registers
+// (that is what lets 3-4 tokens at K = 4096, or 2 at K = 8192, run in one
+// pass).  A wave first issues the weight loads of its first kRows rows
 // (unconditional: rows past its run re-read its last row and are not
 // stored), then the block stages x in LDS once (f32, K-contiguous per token)
 // and every lane copies its 16-value slices into registers; rows are then
 // consumed kRows at a time with the next group's loads issued before the
 // current group's arithmetic.  x crosses L2 once per block instead of once per
-// wave.
+// wave.  A pair's two partial sums of a row meet in LDS after the row loop
+// and are added in a fixed order (first half + second half).
 constexpr int kBlockW8 = 512;
 constexpr int kWavesW8 = kBlockW8 / kWave;
+constexpr int kMaxPairRows = 64;  // rows per wave pair that the LDS partial sums hold
 
-template <class Code, int kM, int kChunks, int kRows>
+template <class Code, int kM, int kChunks, int kRows, int kKS>
 __global__ __launch_bounds__(kBlockW8) void k_gemv_w8(const float* __restrict__ x, int64_t x_stride,
                                                       const typename Code::code_t* __restrict__ q,
                                                       const float* __restrict__ s,
                                                       const float* __restrict__ bias, int64_t n,
                                                       int64_t k, float* __restrict__ y,
                                                       int64_t y_stride, int64_t rows_per_wave) {
+    static_assert(kKS == 1 || kKS == 2, "K split over one or two waves");
+    constexpr int kC0 = (kChunks + kKS - 1) / kKS;  // chunks of the first (or only) wave of a pair
     __shared__ f32x4 xs[kM][kChunks * 256];
+    __shared__ float part[kKS == 2 ? kWavesW8 : 1][kKS == 2 ? kMaxPairRows : 1][kM];
     const int lane = threadIdx.x & (kWave - 1);
-    const int64_t wave = uniform(static_cast<int64_t>(blockIdx.x) * kWavesW8 + (threadIdx.x >> 6));
+    const int wv = threadIdx.x >> 6;
+    const int half = kKS == 2 ? (wv & 1) : 0;
+    // chunks [cb, cb + nc) of every row; the second wave of a pair may have fewer
+    const int cb = half * kC0, nc = half == 0 ? kC0 : kChunks - kC0;
+    const int64_t wave = uniform(static_cast<int64_t>(blockIdx.x) * (kWavesW8 / kKS) + wv / kKS);
     const int64_t row_begin = wave * rows_per_wave;
     const int64_t row_end = min(n, row_begin + rows_per_wave);
     const int64_t row_last = max(row_begin, row_end - 1);  // clamp target (valid when the run is empty too)
     const int64_t row_clamp = min(row_last, n - 1);
 
-    auto load_rows = [&](int64_t row0, i32x4 (&wq)[kRows][kChunks]) {
+    auto load_rows = [&](int64_t row0, i32x4 (&wq)[kRows][kC0]) {
 #pragma unroll
         for (int r = 0; r < kRows; ++r)
 #pragma unroll
-            for (int c = 0; c < kChunks; ++c) {
+            for (int c = 0; c < kC0; ++c) {
                 const int64_t row = min(row0 + r, row_clamp);
-                const int64_t kb = min<int64_t>(1024 * c + 16 * lane, k - 16);
+                const int64_t kb = min<int64_t>(1024 * (cb + min(c, nc - 1)) + 16 * lane, k - 16);
                 wq[r][c] = __builtin_nontemporal_load(reinterpret_cast<const i32x4*>(q + row * k + kb));
             }
     };
@@ -96,7 +109,7 @@ __global__ __launch_bounds__(kBlockW8) void k_gemv_w8(const float* __restrict__ 
         xv[qi] = i < kXItems && j < k4 ? *reinterpret_cast<const f32x4*>(x + m * x_stride + 4 * j)
                                        : f32x4{0.f, 0.f, 0.f, 0.f};
     }
-    i32x4 wq[kRows][kChunks];
+    i32x4 wq[kRows][kC0];
     load_rows(row_begin, wq);
 #pragma unroll
     for (int qi = 0; qi < kXPer; ++qi) {
@@ -105,27 +118,27 @@ __global__ __launch_bounds__(kBlockW8) void k_gemv_w8(const float* __restrict__ 
         if (i < kXItems) xs[m][j] = xv[qi];
     }
     __syncthreads();
-    float xr[kM][kChunks][16];
+    float xr[kM][kC0][16];
 #pragma unroll
     for (int m = 0; m < kM; ++m)
 #pragma unroll
-        for (int c = 0; c < kChunks; ++c)
+        for (int c = 0; c < kC0; ++c)
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                const f32x4 v = xs[m][c * 256 + 4 * lane + j];
+                // the second wave's chunks past nc read zeros' stand-in (never used)
+                const f32x4 v = xs[m][min(cb + c, kChunks - 1) * 256 + 4 * lane + j];
                 xr[m][c][4 * j + 0] = v.x;
                 xr[m][c][4 * j + 1] = v.y;
                 xr[m][c][4 * j + 2] = v.z;
                 xr[m][c][4 * j + 3] = v.w;
             }
-    if (row_begin >= row_end) return;
 
     for (int64_t row0 = row_begin; row0 < row_end; row0 += kRows) {
-        i32x4 cur[kRows][kChunks];
+        i32x4 cur[kRows][kC0];
 #pragma unroll
         for (int r = 0; r < kRows; ++r)
 #pragma unroll
-            for (int c = 0; c < kChunks; ++c) cur[r][c] = wq[r][c];
+            for (int c = 0; c < kC0; ++c) cur[r][c] = wq[r][c];
         if (row0 + kRows < row_end) load_rows(row0 + kRows, wq);
 #pragma unroll
         for (int r = 0; r < kRows; ++r) {
@@ -133,24 +146,45 @@ __global__ __launch_bounds__(kBlockW8) void k_gemv_w8(const float* __restrict__ 
 #pragma unroll
             for (int m = 0; m < kM; ++m) acc[m] = 0.0f;
 #pragma unroll
-            for (int c = 0; c < kChunks; ++c) {
+            for (int c = 0; c < kC0; ++c) {
+                if (c >= nc) break;  // uniform: the second wave of a pair with fewer chunks
                 const int words[4] = {cur[r][c].x, cur[r][c].y, cur[r][c].z, cur[r][c].w};
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
-                    float wv[4];
-                    Code::decode4(words[j], wv);
+                    float wv4[4];
+                    Code::decode4(words[j], wv4);
 #pragma unroll
                     for (int b = 0; b < 4; ++b)
 #pragma unroll
-                        for (int m = 0; m < kM; ++m) acc[m] = fmaf(wv[b], xr[m][c][4 * j + b], acc[m]);
+                        for (int m = 0; m < kM; ++m) acc[m] = fmaf(wv4[b], xr[m][c][4 * j + b], acc[m]);
                 }
             }
             const int64_t row = row0 + r;
-            const float sc = s[min(row, row_clamp)];
+            if constexpr (kKS == 1) {
+                const float sc = s[min(row, row_clamp)];
 #pragma unroll
-            for (int m = 0; m < kM; ++m) {
-                const float v = wave_sum(acc[m]);
-                if (lane == 0 && row < row_end) y[m * y_stride + row] = sc * v + (bias ? bias[row] : 0.0f);
+                for (int m = 0; m < kM; ++m) {
+                    const float v = wave_sum(acc[m]);
+                    if (lane == 0 && row < row_end) y[m * y_stride + row] = sc * v + (bias ? bias[row] : 0.0f);
+                }
+            } else {
+#pragma unroll
+                for (int m = 0; m < kM; ++m) {
+                    const float v = wave_sum(acc[m]);
+                    if (lane == 0 && row < row_end) part[wv][row - row_begin][m] = v;
+                }
+            }
+        }
+    }
+    if constexpr (kKS == 2) {
+        __syncthreads();
+        // the first wave of each pair adds the two halves of its rows
+        if (half == 0) {
+            for (int i = lane; i < (row_end - row_begin) * kM; i += kWave) {
+                const int ri = i / kM, m = i - ri * kM;
+                const int64_t row = row_begin + ri;
+                const float v = part[wv][ri][m] + part[wv + 1][ri][m];
+                y[m * y_stride + row] = s[row] * v + (bias ? bias[row] : 0.0f);
             }
         }
     }
@@ -339,17 +373,20 @@ __global__ __launch_bounds__(kBlockW8) void k_gemv_a8(const float* __restrict__ 
 }
 
 // Persistent grid: one block per CU (fewer if there are few rows), contiguous
-// row runs per wave, a multiple of kRows each.
+// row runs per wave (or wave pair: `runs_per_block` runs per block), a
+// multiple of kRows each.
 template <int kRows>
-void grid_for_rows(int64_t n, int64_t* blocks, int64_t* rows_per_wave) {
-    const int64_t slots = static_cast<int64_t>(device_cu_count()) * kWavesW8;
+void grid_for_rows(int64_t n, int64_t* blocks, int64_t* rows_per_wave, int runs_per_block = kWavesW8,
+                   int64_t max_rows = INT64_MAX) {
+    const int64_t slots = static_cast<int64_t>(device_cu_count()) * runs_per_block;
     int64_t waves = (n + kRows - 1) / kRows;
     if (waves > slots) waves = slots;
+    if ((n + waves - 1) / waves > max_rows) waves = (n + max_rows - 1) / max_rows;  // more blocks than CUs
     int64_t rpw = (n + waves - 1) / waves;
     rpw = (rpw + kRows - 1) / kRows * kRows;
     *rows_per_wave = rpw;
     waves = (n + rpw - 1) / rpw;
-    *blocks = (waves + kWavesW8 - 1) / kWavesW8;
+    *blocks = (waves + runs_per_block - 1) / runs_per_block;
 }
 
 // Rows in flight per wave: two, unless the x slices held in registers (16 values
@@ -357,24 +394,35 @@ void grid_for_rows(int64_t n, int64_t* blocks, int64_t* rows_per_wave) {
 // weight rows (the compiler then spills): one at kM * kChunks > 4.
 constexpr int rows_in_flight(int x_regs) { return x_regs <= 64 ? 2 : 1; }
 
-// Token counts and K chunks a pass runs together: 4 tokens up to K = 2048, 2 up
-// to 4096, 1 beyond (the dispatch below never asks for more).
+// Token counts and K chunks a pass runs together (the dispatch below never asks
+// for more).  Weight-only GEMV (x split over a wave pair beyond one token): 4
+// tokens up to K = 4096, 2 up to 8192.  Fused-activation GEMV (no split): 4
+// tokens up to K = 2048, 2 up to 4096, 1 beyond.
+constexpr bool pass_shape_w8(int m, int chunks) { return m <= 4 && (chunks <= 4 || m <= 2); }
 constexpr bool pass_shape(int m, int chunks) { return m * chunks <= 8 && (m <= 2 || chunks <= 2); }
+
+// K split over a wave pair once x would take more than 128 registers per lane
+// (3-4 tokens at K = 4096, 2 at K = 8192): one pass instead of two.  Measured
+// at 2 tokens and K = 4096, where the split is not needed, it is slower (6.7
+// against 6.0 us), so smaller shapes keep every wave on all of K.
+constexpr int ks_for(int m, int chunks) { return (m >= 2 && m * chunks > 8) ? 2 : 1; }
 
 template <class Code, int kM, int kChunks>
 void launch_w8(const float* x, int64_t xs, const typename Code::code_t* q, const float* s, const float* b,
                int64_t n, int64_t k, float* y, int64_t ys, hipStream_t st) {
-    constexpr int kRows = rows_in_flight(kM * kChunks * 16);
+    constexpr int kKS = ks_for(kM, kChunks);
+    constexpr int kRows = rows_in_flight(kM * ((kChunks + kKS - 1) / kKS) * 16);
     int64_t blocks, rpw;
-    grid_for_rows<kRows>(n, &blocks, &rpw);
-    k_gemv_w8<Code, kM, kChunks, kRows><<<static_cast<unsigned>(blocks), kBlockW8, 0, st>>>(x, xs, q, s, b, n, k,
-                                                                                          y, ys, rpw);
+    static_assert(kMaxPairRows % kRows == 0, "row runs are whole row groups");
+    grid_for_rows<kRows>(n, &blocks, &rpw, kWavesW8 / kKS, kKS == 2 ? kMaxPairRows : INT64_MAX);
+    k_gemv_w8<Code, kM, kChunks, kRows, kKS><<<static_cast<unsigned>(blocks), kBlockW8, 0, st>>>(x, xs, q, s, b, n,
+                                                                                               k, y, ys, rpw);
 }
 
 template <class Code, int kM, int kChunks = 1>
 void dispatch_w8(int chunks, const float* x, int64_t xs, const typename Code::code_t* q, const float* s,
                  const float* b, int64_t n, int64_t k, float* y, int64_t ys, hipStream_t st) {
-    if constexpr (kChunks < 8 && pass_shape(kM, kChunks + 1)) {
+    if constexpr (kChunks < 8 && pass_shape_w8(kM, kChunks + 1)) {
         if (chunks > kChunks) return dispatch_w8<Code, kM, kChunks + 1>(chunks, x, xs, q, s, b, n, k, y, ys, st);
     }
     launch_w8<Code, kM, kChunks>(x, xs, q, s, b, n, k, y, ys, st);
@@ -444,7 +492,7 @@ int gemv_8bit(const float* x, int64_t m, const typename Code::code_t* q, const f
     if (k == 0 || k % 16 != 0 || k > 8 * 1024 || !aligned(x, 16) || !aligned(q, 16))
         return launch_linear_8bit_generic(x, m, q, s, bias, n, k, y, st);
     const int chunks = static_cast<int>((k + 1023) / 1024);
-    const int64_t per_pass = chunks <= 2 ? 4 : (chunks <= 4 ? 2 : 1);
+    const int64_t per_pass = chunks <= 4 ? 4 : 2;
     for (int64_t m0 = 0; m0 < m; m0 += per_pass) {
         const int64_t mm = (m - m0) < per_pass ? (m - m0) : per_pass;
         const float* xp = x + m0 * k;

@@ -78,9 +78,12 @@ def test_gemv_w8_config2(tq, c2, m):
     assert_close(host(y), ref[:m], RTOL, ATOL, f"gemv_w8 M={m}")
 
 
-# K % 16 != 0 and K > 8192 take the shape-general kernel (e.g. the reference's Linear(3, 2))
+# K % 16 != 0 and K > 8192 take the shape-general kernel (e.g. the reference's Linear(3, 2));
+# 2-4 tokens with K split over a wave pair: a second half with fewer chunks (K = 3088,
+# 3072), rows per pair past the LDS partials (N = 70000: more blocks than CUs)
 @pytest.mark.parametrize("n,k,m", [(1000, 1024, 1), (17, 16, 2), (333, 3088, 3), (64, 8192, 4), (5, 2000, 16),
-                                   (2, 3, 4), (50, 100, 3), (64, 9000, 2)])
+                                   (2, 3, 4), (50, 100, 3), (64, 9000, 2), (70000, 2048, 3), (4100, 3072, 4),
+                                   (515, 8192, 2)])
 def test_gemv_w8_shapes_bias(tq, oracle, n, k, m):
     w = normal(50, (n, k), 0.02)
     x = normal(50, (m, k), 1.0, stream=1)

@@ -339,16 +339,16 @@ int tq_mlp_w4g128_decode(const uint16_t* x_bf16, int64_t m, int64_t d, int64_t f
 /* The decode FFN above with no workspace argument and no allocation, for
  * callers that cannot allocate device memory (code under HIP graph capture,
  * serving loops, harnesses that forbid hipMalloc).  It has no counterpart in
- * the reference.  h lives in a scratch array inside libtq.so, one per device,
- * of TQ_MLP_DECODE_SCRATCH_BYTES (16 tokens at F = 16384), held until the
- * process ends; shapes needing more (tq_mlp_w4g128_decode_workspace_bytes) are
- * rejected with TQ_EINVAL.  The result equals tq_mlp_w4g128_decode's bit for
+ * the reference.  h (and its block sums) lives in a scratch array inside
+ * libtq.so, one per device, of TQ_MLP_DECODE_SCRATCH_BYTES (16 tokens at
+ * F = 16384), held until the process ends; shapes needing more
+ * (tq_mlp_w4g128_decode_workspace_bytes) are rejected with TQ_EINVAL.  The result equals tq_mlp_w4g128_decode's bit for
  * bit.  Every call on one device shares that device's scratch, so calls that
  * overlap in time on one device (distinct streams, or distinct threads without
  * ordering) race and give undefined results; calls ordered on one stream are
  * safe.  The first call on a device resolves the scratch address once
  * (thread-safe); nothing is allocated. */
-#define TQ_MLP_DECODE_SCRATCH_BYTES (1 << 20)
+#define TQ_MLP_DECODE_SCRATCH_BYTES ((1 << 20) + (1 << 16))
 int tq_mlp_w4g128_decode_noalloc(const uint16_t* x_bf16, int64_t m, int64_t d, int64_t f,
                                  const uint8_t* gate_up_t, const uint16_t* gate_up_s_t,
                                  const uint8_t* down_t, const uint16_t* down_s_t,

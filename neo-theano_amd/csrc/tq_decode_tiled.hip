@@ -126,10 +126,8 @@ __global__ __launch_bounds__(kBlock) void k_decode_tiled(const uint16_t* __restr
         const int itc = min(it, kM * kCPW * 8 - 1);
         const int j = itc / (kCPW * 8), r = itc - j * (kCPW * 8);
         const uint2 v = xv[q];
-        float sm = bf16_lo(v.x) + bf16_hi(v.x) + bf16_lo(v.y) + bf16_hi(v.y);
-        sm += __shfl_xor(sm, 1, kWave);
-        sm += __shfl_xor(sm, 2, kWave);
-        sm += __shfl_xor(sm, 4, kWave);
+        // a chunk's 8 items sit in 8 aligned lanes
+        const float sm = lane_group_sum<8>(bf16_lo(v.x) + bf16_hi(v.x) + bf16_lo(v.y) + bf16_hi(v.y));
         if (it < kM * kCPW * 8) {
             *reinterpret_cast<uint2*>(sx + j * kCPW * 16 + 2 * r) =
                 make_uint2((v.x & 0xFFFFu) | (v.y << 16), (v.x >> 16) | (v.y & 0xFFFF0000u));
@@ -349,7 +347,10 @@ __device__ __forceinline__ u32x4 unpack_w4_136(uint32_t w) {
 //
 // Each wave stages its K slice of every token's x in a private LDS strip (slot
 // order as above; a zero strip of the same size serves the other B lanes) and
-// keeps 136 X_g per (token, group) in registers.  Loads are issued x first,
+// keeps 136 X_g per (token, group) in registers.  The caller's x is put in slot
+// order and summed on the way (DPP, no LDS round trips); the down projection's x
+// (kEpiFold) is h as kEpiGateUp wrote it, already in slot order with the sums
+// of its 32-column blocks beside it, and is copied as it is.  Loads are issued x first,
 // then scales, then kWin steps of weights ahead of the arithmetic (in-order
 // vmcnt), and every wave runs all its groups (groups past K read clamped
 // addresses with a zero scale) so the refills are not moved behind a branch.
@@ -361,7 +362,9 @@ __device__ __forceinline__ u32x4 unpack_w4_136(uint32_t w) {
 //  kEpiGateUp: the 64-row tile holds gate rows 32 tile .. + 31 (rows 0-31) and
 //              the up rows of the same indices (rows 32-63) of a Llama FFN;
 //              h = g / (1 + exp(-g)) * u goes out as bf16 hi = bf16(h) and lo =
-//              bf16(h - hi) into the down projection's input rows (see MlpRows).
+//              bf16(h - hi) into the down projection's input rows (see MlpRows),
+//              in slot order (h_slot), and the f32 sums of the tile's 32 hi and
+//              32 lo values to xsum[row][tile].
 enum DiagEpi { kEpiPlain = 0, kEpiFold = 1, kEpiGateUp = 2 };
 
 // Rows of the down projection's bf16 input for token J of an m-token FFN.
@@ -371,6 +374,15 @@ enum DiagEpi { kEpiPlain = 0, kEpiFold = 1, kEpiGateUp = 2 };
 // Quads (`block` set): the same with blocks of up to four tokens, block c = J / 4
 // with t = min(4, m - 4c) tokens at rows 8c .. 8c + 2t - 1; for m <= 4 that is
 // the m hi rows, then the m lo rows.
+// Position of h column c in its row: 8-blocks in slot order, columns 8b + e at
+// 8b + 2e (e < 4) and 8b + 2(e - 4) + 1 (e >= 4).
+__host__ __device__ inline int64_t h_slot(int64_t c) { return (c & ~int64_t{7}) | ((c & 3) << 1) | ((c >> 2) & 1); }
+
+// Decode FFN workspace: the 2m bf16 rows of h (hi and lo of each token), then
+// the f32 sums of their 32-column blocks, [2m][F / 32].
+constexpr int64_t round_up256(int64_t b) { return (b + 255) / 256 * 256; }
+constexpr int64_t mlp_h_bytes(int64_t m, int64_t f) { return round_up256(2 * m * f * 2); }
+
 struct MlpRows {
     __host__ __device__ static int64_t hi(int64_t j, int64_t m, bool block) {
         return block ? 8 * (j / 4) + (j % 4) : 4 * (j / 2) + (j % 2);
@@ -388,7 +400,7 @@ __global__ __launch_bounds__(kBlock) void k_decode_diag(const uint16_t* __restri
                                                         const uint16_t* __restrict__ st,
                                                         const float* __restrict__ bias, int64_t n, int64_t k,
                                                         float* __restrict__ y, uint16_t* __restrict__ hout,
-                                                        int tok0, int mtot, int rows_block,
+                                                        float* __restrict__ xsum, int tok0, int mtot, int rows_block,
                                                         float* __restrict__ yz, int64_t yz_n) {
     static_assert(kM * kR <= 16, "columns are (token, row group) pairs");
     static_assert(kEpi != kEpiGateUp || kR == 4, "gate/up tiles are 64 rows");
@@ -397,7 +409,8 @@ __global__ __launch_bounds__(kBlock) void k_decode_diag(const uint16_t* __restri
     constexpr int kCPW = 4 * kGPW;              // chunks per wave
     constexpr int kSteps = kCPW / kS;           // weight loads per lane
     constexpr int kStrip = kCPW * 64;           // bytes of one token's slice (bf16)
-    constexpr int kItems = kM * kCPW * 8;       // 4-element items of the slices
+    constexpr bool kPre = kEpi == kEpiFold;     // x in slot order with its block sums
+    constexpr int kItems = kM * kCPW * (kPre ? 4 : 8);  // 8- (kPre) or 4-element items
     constexpr int kIPL = (kItems + kWave - 1) / kWave;
     constexpr int kW = kWinD < kSteps ? kWinD : kSteps;
     __shared__ __attribute__((aligned(16))) uint8_t xs[kWaves][kM][kStrip];
@@ -416,14 +429,34 @@ __global__ __launch_bounds__(kBlock) void k_decode_diag(const uint16_t* __restri
     const int row0 = 16 * (col % kR) + 4 * kg;  // first of its four output rows
 
     // x items: item it -> token it / (8 kCPW), elements 4 (it % (8 kCPW)) .. + 3 of
-    // the wave's slice (clamped past K; zero past m)
-    uint2 xv[kIPL];
+    // the wave's slice (clamped past K; zero past m).  kPre: token it / (4 kCPW),
+    // elements 8 (it % (4 kCPW)) .. + 7, and tokens past m repeat token m - 1 (their
+    // output columns are never stored); xsb: the 32-column sums of the wave's
+    // groups, item it -> token it / (4 kGPW), block it % (4 kGPW) of the slice.
+    using XItem = std::conditional_t<kPre, u32x4, uint2>;
+    XItem xv[kIPL];
+    constexpr int kSItems = kM * kGPW * 4, kSPL = (kSItems + kWave - 1) / kWave;
+    float xsb[kPre ? kSPL : 1];
 #pragma unroll
     for (int q = 0; q < kIPL; ++q) {
         const int it = min(lane + kWave * q, kItems - 1);
-        const int j = it / (kCPW * 8), r = it - j * (kCPW * 8);
-        const int64_t kx = min<int64_t>(c0 * 32 + 4 * r, ge * 128 - 4);
-        xv[q] = j < m ? *reinterpret_cast<const uint2*>(x + j * k + kx) : make_uint2(0u, 0u);
+        if constexpr (kPre) {
+            const int j = it / (kCPW * 4), r = it - j * (kCPW * 4);
+            const int64_t kx = min<int64_t>(c0 * 32 + 8 * r, ge * 128 - 8);
+            xv[q] = *reinterpret_cast<const u32x4*>(x + min(j, m - 1) * k + kx);
+        } else {
+            const int j = it / (kCPW * 8), r = it - j * (kCPW * 8);
+            const int64_t kx = min<int64_t>(c0 * 32 + 4 * r, ge * 128 - 4);
+            xv[q] = j < m ? *reinterpret_cast<const uint2*>(x + j * k + kx) : make_uint2(0u, 0u);
+        }
+    }
+    if constexpr (kPre) {
+#pragma unroll
+        for (int q = 0; q < kSPL; ++q) {
+            const int it = min(lane + kWave * q, kSItems - 1);
+            const int j = it / (4 * kGPW), b = it - j * (4 * kGPW);
+            xsb[q] = xsum[min(j, m - 1) * (k >> 5) + 4 * min<int64_t>(g0 + (b >> 2), ge - 1) + (b & 3)];
+        }
     }
     uint2 sc[kGPW];
 #pragma unroll
@@ -439,41 +472,62 @@ __global__ __launch_bounds__(kBlock) void k_decode_diag(const uint16_t* __restri
     // every wave zeroes the shared zero strip (the same value from every writer, so
     // no barrier is needed before a wave reads what it wrote itself)
     for (int b = lane * 16; b < kStrip; b += kWave * 16) *reinterpret_cast<u32x4*>(&zs[b]) = u32x4{0u, 0u, 0u, 0u};
-    // stage: lanes 2b, 2b+1 hold an 8-block's (x0..x3) and (x4..x7); the even lane
-    // writes slots (x0,x4)(x1,x5), the odd lane (x2,x6)(x3,x7)
-    float gsum[kIPL];
-#pragma unroll
-    for (int q = 0; q < kIPL; ++q) {
-        const int it = lane + kWave * q;
-        const int itc = min(it, kItems - 1);
-        const int j = itc / (kCPW * 8), r = itc - j * (kCPW * 8);
-        const uint2 v = xv[q];
-        const uint2 p = make_uint2(__shfl_xor(v.x, 1, kWave), __shfl_xor(v.y, 1, kWave));
-        const bool odd = r & 1;
-        const uint32_t hi = odd ? v.y : p.x, lo = odd ? p.y : v.x;
-        if (it < kItems)
-            *reinterpret_cast<uint2*>(&xs[wave][j][(r >> 1) * 16 + (odd ? 8 : 0)]) =
-                make_uint2(__builtin_amdgcn_perm(hi, lo, 0x05040100u), __builtin_amdgcn_perm(hi, lo, 0x07060302u));
-        // group sums: a group is 32 consecutive items, i.e. one half of the wave
-        float s = bf16_lo(v.x) + bf16_hi(v.x) + bf16_lo(v.y) + bf16_hi(v.y);
-        s += __shfl_xor(s, 1, kWave);
-        s += __shfl_xor(s, 2, kWave);
-        s += __shfl_xor(s, 4, kWave);
-        s += __shfl_xor(s, 8, kWave);
-        s += __shfl_xor(s, 16, kWave);
-        gsum[q] = s;
-    }
     float corr[kGPW];
+    if constexpr (kPre) {
 #pragma unroll
-    for (int g = 0; g < kGPW; ++g) {
-        float c = 0.0f;
-#pragma unroll
-        for (int j = 0; j < kM; ++j) {
-            const int it = j * kCPW * 8 + 32 * g;  // first item of (token j, group g)
-            const float v = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(gsum[it / kWave]), it % kWave));
-            c = tok == j ? v : c;
+        for (int q = 0; q < kIPL; ++q) {
+            const int it = lane + kWave * q;
+            const int j = it / (kCPW * 4), r = it - j * (kCPW * 4);
+            if (it < kItems) *reinterpret_cast<u32x4*>(&xs[wave][j][r * 16]) = xv[q];
         }
-        corr[g] = 136.0f * c;
+        // a group's four block sums sit in 4 aligned lanes
+        float gsum[kSPL];
+#pragma unroll
+        for (int q = 0; q < kSPL; ++q) gsum[q] = lane_group_sum<4>(xsb[q]);
+#pragma unroll
+        for (int g = 0; g < kGPW; ++g) {
+            float c = 0.0f;
+#pragma unroll
+            for (int j = 0; j < kM; ++j) {
+                const int it = j * 4 * kGPW + 4 * g;  // first block of (token j, group g)
+                const float v = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(gsum[it / kWave]), it % kWave));
+                c = tok == j ? v : c;
+            }
+            corr[g] = 136.0f * c;
+        }
+    } else {
+        // stage: lanes 2b, 2b+1 hold an 8-block's (x0..x3) and (x4..x7); the even lane
+        // writes slots (x0,x4)(x1,x5), the odd lane (x2,x6)(x3,x7)
+        float gsum[kIPL];
+#pragma unroll
+        for (int q = 0; q < kIPL; ++q) {
+            const int it = lane + kWave * q;
+            const int itc = min(it, kItems - 1);
+            const int j = itc / (kCPW * 8), r = itc - j * (kCPW * 8);
+            const uint2 v = xv[q];
+            const uint2 p = make_uint2(dpp_u32<kDppXor1>(v.x), dpp_u32<kDppXor1>(v.y));
+            const bool odd = r & 1;
+            const uint32_t hi = odd ? v.y : p.x, lo = odd ? p.y : v.x;
+            if (it < kItems)
+                *reinterpret_cast<uint2*>(&xs[wave][j][(r >> 1) * 16 + (odd ? 8 : 0)]) = make_uint2(
+                    __builtin_amdgcn_perm(hi, lo, 0x05040100u), __builtin_amdgcn_perm(hi, lo, 0x07060302u));
+            // a group is 32 consecutive items (half the wave): the sums of its two
+            // 16-lane rows
+            gsum[q] = lane_group_sum<16>(bf16_lo(v.x) + bf16_hi(v.x) + bf16_lo(v.y) + bf16_hi(v.y));
+        }
+#pragma unroll
+        for (int g = 0; g < kGPW; ++g) {
+            float c = 0.0f;
+#pragma unroll
+            for (int j = 0; j < kM; ++j) {
+                const int it = j * kCPW * 8 + 32 * g;  // first item of (token j, group g)
+                const int src = __float_as_int(gsum[it / kWave]);
+                const float v = __int_as_float(__builtin_amdgcn_readlane(src, it % kWave)) +
+                                __int_as_float(__builtin_amdgcn_readlane(src, it % kWave + 16));
+                c = tok == j ? v : c;
+            }
+            corr[g] = 136.0f * c;
+        }
     }
     const bool diag = col % kR == rg && tok < kM;
     const uint8_t* bsrc = diag ? &xs[wave][tok][cs * 64] : &zs[0];
@@ -537,18 +591,34 @@ __global__ __launch_bounds__(kBlock) void k_decode_diag(const uint16_t* __restri
                 atomicAdd(&y[j * n + row], v);
         }
     } else {
-        const int64_t f = n >> 1;  // h columns: the stacked weight has 2f rows
-        for (int i = threadIdx.x; i < m * 32; i += kBlock) {
+        const int64_t f = n >> 1;  // h columns: the stacked weight has 2f rows, f % 32 == 0
+        // thread i < 32 m (m <= 4): token i / 32, column 32 tile + i % 32, so that the
+        // 32 columns of a token are one half of a wave (two whole DPP rows)
+        const int i = threadIdx.x;
+        if (i < m * 32) {
             const int j = i >> 5, r = i & 31;
             const int64_t hc = tile * 32 + r;
-            if (hc >= f) continue;
             const float g = wsum(j, r), u = wsum(j, 32 + r);
             const float h = g * (1.0f / (1.0f + __expf(-g))) * u;
             const __bf16 hi = static_cast<__bf16>(h);
             const __bf16 lo = static_cast<__bf16>(h - static_cast<float>(hi));
-            const int64_t J = tok0 + j;
-            hout[MlpRows::hi(J, mtot, rows_block) * f + hc] = __builtin_bit_cast(uint16_t, hi);
-            hout[MlpRows::lo(J, mtot, rows_block) * f + hc] = __builtin_bit_cast(uint16_t, lo);
+            const int64_t J = tok0 + j, rh = MlpRows::hi(J, mtot, rows_block), rl = MlpRows::lo(J, mtot, rows_block);
+            hout[rh * f + h_slot(hc)] = __builtin_bit_cast(uint16_t, hi);
+            hout[rl * f + h_slot(hc)] = __builtin_bit_cast(uint16_t, lo);
+            const int sh = __float_as_int(lane_group_sum<16>(static_cast<float>(hi)));
+            const int sl = __float_as_int(lane_group_sum<16>(static_cast<float>(lo)));
+            auto half_sum = [&](int v) {  // rows 0 + 1 for lanes 0-31, rows 2 + 3 for lanes 32-63
+                const float a = __int_as_float(__builtin_amdgcn_readlane(v, 0)) +
+                                __int_as_float(__builtin_amdgcn_readlane(v, 16));
+                const float b = __int_as_float(__builtin_amdgcn_readlane(v, 32)) +
+                                __int_as_float(__builtin_amdgcn_readlane(v, 48));
+                return lane < 32 ? a : b;
+            };
+            const float th = half_sum(sh), tl = half_sum(sl);
+            if (r == 0) {
+                xsum[rh * (f >> 5) + tile] = th;
+                xsum[rl * (f >> 5) + tile] = tl;
+            }
         }
         // the output a K-split down projection accumulates into
         for (int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; i < yz_n;
@@ -570,6 +640,7 @@ struct DiagArgs {
     uint16_t* hout;  // kEpiGateUp
     int tok0, mtot;  // kEpiGateUp
     int rows_block = 0;      // kEpiGateUp: MlpRows layout
+    float* xsum = nullptr;   // kEpiGateUp: h's 32-column sums out; kEpiFold: x's in
     float* yz = nullptr;     // kEpiGateUp: zeroed (yz_n floats)
     int64_t yz_n = 0;
     int ksplit = 1;          // kEpiFold only: blocks per tile along K; their sums are
@@ -583,11 +654,13 @@ int launch_diag(int64_t gpw, int64_t tiles, hipStream_t s, const DiagArgs& a) {
     // only the fold epilogue adds K parts; the others would store one part over another
     if (a.ksplit < 1 || (a.ksplit > 1 && kEpi != kEpiFold))
         return fail(TQ_EINVAL, "tq_gemv_w4g128_tiled: K split %d needs the accumulating epilogue", a.ksplit);
+    if (kEpi != kEpiPlain && (!a.xsum || !aligned(a.xsum, 16) || !aligned(a.x, 16) || a.k % 128 != 0))
+        return fail(TQ_EINVAL, "tq_mlp_w4g128_decode: h rows and their sums must be 16-byte aligned");
     const dim3 grid(static_cast<unsigned>(tiles), static_cast<unsigned>(a.ksplit));
 #define TQ_DIAG(G)                                                                                      \
     k_decode_diag<kR, kM, G, kWinD, kEpi><<<grid, kBlock, 0, s>>>(a.x, a.m, a.pt, a.st, a.b, a.n, a.k, a.y, \
-                                                                  a.hout, a.tok0, a.mtot, a.rows_block,      \
-                                                                  a.yz, a.yz_n)
+                                                                  a.hout, a.xsum, a.tok0, a.mtot,           \
+                                                                  a.rows_block, a.yz, a.yz_n)
     // the exact groups per wave, so that no wave of the block runs dead groups (K =
     // 14336, the Llama FFN's intermediate size, is 7 per wave)
     switch (gpw) {
@@ -793,7 +866,7 @@ int tq_gemv_w4g128_tiled(const uint16_t* x_bf16, int64_t m, const uint8_t* packe
 
 int64_t tq_mlp_w4g128_decode_workspace_bytes(int64_t m, int64_t d, int64_t f) {
     if (m < 0 || d < 0 || f < 0) return -1;
-    return ((2 * m * f * 2 + 255) / 256) * 256;  // bf16 hi and lo rows of h
+    return tq::mlp_h_bytes(m, f) + tq::round_up256(2 * m * ((f + 31) / 32) * 4);
 }
 
 int tq_repack_w4g128_gate_up_tiled(const uint8_t* gate_packed, const uint16_t* gate_s, const uint8_t* up_packed,
@@ -817,11 +890,11 @@ int tq_repack_w4g128_gate_up_tiled(const uint8_t* gate_packed, const uint16_t* g
 namespace tq {
 namespace {
 
-// Scratch of the allocation-free decode FFN: the bf16 hi and lo rows of h for
-// 16 tokens at F = 16384 (the largest decode shape).  One copy per device, held
+// Scratch of the allocation-free decode FFN: the bf16 hi and lo rows of h and
+// their 32-column sums for 16 tokens at F = 16384 (the largest decode shape).  One copy per device, held
 // until the process ends; host code reaches it only through the address that
 // hipGetSymbolAddress returns for the current device.
-constexpr int64_t kMlpDecodeScratch = 2 * 16 * 16384 * 2;
+constexpr int64_t kMlpDecodeScratch = mlp_h_bytes(16, 16384) + round_up256(2 * 16 * (16384 / 32) * 4);
 static_assert(kMlpDecodeScratch == TQ_MLP_DECODE_SCRATCH_BYTES, "tq.h states the scratch size");
 __device__ __align__(256) uint8_t scratch[kMlpDecodeScratch];
 
@@ -881,6 +954,8 @@ int mlp_decode(const char* fn, const uint16_t* x_bf16, int64_t m, int64_t d, int
                "%s: misaligned pointer", fn);
     const hipStream_t st = as_hip(stream);
     uint16_t* h = static_cast<uint16_t*>(workspace);
+    float* hsum = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + mlp_h_bytes(m, f));
+    const int64_t fb = f >> 5;  // 32-column blocks of a row of h
     const int mi = static_cast<int>(m);
     // gate + up with SiLU * up, 4 tokens per launch, into the hi/lo rows of h
     const int kr = down_tile_rows == 16 ? 1 : (down_tile_rows == 32 ? 2 : 4);
@@ -895,6 +970,7 @@ int mlp_decode(const char* fn, const uint16_t* x_bf16, int64_t m, int64_t d, int
         const int mm = mi - j0 < 4 ? mi - j0 : 4;
         DiagArgs a{x_bf16 + j0 * d, mm, gate_up_t, gate_up_s_t, nullptr, 2 * f, d, nullptr, h, j0, mi};
         a.rows_block = block;
+        a.xsum = hsum;
         if (block && j0 == 0) {
             a.yz = y;
             a.yz_n = m * d;
@@ -909,6 +985,7 @@ int mlp_decode(const char* fn, const uint16_t* x_bf16, int64_t m, int64_t d, int
             const int t = mi - 4 * c < 4 ? mi - 4 * c : 4;
             DiagArgs a{h + 8 * c * f, 2 * t, down_t, down_s_t, nullptr, d, f, y + 4 * c * d, nullptr, 0, 0};
             a.ksplit = 2;
+            a.xsum = hsum + 8 * c * fb;
             const int rc = launch_diag_r<kEpiFold>(kr, gpw2, dn_tiles, st, a);
             if (rc != TQ_OK) return rc;
         }
@@ -917,7 +994,8 @@ int mlp_decode(const char* fn, const uint16_t* x_bf16, int64_t m, int64_t d, int
     // down, one launch per token pair: its hi and lo rows in, their sum out
     for (int c = 0; 2 * c < mi; ++c) {
         const int t = mi - 2 * c < 2 ? mi - 2 * c : 2;
-        const DiagArgs a{h + 4 * c * f, 2 * t, down_t, down_s_t, nullptr, d, f, y + 2 * c * d, nullptr, 0, 0};
+        DiagArgs a{h + 4 * c * f, 2 * t, down_t, down_s_t, nullptr, d, f, y + 2 * c * d, nullptr, 0, 0};
+        a.xsum = hsum + 4 * c * fb;
         const int rc = launch_diag_r<kEpiFold>(kr, dn_gpw, dn_tiles, st, a);
         if (rc != TQ_OK) return rc;
     }

@@ -100,7 +100,37 @@ __device__ __forceinline__ void lds_dma4(const void* g, uint32_t la) {
 }
 #pragma clang diagnostic pop
 
-// Wave64 butterfly reductions (DPP / ds_swizzle via __shfl_xor).
+// Lane permutes within rows of 16 lanes through DPP, a VALU operand modifier
+// (__shfl_xor compiles to ds_bpermute, a round trip through the LDS crossbar).
+enum DppCtrl : int {
+    kDppXor1 = 0xB1,         // quad_perm [1, 0, 3, 2]: lane i <- i ^ 1
+    kDppXor2 = 0x4E,         // quad_perm [2, 3, 0, 1]: lane i <- i ^ 2
+    kDppMirror = 0x140,      // lane i <- 15 - i within its row
+    kDppHalfMirror = 0x141,  // lane i <- 7 - i within its half row
+};
+template <int kCtrl>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+    return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), kCtrl, 0xF, 0xF, false));
+}
+template <int kCtrl>
+__device__ __forceinline__ float dpp_f32(float v) {
+    return __uint_as_float(dpp_u32<kCtrl>(__float_as_uint(v)));
+}
+
+// Sum over each aligned group of kWidth (4, 8 or 16) lanes, in every lane of the
+// group, for groups whose lanes are all active: quad butterflies, then the
+// mirrored half row and the mirrored row add the other quad and the other half.
+template <int kWidth>
+__device__ __forceinline__ float lane_group_sum(float v) {
+    static_assert(kWidth == 4 || kWidth == 8 || kWidth == 16, "DPP groups are 4, 8 or 16 lanes");
+    v += dpp_f32<kDppXor1>(v);
+    v += dpp_f32<kDppXor2>(v);
+    if constexpr (kWidth >= 8) v += dpp_f32<kDppHalfMirror>(v);
+    if constexpr (kWidth >= 16) v += dpp_f32<kDppMirror>(v);
+    return v;
+}
+
+// Wave64 butterfly reductions (ds_bpermute via __shfl_xor).
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));

@@ -143,10 +143,11 @@ def test_mlp_workspace_bytes(abi):
 
 def test_mlp_decode_workspace_bytes(abi):
     ws = abi.lib().tq_mlp_w4g128_decode_workspace_bytes
-    # bf16 hi and lo rows of h for each token, rounded up to 256 bytes
-    assert ws(1, 4096, 14336) == 2 * 14336 * 2
-    assert ws(3, 256, 384) == 2 * 3 * 384 * 2
-    assert ws(1, 128, 128) == 512
+    # bf16 hi and lo rows of h for each token, then the f32 sums of their
+    # 32-column blocks, each part rounded up to 256 bytes
+    assert ws(1, 4096, 14336) == 2 * 14336 * 2 + 2 * 448 * 4
+    assert ws(3, 256, 384) == 2 * 3 * 384 * 2 + 512
+    assert ws(1, 128, 128) == 512 + 256
     assert ws(0, 128, 128) == 0 and ws(-1, 128, 128) == -1
 
 

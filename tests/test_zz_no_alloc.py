@@ -54,12 +54,13 @@ def test_noalloc_matches_workspace_entry_point(tq, cases):
 
 
 def test_noalloc_rejects_beyond_scratch(tq):
-    """The scratch holds M <= 16 tokens at F <= 16384 (1 MiB); larger shapes and a
-    null output are rejected before anything is enqueued."""
+    """The scratch holds M <= 16 tokens at F <= 16384 (h: 1 MiB, its block sums:
+    64 KiB); larger shapes and a null output are rejected before anything is
+    enqueued."""
     from theano_quantize import InvalidArgument, _abi
 
     lib = _abi.lib()
-    assert lib.tq_mlp_w4g128_decode_workspace_bytes(16, 4096, 16384) == 1 << 20
+    assert lib.tq_mlp_w4g128_decode_workspace_bytes(16, 4096, 16384) == (1 << 20) + (1 << 16)
     with pytest.raises(InvalidArgument, match="M=17"):
         _abi.call("tq_mlp_w4g128_decode_noalloc", 16, 17, 256, 16384, 16, 16, 16, 16, 16, 16, None)
     with pytest.raises(InvalidArgument, match="F=16512"):

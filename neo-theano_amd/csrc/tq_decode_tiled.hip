@@ -413,7 +413,10 @@ __global__ __launch_bounds__(kBlock) void k_decode_diag(const uint16_t* __restri
     constexpr int kItems = kM * kCPW * (kPre ? 4 : 8);  // 8- (kPre) or 4-element items
     constexpr int kIPL = (kItems + kWave - 1) / kWave;
     constexpr int kW = kWinD < kSteps ? kWinD : kSteps;
-    __shared__ __attribute__((aligned(16))) uint8_t xs[kWaves][kM][kStrip];
+    // token strips padded by 16 bytes: unpadded, the tokens' B-operand reads of one
+    // MFMA (strips 2^n bytes apart) fell in the same LDS banks, an 8-way conflict at
+    // 8 x rows
+    __shared__ __attribute__((aligned(16))) uint8_t xs[kWaves][kM][kStrip + 16];
     __shared__ __attribute__((aligned(16))) uint8_t zs[kStrip];  // zeros, written by every wave
     __shared__ __attribute__((aligned(16))) float part[kWaves][kM][T];
     const int lane = threadIdx.x & 63;

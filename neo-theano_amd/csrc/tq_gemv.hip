@@ -62,6 +62,12 @@ struct CodeFp8 {
 // and are added in a fixed order (first half + second half).
 constexpr int kBlockW8 = 512;
 constexpr int kWavesW8 = kBlockW8 / kWave;
+
+// LDS slot of x item j (4 values) of a token: item 4l + e of a 256-item chunk is
+// lane l's e-th 16-byte slice, and e is xor-ed with bits 2-3 of l, so that the
+// 64 lanes' reads of one e fall in distinct banks (lanes 64 bytes apart collide
+// 16-way unswizzled).
+__device__ __forceinline__ int xslot(int j) { return j ^ ((j >> 4) & 3); }
 constexpr int kMaxPairRows = 64;  // rows per wave pair that the LDS partial sums hold
 
 template <class Code, int kM, int kChunks, int kRows, int kKS>
@@ -115,7 +121,7 @@ __global__ __launch_bounds__(kBlockW8) void k_gemv_w8(const float* __restrict__ 
     for (int qi = 0; qi < kXPer; ++qi) {
         const int i = threadIdx.x + qi * kBlockW8;
         const int m = i / (kChunks * 256), j = i - m * (kChunks * 256);
-        if (i < kXItems) xs[m][j] = xv[qi];
+        if (i < kXItems) xs[m][xslot(j)] = xv[qi];
     }
     __syncthreads();
     float xr[kM][kC0][16];
@@ -126,7 +132,7 @@ __global__ __launch_bounds__(kBlockW8) void k_gemv_w8(const float* __restrict__ 
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 // the second wave's chunks past nc read zeros' stand-in (never used)
-                const f32x4 v = xs[m][min(cb + c, kChunks - 1) * 256 + 4 * lane + j];
+                const f32x4 v = xs[m][xslot(min(cb + c, kChunks - 1) * 256 + 4 * lane + j)];
                 xr[m][c][4 * j + 0] = v.x;
                 xr[m][c][4 * j + 1] = v.y;
                 xr[m][c][4 * j + 2] = v.z;
@@ -302,7 +308,7 @@ __global__ __launch_bounds__(kBlockW8) void k_gemv_a8(const float* __restrict__ 
         if (i >= kXItems) continue;
         const int m = i / (kChunks * 256), j = i - m * (kChunks * 256);
         const f32x4 v = xv[qi];
-        xs[m][j] = v;
+        xs[m][xslot(j)] = v;
         if (j < k4) {
             const float a = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
 #pragma unroll
@@ -324,8 +330,8 @@ __global__ __launch_bounds__(kBlockW8) void k_gemv_a8(const float* __restrict__ 
         for (int i = 1; i < kWavesW8; ++i) r = fmaxf(r, red[i][m]);
         sa[m] = row_scale<Fmt>(absmax_finish(r));
     }
-    // the block codes each 4-value entry once (in place in LDS), then every lane
-    // copies its 16-value slices into registers
+    // the block codes each 4-value entry once (in place in LDS, slot by slot), then
+    // every lane copies its 16-value slices into registers
     for (int i = threadIdx.x; i < kM * kChunks * 256; i += kBlockW8) {
         const int m = i / (kChunks * 256), j = i - m * (kChunks * 256);
         typename P::xreg_t e[P::kRegsPer4];
@@ -342,7 +348,8 @@ __global__ __launch_bounds__(kBlockW8) void k_gemv_a8(const float* __restrict__ 
 #pragma unroll
         for (int c = 0; c < kChunks; ++c)
 #pragma unroll
-            for (int j = 0; j < 4; ++j) P::unpack(xs[m][c * 256 + 4 * lane + j], &xr[m][c][j * P::kRegsPer4]);
+            for (int j = 0; j < 4; ++j)
+                P::unpack(xs[m][xslot(c * 256 + 4 * lane + j)], &xr[m][c][j * P::kRegsPer4]);
     if (row_begin >= row_end) return;
 
     for (int64_t row0 = row_begin; row0 < row_end; row0 += kRows) {

@@ -106,8 +106,7 @@ __global__ __launch_bounds__(kBlock) void k_decode_w4g128(const uint16_t* __rest
         *reinterpret_cast<u32x4*>(strip_x + t * kTStride + b * 16) = slot_order(v);
         float sum = bf16_lo(v.x) + bf16_hi(v.x) + bf16_lo(v.y) + bf16_hi(v.y) + bf16_lo(v.z) + bf16_hi(v.z) +
                     bf16_lo(v.w) + bf16_hi(v.w);
-#pragma unroll
-        for (int o = 8; o > 0; o >>= 1) sum += __shfl_xor(sum, o, kWave);  // a group's 16 lanes are all active
+        sum = lane_group_sum<16>(sum);  // a group's 16 lanes (one DPP row) are all active
         if ((b & 15) == 0) strip_sum[(b >> 4) * 16 + t] = 136.0f * sum;
     };
     constexpr int kPre = 4 * kGPW < 8 ? 4 * kGPW : 8;  // items per lane loaded up front

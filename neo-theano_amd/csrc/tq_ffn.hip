@@ -119,8 +119,7 @@ __global__ __launch_bounds__(256) void k_ffn_prep(const uint16_t* __restrict__ x
     const u32x4 v = *reinterpret_cast<const u32x4*>(x + off);
     float s = (bf16_lo(v.x) + bf16_hi(v.x)) + (bf16_lo(v.y) + bf16_hi(v.y)) + (bf16_lo(v.z) + bf16_hi(v.z)) +
               (bf16_lo(v.w) + bf16_hi(v.w));
-#pragma unroll
-    for (int o = 1; o < 16; o <<= 1) s += __shfl_xor(s, o, 16);
+    s = lane_group_sum<16>(s);  // a group's 16 lanes are one DPP row
     u32x4 o;
     o.x = __builtin_amdgcn_perm(v.y, v.x, 0x05040100u);
     o.y = __builtin_amdgcn_perm(v.y, v.x, 0x07060302u);
@@ -442,8 +441,7 @@ __global__ __launch_bounds__(64 * kWavesM * kWavesN, 1) void k_ffn(FfnArgs p) {
                     u32x4{lb[0] | (lb[1] << 16), lb[2] | (lb[3] << 16), lb[4] | (lb[5] << 16), lb[6] | (lb[7] << 16)};
             }
         }
-#pragma unroll
-        for (int w = 1; w < kTPR; w <<= 1) sum += __shfl_xor(sum, w, kWave);
+        sum = lane_group_sum<kTPR>(sum);
         if (q == 0 && mm < p.m) *reinterpret_cast<uint2*>(p.hs + (tn_blk * p.mpad + mm) * 2) = split3(-kOffset * sum);
     }
 }

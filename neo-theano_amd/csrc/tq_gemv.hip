@@ -219,11 +219,7 @@ struct A8<FmtI8> {
         acc = __builtin_amdgcn_sdot4(w.z, static_cast<int>(x[2]), acc, false);
         acc = __builtin_amdgcn_sdot4(w.w, static_cast<int>(x[3]), acc, false);
     }
-    __device__ static float total(acc_t a) {
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) a += __shfl_xor(a, o, kWave);
-        return static_cast<float>(a);
-    }
+    __device__ static float total(acc_t a) { return static_cast<float>(wave_sum(a)); }
 };
 template <>
 struct A8<FmtFp8> {

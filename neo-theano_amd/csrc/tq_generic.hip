@@ -17,12 +17,6 @@ namespace {
 constexpr int kGenBlock = 256;
 constexpr int kGenWaves = kGenBlock / kWave;
 
-__device__ __forceinline__ int wave_sum_i32(int v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
-    return v;
-}
-
 __device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __uint_as_float(static_cast<uint32_t>(b) << 16); }
 
 // y[i, j] = s[j] * sum_k x[i, k] q[j, k] + b[j]
@@ -92,7 +86,7 @@ __global__ __launch_bounds__(kGenBlock) void k_gemm_w8a8_generic(const int8_t* _
     const int8_t* wr = qw + j * k;
     int acc = 0;
     for (int64_t p = lane; p < k; p += kWave) acc += static_cast<int>(ar[p]) * static_cast<int>(wr[p]);
-    acc = wave_sum_i32(acc);
+    acc = wave_sum(acc);
     if (lane == 0) {
         if (acc_out) acc_out[out] = acc;
         y[out] = fmaf(static_cast<float>(acc) * sa[i], sw[j], bias ? bias[j] : 0.f);

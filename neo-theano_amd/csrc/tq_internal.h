@@ -112,50 +112,63 @@ template <int kCtrl>
 __device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
     return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), kCtrl, 0xF, 0xF, false));
 }
-template <int kCtrl>
-__device__ __forceinline__ float dpp_f32(float v) {
-    return __uint_as_float(dpp_u32<kCtrl>(__float_as_uint(v)));
+template <int kCtrl, class T>
+__device__ __forceinline__ T dpp(T v) {
+    static_assert(sizeof(T) == 4, "32-bit lanes");
+    return __builtin_bit_cast(T, dpp_u32<kCtrl>(__builtin_bit_cast(uint32_t, v)));
+}
+template <class T>
+__device__ __forceinline__ T readlane(T v, int l) {
+    return __builtin_bit_cast(T, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
 }
 
-// Sum over each aligned group of kWidth (4, 8 or 16) lanes, in every lane of the
-// group, for groups whose lanes are all active: quad butterflies, then the
-// mirrored half row and the mirrored row add the other quad and the other half.
+struct OpAdd {
+    template <class T>
+    __device__ T operator()(T a, T b) const { return a + b; }
+};
+struct OpMax {
+    __device__ float operator()(float a, float b) const { return fmaxf(a, b); }
+};
+struct OpMin {
+    __device__ float operator()(float a, float b) const { return fminf(a, b); }
+};
+
+// Reduction over each aligned group of kWidth (1, 2, 4, 8 or 16) lanes, in every
+// lane of the group, for groups whose lanes are all active: quad butterflies,
+// then the mirrored half row and the mirrored row bring in the other quad and
+// the other half.
+template <int kWidth, class T, class Op>
+__device__ __forceinline__ T lane_group_reduce(T v, Op op) {
+    static_assert(kWidth == 1 || kWidth == 2 || kWidth == 4 || kWidth == 8 || kWidth == 16,
+                  "DPP groups are 1, 2, 4, 8 or 16 lanes");
+    if constexpr (kWidth >= 2) v = op(v, dpp<kDppXor1>(v));
+    if constexpr (kWidth >= 4) v = op(v, dpp<kDppXor2>(v));
+    if constexpr (kWidth >= 8) v = op(v, dpp<kDppHalfMirror>(v));
+    if constexpr (kWidth >= 16) v = op(v, dpp<kDppMirror>(v));
+    return v;
+}
 template <int kWidth>
 __device__ __forceinline__ float lane_group_sum(float v) {
-    static_assert(kWidth == 4 || kWidth == 8 || kWidth == 16, "DPP groups are 4, 8 or 16 lanes");
-    v += dpp_f32<kDppXor1>(v);
-    v += dpp_f32<kDppXor2>(v);
-    if constexpr (kWidth >= 8) v += dpp_f32<kDppHalfMirror>(v);
-    if constexpr (kWidth >= 16) v += dpp_f32<kDppMirror>(v);
-    return v;
+    return lane_group_reduce<kWidth>(v, OpAdd{});
 }
-
-// Wave64 butterfly reductions (ds_bpermute via __shfl_xor).
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
-    return v;
-}
-
-__device__ __forceinline__ float wave_min(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fminf(v, __shfl_xor(v, o, kWave));
-    return v;
-}
-
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
-    return v;
-}
-
-// Max over aligned groups of `width` lanes (width a power of two <= 64).
+// Max over aligned groups of kWidth (1 to 16) lanes.
 template <int kWidth>
 __device__ __forceinline__ float group_max(float v) {
-#pragma unroll
-    for (int o = kWidth / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
-    return v;
+    return lane_group_reduce<kWidth>(v, OpMax{});
 }
+
+// Wave64 reductions with every lane active, result uniform: DPP within each
+// 16-lane row, then the four rows' values (v_readlane) combined in a fixed
+// order.  No LDS traffic (a __shfl_xor butterfly is six dependent ds_bpermute).
+template <class T, class Op>
+__device__ __forceinline__ T wave_reduce(T v, Op op) {
+    v = lane_group_reduce<16>(v, op);
+    return op(op(readlane(v, 0), readlane(v, 16)), op(readlane(v, 32), readlane(v, 48)));
+}
+__device__ __forceinline__ float wave_max(float v) { return wave_reduce(v, OpMax{}); }
+__device__ __forceinline__ float wave_min(float v) { return wave_reduce(v, OpMin{}); }
+__device__ __forceinline__ float wave_sum(float v) { return wave_reduce(v, OpAdd{}); }
+__device__ __forceinline__ int wave_sum(int v) { return wave_reduce(v, OpAdd{}); }
 
 // round_half_away_from_zero(a / s) for a >= 0 (or +inf), s > 0 finite normal,
 // exact with respect to the real quotient (the reference rounds the f64

@@ -66,11 +66,7 @@ __device__ __forceinline__ uint32_t bf16_rne(float f) {
 }
 
 // sum over the 16 lanes of a DPP row (lanes 16r .. 16r+15)
-__device__ __forceinline__ float row16_sum(float v) {
-#pragma unroll
-    for (int o = 8; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
-    return v;
-}
+__device__ __forceinline__ float row16_sum(float v) { return lane_group_sum<16>(v); }
 
 // One block computes a 128 (weight rows) x kBM (tokens) tile of
 //   out[m, n] = sum_g s[n, g] * (sum_{k in g} (136 + q[n, k]) * a[m, k] - 136 * A_g[m])

@@ -130,15 +130,17 @@ def _peaks_lib():
     vp, i64, i32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int
     L.tqp_hbm_read.argtypes = [vp, i64, vp, i32, vp]
     L.tqp_hbm_read_chunks.argtypes = [vp, i64, vp, i32, vp]
-    L.tqp_mfma_i8.argtypes = [i32, i32, vp, vp]
-    L.tqp_mfma_bf16.argtypes = [i32, i32, vp, vp]
+    for fn in (L.tqp_mfma_i8, L.tqp_mfma_bf16, L.tqp_mfma_i8_random, L.tqp_mfma_bf16_random):
+        fn.argtypes = [i32, i32, vp, vp]
     return L
 
 
 def measured_peaks(torch, timer, dev, log):
     """HBM read rate over a 4 GiB buffer (16x the MALL) and the dense i8 / bf16
     MFMA rates of register-only loops, one 4-wave block per CU (the layout of
-    the GEMM kernels) and four, on this device."""
+    the GEMM kernels) and four, on this device: with constant operands and
+    with pseudo-random ones (`*_random_operands`), which draw the power real
+    data does (the part then runs the matrix cores at a lower clock)."""
     import ctypes
 
     L = _peaks_lib()
@@ -157,15 +159,17 @@ def measured_peaks(torch, timer, dev, log):
     res = {"hbm_read_GB/s": round(best[0], 1), "hbm_read_blocks": best[1], "hbm_read_bytes": nb,
            "hbm_spec_GB/s": HBM_PEAK_GBS}
     iters = 400
-    for name, fn, per, spec in (("i8_mfma_TOPS", L.tqp_mfma_i8, 65536, I8_PEAK_TOPS),
-                                ("bf16_mfma_TFLOPS", L.tqp_mfma_bf16, 32768, BF16_PEAK_TFLOPS)):
-        vals = {}
-        for bpc in (1, 4):
-            blocks = bpc * cus
-            ms, _ = timer.run(lambda i, b=blocks, f=fn: f(b, iters, out.data_ptr(), st()), 5, 1)
-            vals[bpc] = blocks * 4 * 8 * iters * per / (ms * 1e-3) / 1e12
-        res[name] = round(max(vals.values()), 1)
-        res[name + "_1_block_per_cu"] = round(vals[1], 1)
+    for name, fn, fr, per, spec in (("i8_mfma_TOPS", L.tqp_mfma_i8, L.tqp_mfma_i8_random, 65536, I8_PEAK_TOPS),
+                                    ("bf16_mfma_TFLOPS", L.tqp_mfma_bf16, L.tqp_mfma_bf16_random, 32768,
+                                     BF16_PEAK_TFLOPS)):
+        for suffix, f in (("", fn), ("_random_operands", fr)):
+            vals = {}
+            for bpc in (1, 4):
+                blocks = bpc * cus
+                ms, _ = timer.run(lambda i, b=blocks, f=f: f(b, iters, out.data_ptr(), st()), 5, 1)
+                vals[bpc] = blocks * 4 * 8 * iters * per / (ms * 1e-3) / 1e12
+            res[name + suffix] = round(max(vals.values()), 1)
+            res[name + suffix + "_1_block_per_cu"] = round(vals[1], 1)
         res[name.replace("_T", "_spec_T")] = spec
     log(f"measured peaks: {res}")
     return res
@@ -398,6 +402,11 @@ def main():
     peaks = None
     if not args.no_secondary and (only is None or only == "peaks"):
         peaks = measured_peaks(torch, timer, dev, log)
+
+    def of_random_peak(rate, key):
+        # fraction of the matrix-core rate measured on random operands (None when
+        # the peaks leg did not run)
+        return round(rate / peaks[key], 4) if peaks else None
         secondary["measured_peaks"] = peaks
 
     # ----------------- plain streaming read of the headline's bytes per launch
@@ -536,6 +545,7 @@ def main():
         msq, _ = timer.run(launch_q, steps, 2)
         secondary["w8a8_gemm_m2048"] = {
             "us": round(ms * 1e3, 3), "timing": mode, "TOPS": round(tops, 1), "i8_mfma_frac": round(tops / I8_PEAK_TOPS, 4),
+            "i8_mfma_frac_of_random_operand_peak": of_random_peak(tops, "i8_mfma_TOPS_random_operands"),
             "act_quant_us": round(msq * 1e3, 3), "act_quant_GB/s": round(qbytes / (msq * 1e-3) / 1e9, 1)}
         log(f"w8a8 M=2048: {ms * 1e3:.2f} us  {tops:.0f} TOPS; act quant {msq * 1e3:.2f} us")
         del qa, qw, y, xd
@@ -651,7 +661,9 @@ def main():
         flops = 6.0 * m5 * f5 * d5
         tf = flops / (ms * 1e-3) / 1e12
         secondary["mlp_w4g128_m512"] = {"us": round(ms * 1e3, 2), "timing": mode, "tokens/s": round(m5 / (ms * 1e-3), 1),
-                                        "TFLOP/s": round(tf, 1), "bf16_mfma_frac": round(tf / BF16_PEAK_TFLOPS, 4)}
+                                        "TFLOP/s": round(tf, 1), "bf16_mfma_frac": round(tf / BF16_PEAK_TFLOPS, 4),
+                                        "bf16_mfma_frac_of_random_operand_peak":
+                                            of_random_peak(tf, "bf16_mfma_TFLOPS_random_operands")}
         log(f"mlp M=512: {ms * 1e3:.1f} us  {m5 / (ms * 1e-3):.0f} tok/s  {tf:.0f} TFLOP/s")
 
         # prefill INT4 Linear on the gate weight alone: [512, 4096] x [14336, 4096]^T
@@ -666,7 +678,9 @@ def main():
         ms, mode = timer.run(launch_lin, steps, 2)
         tf = 2.0 * m5 * f5 * d5 / (ms * 1e-3) / 1e12
         secondary["w4a16_linear_m512_n14336_k4096"] = {"us": round(ms * 1e3, 2), "timing": mode, "TFLOP/s": round(tf, 1),
-                                                       "bf16_mfma_frac": round(tf / BF16_PEAK_TFLOPS, 4)}
+                                                       "bf16_mfma_frac": round(tf / BF16_PEAK_TFLOPS, 4),
+                                                       "bf16_mfma_frac_of_random_operand_peak":
+                                                           of_random_peak(tf, "bf16_mfma_TFLOPS_random_operands")}
         log(f"w4a16 linear M=512 N=14336 K=4096: {ms * 1e3:.1f} us  {tf:.0f} TFLOP/s")
         del mlp, wsl, yl
 

@@ -11,7 +11,11 @@
 //  * tqp_mfma_i8 / tqp_mfma_bf16: every wave runs `iters` rounds of 8
 //    independent v_mfma_i32_32x32x32_i8 / v_mfma_f32_32x32x16_bf16 on register
 //    operands (no memory traffic), one 256-thread block per CU per round of
-//    blocks; ops / time is the sustained dense matrix-core rate.
+//    blocks; ops / time is the sustained dense matrix-core rate.  The plain
+//    forms use constant operands; the _random forms give every lane and chain
+//    its own pseudo-random operands (i8: any code; bf16: random sign and
+//    mantissa, magnitudes in [1/4, 4)), which switch the matrix cores as real
+//    data does: they draw more power and the part holds a lower clock.
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -86,6 +90,74 @@ __global__ __launch_bounds__(256, 1) void k_mfma_i8(int iters, int32_t seed, int
     out[blockIdx.x * 256 + threadIdx.x] = r;
 }
 
+__device__ __forceinline__ uint32_t mix(uint32_t x) {
+    x ^= x >> 16;
+    x *= 0x7feb352dU;
+    x ^= x >> 15;
+    x *= 0x846ca68bU;
+    x ^= x >> 16;
+    return x;
+}
+// two bf16 of random sign and mantissa with exponents 2^-2 .. 2^1
+__device__ __forceinline__ uint32_t rnd_bf16_pair(uint32_t h) {
+    const uint32_t lo = (h & 0x807Fu) | ((0x7Du + ((h >> 7) & 3u)) << 7);
+    const uint32_t hi = ((h >> 16) & 0x807Fu) | ((0x7Du + ((h >> 23) & 3u)) << 7);
+    return lo | (hi << 16);
+}
+
+template <bool kBf16>
+__device__ __forceinline__ void random_operands(int32_t seed, u32x4 (&a)[8], u32x4 (&b)[8]) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const uint32_t h = mix(threadIdx.x * 977u + blockIdx.x * 131071u + j * 7919u + static_cast<uint32_t>(seed));
+        uint32_t r[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) r[e] = kBf16 ? rnd_bf16_pair(mix(h + e + 1)) : mix(h + e + 1);
+        a[j] = u32x4{r[0], r[1], r[2], r[3]};
+        b[j] = u32x4{r[4], r[5], r[6], r[7]};
+    }
+}
+
+__global__ __launch_bounds__(256, 1) void k_mfma_i8_random(int iters, int32_t seed, int32_t* __restrict__ out) {
+    u32x4 a[8], b[8];
+    random_operands<false>(seed, a, b);
+    i32x16 c[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) c[j] = i32x16{};
+    for (int it = 0; it < iters; ++it) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            c[j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(i32x4, a[j]),
+                                                         __builtin_bit_cast(i32x4, b[(j + 1) & 7]), c[j], 0, 0, 0);
+    }
+    int32_t r = 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) r += c[j][e];
+    out[blockIdx.x * 256 + threadIdx.x] = r;
+}
+
+__global__ __launch_bounds__(256, 1) void k_mfma_bf16_random(int iters, int32_t seed, float* __restrict__ out) {
+    u32x4 a[8], b[8];
+    random_operands<true>(seed, a, b);
+    f32x16 c[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) c[j] = f32x16{};
+    for (int it = 0; it < iters; ++it) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            c[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a[j]),
+                                                           __builtin_bit_cast(bf16x8, b[(j + 1) & 7]), c[j], 0, 0, 0);
+    }
+    float r = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) r += c[j][e];
+    out[blockIdx.x * 256 + threadIdx.x] = r;
+}
+
 __global__ __launch_bounds__(256, 1) void k_mfma_bf16(int iters, float seed, float* __restrict__ out) {
     const __bf16 s = static_cast<__bf16>(seed);
     const bf16x8 a = bf16x8{s, s, s, s, s, s, s, s};
@@ -139,6 +211,17 @@ int tqp_mfma_i8(int blocks, int iters, int32_t* out, hipStream_t stream) {
 
 int tqp_mfma_bf16(int blocks, int iters, float* out, hipStream_t stream) {
     k_mfma_bf16<<<blocks, 256, 0, stream>>>(iters, 1.0f, out);
+    return static_cast<int>(hipGetLastError());
+}
+
+// The same loops on pseudo-random operands (see the header).
+int tqp_mfma_i8_random(int blocks, int iters, int32_t* out, hipStream_t stream) {
+    k_mfma_i8_random<<<blocks, 256, 0, stream>>>(iters, 1, out);
+    return static_cast<int>(hipGetLastError());
+}
+
+int tqp_mfma_bf16_random(int blocks, int iters, float* out, hipStream_t stream) {
+    k_mfma_bf16_random<<<blocks, 256, 0, stream>>>(iters, 1, out);
     return static_cast<int>(hipGetLastError());
 }
 

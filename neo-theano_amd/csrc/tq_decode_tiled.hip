@@ -34,7 +34,7 @@
 // group scale is applied.  Weight loads are unconditional (clamped addresses)
 // and run kWin chunks ahead of the arithmetic; the waves' partial sums meet in
 // LDS in a fixed order.  Its arithmetic grows with the token count.
-//  * k_decode_tiled_mfma (3-16 tokens, T a multiple of 16): unpacked bf16
+//  * k_decode_tiled_mfma (5-16 tokens, T a multiple of 16): unpacked bf16
 //    weights feed v_mfma_f32_16x16x32_bf16 with the tokens as the other operand,
 //    so the cost is nearly flat in the token count.  Each wave owns the whole
 //    tile and a run of groups, reads its tokens' x straight from L2 (no LDS
@@ -840,12 +840,13 @@ int tq_gemv_w4g128_tiled(const uint16_t* x_bf16, int64_t m, const uint8_t* packe
     const hipStream_t st = as_hip(stream);
     const int kr = T == 16 ? 1 : (T == 32 ? 2 : (T == 64 ? 4 : 0));
     const int64_t gpw = ((k >> 7) + kWaves - 1) / kWaves;
-    // 1-2 tokens (and 3-4 on 16- and 32-row tiles): the diagonal MFMA kernel
-    if (kr && aligned(x_bf16, 8) && aligned(s_t, 8) && (m <= 2 || (m <= 4 && (kr < 4 || gpw > 4)))) {
+    // 1-4 tokens: the diagonal MFMA kernel (3-4 tokens on 64-row tiles: 7.6-8.0
+    // against 8.4 us for the kernel below at 14336 x 4096)
+    if (kr && aligned(x_bf16, 8) && aligned(s_t, 8) && m <= 4) {
         const DiagArgs a{x_bf16, static_cast<int>(m), packed_t, s_t, bias, n, k, y, nullptr, 0, 0};
         return launch_diag_r<kEpiPlain>(kr, gpw, tiles, st, a);
     }
-    // 3..16 tokens: the MFMA kernel where the tile is 16, 32 or 64 rows, the 16 waves'
+    // 5..16 tokens: the MFMA kernel where the tile is 16, 32 or 64 rows, the 16 waves'
     // K runs are at most 4 groups (K <= 8192) and x rows are 16-byte aligned
     if (m >= 3 && kr && gpw <= 4 && aligned(x_bf16, 16) && aligned(s_t, 8)) {
         const int mi = static_cast<int>(m);

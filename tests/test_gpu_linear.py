@@ -409,6 +409,32 @@ def test_mlp_decode_path(tq, oracle, m, d, f):
     assert_close(y, oracle.mlp_w4g128(xb, *args), RTOL, ATOL, f"mlp decode {m}x{d}x{f}")
 
 
+# The C ABI takes down copies of 16, 32 or 64 rows per tile.  16-row tiles run
+# the down projection per token pair (M = 1-2, 5-8) or per four tokens with K
+# split in two (M = 3-4); 64-row tiles always per token pair.
+@pytest.mark.parametrize("tile_rows", [16, 64])
+@pytest.mark.parametrize("m,d,f", [(1, 512, 1536), (2, 256, 384), (3, 512, 1024), (4, 1024, 640), (5, 256, 512),
+                                   (8, 384, 1152), (4, 4096, 14336), (2, 4096, 14336), (3, 640, 16384)])
+def test_mlp_decode_down_tile_heights(tq, oracle, tile_rows, m, d, f):
+    import torch
+    from theano_quantize import _abi
+    from theano_quantize._tensor import ptr, stream
+
+    print(f"decode FFN, {tile_rows}-row down tiles: M={m} D={d} F={f}", flush=True)
+    mlp, xb = _mlp_case(tq, m, d, f, seed=63)
+    gu_t, gu_st, _, _, _ = mlp.decode
+    dn_t, dn_st, t = tq.repack_i4_g128_tiled(mlp.down[0], mlp.down[1], tile_rows)
+    assert t == tile_rows
+    nb = int(_abi.lib().tq_mlp_w4g128_decode_workspace_bytes(m, d, f))
+    ws = torch.empty((nb,), dtype=torch.uint8, device="cuda")
+    x = bf16_dev(xb)
+    y = torch.full((m, d), float("nan"), dtype=torch.float32, device="cuda")
+    _abi.call("tq_mlp_w4g128_decode", ptr(x), m, d, f, ptr(gu_t), ptr(gu_st), ptr(dn_t), ptr(dn_st), tile_rows,
+              ptr(ws), nb, ptr(y), stream())
+    args = [a for w in (mlp.gate, mlp.up, mlp.down) for a in (host(w[0]), host(w[1]).view(np.uint16))]
+    assert_close(host(y), oracle.mlp_w4g128(xb, *args), RTOL, ATOL, f"mlp decode {tile_rows}-row down, {m}x{d}x{f}")
+
+
 def test_mlp_decode_and_prefill_agree_and_reuse_workspace(tq, oracle):
     """Both paths meet the tolerance on the same weights; one decode workspace
     serves calls of decreasing M; a short one is rejected."""

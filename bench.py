@@ -684,7 +684,7 @@ def main():
         log(f"w4a16 linear M=512 N=14336 K=4096: {ms * 1e3:.1f} us  {tf:.0f} TFLOP/s")
         del mlp, wsl, yl
 
-    # ------------------------------------ decode FFN (C5 weights, M = 1, 4)
+    # ------------------------------- decode FFN (C5 weights, M = 1, 2, 4, 8, 16)
     if not args.no_secondary and want("mlp_decode"):
         d5, f5 = 4096, 14336
         base = tq.QuantizedMLP.from_tensors(dt(normal_f32(4, (f5, d5), 0.02)), dt(normal_f32(4, (f5, d5), 0.02, 1)),
@@ -693,7 +693,7 @@ def main():
         copies = [base.decode] + [tuple(t.clone() if hasattr(t, "clone") else t for t in base.decode)
                                   for _ in range(rotation(wbytes) - 1)]
         res = {}
-        for md in (1, 2, 4, 8):
+        for md in (1, 2, 4, 8, 16):
             x = bf16(normal_f32(4, (md, d5), 1.0, stream=3))
             ws = torch.empty((base.workspace_bytes(md),), dtype=torch.uint8, device=dev)
             y = torch.empty((md, d5), dtype=torch.float32, device=dev)

@@ -312,8 +312,9 @@ int tq_mlp_w4g128(const uint16_t* x_bf16, int64_t m, int64_t d, int64_t f,
                   const uint8_t* down_packed, const uint16_t* down_s,
                   void* workspace, int64_t workspace_bytes, float* y, tq_stream_t stream);
 
-/* The same FFN for decode shapes (M <= 16; faster than tq_mlp_w4g128 up to
- * M = 8) on row-tiled copies of the weights (permutations of the packed bytes):
+/* The same FFN for decode shapes (M <= 16; at D = 4096, F = 14336 faster than
+ * tq_mlp_w4g128 at every such M: 35-60 against 134-136 us at M = 5-16) on
+ * row-tiled copies of the weights (permutations of the packed bytes):
  *   gate and up:  tq_repack_w4g128_gate_up_tiled -> 64-row tiles, tile t holding
  *                 gate rows 32t..32t+31 then up rows 32t..32t+31, padded to F
  *                 rounded up to 32 with zeros ((F+31)/32 * 64 * D/2 bytes and

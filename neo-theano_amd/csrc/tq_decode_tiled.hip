@@ -394,6 +394,60 @@ struct MlpRows {
     }
 };
 
+// Epilogues shared by the diagonal kernels; wsum(j, r) is the block's dot
+// product of token j with tile row r (the waves' partial sums added in order).
+template <class WSum>
+__device__ __forceinline__ void plain_epilogue(const WSum& wsum, int m, int T, int64_t tile, int64_t n,
+                                               const float* bias, float* y) {
+    for (int i = threadIdx.x; i < m * T; i += kBlock) {
+        const int j = i / T, r = i - j * T;
+        const int64_t row = tile * T + r;
+        if (row >= n) continue;
+        y[j * n + row] = wsum(j, r) + (bias ? bias[row] : 0.0f);
+    }
+}
+
+// kEpiGateUp for m <= 16 tokens of a 64-row gate/up tile (n = 2f stacked rows).
+template <class WSum>
+__device__ __forceinline__ void gate_up_epilogue(const WSum& wsum, int m, int64_t tile, int64_t n, uint16_t* hout,
+                                                 float* xsum, int tok0, int mtot, int rows_block, float* yz,
+                                                 int64_t yz_n) {
+    const int64_t f = n >> 1;  // h columns: the stacked weight has 2f rows, f % 32 == 0
+    const int lane = threadIdx.x & 63;
+    // thread i < 32 m: token i / 32, column 32 tile + i % 32, so that the 32
+    // columns of a token are one half of a wave (two whole DPP rows)
+    const int i = threadIdx.x;
+    if (i < m * 32) {
+        const int j = i >> 5, r = i & 31;
+        const int64_t hc = tile * 32 + r;
+        const float g = wsum(j, r), u = wsum(j, 32 + r);
+        const float h = g * (1.0f / (1.0f + __expf(-g))) * u;
+        const __bf16 hi = static_cast<__bf16>(h);
+        const __bf16 lo = static_cast<__bf16>(h - static_cast<float>(hi));
+        const int64_t J = tok0 + j, rh = MlpRows::hi(J, mtot, rows_block), rl = MlpRows::lo(J, mtot, rows_block);
+        hout[rh * f + h_slot(hc)] = __builtin_bit_cast(uint16_t, hi);
+        hout[rl * f + h_slot(hc)] = __builtin_bit_cast(uint16_t, lo);
+        const int sh = __float_as_int(lane_group_sum<16>(static_cast<float>(hi)));
+        const int sl = __float_as_int(lane_group_sum<16>(static_cast<float>(lo)));
+        auto half_sum = [&](int v) {  // rows 0 + 1 for lanes 0-31, rows 2 + 3 for lanes 32-63
+            const float a = __int_as_float(__builtin_amdgcn_readlane(v, 0)) +
+                            __int_as_float(__builtin_amdgcn_readlane(v, 16));
+            const float b = __int_as_float(__builtin_amdgcn_readlane(v, 32)) +
+                            __int_as_float(__builtin_amdgcn_readlane(v, 48));
+            return lane < 32 ? a : b;
+        };
+        const float th = half_sum(sh), tl = half_sum(sl);
+        if (r == 0) {
+            xsum[rh * (f >> 5) + tile] = th;
+            xsum[rl * (f >> 5) + tile] = tl;
+        }
+    }
+    // the output a K-split down projection accumulates into
+    for (int64_t q = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; q < yz_n;
+         q += static_cast<int64_t>(gridDim.x) * kBlock)
+        yz[q] = 0.0f;
+}
+
 template <int kR, int kM, int kGPW, int kWinD, int kEpi>
 __global__ __launch_bounds__(kBlock) void k_decode_diag(const uint16_t* __restrict__ x, int m,
                                                         const uint8_t* __restrict__ pt,
@@ -575,12 +629,7 @@ __global__ __launch_bounds__(kBlock) void k_decode_diag(const uint16_t* __restri
         return s;
     };
     if constexpr (kEpi == kEpiPlain) {
-        for (int i = threadIdx.x; i < m * T; i += kBlock) {
-            const int j = i / T, r = i - j * T;
-            const int64_t row = tile * T + r;
-            if (row >= n) continue;
-            y[j * n + row] = wsum(j, r) + (bias ? bias[row] : 0.0f);
-        }
+        plain_epilogue(wsum, m, T, tile, n, bias, y);
     } else if constexpr (kEpi == kEpiFold) {
         const int t = m >> 1;
         for (int i = threadIdx.x; i < t * T; i += kBlock) {
@@ -594,40 +643,182 @@ __global__ __launch_bounds__(kBlock) void k_decode_diag(const uint16_t* __restri
                 atomicAdd(&y[j * n + row], v);
         }
     } else {
-        const int64_t f = n >> 1;  // h columns: the stacked weight has 2f rows, f % 32 == 0
-        // thread i < 32 m (m <= 4): token i / 32, column 32 tile + i % 32, so that the
-        // 32 columns of a token are one half of a wave (two whole DPP rows)
-        const int i = threadIdx.x;
-        if (i < m * 32) {
-            const int j = i >> 5, r = i & 31;
-            const int64_t hc = tile * 32 + r;
-            const float g = wsum(j, r), u = wsum(j, 32 + r);
-            const float h = g * (1.0f / (1.0f + __expf(-g))) * u;
-            const __bf16 hi = static_cast<__bf16>(h);
-            const __bf16 lo = static_cast<__bf16>(h - static_cast<float>(hi));
-            const int64_t J = tok0 + j, rh = MlpRows::hi(J, mtot, rows_block), rl = MlpRows::lo(J, mtot, rows_block);
-            hout[rh * f + h_slot(hc)] = __builtin_bit_cast(uint16_t, hi);
-            hout[rl * f + h_slot(hc)] = __builtin_bit_cast(uint16_t, lo);
-            const int sh = __float_as_int(lane_group_sum<16>(static_cast<float>(hi)));
-            const int sl = __float_as_int(lane_group_sum<16>(static_cast<float>(lo)));
-            auto half_sum = [&](int v) {  // rows 0 + 1 for lanes 0-31, rows 2 + 3 for lanes 32-63
-                const float a = __int_as_float(__builtin_amdgcn_readlane(v, 0)) +
-                                __int_as_float(__builtin_amdgcn_readlane(v, 16));
-                const float b = __int_as_float(__builtin_amdgcn_readlane(v, 32)) +
-                                __int_as_float(__builtin_amdgcn_readlane(v, 48));
-                return lane < 32 ? a : b;
-            };
-            const float th = half_sum(sh), tl = half_sum(sl);
-            if (r == 0) {
-                xsum[rh * (f >> 5) + tile] = th;
-                xsum[rl * (f >> 5) + tile] = tl;
+        gate_up_epilogue(wsum, m, tile, n, hout, xsum, tok0, mtot, rows_block, yz, yz_n);
+    }
+}
+
+__device__ __forceinline__ f32x16 mfma32_bf16(u32x4 a, u32x4 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
+                                                   0, 0, 0);
+}
+
+// The diagonal kernel on v_mfma_f32_32x32x16_bf16, for the FFN's gate/up at 5-16
+// tokens: T = 32 kR rows per tile (kR = 2: 32 gate rows, then 32 up rows); the
+// MFMA's two k-groups (lanes 0-31, 32-63) are kR row groups of 32 rows times
+// 2 / kR chunks, and its 32 columns hold the (token, row group) pairs c = j kR +
+// row group, so a 64-row tile takes 16 tokens in one pass (the 16x16x32 form
+// stops at 4 and would read the weights once per 4 tokens).  A 32x32x16 MFMA
+// keeps the pipe twice as long per weight byte as a 16x16x32 one, so the plain
+// GEMV at 5-16 tokens stays on k_decode_tiled_mfma (measured faster: 8.8 against
+// 9.9 us at 5 tokens, 14336 x 4096).
+//
+// Lane l (kg = l / 32) loads, per step, the 16 bytes of tile row 32 (kg % kR) +
+// l % 32 at chunk kS step + kg / kR (kS = 2 / kR chunks per step) and feeds each
+// of their 4 dwords to one MFMA as A row l % 32 of k-group kg.  B lane (kg, c)
+// holds token c / kR's 8 values of that k-slice when c % kR == kg % kR, zeros
+// otherwise.  A lane of the result holds D[8 (q / 4) + 4 kg + q % 4][l % 32],
+// q = 0..15: 16 rows (four runs of four) of row group c % kR for token c / kR.
+// x staging (slot order, DPP group sums), group scales, the refill window and
+// the epilogues are those of k_decode_diag; no K split.  Each wave's partial
+// sums go to its own x strips once its loop is done (no other wave reads them).
+template <int kR, int kM, int kGPW, int kWinD, int kEpi>
+__global__ __launch_bounds__(kBlock) void k_decode_diag32(const uint16_t* __restrict__ x, int m,
+                                                          const uint8_t* __restrict__ pt,
+                                                          const uint16_t* __restrict__ st,
+                                                          const float* __restrict__ bias, int64_t n, int64_t k,
+                                                          float* __restrict__ y, uint16_t* __restrict__ hout,
+                                                          float* __restrict__ xsum, int tok0, int mtot,
+                                                          int rows_block, float* __restrict__ yz, int64_t yz_n) {
+    static_assert(kR == 2 && kEpi == kEpiGateUp, "gate/up tiles: 64 rows, two row groups of 32");
+    static_assert(kM * kR <= 32, "columns are (token, row group) pairs");
+    constexpr int T = 32 * kR;
+    constexpr int kS = 2 / kR;             // chunks per step
+    constexpr int kSPG = 4 / kS;           // steps per group
+    constexpr int kCPW = 4 * kGPW;         // chunks per wave
+    constexpr int kSteps = kCPW / kS;      // weight loads per lane
+    constexpr int kStrip = kCPW * 64;      // bytes of one token's slice (bf16)
+    constexpr int kStripP = kStrip + 16;   // padded, as in k_decode_diag
+    constexpr int kItems = kM * kCPW * 8;  // 4-element items of the slices
+    constexpr int kIPL = (kItems + kWave - 1) / kWave;
+    constexpr int kW = kWinD < kSteps ? kWinD : kSteps;
+    static_assert(T * 4 <= kStripP, "a wave's partial sums fit in its x strips");
+    __shared__ __attribute__((aligned(16))) uint8_t xs[kWaves][kM][kStripP];
+    __shared__ __attribute__((aligned(16))) uint8_t zs[kStrip];  // zeros, written by every wave
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int64_t tile = blockIdx.x;
+    const int64_t C = k >> 5, G = k >> 7;
+    const int64_t g0 = static_cast<int64_t>(wave) * kGPW, c0 = 4 * g0;
+    const int l32 = lane & 31, kg = lane >> 5;
+    const int rg = kg % kR, cs = kg / kR;  // this lane's row group and chunk slot (loads)
+    const int tok = l32 / kR;              // token of this lane's output column
+    const int rgc = l32 % kR;              // row group of this lane's output column
+    const int rbase = 32 * rgc + 4 * kg;   // its output rows: rbase + 8 r4 + e, r4, e = 0..3
+
+    // x items: item it -> token it / (8 kCPW), elements 4 (it % (8 kCPW)) .. + 3 of
+    // the wave's slice (clamped past K; zero past m)
+    uint2 xv[kIPL];
+#pragma unroll
+    for (int q = 0; q < kIPL; ++q) {
+        const int it = min(lane + kWave * q, kItems - 1);
+        const int j = it / (kCPW * 8), r = it - j * (kCPW * 8);
+        const int64_t kx = min<int64_t>(c0 * 32 + 4 * r, k - 4);
+        xv[q] = j < m ? *reinterpret_cast<const uint2*>(x + j * k + kx) : make_uint2(0u, 0u);
+    }
+    uint2 sc[kGPW][4];
+#pragma unroll
+    for (int g = 0; g < kGPW; ++g)
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4)
+            sc[g][r4] = *reinterpret_cast<const uint2*>(st + (tile * G + min<int64_t>(g0 + g, G - 1)) * T + rbase +
+                                                        8 * r4);
+    const uint8_t* wb = pt + (tile * C * T + 32 * rg + l32) * 16;
+    u32x4 w[kW];
+#pragma unroll
+    for (int i = 0; i < kW; ++i)
+        w[i] = __builtin_nontemporal_load(
+            reinterpret_cast<const u32x4*>(wb + min<int64_t>(c0 + i * kS + cs, 4 * G - 1) * T * 16));
+
+    for (int b = lane * 16; b < kStrip; b += kWave * 16) *reinterpret_cast<u32x4*>(&zs[b]) = u32x4{0u, 0u, 0u, 0u};
+    // stage: lanes 2b, 2b+1 hold an 8-block's (x0..x3) and (x4..x7); the even lane
+    // writes slots (x0,x4)(x1,x5), the odd lane (x2,x6)(x3,x7)
+    float gsum[kIPL];
+#pragma unroll
+    for (int q = 0; q < kIPL; ++q) {
+        const int it = lane + kWave * q;
+        const int itc = min(it, kItems - 1);
+        const int j = itc / (kCPW * 8), r = itc - j * (kCPW * 8);
+        const uint2 v = xv[q];
+        const uint2 p = make_uint2(dpp_u32<kDppXor1>(v.x), dpp_u32<kDppXor1>(v.y));
+        const bool odd = r & 1;
+        const uint32_t hi = odd ? v.y : p.x, lo = odd ? p.y : v.x;
+        if (it < kItems)
+            *reinterpret_cast<uint2*>(&xs[wave][j][(r >> 1) * 16 + (odd ? 8 : 0)]) =
+                make_uint2(__builtin_amdgcn_perm(hi, lo, 0x05040100u), __builtin_amdgcn_perm(hi, lo, 0x07060302u));
+        // a group is 32 consecutive items (half the wave): the sums of its two rows
+        gsum[q] = lane_group_sum<16>(bf16_lo(v.x) + bf16_hi(v.x) + bf16_lo(v.y) + bf16_hi(v.y));
+    }
+    float corr[kGPW];
+#pragma unroll
+    for (int g = 0; g < kGPW; ++g) {
+        float c = 0.0f;
+#pragma unroll
+        for (int j = 0; j < kM; ++j) {
+            const int it = j * kCPW * 8 + 32 * g;  // first item of (token j, group g)
+            const int src = __float_as_int(gsum[it / kWave]);
+            const float v = __int_as_float(__builtin_amdgcn_readlane(src, it % kWave)) +
+                            __int_as_float(__builtin_amdgcn_readlane(src, it % kWave + 16));
+            c = tok == j ? v : c;
+        }
+        corr[g] = 136.0f * c;
+    }
+    const bool diag = rgc == rg && tok < kM;
+    const uint8_t* bsrc = diag ? &xs[wave][tok][cs * 64] : &zs[0];
+
+    f32x16 tot = f32x16{};
+#pragma unroll
+    for (int g = 0; g < kGPW; ++g) {
+        const bool live = g0 + g < G;
+        f32x16 a0 = f32x16{}, a1 = f32x16{};
+#pragma unroll
+        for (int ss = 0; ss < kSPG; ++ss) {
+            const int i = kSPG * g + ss;  // step
+            const int slot = i % kW;
+            const uint32_t ws[4] = {w[slot].x, w[slot].y, w[slot].z, w[slot].w};
+#pragma unroll
+            for (int d = 0; d < 4; ++d) {
+                const u32x4 b = *reinterpret_cast<const u32x4*>(bsrc + (i * kS * 4 + d) * 16);
+                if (d & 1)
+                    a1 = mfma32_bf16(unpack_w4_136(ws[d]), b, a1);
+                else
+                    a0 = mfma32_bf16(unpack_w4_136(ws[d]), b, a0);
+            }
+            if (i + kW < kSteps) {
+                w[slot] = __builtin_nontemporal_load(
+                    reinterpret_cast<const u32x4*>(wb + min<int64_t>(c0 + (i + kW) * kS + cs, 4 * G - 1) * T * 16));
+                __builtin_amdgcn_sched_barrier(0);  // the refill is issued here, not after the group
             }
         }
-        // the output a K-split down projection accumulates into
-        for (int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; i < yz_n;
-             i += static_cast<int64_t>(gridDim.x) * kBlock)
-            yz[i] = 0.0f;
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4) {
+            const uint32_t s01 = live ? sc[g][r4].x : 0u, s23 = live ? sc[g][r4].y : 0u;
+            const float sv[4] = {__half2float(__ushort_as_half(static_cast<uint16_t>(s01))),
+                                 __half2float(__ushort_as_half(static_cast<uint16_t>(s01 >> 16))),
+                                 __half2float(__ushort_as_half(static_cast<uint16_t>(s23))),
+                                 __half2float(__ushort_as_half(static_cast<uint16_t>(s23 >> 16)))};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int q = 4 * r4 + e;
+                tot[q] = fmaf(sv[e], (a0[q] + a1[q]) - corr[g], tot[q]);
+            }
+        }
     }
+    // this wave's strips are dead: its partial sums, [token][tile row] f32, go there
+    float* part = reinterpret_cast<float*>(&xs[wave][0][0]);
+    if (tok < kM) {
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4)
+            *reinterpret_cast<f32x4*>(&part[tok * T + rbase + 8 * r4]) =
+                f32x4{tot[4 * r4], tot[4 * r4 + 1], tot[4 * r4 + 2], tot[4 * r4 + 3]};
+    }
+    __syncthreads();
+    auto wsum = [&](int j, int r) {
+        float s = 0.0f;
+#pragma unroll
+        for (int v = 0; v < kWaves; ++v) s += reinterpret_cast<const float*>(&xs[v][0][0])[j * T + r];
+        return s;
+    };
+    gate_up_epilogue(wsum, m, tile, n, hout, xsum, tok0, mtot, rows_block, yz, yz_n);
 }
 
 // kR in {1, 2, 4}; kM in {1, 2, 4} (3 tokens run as 4 with a zero token); groups per
@@ -657,8 +848,10 @@ int launch_diag(int64_t gpw, int64_t tiles, hipStream_t s, const DiagArgs& a) {
     // only the fold epilogue adds K parts; the others would store one part over another
     if (a.ksplit < 1 || (a.ksplit > 1 && kEpi != kEpiFold))
         return fail(TQ_EINVAL, "tq_gemv_w4g128_tiled: K split %d needs the accumulating epilogue", a.ksplit);
-    if (kEpi != kEpiPlain && (!a.xsum || !aligned(a.xsum, 16) || !aligned(a.x, 16) || a.k % 128 != 0))
+    if (kEpi == kEpiFold && (!a.xsum || !aligned(a.xsum, 16) || !aligned(a.x, 16) || a.k % 128 != 0))
         return fail(TQ_EINVAL, "tq_mlp_w4g128_decode: h rows and their sums must be 16-byte aligned");
+    if (kEpi == kEpiGateUp && (!a.xsum || !aligned(a.xsum, 4)))
+        return fail(TQ_EINVAL, "tq_mlp_w4g128_decode: no place for the block sums of h");
     const dim3 grid(static_cast<unsigned>(tiles), static_cast<unsigned>(a.ksplit));
 #define TQ_DIAG(G)                                                                                      \
     k_decode_diag<kR, kM, G, kWinD, kEpi><<<grid, kBlock, 0, s>>>(a.x, a.m, a.pt, a.st, a.b, a.n, a.k, a.y, \
@@ -695,6 +888,36 @@ int launch_diag_m(int64_t gpw, int64_t tiles, hipStream_t s, const DiagArgs& a) 
     if constexpr (kR <= 2 && kEpi == kEpiFold)
         if (a.m > 4) return launch_diag<kR, 8, kEpi>(gpw, tiles, s, a);  // 3-4 tokens' hi and lo rows
     return launch_diag<kR, 4, kEpi>(gpw, tiles, s, a);
+}
+
+// The 32x32 gate/up kernel for 5-16 tokens (rounded up to 8 or 16), at most 2
+// groups per wave (D <= 4096 over 16 waves; with more, x, its sums and the
+// scales held per lane would spill).
+constexpr bool diag32_fits(int64_t m, int64_t gpw) { return m >= 5 && m <= 16 && gpw <= 2; }
+
+template <int kR, int kM, int kEpi>
+int launch_diag32(int64_t gpw, int64_t tiles, hipStream_t s, const DiagArgs& a) {
+    if (a.ksplit != 1 || !diag32_fits(a.m, gpw))
+        return fail(TQ_EINVAL, "tq_gemv_w4g128_tiled: %d tokens at %lld groups per wave", a.m, (long long)gpw);
+    if (kEpi == kEpiGateUp && (!a.xsum || !aligned(a.xsum, 4)))
+        return fail(TQ_EINVAL, "tq_mlp_w4g128_decode: no place for the block sums of h");
+    const unsigned grid = static_cast<unsigned>(tiles);
+#define TQ_DIAG32(G)                                                                                          \
+    k_decode_diag32<kR, kM, G, 3, kEpi><<<grid, kBlock, 0, s>>>(a.x, a.m, a.pt, a.st, a.b, a.n, a.k, a.y, a.hout, \
+                                                                a.xsum, a.tok0, a.mtot, a.rows_block, a.yz,     \
+                                                                a.yz_n)
+    if (gpw <= 1)
+        TQ_DIAG32(1);
+    else
+        TQ_DIAG32(2);
+#undef TQ_DIAG32
+    return check_launch("tq_gemv_w4g128_tiled");
+}
+
+template <int kR, int kEpi>
+int launch_diag32_m(int64_t gpw, int64_t tiles, hipStream_t s, const DiagArgs& a) {
+    if (a.m <= 8) return launch_diag32<kR, 8, kEpi>(gpw, tiles, s, a);
+    return launch_diag32<kR, 16, kEpi>(gpw, tiles, s, a);
 }
 
 template <int kEpi>
@@ -970,7 +1193,20 @@ int mlp_decode(const char* fn, const uint16_t* x_bf16, int64_t m, int64_t d, int
     // halves fill 256 CUs in one round at D = 4096.
     const bool block = (kr == 1 && (mi == 3 || mi == 4)) || kr == 2;
     const int64_t gu_tiles = (f + 31) / 32, gu_gpw = ((d >> 7) + kWaves - 1) / kWaves;
-    for (int j0 = 0; j0 < mi; j0 += 4) {
+    // 5-16 tokens: one launch of the 32x32 kernel where its x strips fit the LDS
+    const bool gu32 = diag32_fits(mi, gu_gpw);
+    if (gu32) {
+        DiagArgs a{x_bf16, mi, gate_up_t, gate_up_s_t, nullptr, 2 * f, d, nullptr, h, 0, mi};
+        a.rows_block = block;
+        a.xsum = hsum;
+        if (block) {
+            a.yz = y;
+            a.yz_n = m * d;
+        }
+        const int rc = launch_diag32_m<2, kEpiGateUp>(gu_gpw, gu_tiles, st, a);
+        if (rc != TQ_OK) return rc;
+    }
+    for (int j0 = 0; j0 < mi && !gu32; j0 += 4) {
         const int mm = mi - j0 < 4 ? mi - j0 : 4;
         DiagArgs a{x_bf16 + j0 * d, mm, gate_up_t, gate_up_s_t, nullptr, 2 * f, d, nullptr, h, j0, mi};
         a.rows_block = block;

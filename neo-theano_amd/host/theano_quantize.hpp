@@ -394,10 +394,16 @@ class QuantizedMLP : public Module {
                                      hipStream_t stream = nullptr);
     size_t hidden() const { return d_; }
     size_t intermediate() const { return f_; }
-    // decode shapes (1 <= m <= kDecodeMaxM, D and F at most 16384) run
-    // tq_mlp_w4g128_decode on row-tiled copies of the weights, others tq_mlp_w4g128
-    static constexpr int64_t kDecodeMaxM = 8;
-    bool decode_path(int64_t m) const { return gu_tiled_.size() > 0 && m >= 1 && m <= kDecodeMaxM; }
+    // decode shapes (D and F at most 16384; 1 <= m <= 8, or m <= kDecodeMaxM where
+    // D <= kDecodeOnePassD, whose gate/up takes all tokens in one launch) run
+    // tq_mlp_w4g128_decode on row-tiled copies of the weights, others
+    // tq_mlp_w4g128 (at D = 4096, F = 14336: 35-60 us for 5-16 tokens against
+    // 134-136 us)
+    static constexpr int64_t kDecodeMaxM = 16;
+    static constexpr size_t kDecodeOnePassD = 4096;
+    bool decode_path(int64_t m) const {
+        return gu_tiled_.size() > 0 && m >= 1 && (m <= 8 || (m <= kDecodeMaxM && d_ <= kDecodeOnePassD));
+    }
 
    private:
     void make_decode_copies();

@@ -527,8 +527,8 @@ TEST_GPU(test_parity_quantized_linear_fp8) {
 }
 
 TEST_GPU(test_parity_quantized_mlp) {
-    // M = 1, 2, 4, 5 run the decode kernels (M = 4: one K-split down launch), M = 9
-    // the prefill FFN
+    // M = 1, 2, 4, 5, 9, 16 run the decode kernels (M = 4: one K-split down launch;
+    // M >= 5: one gate/up launch, D <= 4096), M = 17 the prefill FFN
     const size_t d = 256, f = 384;
     const auto gv = randn(f * d, 0.02, 61), uv = randn(f * d, 0.02, 62), dv = randn(d * f, 0.02, 63);
     const QuantizedMLP mlp = QuantizedMLP::from_tensors(Tensor::from_slice(gv, {f, d}), Tensor::from_slice(uv, {f, d}),
@@ -540,8 +540,8 @@ TEST_GPU(test_parity_quantized_mlp) {
     tqo_quantize_i4_g128(g32.data(), f, d, pg.data(), sg.data());
     tqo_quantize_i4_g128(u32.data(), f, d, pu.data(), su.data());
     tqo_quantize_i4_g128(d32.data(), d, f, pd.data(), sd.data());
-    for (size_t m : {1, 2, 4, 5, 9}) {
-        ASSERT(mlp.decode_path(static_cast<int64_t>(m)) == (m <= 8));
+    for (size_t m : {1, 2, 4, 5, 9, 16, 17}) {
+        ASSERT(mlp.decode_path(static_cast<int64_t>(m)) == (m <= 16));
         const auto xv = randn(m * d, 1.0, 64 + m);
         const auto y = mlp.forward(Tensor::from_slice(xv, {m, d})).to_vec_f64().unwrap();
         std::vector<uint16_t> xb(m * d);
@@ -549,7 +549,7 @@ TEST_GPU(test_parity_quantized_mlp) {
         std::vector<double> ref(m * d);
         tqo_mlp_w4g128(xb.data(), m, d, f, pg.data(), sg.data(), pu.data(), su.data(), pd.data(), sd.data(),
                        ref.data());
-        assert_close(y, ref, m <= 8 ? "mlp decode" : "mlp prefill");
+        assert_close(y, ref, m <= 16 ? "mlp decode" : "mlp prefill");
     }
 }
 

@@ -152,10 +152,10 @@ def test_gemv_w4g128_tiled_config3(tq, c3, m):
     assert_close(host(y), ref[:m], RTOL, ATOL, f"gemv_w4g128_tiled M={m} T={t}")
 
 
-# Tiles of 16, 32 or 64 rows: 1-2 tokens (3-4 on 16- and 32-row tiles, and on 64-row
-# tiles at K > 8192) run the diagonal MFMA kernel (one to eight groups per wave,
-# waves past K, tail tiles); 3-16 tokens otherwise the MFMA kernel with x from L2
-# (token passes, K <= 8192); other tile heights run the dot2 kernel.
+# Tiles of 16, 32 or 64 rows: 1-4 tokens run the diagonal MFMA kernel (one to
+# eight groups per wave, waves past K, tail tiles); 5-16 tokens the MFMA kernel
+# with x from L2 (token passes, K <= 8192); other tile heights run the dot2
+# kernel.
 @pytest.mark.parametrize("n,k,m,t", [(100, 128, 1, 8), (7, 2176, 2, 8), (256, 14336, 1, 16), (48, 16384, 3, 24),
                                      (1000, 4096, 4, 64), (333, 640, 2, 40),
                                      (1000, 4096, 5, 64), (70, 1024, 16, 16), (200, 6144, 7, 32),
@@ -388,15 +388,19 @@ def _mlp_case(tq, m, d, f, seed=57):
     return mlp, xb
 
 
-# Decode path (M <= 8): gate and up interleaved in 64-row tiles with SiLU * up in
-# the epilogue (4 tokens per launch), down on h as bf16 hi + lo rows in 32-row
-# tiles, one launch per four tokens with K split over two blocks per tile
-# (including F = 128 where the second block has no groups, and two launches for
-# M > 4); one to eight groups per wave, F not a multiple of 64, the Llama shape.
+# Decode path (M <= 8, and M <= 16 where D <= 4096): gate and up interleaved in
+# 64-row tiles with SiLU * up in the epilogue (4 tokens per launch up to M = 4;
+# 5-16 tokens in one launch of the 32x32 kernel where D <= 4096, else 4 per
+# launch), down on h as bf16 hi + lo rows in 32-row tiles, one launch per four
+# tokens with K split over two blocks per tile (including F = 128 where the
+# second block has no groups, and several launches for M > 4); one to eight
+# groups per wave, F not a multiple of 64, the Llama shape.
 @pytest.mark.parametrize("m,d,f", [(1, 128, 128), (2, 256, 384), (3, 512, 1024), (4, 1024, 640), (5, 256, 512),
                                    (7, 384, 1152), (8, 2048, 256), (1, 4096, 14336), (2, 14336, 4096),
                                    (6, 16384, 128), (3, 4096, 14336), (4, 4096, 14336), (4, 256, 128),
-                                   (3, 640, 16384), (6, 4096, 14336), (8, 4096, 14336), (2, 4096, 14336)])
+                                   (3, 640, 16384), (6, 4096, 14336), (8, 4096, 14336), (2, 4096, 14336),
+                                   (9, 256, 512), (12, 4096, 14336), (16, 1024, 640), (16, 4096, 14336),
+                                   (13, 128, 384), (7, 8192, 1024)])
 def test_mlp_decode_path(tq, oracle, m, d, f):
     wg = normal(60, (f, d), 0.02)
     wu = normal(60, (f, d), 0.02, stream=1)
@@ -404,6 +408,7 @@ def test_mlp_decode_path(tq, oracle, m, d, f):
     xb = to_bf16_bits(normal(60, (m, d), 1.0, stream=3))
     mlp = tq.QuantizedMLP.from_tensors(dev_tensor(wg), dev_tensor(wu), dev_tensor(wd))
     assert mlp._decode_path(m)
+    assert mlp._decode_path(16) == (d <= 4096) and not mlp._decode_path(17)
     y = host(mlp(bf16_dev(xb)))
     args = [a for t in (mlp.gate, mlp.up, mlp.down) for a in (host(t[0]), host(t[1]).view(np.uint16))]
     assert_close(y, oracle.mlp_w4g128(xb, *args), RTOL, ATOL, f"mlp decode {m}x{d}x{f}")

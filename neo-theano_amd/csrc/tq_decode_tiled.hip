@@ -217,7 +217,20 @@ __device__ __forceinline__ f32x4 mfma16_bf16(u32x4 a, u32x4 b, f32x4 c) {
                                                    0, 0, 0);
 }
 
-// MFMA kernel for 3..16 tokens.  Block: one tile of T = 16 kR rows; its 16 waves
+// Packed dword (nibbles k..k+7, two's complement) -> bf16 136 + q in the slot
+// order (k, k+4), (k+1, k+5), (k+2, k+6), (k+3, k+7): nibble pair s of the dword
+// sits at bits 4s and 16 + 4s, so a shift, a mask and an xor (which turns the
+// nibble into q + 8 and sets the exponent of 128) make each slot pair.
+__device__ __forceinline__ u32x4 unpack_w4_136(uint32_t w) {
+    u32x4 a;
+    a.x = (w & 0x000F000Fu) ^ 0x43084308u;
+    a.y = ((w >> 4) & 0x000F000Fu) ^ 0x43084308u;
+    a.z = ((w >> 8) & 0x000F000Fu) ^ 0x43084308u;
+    a.w = ((w >> 12) & 0x000F000Fu) ^ 0x43084308u;
+    return a;
+}
+
+// MFMA kernel for 5..16 tokens.  Block: one tile of T = 16 kR rows; its 16 waves
 // split K into runs of kGPW groups (no LDS staging of x, no barrier before the
 // arithmetic: every wave issues all of its loads at once and consumes them in
 // order).  Lane (r16 = l % 16, q = l / 16) holds, per group g, the 16 bytes of
@@ -229,7 +242,13 @@ __device__ __forceinline__ f32x4 mfma16_bf16(u32x4 a, u32x4 b, f32x4 c) {
 // of the group for every token, the start value of each row group's chain, so
 // the offset cancels inside the MFMA accumulator; the f16 scale is applied per
 // group, the factor 1/8 at the end.  The K runs meet in LDS in a fixed order.
-template <int kR, int kGPW>
+// kFold: the decode FFN's down projection on h as kEpiGateUp wrote it (each
+// 8-block in the slot order of unpack_w4_136, which then unpacks the weights as
+// 136 + q, with -136 as the constant operand and no factor), m = 2t rows of t
+// tokens (hi rows, then lo rows) whose two halves are added per token, and K
+// split over gridDim.y blocks per tile added into a zeroed y (two addends onto
+// zero: the same sum in either order).
+template <int kR, int kGPW, bool kFold = false>
 __global__ __launch_bounds__(kBlock) void k_decode_tiled_mfma(const uint16_t* __restrict__ x, int m,
                                                               const uint8_t* __restrict__ pt,
                                                               const uint16_t* __restrict__ st,
@@ -242,15 +261,18 @@ __global__ __launch_bounds__(kBlock) void k_decode_tiled_mfma(const uint16_t* __
     const int q = lane >> 4, r16 = lane & 15;
     const int64_t tile = blockIdx.x;
     const int64_t C = k >> 5, G = k >> 7;
-    const int64_t g0 = static_cast<int64_t>(wave) * kGPW;
+    // K split over gridDim.y blocks per tile: this block takes groups [gb, ge)
+    const int64_t gh = (G + gridDim.y - 1) / gridDim.y, gb = blockIdx.y * gh, ge = min(G, gb + gh);
+    const int64_t g0 = gb + static_cast<int64_t>(wave) * kGPW;
 
-    // x of token r16 (zero past m); groups past G are clamped (and skipped below)
+    // x of token r16 (zero past m); groups past ge are clamped (and skipped below)
     u32x4 xf[kGPW][4];
     const bool tok = r16 < m;
     const uint16_t* xr = x + static_cast<int64_t>(tok ? r16 : 0) * k + 32 * q;
+    const int64_t gl = max<int64_t>(ge - 1, 0);  // last group of the block (clamp target)
 #pragma unroll
     for (int i = 0; i < kGPW; ++i) {
-        const int64_t g = min<int64_t>(g0 + i, G - 1);
+        const int64_t g = min<int64_t>(g0 + i, gl);
 #pragma unroll
         for (int j = 0; j < 4; ++j)
             xf[i][j] = tok ? *reinterpret_cast<const u32x4*>(xr + g * 128 + 8 * j) : u32x4{0u, 0u, 0u, 0u};
@@ -259,7 +281,7 @@ __global__ __launch_bounds__(kBlock) void k_decode_tiled_mfma(const uint16_t* __
     uint2 sc[kGPW][kR];
 #pragma unroll
     for (int i = 0; i < kGPW; ++i) {
-        const int64_t g = min<int64_t>(g0 + i, G - 1);
+        const int64_t g = min<int64_t>(g0 + i, gl);
 #pragma unroll
         for (int r = 0; r < kR; ++r)
             sc[i][r] = *reinterpret_cast<const uint2*>(st + (tile * G + g) * T + 16 * r + 4 * q);
@@ -269,22 +291,24 @@ __global__ __launch_bounds__(kBlock) void k_decode_tiled_mfma(const uint16_t* __
     u32x4 w[kGPW][kR];
 #pragma unroll
     for (int i = 0; i < kGPW; ++i) {
-        const int64_t g = min<int64_t>(g0 + i, G - 1);
+        const int64_t g = min<int64_t>(g0 + i, gl);
 #pragma unroll
         for (int r = 0; r < kR; ++r)
             w[i][r] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wb + ((4 * g + q) * T + 16 * r) * 16));
     }
 
-    const u32x4 aoff = u32x4{0xC340C340u, 0xC340C340u, 0xC340C340u, 0xC340C340u};  // bf16 -192
+    // bf16 -136 (kFold) or -192: minus the offset of the unpacked weights
+    const u32x4 aoff = kFold ? u32x4{0xC308C308u, 0xC308C308u, 0xC308C308u, 0xC308C308u}
+                             : u32x4{0xC340C340u, 0xC340C340u, 0xC340C340u, 0xC340C340u};
     f32x4 acc[kR];
 #pragma unroll
     for (int r = 0; r < kR; ++r) acc[r] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int i = 0; i < kGPW; ++i) {
-        if (g0 + i >= G) break;  // wave-uniform
+        if (g0 + i >= ge) break;  // wave-uniform
         u32x4 xb[4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) xb[j] = pair_slots(xf[i][j]);
+        for (int j = 0; j < 4; ++j) xb[j] = kFold ? xf[i][j] : pair_slots(xf[i][j]);
         f32x4 xs = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int j = 0; j < 4; ++j) xs = mfma16_bf16(aoff, xb[j], xs);
@@ -293,7 +317,7 @@ __global__ __launch_bounds__(kBlock) void k_decode_tiled_mfma(const uint16_t* __
             const uint32_t ws[4] = {w[i][r].x, w[i][r].y, w[i][r].z, w[i][r].w};
             f32x4 d = xs;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) d = mfma16_bf16(unpack_w4_24(ws[j]), xb[j], d);
+            for (int j = 0; j < 4; ++j) d = mfma16_bf16(kFold ? unpack_w4_136(ws[j]) : unpack_w4_24(ws[j]), xb[j], d);
             const uint32_t s01 = sc[i][r].x, s23 = sc[i][r].y;
             acc[r].x = fmaf(__half2float(__ushort_as_half(static_cast<uint16_t>(s01))), d.x, acc[r].x);
             acc[r].y = fmaf(__half2float(__ushort_as_half(static_cast<uint16_t>(s01 >> 16))), d.y, acc[r].y);
@@ -307,28 +331,32 @@ __global__ __launch_bounds__(kBlock) void k_decode_tiled_mfma(const uint16_t* __
 #pragma unroll
         for (int e = 0; e < 4; ++e) part[wave][16 * r + 4 * q + e][r16] = acc[r][e];
     __syncthreads();
-    for (int i = threadIdx.x; i < T * m; i += kBlock) {
-        const int row = i / m, t = i - row * m;
-        const int64_t grow = tile * T + row;
-        if (grow >= n) continue;
+    auto wsum = [&](int row, int t) {
         float sum = 0.0f;
 #pragma unroll
         for (int v = 0; v < kWaves; ++v) sum += part[v][row][t];
-        y[t * n + grow] = 0.125f * sum + (bias ? bias[grow] : 0.0f);
+        return sum;
+    };
+    if constexpr (kFold) {
+        const int tt = m >> 1;
+        for (int i = threadIdx.x; i < T * tt; i += kBlock) {
+            const int row = i / tt, t = i - row * tt;
+            const int64_t grow = tile * T + row;
+            if (grow >= n) continue;
+            const float v = (wsum(row, t) + wsum(row, tt + t)) + (bias && blockIdx.y == 0 ? bias[grow] : 0.0f);
+            if (gridDim.y == 1)
+                y[t * n + grow] = v;
+            else
+                atomicAdd(&y[t * n + grow], v);
+        }
+    } else {
+        for (int i = threadIdx.x; i < T * m; i += kBlock) {
+            const int row = i / m, t = i - row * m;
+            const int64_t grow = tile * T + row;
+            if (grow >= n) continue;
+            y[t * n + grow] = 0.125f * wsum(row, t) + (bias ? bias[grow] : 0.0f);
+        }
     }
-}
-
-// Packed dword (nibbles k..k+7, two's complement) -> bf16 136 + q in the slot
-// order (k, k+4), (k+1, k+5), (k+2, k+6), (k+3, k+7): nibble pair s of the dword
-// sits at bits 4s and 16 + 4s, so a shift, a mask and an xor (which turns the
-// nibble into q + 8 and sets the exponent of 128) make each slot pair.
-__device__ __forceinline__ u32x4 unpack_w4_136(uint32_t w) {
-    u32x4 a;
-    a.x = (w & 0x000F000Fu) ^ 0x43084308u;
-    a.y = ((w >> 4) & 0x000F000Fu) ^ 0x43084308u;
-    a.z = ((w >> 8) & 0x000F000Fu) ^ 0x43084308u;
-    a.w = ((w >> 12) & 0x000F000Fu) ^ 0x43084308u;
-    return a;
 }
 
 // Decode kernel for 1..kM tokens (kM * kR <= 16), T = 16 kR rows per tile.
@@ -367,13 +395,6 @@ __device__ __forceinline__ u32x4 unpack_w4_136(uint32_t w) {
 //              32 lo values to xsum[row][tile].
 enum DiagEpi { kEpiPlain = 0, kEpiFold = 1, kEpiGateUp = 2 };
 
-// Rows of the down projection's bf16 input for token J of an m-token FFN.
-// Pairs (`block` unset): pair c = J / 2 with t = min(2, m - 2c) tokens occupies
-// rows 4c .. 4c + 2t - 1 as (hi of its tokens, lo of its tokens), so each pair
-// is one kEpiFold launch of 2t contiguous rows.
-// Quads (`block` set): the same with blocks of up to four tokens, block c = J / 4
-// with t = min(4, m - 4c) tokens at rows 8c .. 8c + 2t - 1; for m <= 4 that is
-// the m hi rows, then the m lo rows.
 // Position of h column c in its row: 8-blocks in slot order, columns 8b + e at
 // 8b + 2e (e < 4) and 8b + 2(e - 4) + 1 (e >= 4).
 __host__ __device__ inline int64_t h_slot(int64_t c) { return (c & ~int64_t{7}) | ((c & 3) << 1) | ((c >> 2) & 1); }
@@ -383,12 +404,14 @@ __host__ __device__ inline int64_t h_slot(int64_t c) { return (c & ~int64_t{7}) 
 constexpr int64_t round_up256(int64_t b) { return (b + 255) / 256 * 256; }
 constexpr int64_t mlp_h_bytes(int64_t m, int64_t f) { return round_up256(2 * m * f * 2); }
 
+// Rows of the down projection's bf16 input for token J of an m-token FFN, in
+// groups of q tokens (q = 2, 4 or 8; one down launch per group): group c = J / q
+// with t = min(q, m - q c) tokens occupies rows 2 q c .. 2 q c + 2t - 1 as (hi of
+// its tokens, lo of its tokens), so each group is one launch of 2t contiguous
+// rows; for m <= q that is the m hi rows, then the m lo rows.
 struct MlpRows {
-    __host__ __device__ static int64_t hi(int64_t j, int64_t m, bool block) {
-        return block ? 8 * (j / 4) + (j % 4) : 4 * (j / 2) + (j % 2);
-    }
-    __host__ __device__ static int64_t lo(int64_t j, int64_t m, bool block) {
-        const int64_t q = block ? 4 : 2;
+    __host__ __device__ static int64_t hi(int64_t j, int64_t m, int q) { return 2 * q * (j / q) + (j % q); }
+    __host__ __device__ static int64_t lo(int64_t j, int64_t m, int q) {
         const int64_t c = j / q, t = m - q * c < q ? m - q * c : q;
         return 2 * q * c + t + (j % q);
     }
@@ -410,7 +433,7 @@ __device__ __forceinline__ void plain_epilogue(const WSum& wsum, int m, int T, i
 // kEpiGateUp for m <= 16 tokens of a 64-row gate/up tile (n = 2f stacked rows).
 template <class WSum>
 __device__ __forceinline__ void gate_up_epilogue(const WSum& wsum, int m, int64_t tile, int64_t n, uint16_t* hout,
-                                                 float* xsum, int tok0, int mtot, int rows_block, float* yz,
+                                                 float* xsum, int tok0, int mtot, int rows_group, float* yz,
                                                  int64_t yz_n) {
     const int64_t f = n >> 1;  // h columns: the stacked weight has 2f rows, f % 32 == 0
     const int lane = threadIdx.x & 63;
@@ -424,7 +447,7 @@ __device__ __forceinline__ void gate_up_epilogue(const WSum& wsum, int m, int64_
         const float h = g * (1.0f / (1.0f + __expf(-g))) * u;
         const __bf16 hi = static_cast<__bf16>(h);
         const __bf16 lo = static_cast<__bf16>(h - static_cast<float>(hi));
-        const int64_t J = tok0 + j, rh = MlpRows::hi(J, mtot, rows_block), rl = MlpRows::lo(J, mtot, rows_block);
+        const int64_t J = tok0 + j, rh = MlpRows::hi(J, mtot, rows_group), rl = MlpRows::lo(J, mtot, rows_group);
         hout[rh * f + h_slot(hc)] = __builtin_bit_cast(uint16_t, hi);
         hout[rl * f + h_slot(hc)] = __builtin_bit_cast(uint16_t, lo);
         const int sh = __float_as_int(lane_group_sum<16>(static_cast<float>(hi)));
@@ -454,7 +477,7 @@ __global__ __launch_bounds__(kBlock) void k_decode_diag(const uint16_t* __restri
                                                         const uint16_t* __restrict__ st,
                                                         const float* __restrict__ bias, int64_t n, int64_t k,
                                                         float* __restrict__ y, uint16_t* __restrict__ hout,
-                                                        float* __restrict__ xsum, int tok0, int mtot, int rows_block,
+                                                        float* __restrict__ xsum, int tok0, int mtot, int rows_group,
                                                         float* __restrict__ yz, int64_t yz_n) {
     static_assert(kM * kR <= 16, "columns are (token, row group) pairs");
     static_assert(kEpi != kEpiGateUp || kR == 4, "gate/up tiles are 64 rows");
@@ -643,7 +666,7 @@ __global__ __launch_bounds__(kBlock) void k_decode_diag(const uint16_t* __restri
                 atomicAdd(&y[j * n + row], v);
         }
     } else {
-        gate_up_epilogue(wsum, m, tile, n, hout, xsum, tok0, mtot, rows_block, yz, yz_n);
+        gate_up_epilogue(wsum, m, tile, n, hout, xsum, tok0, mtot, rows_group, yz, yz_n);
     }
 }
 
@@ -678,7 +701,7 @@ __global__ __launch_bounds__(kBlock) void k_decode_diag32(const uint16_t* __rest
                                                           const float* __restrict__ bias, int64_t n, int64_t k,
                                                           float* __restrict__ y, uint16_t* __restrict__ hout,
                                                           float* __restrict__ xsum, int tok0, int mtot,
-                                                          int rows_block, float* __restrict__ yz, int64_t yz_n) {
+                                                          int rows_group, float* __restrict__ yz, int64_t yz_n) {
     static_assert(kR == 2 && kEpi == kEpiGateUp, "gate/up tiles: 64 rows, two row groups of 32");
     static_assert(kM * kR <= 32, "columns are (token, row group) pairs");
     constexpr int T = 32 * kR;
@@ -818,7 +841,7 @@ __global__ __launch_bounds__(kBlock) void k_decode_diag32(const uint16_t* __rest
         for (int v = 0; v < kWaves; ++v) s += reinterpret_cast<const float*>(&xs[v][0][0])[j * T + r];
         return s;
     };
-    gate_up_epilogue(wsum, m, tile, n, hout, xsum, tok0, mtot, rows_block, yz, yz_n);
+    gate_up_epilogue(wsum, m, tile, n, hout, xsum, tok0, mtot, rows_group, yz, yz_n);
 }
 
 // kR in {1, 2, 4}; kM in {1, 2, 4} (3 tokens run as 4 with a zero token); groups per
@@ -833,7 +856,7 @@ struct DiagArgs {
     float* y;
     uint16_t* hout;  // kEpiGateUp
     int tok0, mtot;  // kEpiGateUp
-    int rows_block = 0;      // kEpiGateUp: MlpRows layout
+    int rows_group = 2;      // kEpiGateUp: tokens per MlpRows group
     float* xsum = nullptr;   // kEpiGateUp: h's 32-column sums out; kEpiFold: x's in
     float* yz = nullptr;     // kEpiGateUp: zeroed (yz_n floats)
     int64_t yz_n = 0;
@@ -856,7 +879,7 @@ int launch_diag(int64_t gpw, int64_t tiles, hipStream_t s, const DiagArgs& a) {
 #define TQ_DIAG(G)                                                                                      \
     k_decode_diag<kR, kM, G, kWinD, kEpi><<<grid, kBlock, 0, s>>>(a.x, a.m, a.pt, a.st, a.b, a.n, a.k, a.y, \
                                                                   a.hout, a.xsum, a.tok0, a.mtot,           \
-                                                                  a.rows_block, a.yz, a.yz_n)
+                                                                  a.rows_group, a.yz, a.yz_n)
     // the exact groups per wave, so that no wave of the block runs dead groups (K =
     // 14336, the Llama FFN's intermediate size, is 7 per wave)
     switch (gpw) {
@@ -904,7 +927,7 @@ int launch_diag32(int64_t gpw, int64_t tiles, hipStream_t s, const DiagArgs& a) 
     const unsigned grid = static_cast<unsigned>(tiles);
 #define TQ_DIAG32(G)                                                                                          \
     k_decode_diag32<kR, kM, G, 3, kEpi><<<grid, kBlock, 0, s>>>(a.x, a.m, a.pt, a.st, a.b, a.n, a.k, a.y, a.hout, \
-                                                                a.xsum, a.tok0, a.mtot, a.rows_block, a.yz,     \
+                                                                a.xsum, a.tok0, a.mtot, a.rows_group, a.yz,     \
                                                                 a.yz_n)
     if (gpw <= 1)
         TQ_DIAG32(1);
@@ -938,6 +961,24 @@ int launch_mfma(int64_t gpw, int64_t tiles, hipStream_t s, const uint16_t* x, in
     else
         k_decode_tiled_mfma<kR, 4><<<grid, kBlock, 0, s>>>(x, m, pt, st, b, n, k, y);
     return check_launch("tq_gemv_w4g128_tiled");
+}
+
+// The decode FFN's down projection for up to 8 tokens per launch (2t <= 16 rows of
+// h): the MFMA kernel in fold mode, K split in two onto a zeroed y; gpw is the
+// groups per wave of one K half.
+template <int kR>
+int launch_mfma_fold(int64_t gpw, int64_t tiles, hipStream_t s, const uint16_t* h, int rows, const uint8_t* pt,
+                     const uint16_t* st, int64_t n, int64_t k, float* y) {
+    if (gpw > 4 || rows > 16 || rows % 2 != 0)
+        return fail(TQ_EINVAL, "tq_mlp_w4g128_decode: %d rows of h at %lld groups per wave", rows, (long long)gpw);
+    const dim3 grid(static_cast<unsigned>(tiles), 2u);
+    if (gpw <= 1)
+        k_decode_tiled_mfma<kR, 1, true><<<grid, kBlock, 0, s>>>(h, rows, pt, st, nullptr, n, k, y);
+    else if (gpw <= 2)
+        k_decode_tiled_mfma<kR, 2, true><<<grid, kBlock, 0, s>>>(h, rows, pt, st, nullptr, n, k, y);
+    else
+        k_decode_tiled_mfma<kR, 4, true><<<grid, kBlock, 0, s>>>(h, rows, pt, st, nullptr, n, k, y);
+    return check_launch("tq_mlp_w4g128_decode");
 }
 
 // Repack into the tiled layout through LDS: a block takes 2048 / T chunks (rounded
@@ -1189,15 +1230,20 @@ int mlp_decode(const char* fn, const uint16_t* x_bf16, int64_t m, int64_t d, int
     // Quads: one down launch per four tokens (their 2t hi/lo rows as MFMA
     // columns), K split over two blocks per tile so that the x rows fit the LDS;
     // the gate/up launch zeroes y for the two halves.  Taken for 3-4 tokens on
-    // 16-row down tiles and for every M on 32-row tiles, whose 128 tiles x 2 K
+    // 16-row down tiles and for 1-4 tokens on 32-row tiles, whose 128 tiles x 2 K
     // halves fill 256 CUs in one round at D = 4096.
     const bool block = (kr == 1 && (mi == 3 || mi == 4)) || kr == 2;
+    // Octets (5-16 tokens on 32-row down tiles): one down launch per eight tokens,
+    // their 2t <= 16 rows as the columns of the MFMA kernel (x read from L2, no
+    // LDS strips to fit), K split in two as for quads.
+    const bool octets = kr == 2 && mi >= 5;
+    const int group = octets ? 8 : (block ? 4 : 2);  // tokens per MlpRows group
     const int64_t gu_tiles = (f + 31) / 32, gu_gpw = ((d >> 7) + kWaves - 1) / kWaves;
     // 5-16 tokens: one launch of the 32x32 kernel where its x strips fit the LDS
     const bool gu32 = diag32_fits(mi, gu_gpw);
     if (gu32) {
         DiagArgs a{x_bf16, mi, gate_up_t, gate_up_s_t, nullptr, 2 * f, d, nullptr, h, 0, mi};
-        a.rows_block = block;
+        a.rows_group = group;
         a.xsum = hsum;
         if (block) {
             a.yz = y;
@@ -1209,7 +1255,7 @@ int mlp_decode(const char* fn, const uint16_t* x_bf16, int64_t m, int64_t d, int
     for (int j0 = 0; j0 < mi && !gu32; j0 += 4) {
         const int mm = mi - j0 < 4 ? mi - j0 : 4;
         DiagArgs a{x_bf16 + j0 * d, mm, gate_up_t, gate_up_s_t, nullptr, 2 * f, d, nullptr, h, j0, mi};
-        a.rows_block = block;
+        a.rows_group = group;
         a.xsum = hsum;
         if (block && j0 == 0) {
             a.yz = y;
@@ -1219,8 +1265,17 @@ int mlp_decode(const char* fn, const uint16_t* x_bf16, int64_t m, int64_t d, int
         if (rc != TQ_OK) return rc;
     }
     const int64_t dn_tiles = (d + down_tile_rows - 1) / down_tile_rows, dn_gpw = ((f >> 7) + kWaves - 1) / kWaves;
+    const int64_t gpw2 = (((f >> 7) + 1) / 2 + kWaves - 1) / kWaves;  // of a K half
+    if (octets) {
+        for (int c = 0; 8 * c < mi; ++c) {
+            const int t = mi - 8 * c < 8 ? mi - 8 * c : 8;
+            const int rc = launch_mfma_fold<2>(gpw2, dn_tiles, st, h + 16 * c * f, 2 * t, down_t, down_s_t, d, f,
+                                               y + 8 * c * d);
+            if (rc != TQ_OK) return rc;
+        }
+        return TQ_OK;
+    }
     if (block) {
-        const int64_t gpw2 = (((f >> 7) + 1) / 2 + kWaves - 1) / kWaves;
         for (int c = 0; 4 * c < mi; ++c) {
             const int t = mi - 4 * c < 4 ? mi - 4 * c : 4;
             DiagArgs a{h + 8 * c * f, 2 * t, down_t, down_s_t, nullptr, d, f, y + 4 * c * d, nullptr, 0, 0};

@@ -563,7 +563,7 @@ Result<QuantizedLinear> QuantizedLinear::from_tensors(const Tensor& weight, cons
 
 size_t QuantizedLinear::workspace_bytes(int64_t m) const {
     if (mode_ == Mode::FP8 && m <= 16) return static_cast<size_t>(m) * in_ * sizeof(float);
-    if (mode_ != Mode::W4 || m <= 16) return 0;
+    if (mode_ != Mode::W4 || m <= 16 || (w4_.tile_rows > 0 && m <= kTiledPassesMaxM)) return 0;
     return static_cast<size_t>(tq_gemm_w4g128_bf16_workspace_bytes(m, static_cast<int64_t>(in_)));
 }
 
@@ -576,10 +576,13 @@ Result<void> QuantizedLinear::forward_device(const void* x, int64_t m, float* y,
     switch (mode_) {
         case Mode::W4: {
             const auto* xb = static_cast<const uint16_t*>(x);
-            if (m <= 16 && w4_.tile_rows > 0)
-                st = tq_gemv_w4g128_tiled(xb, m, w4_.packed_tiled.data(), w4_.scales_tiled.data(), b, n, k,
-                                          w4_.tile_rows, y, ts);
-            else if (m <= 16)
+            if (m <= kTiledPassesMaxM && w4_.tile_rows > 0) {
+                for (int64_t m0 = 0; m0 < m && st == TQ_OK; m0 += 16) {
+                    const int64_t mm = std::min<int64_t>(16, m - m0);
+                    st = tq_gemv_w4g128_tiled(xb + m0 * k, mm, w4_.packed_tiled.data(), w4_.scales_tiled.data(), b,
+                                              n, k, w4_.tile_rows, y + m0 * n, ts);
+                }
+            } else if (m <= 16)
                 st = tq_gemv_w4g128(xb, m, w4_.packed.data(), w4_.scales.data(), b, n, k, y, ts);
             else if (workspace)
                 st = tq_gemm_w4g128_bf16_ws(xb, m, w4_.packed.data(), w4_.scales.data(), b, n, k, workspace,
@@ -779,8 +782,8 @@ void QuantizedMLP::make_decode_copies() {
 
 size_t QuantizedMLP::workspace_bytes(int64_t m) const {
     if (decode_path(m))
-        return static_cast<size_t>(
-            tq_mlp_w4g128_decode_workspace_bytes(m, static_cast<int64_t>(d_), static_cast<int64_t>(f_)));
+        return static_cast<size_t>(tq_mlp_w4g128_decode_workspace_bytes(
+            std::min<int64_t>(m, kDecodePassM), static_cast<int64_t>(d_), static_cast<int64_t>(f_)));
     return static_cast<size_t>(
         tq_mlp_w4g128_workspace_bytes(m, static_cast<int64_t>(d_), static_cast<int64_t>(f_)));
 }
@@ -788,12 +791,17 @@ size_t QuantizedMLP::workspace_bytes(int64_t m) const {
 Result<void> QuantizedMLP::forward_device(const uint16_t* x, int64_t m, void* workspace, size_t workspace_bytes,
                                           float* y, hipStream_t stream) const {
     if (decode_path(m)) {
-        const int st = tq_mlp_w4g128_decode(x, m, static_cast<int64_t>(d_), static_cast<int64_t>(f_), gu_tiled_.data(),
-                                            gu_scales_tiled_.data(), down_.packed_tiled.data(),
-                                            down_.scales_tiled.data(), down_.tile_rows, workspace,
-                                            static_cast<int64_t>(workspace_bytes), y,
-                                            reinterpret_cast<tq_stream_t>(stream));
-        if (st != TQ_OK) return TheanoError::from_status(st, "QuantizedMLP::forward");
+        const int64_t d = static_cast<int64_t>(d_);
+        // passes of kDecodePassM tokens, ordered on the stream, share the workspace
+        for (int64_t m0 = 0; m0 < m; m0 += kDecodePassM) {
+            const int64_t mm = std::min<int64_t>(kDecodePassM, m - m0);
+            const int st = tq_mlp_w4g128_decode(x + m0 * d, mm, d, static_cast<int64_t>(f_), gu_tiled_.data(),
+                                                gu_scales_tiled_.data(), down_.packed_tiled.data(),
+                                                down_.scales_tiled.data(), down_.tile_rows, workspace,
+                                                static_cast<int64_t>(workspace_bytes), y + m0 * d,
+                                                reinterpret_cast<tq_stream_t>(stream));
+            if (st != TQ_OK) return TheanoError::from_status(st, "QuantizedMLP::forward");
+        }
         return {};
     }
     const int st = tq_mlp_w4g128(x, m, static_cast<int64_t>(d_), static_cast<int64_t>(f_), gate_.packed.data(),

@@ -339,13 +339,17 @@ class QuantizedLinear : public Module {
     // (f32 [m]) device scratch.  With m <= 16 both quantize x inside the decode
     // GEMV (tq_gemv_w8a8 / tq_gemv_fp8a8) when K % 16 == 0, K <= 8192 and x is
     // 16-byte aligned; otherwise fp8 runs the GEMV on the fake-quantized
-    // activations held in `workspace` (workspace_bytes(m) bytes).  w4 with
-    // m > 16 uses `workspace` (workspace_bytes(m) bytes) when given.
+    // activations held in `workspace` (workspace_bytes(m) bytes).  w4 runs the
+    // tiled GEMV in passes of 16 tokens up to m = kTiledPassesMaxM (at N = 14336,
+    // K = 4096: 22 / 42 us at m = 32 / 64 against 40 / 50 us for the prefill GEMM,
+    // 85 against 53 us at m = 128), the prefill GEMM beyond, with `workspace`
+    // (workspace_bytes(m) bytes) when given.
     Result<void> forward_device(const void* x, int64_t m, float* y, hipStream_t stream,
                                 int8_t* act_codes = nullptr, float* act_scales = nullptr,
                                 void* workspace = nullptr, size_t workspace_bytes = 0) const;
-    // device scratch for m tokens: the w4 prefill path (m > 16) and the fp8
-    // decode path (m <= 16); 0 otherwise
+    static constexpr int64_t kTiledPassesMaxM = 64;
+    // device scratch for m tokens: the w4 prefill path and the fp8 decode path
+    // (m <= 16); 0 otherwise
     size_t workspace_bytes(int64_t m) const;
     // Quantized checkpoint entries under `name` (layout in theano_serialize.hpp):
     // codes and scales as stored on the device, loaded back without re-quantizing.
@@ -395,11 +399,12 @@ class QuantizedMLP : public Module {
     size_t hidden() const { return d_; }
     size_t intermediate() const { return f_; }
     // decode shapes (D and F at most 16384; 1 <= m <= 8, or m <= kDecodeMaxM where
-    // D <= kDecodeOnePassD, whose gate/up takes all tokens in one launch) run
-    // tq_mlp_w4g128_decode on row-tiled copies of the weights, others
-    // tq_mlp_w4g128 (at D = 4096, F = 14336: 35-60 us for 5-16 tokens against
-    // 134-136 us)
-    static constexpr int64_t kDecodeMaxM = 16;
+    // D <= kDecodeOnePassD, whose gate/up takes 16 tokens in one launch) run
+    // tq_mlp_w4g128_decode on row-tiled copies of the weights, in passes of
+    // kDecodePassM tokens; others tq_mlp_w4g128 (at D = 4096, F = 14336: 35-60 us
+    // for 5-16 tokens and 74-108 us for 17-32, against 134-143 us)
+    static constexpr int64_t kDecodeMaxM = 32;
+    static constexpr int64_t kDecodePassM = 16;
     static constexpr size_t kDecodeOnePassD = 4096;
     bool decode_path(int64_t m) const {
         return gu_tiled_.size() > 0 && m >= 1 && (m <= 8 || (m <= kDecodeMaxM && d_ <= kDecodeOnePassD));

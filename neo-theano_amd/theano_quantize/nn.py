@@ -19,8 +19,10 @@ Modes (chosen from the QConfig):
            activations not FP8).
 Decode shapes (M <= 16 tokens) run the dequant-GEMV kernels; in "w8a8" and
 "fp8" modes the GEMV quantizes the activation rows itself (the same codes and
-product as quantize + GEMM, one launch).  Prefill shapes run the i8-MFMA W8A8
-GEMM, the fp8-MFMA GEMM or the bf16-MFMA W4A16 GEMM.
+product as quantize + GEMM, one launch).  "w4" runs the tiled GEMV in passes of
+16 tokens up to M = 64, where it is faster than the prefill GEMM, whose 128-row
+M tiles are mostly empty there.  Prefill shapes run the i8-MFMA W8A8 GEMM, the
+fp8-MFMA GEMM or the bf16-MFMA W4A16 GEMM.
 """
 from __future__ import annotations
 
@@ -34,11 +36,17 @@ from .formats import (quantize_i4_g128, quantize_per_channel_fp8, quantize_per_c
 from .qconfig import QConfig, QuantDType
 
 DECODE_MAX_M = 16
-TILED_MAX_M = 16  # decode shapes run on the row-tiled copy of an INT4 weight
-# QuantizedMLP runs the decode kernels for up to 8 tokens, and up to 16 where D <=
-# 4096 (its gate/up then takes all tokens in one launch); the prefill FFN beyond.
-# At D = 4096, F = 14336: 35-60 us for 5-16 tokens against 134-136 us.
-DECODE_MLP_MAX_M = 16
+TILED_MAX_M = 16  # tokens per launch of the INT4 GEMV on the row-tiled copy
+# INT4 Linear: the tiled GEMV in passes of TILED_MAX_M tokens up to this M (at N =
+# 14336, K = 4096: 22 / 42 us at M = 32 / 64 against 40 / 50 us for the prefill
+# GEMM, 85 against 53 us at M = 128)
+TILED_PASSES_MAX_M = 64
+# QuantizedMLP runs the decode kernels for up to 8 tokens, and, where D <= 4096
+# (its gate/up then takes 16 tokens in one launch), up to 32 tokens in passes of
+# 16; the prefill FFN beyond.  At D = 4096, F = 14336: 35-60 us for 5-16 tokens
+# and 74-108 us for 17-32, against 134-143 us.
+DECODE_MLP_MAX_M = 32
+DECODE_MLP_PASS_M = 16
 DECODE_MLP_ONE_PASS_D = 4096
 MLP_DOWN_TILE_ROWS = 32  # tile height of the FFN's decode copy of down
 
@@ -92,7 +100,8 @@ class QuantizedLinear(Module):
         self.bias = bias
         self.tiled = None
         if tiled and mode == "w4" and self.in_features <= 16384:
-            # row-tiled copy (a permutation of qweight) for the decode GEMV, M <= 16
+            # row-tiled copy (a permutation of qweight) for the decode GEMV (passes
+            # of 16 tokens up to M = 64)
             self.tiled = repack_i4_g128_tiled(qweight, scales)
 
     @staticmethod
@@ -138,10 +147,12 @@ class QuantizedLinear(Module):
         y = torch.empty((m, self.out_features), dtype=torch.float32, device=x.device)
         n, k = self.out_features, self.in_features
         if self.mode == "w4":
-            if m <= TILED_MAX_M and self.tiled is not None:
+            if m <= TILED_PASSES_MAX_M and self.tiled is not None:
                 pt, st, t = self.tiled
-                _abi.call("tq_gemv_w4g128_tiled", ptr(x), m, ptr(pt), ptr(st), ptr(self.bias), n, k, t,
-                          ptr(y), stream())
+                for m0 in range(0, m, TILED_MAX_M):
+                    mm = min(TILED_MAX_M, m - m0)
+                    _abi.call("tq_gemv_w4g128_tiled", ptr(x[m0:m0 + mm]), mm, ptr(pt), ptr(st), ptr(self.bias), n,
+                              k, t, ptr(y[m0:m0 + mm]), stream())
             elif m <= DECODE_MAX_M:
                 _abi.call("tq_gemv_w4g128", ptr(x), m, ptr(self.qweight), ptr(self.scales), ptr(self.bias), n, k,
                           ptr(y), stream())
@@ -231,7 +242,8 @@ class QuantizedMLP(Module):
     def workspace_bytes(self, m: int) -> int:
         """Device bytes of intermediates forward() needs for m tokens."""
         if self._decode_path(m):
-            return int(_abi.lib().tq_mlp_w4g128_decode_workspace_bytes(m, self.d, self.f))
+            mm = min(m, DECODE_MLP_PASS_M)  # one pass at a time
+            return int(_abi.lib().tq_mlp_w4g128_decode_workspace_bytes(mm, self.d, self.f))
         return int(_abi.lib().tq_mlp_w4g128_workspace_bytes(m, self.d, self.f))
 
     def forward(self, x, workspace=None):
@@ -248,8 +260,10 @@ class QuantizedMLP(Module):
         wsb = workspace.numel() * workspace.element_size()
         if self._decode_path(m):
             gu_t, gu_st, dn_t, dn_st, dn_rows = self.decode
-            _abi.call("tq_mlp_w4g128_decode", ptr(x), m, self.d, self.f, ptr(gu_t), ptr(gu_st), ptr(dn_t),
-                      ptr(dn_st), dn_rows, ptr(workspace), wsb, ptr(y), stream())
+            for m0 in range(0, m, DECODE_MLP_PASS_M):  # passes ordered on the stream share the workspace
+                mm = min(DECODE_MLP_PASS_M, m - m0)
+                _abi.call("tq_mlp_w4g128_decode", ptr(x[m0:m0 + mm]), mm, self.d, self.f, ptr(gu_t), ptr(gu_st),
+                          ptr(dn_t), ptr(dn_st), dn_rows, ptr(workspace), wsb, ptr(y[m0:m0 + mm]), stream())
             return y
         _abi.call("tq_mlp_w4g128", ptr(x), m, self.d, self.f, ptr(self.gate[0]), ptr(self.gate[1]),
                   ptr(self.up[0]), ptr(self.up[1]), ptr(self.down[0]), ptr(self.down[1]),

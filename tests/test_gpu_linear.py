@@ -181,8 +181,10 @@ def test_gemv_w4g128_tiled_shapes(tq, oracle, n, k, m, t):
     assert_close(host(y), oracle.linear_w4g128_bf16(xb, rp, rs, b), RTOL, ATOL, f"tiled {n}x{k} M={m} T={t}")
 
 
+# QuantizedLinear "w4" up to M = 64 runs the tiled GEMV in passes of 16 tokens
+# (17, 40, 64 below)
 @pytest.mark.parametrize("n,k,m", [(100, 128, 1), (7, 2176, 2), (256, 14336, 1), (48, 16384, 3), (9, 4096, 16),
-                                   (33, 16512, 2)])
+                                   (33, 16512, 2), (100, 1024, 17), (9, 4096, 40), (300, 2048, 64)])
 def test_gemv_w4g128_shapes_bias(tq, oracle, n, k, m):
     w = normal(51, (n, k), 0.02)
     xb = to_bf16_bits(normal(51, (m, k), 1.0, stream=1))
@@ -314,7 +316,8 @@ def test_misaligned_inputs_take_the_general_kernels(tq, oracle):
 # ----------------------------------------------------------------- W4A16
 # (17, 256, 512), (300, 512, 768), (64, 1024, 4096), (129, 768, 2048) run the
 # pipelined kernels (K split in two where the grid is small); the rest the
-# 16x16x32 / shape-general kernels
+# 16x16x32 / shape-general kernels.  The layer has no tiled copy, so that every
+# M takes the prefill GEMM.
 @pytest.mark.parametrize("m,n,k", [(17, 256, 512), (130, 64, 4096), (300, 128, 1024), (33, 16, 128),
                                    (40, 200, 1024), (20, 7, 256), (300, 512, 768), (64, 1024, 4096),
                                    (129, 768, 2048)])
@@ -322,7 +325,9 @@ def test_gemm_w4g128_bf16_shapes(tq, oracle, m, n, k):
     w = normal(55, (n, k), 0.02)
     xb = to_bf16_bits(normal(55, (m, k), 1.0, stream=1))
     b = normal(55, (n,), 0.1, stream=2)
-    lin = tq.QuantizedLinear.from_tensors(dev_tensor(w), dev_tensor(b), tq.QConfig.default_int4())
+    p, s = tq.quantize_i4_g128(dev_tensor(w))
+    lin = tq.QuantizedLinear("w4", k, n, p, s, dev_tensor(b), tiled=False)
+    assert lin.tiled is None
     y = host(lin(bf16_dev(xb)))
     rp, rs = oracle.quantize_i4_g128(w)
     assert_close(y, oracle.linear_w4g128_bf16(xb, rp, rs, b), RTOL, ATOL, f"w4a16 {m}x{n}x{k}")
@@ -388,19 +393,20 @@ def _mlp_case(tq, m, d, f, seed=57):
     return mlp, xb
 
 
-# Decode path (M <= 8, and M <= 16 where D <= 4096): gate and up interleaved in
-# 64-row tiles with SiLU * up in the epilogue (4 tokens per launch up to M = 4;
-# 5-16 tokens in one launch of the 32x32 kernel where D <= 4096, else 4 per
-# launch), down on h as bf16 hi + lo rows in 32-row tiles, one launch per four
-# tokens with K split over two blocks per tile (including F = 128 where the
-# second block has no groups, and several launches for M > 4); one to eight
-# groups per wave, F not a multiple of 64, the Llama shape.
+# Decode path (M <= 8, and M <= 32 where D <= 4096, in passes of 16 tokens): gate
+# and up interleaved in 64-row tiles with SiLU * up in the epilogue (4 tokens per
+# launch up to M = 4; 5-16 tokens in one launch of the 32x32 kernel where D <=
+# 4096, else 4 per launch), down on h as bf16 hi + lo rows in 32-row tiles, one
+# launch per four tokens (eight at M >= 5) with K split over two blocks per tile
+# (including F = 128 where the second block has no groups); one to eight groups
+# per wave, F not a multiple of 64, the Llama shape.
 @pytest.mark.parametrize("m,d,f", [(1, 128, 128), (2, 256, 384), (3, 512, 1024), (4, 1024, 640), (5, 256, 512),
                                    (7, 384, 1152), (8, 2048, 256), (1, 4096, 14336), (2, 14336, 4096),
                                    (6, 16384, 128), (3, 4096, 14336), (4, 4096, 14336), (4, 256, 128),
                                    (3, 640, 16384), (6, 4096, 14336), (8, 4096, 14336), (2, 4096, 14336),
                                    (9, 256, 512), (12, 4096, 14336), (16, 1024, 640), (16, 4096, 14336),
-                                   (13, 128, 384), (7, 8192, 1024)])
+                                   (13, 128, 384), (7, 8192, 1024), (17, 4096, 14336), (32, 512, 1536),
+                                   (25, 256, 384)])
 def test_mlp_decode_path(tq, oracle, m, d, f):
     wg = normal(60, (f, d), 0.02)
     wu = normal(60, (f, d), 0.02, stream=1)
@@ -408,7 +414,7 @@ def test_mlp_decode_path(tq, oracle, m, d, f):
     xb = to_bf16_bits(normal(60, (m, d), 1.0, stream=3))
     mlp = tq.QuantizedMLP.from_tensors(dev_tensor(wg), dev_tensor(wu), dev_tensor(wd))
     assert mlp._decode_path(m)
-    assert mlp._decode_path(16) == (d <= 4096) and not mlp._decode_path(17)
+    assert mlp._decode_path(32) == (d <= 4096) and not mlp._decode_path(33)
     y = host(mlp(bf16_dev(xb)))
     args = [a for t in (mlp.gate, mlp.up, mlp.down) for a in (host(t[0]), host(t[1]).view(np.uint16))]
     assert_close(y, oracle.mlp_w4g128(xb, *args), RTOL, ATOL, f"mlp decode {m}x{d}x{f}")

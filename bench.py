@@ -476,28 +476,30 @@ def main():
                 ("w8a8", tq.quantize_per_channel_i8, "tq_gemv_w8a8", "tq_quantize_i8_rowwise", "tq_gemm_w8a8"),
                 ("fp8", tq.quantize_per_channel_fp8, "tq_gemv_fp8a8", "tq_quantize_fp8_rowwise", "tq_gemm_fp8")):
             copies = quant_copies(w, qfn, rotation(n2 * k2))
-            x = dt(normal_f32(1, (1, k2), 1.0, stream=1))
-            y = torch.empty((1, n2), dtype=torch.float32, device=dev)
-            qa = torch.empty((1, k2), dtype=torch.int8 if kind == "w8a8" else torch.uint8, device=dev)
-            sa = torch.empty(1, dtype=torch.float32, device=dev)
+            for md in ((1, 4, 16) if kind == "w8a8" else (1,)):
+                x = dt(normal_f32(1, (md, k2), 1.0, stream=1))
+                y = torch.empty((md, n2), dtype=torch.float32, device=dev)
+                qa = torch.empty((md, k2), dtype=torch.int8 if kind == "w8a8" else torch.uint8, device=dev)
+                sa = torch.empty(md, dtype=torch.float32, device=dev)
 
-            def launch_fused(i, fused=fused, copies=copies, x=x, y=y):
-                q, s = copies[i % len(copies)]
-                _abi.call(fused, ptr(x), 1, ptr(q), ptr(s), None, n2, k2, ptr(y), stream())
+                def launch_fused(i, fused=fused, copies=copies, x=x, y=y, md=md):
+                    q, s = copies[i % len(copies)]
+                    _abi.call(fused, ptr(x), md, ptr(q), ptr(s), None, n2, k2, ptr(y), stream())
 
-            def launch_two(i, quant=quant, gemm=gemm, copies=copies, x=x, y=y, qa=qa, sa=sa, kind=kind):
-                q, s = copies[i % len(copies)]
-                _abi.call(quant, ptr(x), 1, k2, ptr(qa), ptr(sa), stream())
-                if kind == "w8a8":
-                    _abi.call(gemm, ptr(qa), ptr(sa), ptr(q), ptr(s), None, 1, n2, k2, None, ptr(y), stream())
-                else:
-                    _abi.call(gemm, ptr(qa), ptr(sa), ptr(q), ptr(s), None, 1, n2, k2, ptr(y), stream())
+                def launch_two(i, quant=quant, gemm=gemm, copies=copies, x=x, y=y, qa=qa, sa=sa, kind=kind, md=md):
+                    q, s = copies[i % len(copies)]
+                    _abi.call(quant, ptr(x), md, k2, ptr(qa), ptr(sa), stream())
+                    if kind == "w8a8":
+                        _abi.call(gemm, ptr(qa), ptr(sa), ptr(q), ptr(s), None, md, n2, k2, None, ptr(y), stream())
+                    else:
+                        _abi.call(gemm, ptr(qa), ptr(sa), ptr(q), ptr(s), None, md, n2, k2, ptr(y), stream())
 
-            ms_f, mode_f = timer.run(launch_fused, args.steps, args.warmup)
-            ms_t, _ = timer.run(launch_two, args.steps, args.warmup)
-            res[kind] = {"fused_us": round(ms_f * 1e3, 3), "quantize_plus_gemm_us": round(ms_t * 1e3, 3),
-                         "timing": mode_f}
-            log(f"decode {kind} M=1 4096x4096: fused {ms_f * 1e3:.2f} us, quantize + GEMM {ms_t * 1e3:.2f} us")
+                ms_f, mode_f = timer.run(launch_fused, args.steps, args.warmup)
+                ms_t, _ = timer.run(launch_two, args.steps, args.warmup)
+                key = kind if md == 1 else f"{kind}_m{md}"
+                res[key] = {"fused_us": round(ms_f * 1e3, 3), "quantize_plus_gemm_us": round(ms_t * 1e3, 3),
+                            "timing": mode_f}
+                log(f"decode {kind} M={md} 4096x4096: fused {ms_f * 1e3:.2f} us, quantize + GEMM {ms_t * 1e3:.2f} us")
             del copies
         secondary["a8_decode_m1_n4096_k4096"] = res
 

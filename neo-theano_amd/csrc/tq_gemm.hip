@@ -495,6 +495,66 @@ __global__ __launch_bounds__(256, 1) void k_gemm_fp8_dma(const int8_t* __restric
     dma_epilogue(acc, c, lds, m0, n0, m, n, sa, sw, bias, nullptr, y);
 }
 
+
+// Skinny W8A8 for M <= 16 tokens (decode batches), K % 64 == 0: one block of 16
+// waves per 16 weight rows, the waves splitting K into runs of kCPW 64-byte
+// chunks.  Lane (q = l / 16, r16 = l % 16) loads 16 bytes at k = 64 c + 16 q of
+// weight row r16 (the A operand of v_mfma_i32_16x16x64_i8) and of token r16's
+// codes (the B operand, zero past M); A and B take a lane's bytes into the same
+// k slots, so each MFMA adds the 64-k dot products of 16 rows x 16 tokens.  Every
+// wave issues all of its loads at once.  A lane of the result holds D[4 q + e]
+// [r16], e = 0..3: rows 4q..4q+3 for token r16.  The waves' int32 partials meet
+// in LDS (exact, in any order) and the epilogue is the GEMM's, so acc and y equal
+// the tiled kernels' bit for bit; 16 x 4096 tokens x weights in one round of
+// 256 blocks instead of 16 blocks of 128 x 256 tiles.  K <= 8192 (kCPW <= 8).
+constexpr int kSkinnyBlock = 1024, kSkinnyWaves = kSkinnyBlock / kWave;
+
+template <int kCPW>
+__global__ __launch_bounds__(kSkinnyBlock) void k_gemm_w8a8_skinny(const int8_t* __restrict__ qa,
+                                                                   const float* __restrict__ sa,
+                                                                   const int8_t* __restrict__ qw,
+                                                                   const float* __restrict__ sw,
+                                                                   const float* __restrict__ bias, int m, int n,
+                                                                   int64_t k, int32_t* __restrict__ acc_out,
+                                                                   float* __restrict__ y) {
+    __shared__ i32x4 part[kSkinnyWaves][64];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int q = lane >> 4, r16 = lane & 15;
+    const int64_t n0 = static_cast<int64_t>(blockIdx.x) * 16;
+    const int64_t C = k >> 6, c0 = static_cast<int64_t>(wave) * kCPW;
+    const bool tok = r16 < m;
+    const int8_t* wr = qw + (n0 + r16) * k + 16 * q;
+    const int8_t* ar = qa + static_cast<int64_t>(tok ? r16 : 0) * k + 16 * q;
+    i32x4 w[kCPW], a[kCPW];
+#pragma unroll
+    for (int i = 0; i < kCPW; ++i) {
+        const int64_t c = min<int64_t>(c0 + i, C - 1);  // chunks past K: clamped, skipped below
+        w[i] = __builtin_nontemporal_load(reinterpret_cast<const i32x4*>(wr + c * 64));
+        a[i] = tok ? *reinterpret_cast<const i32x4*>(ar + c * 64) : i32x4{0, 0, 0, 0};
+    }
+    i32x4 d = i32x4{0, 0, 0, 0};
+#pragma unroll
+    for (int i = 0; i < kCPW; ++i)
+        if (c0 + i < C) d = mfma_i8(w[i], a[i], d);  // wave-uniform
+    part[wave][lane] = d;
+    __syncthreads();
+    // thread t < 256: row t / 16, token t % 16 of the tile
+    const int t = threadIdx.x;
+    if (t < 256) {
+        const int row = t >> 4, j = t & 15;
+        const int e = row & 3, src = (row >> 2) * 16 + j;  // lane (q = row / 4, r16 = j), element row % 4
+        int32_t v = 0;
+#pragma unroll
+        for (int wv = 0; wv < kSkinnyWaves; ++wv) v += part[wv][src][e];
+        const int64_t nn = n0 + row;
+        if (j < m) {
+            if (acc_out) acc_out[static_cast<int64_t>(j) * n + nn] = v;
+            y[static_cast<int64_t>(j) * n + nn] = fmaf(static_cast<float>(v) * sa[j], sw[nn], bias ? bias[nn] : 0.0f);
+        }
+    }
+}
+
 }  // namespace
 }  // namespace tq
 
@@ -513,6 +573,25 @@ extern "C" int tq_gemm_w8a8(const int8_t* qa, const float* sa, const int8_t* qw,
     if (k == 0 || n % 16 != 0 || k % 16 != 0 || !aligned(qa, 16) || !aligned(qw, 16) || !aligned(sw, 16) ||
         !aligned(y, 16) || (acc && !aligned(acc, 16)) || (bias && !aligned(bias, 16)))
         return launch_gemm_w8a8_generic(qa, sa, qw, sw, bias, m, n, k, acc, y, as_hip(stream));
+    // decode batches: the skinny kernel, N / 16 blocks (K <= 8192: runs of up to 8
+    // chunks per wave, whose loads all fit the registers)
+    if (m <= 16 && k % 64 == 0 && k <= 8192 && n < (int64_t(1) << 31)) {
+        const int64_t cpw = ((k >> 6) + kSkinnyWaves - 1) / kSkinnyWaves;
+        const unsigned grid = static_cast<unsigned>(n / 16);
+        const int mi = static_cast<int>(m), ni = static_cast<int>(n);
+#define TQ_SKINNY(P) \
+    k_gemm_w8a8_skinny<P><<<grid, kSkinnyBlock, 0, as_hip(stream)>>>(qa, sa, qw, sw, bias, mi, ni, k, acc, y)
+        if (cpw <= 1)
+            TQ_SKINNY(1);
+        else if (cpw <= 2)
+            TQ_SKINNY(2);
+        else if (cpw <= 4)
+            TQ_SKINNY(4);
+        else
+            TQ_SKINNY(8);
+#undef TQ_SKINNY
+        return check_launch("tq_gemm_w8a8");
+    }
     if (k % kDmaBK == 0 && m < (int64_t(1) << 31) && n < (int64_t(1) << 31) && k < (int64_t(1) << 31)) {
         const int64_t tm = (m + kDmaBM - 1) / kDmaBM, tn = (n + kDmaBN - 1) / kDmaBN;
         if (tm * tn < (int64_t(1) << 31)) {

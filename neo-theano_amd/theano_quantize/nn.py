@@ -36,6 +36,10 @@ from .formats import (quantize_i4_g128, quantize_per_channel_fp8, quantize_per_c
 from .qconfig import QConfig, QuantDType
 
 DECODE_MAX_M = 16
+# "w8a8": the GEMV with activation quantization inside up to this M (at 4096 x
+# 4096: 5.4 / 7.0 us at M = 1 / 2); beyond, quantize + the GEMM's skinny kernel
+# (10.6 / 12.5 us at M = 3 / 16, against 12.0 / 52.3 us for the fused GEMV)
+FUSED_W8A8_MAX_M = 2
 TILED_MAX_M = 16  # tokens per launch of the INT4 GEMV on the row-tiled copy
 # INT4 Linear: the tiled GEMV in passes of TILED_MAX_M tokens up to this M (at N =
 # 14336, K = 4096: 22 / 42 us at M = 32 / 64 against 40 / 50 us for the prefill
@@ -167,7 +171,8 @@ class QuantizedLinear(Module):
                 mm = min(DECODE_MAX_M, m - m0)
                 _abi.call("tq_gemv_w8", ptr(x[m0:m0 + mm]), mm, ptr(self.qweight), ptr(self.scales),
                           ptr(self.bias), n, k, ptr(y[m0:m0 + mm]), stream())
-        elif self.mode in ("w8a8", "fp8") and m <= DECODE_MAX_M and _fused_a8_ok(x, self.qweight, k):
+        elif (self.mode in ("w8a8", "fp8") and m <= (FUSED_W8A8_MAX_M if self.mode == "w8a8" else DECODE_MAX_M)
+              and _fused_a8_ok(x, self.qweight, k)):
             # activation quantization fused into the decode GEMV (one launch)
             _abi.call("tq_gemv_w8a8" if self.mode == "w8a8" else "tq_gemv_fp8a8", ptr(x), m, ptr(self.qweight),
                       ptr(self.scales), ptr(self.bias), n, k, ptr(y), stream())

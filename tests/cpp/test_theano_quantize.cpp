@@ -471,20 +471,27 @@ TEST_GPU(test_parity_quantized_linear_w4_prefill) {
 }
 
 TEST_GPU(test_parity_quantized_linear_w8a8) {
-    const size_t n = 272, k = 1024, m = 37;
-    const auto wv = randn(n * k, 0.02, 51), xv = randn(m * k, 1.0, 52);
+    // m = 2: the fused GEMV; 5, 16: quantize + the skinny GEMM; 37: the tiled GEMM
+    const size_t n = 272, k = 1024;
+    const auto wv = randn(n * k, 0.02, 51);
     const QConfig cfg{QuantDType::Int8, QuantDType::Int8, true, true};
     const QuantizedLinear layer = QuantizedLinear::from_tensors(Tensor::from_slice(wv, {n, k}), std::nullopt, cfg).unwrap();
     ASSERT(layer.mode() == QuantizedLinear::Mode::W8A8);
-    const auto y = layer.forward(Tensor::from_slice(xv, {m, k})).to_vec_f64().unwrap();
-    const auto w32 = f32(wv), x32 = f32(xv);
-    std::vector<int8_t> qw(n * k), qa(m * k);
-    std::vector<float> sw(n), sa(m);
+    const auto w32 = f32(wv);
+    std::vector<int8_t> qw(n * k);
+    std::vector<float> sw(n);
     tqo_quantize_i8_rowwise(w32.data(), n, k, qw.data(), sw.data());
-    tqo_quantize_i8_rowwise(x32.data(), m, k, qa.data(), sa.data());
-    std::vector<double> ref(m * n);
-    tqo_linear_w8a8(qa.data(), sa.data(), qw.data(), sw.data(), nullptr, m, n, k, ref.data());
-    assert_close(y, ref, "w8a8 linear");
+    for (size_t m : {2u, 5u, 16u, 37u}) {
+        const auto xv = randn(m * k, 1.0, 52 + m);
+        const auto y = layer.forward(Tensor::from_slice(xv, {m, k})).to_vec_f64().unwrap();
+        const auto x32 = f32(xv);
+        std::vector<int8_t> qa(m * k);
+        std::vector<float> sa(m);
+        tqo_quantize_i8_rowwise(x32.data(), m, k, qa.data(), sa.data());
+        std::vector<double> ref(m * n);
+        tqo_linear_w8a8(qa.data(), sa.data(), qw.data(), sw.data(), nullptr, m, n, k, ref.data());
+        assert_close(y, ref, "w8a8 linear");
+    }
 }
 
 TEST_GPU(test_parity_quantized_linear_fp8) {

@@ -243,13 +243,17 @@ def test_w8a8_config4_full(tq, oracle):
     assert_close(y[rows], oracle.linear_w8a8(qa[rows], sa[rows], qw, sw), RTOL, ATOL, "w8a8 y vs oracle")
 
 
-# K % 128 == 0 takes the LDS-DMA kernel (1, 2, 3 and more stages; M, N tails; tile
-# groups with and without the XCD remap), other K the general kernel.
+# M <= 16 with K % 64 == 0 (K <= 8192) takes the skinny kernel (one to eight
+# chunks per wave, waves past K, one-block grids); K % 128 == 0 the LDS-DMA kernel
+# (1, 2, 3 and more stages; M, N tails; tile groups with and without the XCD
+# remap), other K the general kernel.
 @pytest.mark.parametrize("m,n,k", [(1, 16, 16), (130, 48, 208), (64, 160, 80),
                                    (7, 272, 1024), (257, 128, 4096), (300, 512, 128),
                                    (129, 4096, 256), (100, 272, 384), (384, 2048, 256),
                                    (1, 256, 640), (1031, 528, 512),
-                                   (5, 8, 256), (33, 50, 100), (17, 16, 1000)])
+                                   (5, 8, 256), (33, 50, 100), (17, 16, 1000),
+                                   (16, 4096, 4096), (3, 64, 8192), (16, 16, 64), (9, 1024, 192),
+                                   (2, 48, 4096), (16, 32, 8256)])
 def test_w8a8_shapes_bias(tq, oracle, m, n, k):
     x = normal(52, (m, k), 1.0)
     w = normal(52, (n, k), 0.02, stream=1)
@@ -272,11 +276,13 @@ def test_w8a8_extreme_codes(tq, oracle):
     assert acc[0, 0] == 4096 * 127 * 127
 
 
-def test_quantized_linear_w8a8_module(tq, oracle):
+# M = 1, 2: the fused GEMV; 3, 16: quantize + the skinny GEMM; 100: the tiled GEMM
+@pytest.mark.parametrize("m", [1, 2, 3, 16, 100])
+def test_quantized_linear_w8a8_module(tq, oracle, m):
     from theano_quantize import QConfig, QuantDType
 
     w = normal(54, (256, 512), 0.02)
-    x = normal(54, (100, 512), 1.0, stream=1)
+    x = normal(54, (m, 512), 1.0, stream=1)
     cfg = QConfig(QuantDType.Int8, QuantDType.Int8, True, True)
     lin = tq.QuantizedLinear.from_tensors(dev_tensor(w), None, cfg)
     y = host(lin(dev_tensor(x)))

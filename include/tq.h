@@ -225,7 +225,9 @@ int tq_gemv_fp8(const float* x, int64_t m, const uint8_t* q, const float* s,
 int tq_gemv_w8a8(const float* x, int64_t m, const int8_t* qw, const float* sw,
                  const float* bias, int64_t n, int64_t k, float* y, tq_stream_t stream);
 /* The FP8 counterpart (tq_quantize_fp8_rowwise + tq_gemm_fp8 in one launch;
- * f32 accumulation, so equal to the GEMM within the float tolerance). */
+ * f32 accumulation, so equal to the GEMM within the float tolerance).  Faster
+ * than the two-step path at 4096 x 4096 for M <= 2 (6.2 / 6.9 against 9.3 /
+ * 9.5 us), slower from M = 3 (12.9 against 10.0 us; 54.0 against 11.3 at 16). */
 int tq_gemv_fp8a8(const float* x, int64_t m, const uint8_t* qw, const float* sw,
                   const float* bias, int64_t n, int64_t k, float* y, tq_stream_t stream);
 
@@ -270,8 +272,9 @@ int tq_gemm_w8a8(const int8_t* qa, const float* sa, const int8_t* qw, const floa
  * y[i,j] = fma(f32(sum_p e4m3(qa[i,p]) * e4m3(qw[j,p])) * sa[i], sw[j], bias[j] or 0);
  * products exact, f32 accumulation.  The reference value is Linear over the
  * dequantized operands (linear.rs:111-121, tensor_ops.rs:379-410).  Any M, N,
- * K.  The FP8 MFMA kernel serves K % 128 == 0 and N % 16 == 0 with 16-byte
- * aligned qa, qw, sw, bias and y; other cases take a shape-general kernel. */
+ * K.  The FP8 MFMA kernels serve K % 128 == 0 and N % 16 == 0 with 16-byte
+ * aligned qa, qw, sw, bias and y (M <= 16 with K <= 8192: a skinny kernel of N/16
+ * blocks); other cases take a shape-general kernel. */
 int tq_gemm_fp8(const uint8_t* qa, const float* sa, const uint8_t* qw, const float* sw,
                 const float* bias, int64_t m, int64_t n, int64_t k, float* y, tq_stream_t stream);
 

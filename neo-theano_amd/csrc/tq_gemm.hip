@@ -555,6 +555,61 @@ __global__ __launch_bounds__(kSkinnyBlock) void k_gemm_w8a8_skinny(const int8_t*
     }
 }
 
+
+// The FP8 (e4m3) counterpart for M <= 16, K % 128 == 0: lanes take 32 bytes at k
+// = 128 c + 32 q of their weight row and token (the A and B operands of the
+// unscaled v_mfma_f32_16x16x128_f8f6f4; products exact in f32), f32 partials of
+// the waves added in LDS in a fixed order, the GEMM's epilogue.  The sums run in
+// another order than the tiled kernel's, so y agrees with it to f32 rounding.
+// K <= 8192 (4 chunks per wave).
+template <int kCPW>
+__global__ __launch_bounds__(kSkinnyBlock) void k_gemm_fp8_skinny(const int8_t* __restrict__ qa,
+                                                                  const float* __restrict__ sa,
+                                                                  const int8_t* __restrict__ qw,
+                                                                  const float* __restrict__ sw,
+                                                                  const float* __restrict__ bias, int m, int n,
+                                                                  int64_t k, float* __restrict__ y) {
+    __shared__ f32x4 part[kSkinnyWaves][64];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int q = lane >> 4, r16 = lane & 15;
+    const int64_t n0 = static_cast<int64_t>(blockIdx.x) * 16;
+    const int64_t C = k >> 7, c0 = static_cast<int64_t>(wave) * kCPW;
+    const bool tok = r16 < m;
+    const int8_t* wr = qw + (n0 + r16) * k + 32 * q;
+    const int8_t* ar = qa + static_cast<int64_t>(tok ? r16 : 0) * k + 32 * q;
+    i32x8 w[kCPW], a[kCPW];
+#pragma unroll
+    for (int i = 0; i < kCPW; ++i) {
+        const int64_t c = min<int64_t>(c0 + i, C - 1);  // chunks past K: clamped, skipped below
+        const i32x4 w0 = __builtin_nontemporal_load(reinterpret_cast<const i32x4*>(wr + c * 128));
+        const i32x4 w1 = __builtin_nontemporal_load(reinterpret_cast<const i32x4*>(wr + c * 128 + 16));
+        w[i] = i32x8{w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+        i32x4 a0 = i32x4{0, 0, 0, 0}, a1 = a0;
+        if (tok) {
+            a0 = *reinterpret_cast<const i32x4*>(ar + c * 128);
+            a1 = *reinterpret_cast<const i32x4*>(ar + c * 128 + 16);
+        }
+        a[i] = i32x8{a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+    }
+    f32x4 d = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < kCPW; ++i)
+        if (c0 + i < C) d = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(w[i], a[i], d, 0, 0, 0, 0, 0, 0);
+    part[wave][lane] = d;
+    __syncthreads();
+    const int t = threadIdx.x;
+    if (t < 256) {
+        const int row = t >> 4, j = t & 15;
+        const int e = row & 3, src = (row >> 2) * 16 + j;
+        float v = 0.0f;
+#pragma unroll
+        for (int wv = 0; wv < kSkinnyWaves; ++wv) v += part[wv][src][e];
+        const int64_t nn = n0 + row;
+        if (j < m) y[static_cast<int64_t>(j) * n + nn] = fmaf(v * sa[j], sw[nn], bias ? bias[nn] : 0.0f);
+    }
+}
+
 }  // namespace
 }  // namespace tq
 
@@ -620,6 +675,20 @@ extern "C" int tq_gemm_fp8(const uint8_t* qa, const float* sa, const uint8_t* qw
     const bool fast = k > 0 && k % kDmaBK == 0 && n % 16 == 0 && aligned(qa, 16) && aligned(qw, 16) &&
                       aligned(sw, 16) && aligned(y, 16) && (!bias || aligned(bias, 16)) &&
                       m < (int64_t(1) << 31) && n < (int64_t(1) << 31) && k < (int64_t(1) << 31);
+    if (fast && m <= 16 && k <= 8192) {  // decode batches: the skinny kernel, N / 16 blocks
+        const int64_t cpw = ((k >> 7) + kSkinnyWaves - 1) / kSkinnyWaves;
+        const unsigned grid = static_cast<unsigned>(n / 16);
+        const auto* a = reinterpret_cast<const int8_t*>(qa);
+        const auto* w = reinterpret_cast<const int8_t*>(qw);
+        const int mi = static_cast<int>(m), ni = static_cast<int>(n);
+        if (cpw <= 1)
+            k_gemm_fp8_skinny<1><<<grid, kSkinnyBlock, 0, as_hip(stream)>>>(a, sa, w, sw, bias, mi, ni, k, y);
+        else if (cpw <= 2)
+            k_gemm_fp8_skinny<2><<<grid, kSkinnyBlock, 0, as_hip(stream)>>>(a, sa, w, sw, bias, mi, ni, k, y);
+        else
+            k_gemm_fp8_skinny<4><<<grid, kSkinnyBlock, 0, as_hip(stream)>>>(a, sa, w, sw, bias, mi, ni, k, y);
+        return check_launch("tq_gemm_fp8");
+    }
     if (fast) {
         const int64_t tm = (m + kDmaBM - 1) / kDmaBM, tn = (n + kDmaBN - 1) / kDmaBN;
         if (tm * tn < (int64_t(1) << 31)) {

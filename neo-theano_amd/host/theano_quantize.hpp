@@ -336,11 +336,12 @@ class QuantizedLinear : public Module {
     // Device-resident forward: x is f32 [m, in] (w8, w8a8, fp8) or bf16 bits [m, in]
     // (w4), y is f32 [m, out]; enqueued on `stream`, no host synchronisation.  w8a8
     // and fp8 need `act_codes` (one byte per element, [m, in]) and `act_scales`
-    // (f32 [m]) device scratch.  w8a8 with m <= kFusedW8A8MaxM and fp8 with m <= 16
-    // quantize x inside the decode GEMV (tq_gemv_w8a8 / tq_gemv_fp8a8) when K % 16
-    // == 0, K <= 8192 and x is 16-byte aligned (w8a8 beyond: quantize + the GEMM,
-    // whose skinny kernel serves m <= 16); otherwise fp8 runs the GEMV on the fake-quantized
-    // activations held in `workspace` (workspace_bytes(m) bytes).  w4 runs the
+    // (f32 [m]) device scratch.  With m <= kFusedA8MaxM both quantize x inside the
+    // decode GEMV (tq_gemv_w8a8 / tq_gemv_fp8a8) when K % 16 == 0, K <= 8192 and x
+    // is 16-byte aligned, otherwise fp8 runs the GEMV on the fake-quantized
+    // activations held in `workspace` (workspace_bytes(m) bytes); larger m
+    // quantize x into the scratch and run the GEMM (its skinny kernel up to 16
+    // tokens: faster than the fused GEMV from 3 tokens).  w4 runs the
     // tiled GEMV in passes of 16 tokens up to m = kTiledPassesMaxM (at N = 14336,
     // K = 4096: 22 / 42 us at m = 32 / 64 against 40 / 50 us for the prefill GEMM,
     // 85 against 53 us at m = 128), the prefill GEMM beyond, with `workspace`
@@ -349,9 +350,9 @@ class QuantizedLinear : public Module {
                                 int8_t* act_codes = nullptr, float* act_scales = nullptr,
                                 void* workspace = nullptr, size_t workspace_bytes = 0) const;
     static constexpr int64_t kTiledPassesMaxM = 64;
-    static constexpr int64_t kFusedW8A8MaxM = 2;
-    // device scratch for m tokens: the w4 prefill path and the fp8 decode path
-    // (m <= 16); 0 otherwise
+    static constexpr int64_t kFusedA8MaxM = 2;
+    // device scratch for m tokens: the w4 prefill path and the fp8 GEMV on
+    // fake-quantized activations (m <= kFusedA8MaxM); 0 otherwise
     size_t workspace_bytes(int64_t m) const;
     // Quantized checkpoint entries under `name` (layout in theano_serialize.hpp):
     // codes and scales as stored on the device, loaded back without re-quantizing.

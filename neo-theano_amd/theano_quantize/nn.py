@@ -36,10 +36,11 @@ from .formats import (quantize_i4_g128, quantize_per_channel_fp8, quantize_per_c
 from .qconfig import QConfig, QuantDType
 
 DECODE_MAX_M = 16
-# "w8a8": the GEMV with activation quantization inside up to this M (at 4096 x
-# 4096: 5.4 / 7.0 us at M = 1 / 2); beyond, quantize + the GEMM's skinny kernel
-# (10.6 / 12.5 us at M = 3 / 16, against 12.0 / 52.3 us for the fused GEMV)
-FUSED_W8A8_MAX_M = 2
+# "w8a8" and "fp8": the GEMV with activation quantization inside up to this M (at
+# 4096 x 4096: 5.4 / 7.0 us at M = 1 / 2 for INT8, 6.2 / 6.9 for FP8); beyond,
+# quantize + the GEMM's skinny kernel (INT8 10.6 / 12.5 us at M = 3 / 16, FP8
+# 10.0 / 11.3, against 12.0 / 52.3 and 12.9 / 54.0 us for the fused GEMV)
+FUSED_A8_MAX_M = 2
 TILED_MAX_M = 16  # tokens per launch of the INT4 GEMV on the row-tiled copy
 # INT4 Linear: the tiled GEMV in passes of TILED_MAX_M tokens up to this M (at N =
 # 14336, K = 4096: 22 / 42 us at M = 32 / 64 against 40 / 50 us for the prefill
@@ -171,12 +172,11 @@ class QuantizedLinear(Module):
                 mm = min(DECODE_MAX_M, m - m0)
                 _abi.call("tq_gemv_w8", ptr(x[m0:m0 + mm]), mm, ptr(self.qweight), ptr(self.scales),
                           ptr(self.bias), n, k, ptr(y[m0:m0 + mm]), stream())
-        elif (self.mode in ("w8a8", "fp8") and m <= (FUSED_W8A8_MAX_M if self.mode == "w8a8" else DECODE_MAX_M)
-              and _fused_a8_ok(x, self.qweight, k)):
+        elif self.mode in ("w8a8", "fp8") and m <= FUSED_A8_MAX_M and _fused_a8_ok(x, self.qweight, k):
             # activation quantization fused into the decode GEMV (one launch)
             _abi.call("tq_gemv_w8a8" if self.mode == "w8a8" else "tq_gemv_fp8a8", ptr(x), m, ptr(self.qweight),
                       ptr(self.scales), ptr(self.bias), n, k, ptr(y), stream())
-        elif self.mode == "fp8" and m > DECODE_MAX_M:
+        elif self.mode == "fp8" and m > FUSED_A8_MAX_M:
             qa = torch.empty((m, k), dtype=torch.uint8, device=x.device)
             sa = torch.empty(m, dtype=torch.float32, device=x.device)
             _abi.call("tq_quantize_fp8_rowwise", ptr(x), m, k, ptr(qa), ptr(sa), stream())

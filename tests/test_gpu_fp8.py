@@ -122,12 +122,15 @@ def run_fp8(tq, x, w, bias=None):
     return qa, sa, qw, sw, y
 
 
-# K % 128 == 0 with N % 16 == 0 takes the FP8 MFMA kernel (1, 2, 3 and more
-# stages; M, N tails; tile groups with and without the XCD remap), the rest the
-# shape-general kernel.
+# K % 128 == 0 with N % 16 == 0 takes the FP8 MFMA kernels: M <= 16 (K <= 8192)
+# the skinny one (one to four chunks per wave, waves past K, one-block grids),
+# otherwise the tiled one (1, 2, 3 and more stages; M, N tails; tile groups with
+# and without the XCD remap); the rest the shape-general kernel.
 @pytest.mark.parametrize("m,n,k", [(1, 16, 128), (130, 48, 256), (7, 272, 1024), (257, 128, 4096),
                                    (300, 512, 128), (129, 4096, 256), (100, 272, 384), (384, 2048, 256),
-                                   (1031, 528, 512), (5, 8, 256), (33, 50, 100), (17, 16, 1000)])
+                                   (1031, 528, 512), (5, 8, 256), (33, 50, 100), (17, 16, 1000),
+                                   (16, 4096, 4096), (3, 64, 8192), (16, 16, 128), (9, 1024, 384),
+                                   (2, 48, 4096)])
 def test_gemm_fp8_shapes_bias(tq, oracle, m, n, k):
     x = normal(74, (m, k), 1.0)
     w = normal(74, (n, k), 0.02, stream=1)
@@ -157,9 +160,10 @@ def test_gemm_fp8_full_size_vs_torch_f64(tq, oracle):
                  RTOL, ATOL, "fp8 full size sampled rows vs oracle")
 
 
-def test_gemm_fp8_extreme_codes(tq, oracle):
+@pytest.mark.parametrize("rows", [32, 16])  # the tiled and the skinny kernel
+def test_gemm_fp8_extreme_codes(tq, oracle, rows):
     """Every product at +-448^2 with constant signs: |acc| = K * 448^2 (exact in f32)."""
-    x = np.where(normal(76, (32, 1024), 1.0) > 0, 448.0, -448.0).astype(np.float32)
+    x = np.where(normal(76, (rows, 1024), 1.0) > 0, 448.0, -448.0).astype(np.float32)
     w = np.where(normal(76, (64, 1024), 1.0, stream=1) > 0, 448.0, -448.0).astype(np.float32)
     x[0] = 448.0
     w[0] = 448.0
@@ -207,9 +211,9 @@ def test_gemv_fp8_shapes_bias(tq, oracle, m, n, k):
 
 @pytest.mark.parametrize("m", [1, 3, 16, 17, 40])
 def test_quantized_linear_fp8_decode_and_weight_only(tq, oracle, m):
-    """fp8 mode at decode sizes (GEMV on the fake-quantized activations) and above
-    (GEMM) give the FP8 W8A8 product; fp8_weight mode gives Linear over the
-    dequantized weight with f32 activations."""
+    """fp8 mode (the fused GEMV up to 2 tokens, quantize + the skinny GEMM to 16,
+    the tiled GEMM above) gives the FP8 W8A8 product; fp8_weight mode gives
+    Linear over the dequantized weight with f32 activations."""
     from theano_quantize import QConfig, QuantDType
 
     n, k = 384, 1024

@@ -62,25 +62,70 @@ def log(*a):
 
 
 class Timer:
-    """Times `steps` calls of launch(i) on the current stream, bracketed by
-    events on that stream, as a HIP graph replay and as eager launches, and
-    returns the faster of the two with its mode ("graph" / "eager"; only eager
-    launches with --eager).  Short kernels need the graph (a Python launch
-    takes longer than the kernel); long ones run back to back either way, and
-    graph replay adds a few microseconds per node on this stack."""
+    """Times `steps` calls of launch(i), bracketed by events on the stream the
+    launches go to, three ways, and returns the fastest with its mode:
+    "hip graph" (the launches captured into a hipGraph by libtq_peaks.so's
+    tqp_graph_time and replayed on its own stream: what a host that calls the C
+    ABI directly sees), "torch graph" (captured with torch.cuda.graph and
+    replayed on torch's current stream) and "eager" (only eager launches with
+    --eager).  Short kernels need a graph (a Python launch takes longer than
+    the kernel); the two graph forms agree to about 0.1 us per launch.  `last`
+    holds every mode's time of the latest run."""
 
     def __init__(self, torch, eager=False, reps=1):
         self.torch = torch
         self.eager = eager
         self.reps = reps  # timed replays of the `steps` launches; the median is returned
+        self.last = {}
 
     def run(self, launch, steps, warmup):
+        self.last = {}
+        cands = []
+        if not self.eager:
+            nat = self._native(launch, steps, warmup)
+            if nat is not None:
+                cands.append((nat, "hip graph"))
         best = self._run(launch, steps, warmup, graph=not self.eager)
+        cands.append(best)
         if best[1] == "graph":
-            eager = self._run(launch, steps, 0, graph=False)
-            if eager[0] < best[0]:
-                best = eager
-        return best
+            cands[-1] = (best[0], "torch graph")
+            cands.append(self._run(launch, steps, 0, graph=False))
+        for ms, mode in cands:
+            self.last[mode] = ms
+        return min(cands, key=lambda c: c[0])
+
+    def _native(self, launch, steps, warmup):
+        """Median ms per step of a hipGraph replay (tqp_graph_time), or None
+        when the launches cannot be captured that way."""
+        import ctypes
+
+        torch = self.torch
+        try:
+            L = _peaks_lib()
+        except Exception as e:  # not built
+            log(f"native graph timing unavailable ({e})")
+            return None
+        failed = []
+
+        def cb(i, s):
+            try:
+                with torch.cuda.stream(torch.cuda.ExternalStream(s)):
+                    launch(i)
+                return 0
+            except Exception as e:  # reported below, after the capture has ended
+                failed.append(e)
+                return 1
+
+        fn = L.tqp_launch_fn(cb)
+        us = (ctypes.c_float * self.reps)()
+        rc = L.tqp_graph_time(fn, steps, warmup, self.reps, us)
+        torch.cuda.synchronize()
+        if rc != 0 or failed:
+            log(f"native graph timing failed (hipError {rc}{', ' + str(failed[0]) if failed else ''}); "
+                "using torch's graph")
+            return None
+        t = sorted(us[i] for i in range(self.reps))
+        return t[len(t) // 2] * 1e-3
 
     def _run(self, launch, steps, warmup, graph):
         torch = self.torch
@@ -129,7 +174,12 @@ def _peaks_lib():
     L = ctypes.CDLL(path)
     vp, i64, i32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int
     L.tqp_hbm_read.argtypes = [vp, i64, vp, i32, vp]
+    L.tqp_launch_fn = ctypes.CFUNCTYPE(ctypes.c_int, ctypes.c_int, ctypes.c_void_p)
+    L.tqp_graph_time.argtypes = [L.tqp_launch_fn, i32, i32, i32, ctypes.POINTER(ctypes.c_float)]
+    L.tqp_graph_time.restype = i32
     L.tqp_hbm_read_chunks.argtypes = [vp, i64, vp, i32, vp]
+    L.tqp_hbm_read_waves.argtypes = [vp, i64, vp, i32, i32, vp]
+    L.tqp_gemv_w4_skeleton.argtypes = [vp, vp, vp, i64, i64, vp, vp]
     for fn in (L.tqp_mfma_i8, L.tqp_mfma_bf16, L.tqp_mfma_i8_random, L.tqp_mfma_bf16_random):
         fn.argtypes = [i32, i32, vp, vp]
     return L
@@ -191,14 +241,20 @@ def read_ceiling(torch, timer, dev, nbytes, args, log):
     best = None
     shapes = [("grid-stride", b) for b in (2 * cus, 4 * cus, 8 * cus, 16 * cus, 32 * cus)]
     shapes += [("one-pass", u) for u in (4, 8, 16)]
+    shapes += [("waves", lw) for lw in ((8, 3), (8, 8), (16, 3))]
     for kind, a in shapes:
         if kind == "grid-stride":
             fn = lambda i, b=a: L.tqp_hbm_read(copies[i % len(copies)].data_ptr(), n16, out.data_ptr(), b, st())
             label = f"grid-stride, {a} blocks"
-        else:
+        elif kind == "one-pass":
             fn = lambda i, u=a: L.tqp_hbm_read_chunks(copies[i % len(copies)].data_ptr(), n16, out.data_ptr(), u,
                                                       st())
             label = f"one-pass, {(n16 // 16 + 256 * a - 1) // (256 * a)} blocks of {4096 * a} B"
+        else:  # the INT4 GEMV's access pattern without its arithmetic
+            fn = lambda i, lw=a: L.tqp_hbm_read_waves(copies[i % len(copies)].data_ptr(), n16, out.data_ptr(), lw[0],
+                                                      lw[1], st())
+            label = (f"GEMV pattern, {(n16 // 16 + 1024 * a[0] - 1) // (1024 * a[0])} blocks of 16 waves, "
+                     f"{a[0]} KB per wave, {a[1]} loads in flight")
         ms, mode = timer.run(fn, args.steps, args.warmup)
         gbs = n16 / (ms * 1e-3) / 1e9
         res["variants"][label] = {"us": round(ms * 1e3, 3), "GB/s": round(gbs, 1)}
@@ -219,10 +275,13 @@ def cpu_baselines(args, secondary, n3, k3, headline_bytes, log):
     forward is Linear::forward (linear.rs:111-121): Tensor::mm gathers the
     transposed weight and runs the i-p-j loop (tensor_ops.rs:379-410); the
     dequantization happens once at load and is not timed.  Configs 4 and 5 are
-    timed at M=1 and on a row subset and extrapolated as t(M) = t(1) + (M - 1) *
-    (t(M') - t(1)) / (M' - 1) (the gather is paid once per forward, the loop per
-    row).  Each secondary config gets its own `cpu_baseline`; the headline's is
-    returned."""
+    timed as one forward at M=1 (the gather plus one row) and the i-p-j loop
+    alone (tqo_mm on the already transposed weight) over a row subset of M'
+    rows, and extrapolated as t(M) = t(1) + (M - 1) * t_loop(M') / M': the
+    gather is paid once per forward, the loop per row.  (A difference of two
+    whole forwards, t(M') - t(1), drowns the rows in the run-to-run spread of
+    the gather, which takes seconds at the FFN's sizes.)  Each secondary config
+    gets its own `cpu_baseline`; the headline's is returned."""
     import numpy as np
 
     import oracle as O  # the CPU restatement of the reference path, timed as the baseline
@@ -281,19 +340,26 @@ def cpu_baselines(args, secondary, n3, k3, headline_bytes, log):
     # C4: activations [M, 4096] quantized per row then dequantized, Linear over the dequantized weight
     xa = normal_f32(3, (32, 4096), 1.0)
 
+    wht = np.ascontiguousarray(wh.T)  # the transposed weight Tensor::mm gathers per forward
+
     def c4(m):
         qa, sa = O.quantize_i8_rowwise(xa[:m])
         O.linear(O.dequantize_i8_rowwise(qa, sa).astype(np.float64), wh)
 
+    def c4_rows(m):  # the per-row part: quantize, dequantize and the i-p-j loop, no gather
+        qa, sa = O.quantize_i8_rowwise(xa[:m])
+        O.mm(O.dequantize_i8_rowwise(qa, sa).astype(np.float64), wht)
+
     t41, _ = timed(lambda: c4(1), 0)
-    t432, _ = timed(lambda: c4(32), 0)
-    t4 = t41 + (2048 - 1) * (t432 - t41) / 31
+    t4r, _ = timed(lambda: c4_rows(32), 0)
+    t4 = t41 + (2048 - 1) * t4r / 32
     if "w8a8_gemm_m2048" in secondary:
         secondary["w8a8_gemm_m2048"]["cpu_baseline"] = entry(
             round(2.0 * 2048 * 4096 * 4096 / t4 / 1e12, 6), "TOPS",
-            f"config 4: per-row quantize + dequantize + Linear::forward at M=1 ({t41 * 1e3:.0f} ms) and "
-            f"M'=32 ({t432 * 1e3:.0f} ms), extrapolated to M=2048: {t4:.1f} s")
-    del wh, w, q, sc
+            f"config 4: per-row quantize + dequantize + Linear::forward at M=1 ({t41 * 1e3:.0f} ms) and the "
+            f"per-row part (quantize, dequantize, i-p-j loop) of M'=32 rows ({t4r * 1e3:.0f} ms), extrapolated "
+            f"to M=2048: {t4:.1f} s")
+    del wh, wht, w, q, sc
     # C5: gate / up [14336, 4096] and down [4096, 14336], each dequantized once
     if "mlp_w4g128_m512" in secondary:
         d5, f5, m5, mp = 4096, 14336, 512, 8
@@ -305,11 +371,12 @@ def cpu_baselines(args, secondary, n3, k3, headline_bytes, log):
             del p5, s5
             x5 = normal_f32(4, (mp, shape[1]), 1.0, stream=3).astype(np.float64)
             ta, _ = timed(lambda: O.linear(x5[:1], wh5), 0)
-            tb, _ = timed(lambda: O.linear(x5, wh5), 0)
-            tm = ta + (m5 - 1) * (tb - ta) / (mp - 1)
+            wt5 = np.ascontiguousarray(wh5.T)
+            tb, _ = timed(lambda: O.mm(x5, wt5), 0)
+            tm = ta + (m5 - 1) * tb / mp
             tot += count * tm
-            parts.append(f"{name} {ta * 1e3:.0f} ms at M=1, {tb * 1e3:.0f} ms at M'={mp}")
-            del wh5
+            parts.append(f"{name} {ta * 1e3:.0f} ms at M=1, i-p-j loop {tb * 1e3:.0f} ms for M'={mp} rows")
+            del wh5, wt5
         secondary["mlp_w4g128_m512"]["cpu_baseline"] = entry(
             round(m5 / tot, 4), "tokens/s",
             f"config 5: Linear::forward (" + "; ".join(parts) + f"), extrapolated to M=512 and summed over "
@@ -387,8 +454,26 @@ def main():
         if want("gemv_w4"):
             ms, mode = timer.run(gemv_w4(1), args.steps, args.warmup)
             gbs = w4_bytes_m(1) / (ms * 1e-3) / 1e9
-            headline = {"ms": ms, "gbs": gbs, "mode": mode}
+            headline = {"ms": ms, "gbs": gbs, "mode": mode, "modes_us": {k: round(v * 1e3, 3) for k, v in timer.last.items()}}
             log(f"gemv_w4 M=1: {ms * 1e3:.2f} us/step  {gbs:.0f} GB/s  ({mode})")
+            if tile == 64 and not args.no_secondary:
+                # the same launch with its arithmetic left out (libtq_peaks.so): what the
+                # loads, x staging and block reduction of this kernel cost on their own
+                Lp = _peaks_lib()
+                sk_out = torch.empty(2 * (n3 // 64) * 64, dtype=torch.int32, device=dev)
+
+                def skeleton(i):
+                    pt, st, _, _ = copies[i % len(copies)]
+                    rc = Lp.tqp_gemv_w4_skeleton(ptr(x), ptr(pt), ptr(st), n3, k3, ptr(sk_out), stream())
+                    if rc != 0:
+                        raise RuntimeError(f"tqp_gemv_w4_skeleton: hipError {rc}")
+
+                mss, modes = timer.run(skeleton, args.steps, args.warmup)
+                secondary["gemv_w4g128_m1_loads_only"] = {
+                    "us": round(mss * 1e3, 3), "GB/s": round(w4_bytes_m(1) / (mss * 1e-3) / 1e9, 1), "timing": modes,
+                    "note": "the headline launch with the nibble unpack and MFMAs replaced by an xor fold: same loads, "
+                            "x staging and block reduction"}
+                log(f"gemv_w4 M=1 without arithmetic: {mss * 1e3:.2f} us/step")
         if not args.no_secondary and (only is None or only == "gemv_w4_m"):
             for m in (2, 4, 8, 16):
                 ms, mode = timer.run(gemv_w4(m), args.steps, args.warmup)
@@ -753,7 +838,8 @@ def main():
         "data": "synthetic (numpy PCG64 normals, seeded; weights rotate over copies > 2x MALL)",
         "config": {"workload": "int4_g128_dequant_gemv", "baseline_config": 3, "n": n3, "k": k3, "m": 1,
                    "group": 128, "weight_layout": "row-tiled",
-                   "timing": f"{headline['mode']}, median of {max(1, args.reps)} timed replays of {args.steps} launches"},
+                   "timing": f"{headline['mode']}, median of {max(1, args.reps)} timed replays of {args.steps} launches",
+                   "us_per_launch_by_timing": headline["modes_us"]},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "algorithmic_bytes_per_launch": w4_bytes_m(1),

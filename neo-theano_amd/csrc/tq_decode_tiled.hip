@@ -40,8 +40,9 @@
 //    tile and a run of groups, reads its tokens' x straight from L2 (no LDS
 //    staging, no barrier before the arithmetic) and consumes its loads in
 //    order; the runs meet in LDS (details at the kernel).
-//    k_decode_tiled_mfma_sx is the same for runs of up to 2 groups with each
-//    wave's x fetched as whole token rows into a private LDS strip.
+//    k_decode_tiled_mfma_sx is the same with each wave's x fetched as whole
+//    token rows into a private LDS strip (runs of up to 2 groups, and the decode
+//    FFN's down projection in two phases of 2 groups).
 #include <mutex>
 
 #include "tq_internal.h"
@@ -244,13 +245,10 @@ __device__ __forceinline__ u32x4 unpack_w4_136(uint32_t w) {
 // of the group for every token, the start value of each row group's chain, so
 // the offset cancels inside the MFMA accumulator; the f16 scale is applied per
 // group, the factor 1/8 at the end.  The K runs meet in LDS in a fixed order.
-// kFold: the decode FFN's down projection on h as kEpiGateUp wrote it (each
-// 8-block in the slot order of unpack_w4_136, which then unpacks the weights as
-// 136 + q, with -136 as the constant operand and no factor), m = 2t rows of t
-// tokens (hi rows, then lo rows) whose two halves are added per token, and K
-// split over gridDim.y blocks per tile added into a zeroed y (two addends onto
-// zero: the same sum in either order).
-template <int kR, int kGPW, bool kFold = false>
+// Runs of 1-2 groups, and the decode FFN's down projection, take
+// k_decode_tiled_mfma_sx (x staged through LDS); this one serves runs of 3-4
+// groups (K up to 8192), whose x would not fit the LDS strips.
+template <int kR, int kGPW>
 __global__ __launch_bounds__(kBlock) void k_decode_tiled_mfma(const uint16_t* __restrict__ x, int m,
                                                               const uint8_t* __restrict__ pt,
                                                               const uint16_t* __restrict__ st,
@@ -263,15 +261,13 @@ __global__ __launch_bounds__(kBlock) void k_decode_tiled_mfma(const uint16_t* __
     const int q = lane >> 4, r16 = lane & 15;
     const int64_t tile = blockIdx.x;
     const int64_t C = k >> 5, G = k >> 7;
-    // K split over gridDim.y blocks per tile: this block takes groups [gb, ge)
-    const int64_t gh = (G + gridDim.y - 1) / gridDim.y, gb = blockIdx.y * gh, ge = min(G, gb + gh);
-    const int64_t g0 = gb + static_cast<int64_t>(wave) * kGPW;
+    const int64_t g0 = static_cast<int64_t>(wave) * kGPW;
 
-    // x of token r16 (zero past m); groups past ge are clamped (and skipped below)
+    // x of token r16 (zero past m); groups past K are clamped (and skipped below)
     u32x4 xf[kGPW][4];
     const bool tok = r16 < m;
     const uint16_t* xr = x + static_cast<int64_t>(tok ? r16 : 0) * k + 32 * q;
-    const int64_t gl = max<int64_t>(ge - 1, 0);  // last group of the block (clamp target)
+    const int64_t gl = G - 1;
 #pragma unroll
     for (int i = 0; i < kGPW; ++i) {
         const int64_t g = min<int64_t>(g0 + i, gl);
@@ -299,18 +295,16 @@ __global__ __launch_bounds__(kBlock) void k_decode_tiled_mfma(const uint16_t* __
             w[i][r] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wb + ((4 * g + q) * T + 16 * r) * 16));
     }
 
-    // bf16 -136 (kFold) or -192: minus the offset of the unpacked weights
-    const u32x4 aoff = kFold ? u32x4{0xC308C308u, 0xC308C308u, 0xC308C308u, 0xC308C308u}
-                             : u32x4{0xC340C340u, 0xC340C340u, 0xC340C340u, 0xC340C340u};
+    const u32x4 aoff = u32x4{0xC340C340u, 0xC340C340u, 0xC340C340u, 0xC340C340u};  // bf16 -192
     f32x4 acc[kR];
 #pragma unroll
     for (int r = 0; r < kR; ++r) acc[r] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int i = 0; i < kGPW; ++i) {
-        if (g0 + i >= ge) break;  // wave-uniform
+        if (g0 + i >= G) break;  // wave-uniform
         u32x4 xb[4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) xb[j] = kFold ? xf[i][j] : pair_slots(xf[i][j]);
+        for (int j = 0; j < 4; ++j) xb[j] = pair_slots(xf[i][j]);
         f32x4 xs = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int j = 0; j < 4; ++j) xs = mfma16_bf16(aoff, xb[j], xs);
@@ -319,7 +313,7 @@ __global__ __launch_bounds__(kBlock) void k_decode_tiled_mfma(const uint16_t* __
             const uint32_t ws[4] = {w[i][r].x, w[i][r].y, w[i][r].z, w[i][r].w};
             f32x4 d = xs;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) d = mfma16_bf16(kFold ? unpack_w4_136(ws[j]) : unpack_w4_24(ws[j]), xb[j], d);
+            for (int j = 0; j < 4; ++j) d = mfma16_bf16(unpack_w4_24(ws[j]), xb[j], d);
             const uint32_t s01 = sc[i][r].x, s23 = sc[i][r].y;
             acc[r].x = fmaf(__half2float(__ushort_as_half(static_cast<uint16_t>(s01))), d.x, acc[r].x);
             acc[r].y = fmaf(__half2float(__ushort_as_half(static_cast<uint16_t>(s01 >> 16))), d.y, acc[r].y);
@@ -333,10 +327,149 @@ __global__ __launch_bounds__(kBlock) void k_decode_tiled_mfma(const uint16_t* __
 #pragma unroll
         for (int e = 0; e < 4; ++e) part[wave][16 * r + 4 * q + e][r16] = acc[r][e];
     __syncthreads();
-    auto wsum = [&](int row, int t) {
+    for (int i = threadIdx.x; i < T * m; i += kBlock) {
+        const int row = i / m, t = i - row * m;
+        const int64_t grow = tile * T + row;
+        if (grow >= n) continue;
         float sum = 0.0f;
 #pragma unroll
         for (int v = 0; v < kWaves; ++v) sum += part[v][row][t];
+        y[t * n + grow] = 0.125f * sum + (bias ? bias[grow] : 0.0f);
+    }
+}
+
+// k_decode_tiled_mfma with x staged through LDS.  Read straight from L2 in the
+// MFMA's operand layout, a wave's x fragments take 16 bytes from each of 16
+// token rows per instruction (16 cache lines, half of each used), and at 16
+// tokens they are as many bytes as the weights: the per-CU load path carried
+// twice the weight stream.  Here each wave fetches its K slice of every token's
+// x as whole rows, two groups at a time (lane l of load i of a phase: token
+// i * 4 / kGP + l / (16 kGP), elements 8 (l % (16 kGP)) .. + 7 of the phase's
+// slice), writes them to a private LDS strip in the slot order of the weight
+// unpack (token rows padded by 16 bytes, so the 16 tokens' B reads of one MFMA
+// hit distinct banks) and reads the B operands back from it.  Runs of 4 groups
+// (the FFN's down projection, K = F split in two) go in two phases through a
+// strip of two groups: the x of both phases is loaded up front and the second
+// phase overwrites the strip after the first has read it (the strip is private
+// to the wave, whose LDS accesses complete in order).  The wave's partial sums
+// go into its own strip once its loop is done.
+// kFold: the decode FFN's down projection on h as kEpiGateUp wrote it (each
+// 8-block in the slot order of unpack_w4_136, which then unpacks the weights as
+// 136 + q, with -136 as the constant operand and no factor), m = 2t rows of t
+// tokens (hi rows, then lo rows) whose two halves are added per token, and K
+// split over gridDim.y blocks per tile added into a zeroed y (two addends onto
+// zero: the same sum in either order).
+template <int kR, int kGPW, bool kFold = false>
+__global__ __launch_bounds__(kBlock) void k_decode_tiled_mfma_sx(const uint16_t* __restrict__ x, int m,
+                                                                 const uint8_t* __restrict__ pt,
+                                                                 const uint16_t* __restrict__ st,
+                                                                 const float* __restrict__ bias, int64_t n,
+                                                                 int64_t k, float* __restrict__ y) {
+    static_assert(kGPW == 1 || kGPW == 2 || kGPW == 4, "runs of 1, 2 or 4 groups per wave");
+    constexpr int kGP = kGPW < 2 ? kGPW : 2;  // groups per phase
+    constexpr int kP = kGPW / kGP;             // phases
+    constexpr int T = 16 * kR;
+    constexpr int kE = 128 * kGP;       // elements of a token's phase slice
+    constexpr int kRow = 2 * kE + 16;   // bytes of a token's padded strip row
+    constexpr int kStrip = 16 * kRow;
+    constexpr int kLPT = 16 * kGP;      // lanes per token row in a load
+    constexpr int kTPI = 64 / kLPT;     // token rows per load
+    constexpr int kNI = 16 / kTPI;      // loads per wave and phase
+    static_assert(T * 16 * 4 <= kStrip, "a wave's partial sums fit in its strip");
+    __shared__ __attribute__((aligned(16))) uint8_t strips[kWaves][kStrip];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int q = lane >> 4, r16 = lane & 15;
+    const int64_t tile = blockIdx.x;
+    const int64_t C = k >> 5, G = k >> 7;
+    // K split over gridDim.y blocks per tile: this block takes groups [gb, ge)
+    const int64_t gh = (G + gridDim.y - 1) / gridDim.y, gb = blockIdx.y * gh, ge = min(G, gb + gh);
+    const int64_t g0 = gb + static_cast<int64_t>(wave) * kGPW;
+    const int64_t gl = max<int64_t>(ge - 1, 0);  // groups past the block's range are clamped (and skipped below)
+
+    // x rows first (vmcnt retires in order), then scales, then weights
+    const int e0 = 8 * (lane % kLPT);
+    u32x4 xl[kP][kNI];
+#pragma unroll
+    for (int p = 0; p < kP; ++p)
+#pragma unroll
+        for (int i = 0; i < kNI; ++i) {
+            const int t = i * kTPI + lane / kLPT;
+            const int64_t ge0 = g0 + p * kGP;  // first group of the phase
+            const bool live = t < m && ge0 + e0 / 128 < ge;
+            xl[p][i] = live ? *reinterpret_cast<const u32x4*>(x + static_cast<int64_t>(t) * k + ge0 * 128 + e0)
+                            : u32x4{0u, 0u, 0u, 0u};
+        }
+    uint2 sc[kGPW][kR];
+#pragma unroll
+    for (int i = 0; i < kGPW; ++i) {
+        const int64_t g = min<int64_t>(g0 + i, gl);
+#pragma unroll
+        for (int r = 0; r < kR; ++r)
+            sc[i][r] = *reinterpret_cast<const uint2*>(st + (tile * G + g) * T + 16 * r + 4 * q);
+    }
+    const uint8_t* wb = pt + (tile * C * T + r16) * 16;
+    u32x4 w[kGPW][kR];
+#pragma unroll
+    for (int i = 0; i < kGPW; ++i) {
+        const int64_t g = min<int64_t>(g0 + i, gl);
+#pragma unroll
+        for (int r = 0; r < kR; ++r)
+            w[i][r] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wb + ((4 * g + q) * T + 16 * r) * 16));
+    }
+    uint8_t* sx = strips[wave];
+
+    // bf16 -136 (kFold) or -192: minus the offset of the unpacked weights
+    const u32x4 aoff = kFold ? u32x4{0xC308C308u, 0xC308C308u, 0xC308C308u, 0xC308C308u}
+                             : u32x4{0xC340C340u, 0xC340C340u, 0xC340C340u, 0xC340C340u};
+    f32x4 acc[kR];
+#pragma unroll
+    for (int r = 0; r < kR; ++r) acc[r] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int p = 0; p < kP; ++p) {
+        if (g0 + p * kGP >= ge) break;  // wave-uniform
+#pragma unroll
+        for (int i = 0; i < kNI; ++i) {
+            const int t = i * kTPI + lane / kLPT;
+            *reinterpret_cast<u32x4*>(sx + t * kRow + 2 * e0) = kFold ? xl[p][i] : pair_slots(xl[p][i]);
+        }
+#pragma unroll
+        for (int ii = 0; ii < kGP; ++ii) {
+            const int i = p * kGP + ii;
+            if (g0 + i >= ge) break;  // wave-uniform
+            u32x4 xb[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                xb[j] = *reinterpret_cast<const u32x4*>(sx + r16 * kRow + 2 * (128 * ii + 32 * q + 8 * j));
+            f32x4 xs = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) xs = mfma16_bf16(aoff, xb[j], xs);
+#pragma unroll
+            for (int r = 0; r < kR; ++r) {
+                const uint32_t ws[4] = {w[i][r].x, w[i][r].y, w[i][r].z, w[i][r].w};
+                f32x4 d = xs;
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    d = mfma16_bf16(kFold ? unpack_w4_136(ws[j]) : unpack_w4_24(ws[j]), xb[j], d);
+                const uint32_t s01 = sc[i][r].x, s23 = sc[i][r].y;
+                acc[r].x = fmaf(__half2float(__ushort_as_half(static_cast<uint16_t>(s01))), d.x, acc[r].x);
+                acc[r].y = fmaf(__half2float(__ushort_as_half(static_cast<uint16_t>(s01 >> 16))), d.y, acc[r].y);
+                acc[r].z = fmaf(__half2float(__ushort_as_half(static_cast<uint16_t>(s23))), d.z, acc[r].z);
+                acc[r].w = fmaf(__half2float(__ushort_as_half(static_cast<uint16_t>(s23 >> 16))), d.w, acc[r].w);
+            }
+        }
+    }
+    // lane holds D[row 16 r + 4 q + e][token r16]; part[row][token] in the wave's strip
+    float* part = reinterpret_cast<float*>(sx);
+#pragma unroll
+    for (int r = 0; r < kR; ++r)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) part[(16 * r + 4 * q + e) * 16 + r16] = acc[r][e];
+    __syncthreads();
+    auto wsum = [&](int row, int t) {
+        float sum = 0.0f;
+#pragma unroll
+        for (int v = 0; v < kWaves; ++v) sum += reinterpret_cast<const float*>(strips[v])[row * 16 + t];
         return sum;
     };
     if constexpr (kFold) {
@@ -358,121 +491,6 @@ __global__ __launch_bounds__(kBlock) void k_decode_tiled_mfma(const uint16_t* __
             if (grow >= n) continue;
             y[t * n + grow] = 0.125f * wsum(row, t) + (bias ? bias[grow] : 0.0f);
         }
-    }
-}
-
-// k_decode_tiled_mfma (plain epilogue) with x staged through LDS, for runs of
-// kGPW <= 2 groups per wave.  Read straight from L2 in the MFMA's operand
-// layout, a wave's x fragments take 16 bytes from each of 16 token rows per
-// instruction (16 cache lines, half of each used), and at 16 tokens they are as
-// many bytes as the weights: the per-CU load path carried twice the weight
-// stream.  Here each wave fetches its K slice of every token's x as whole rows
-// (lane l of load i: token i * 4 / kGPW + l / (16 kGPW), elements 8 (l % (16
-// kGPW)) .. + 7 of the slice), writes them to a private LDS strip in the slot
-// order of unpack_w4_24 (token rows padded by 16 bytes, so the 16 tokens' B
-// reads of one MFMA hit distinct banks) and reads the B operands back from it.
-// The wave's partial sums go into its own strip once its loop is done.
-template <int kR, int kGPW>
-__global__ __launch_bounds__(kBlock) void k_decode_tiled_mfma_sx(const uint16_t* __restrict__ x, int m,
-                                                                 const uint8_t* __restrict__ pt,
-                                                                 const uint16_t* __restrict__ st,
-                                                                 const float* __restrict__ bias, int64_t n,
-                                                                 int64_t k, float* __restrict__ y) {
-    static_assert(kGPW == 1 || kGPW == 2, "16 tokens' strips fit the LDS at up to 2 groups per wave");
-    constexpr int T = 16 * kR;
-    constexpr int kE = 128 * kGPW;      // elements of a token's slice
-    constexpr int kRow = 2 * kE + 16;   // bytes of a token's padded strip row
-    constexpr int kStrip = 16 * kRow;
-    constexpr int kLPT = 16 * kGPW;     // lanes per token row in a load
-    constexpr int kTPI = 64 / kLPT;     // token rows per load
-    constexpr int kNI = 16 / kTPI;      // loads per wave
-    static_assert(T * 16 * 4 <= kStrip, "a wave's partial sums fit in its strip");
-    __shared__ __attribute__((aligned(16))) uint8_t strips[kWaves][kStrip];
-    const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int q = lane >> 4, r16 = lane & 15;
-    const int64_t tile = blockIdx.x;
-    const int64_t C = k >> 5, G = k >> 7;
-    const int64_t g0 = static_cast<int64_t>(wave) * kGPW;
-    const int64_t gl = G - 1;  // groups past K are clamped (and skipped below)
-
-    // x rows first (vmcnt retires in order), then scales, then weights
-    const int e0 = 8 * (lane % kLPT);
-    u32x4 xl[kNI];
-#pragma unroll
-    for (int i = 0; i < kNI; ++i) {
-        const int t = i * kTPI + lane / kLPT;
-        const bool live = t < m && g0 + e0 / 128 < G;
-        xl[i] = live ? *reinterpret_cast<const u32x4*>(x + static_cast<int64_t>(t) * k + g0 * 128 + e0)
-                     : u32x4{0u, 0u, 0u, 0u};
-    }
-    uint2 sc[kGPW][kR];
-#pragma unroll
-    for (int i = 0; i < kGPW; ++i) {
-        const int64_t g = min<int64_t>(g0 + i, gl);
-#pragma unroll
-        for (int r = 0; r < kR; ++r)
-            sc[i][r] = *reinterpret_cast<const uint2*>(st + (tile * G + g) * T + 16 * r + 4 * q);
-    }
-    const uint8_t* wb = pt + (tile * C * T + r16) * 16;
-    u32x4 w[kGPW][kR];
-#pragma unroll
-    for (int i = 0; i < kGPW; ++i) {
-        const int64_t g = min<int64_t>(g0 + i, gl);
-#pragma unroll
-        for (int r = 0; r < kR; ++r)
-            w[i][r] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wb + ((4 * g + q) * T + 16 * r) * 16));
-    }
-    uint8_t* sx = strips[wave];
-#pragma unroll
-    for (int i = 0; i < kNI; ++i) {
-        const int t = i * kTPI + lane / kLPT;
-        *reinterpret_cast<u32x4*>(sx + t * kRow + 2 * e0) = pair_slots(xl[i]);
-    }
-    // the strip is private to the wave: its LDS accesses complete in order
-
-    const u32x4 aoff = u32x4{0xC340C340u, 0xC340C340u, 0xC340C340u, 0xC340C340u};  // bf16 -192
-    f32x4 acc[kR];
-#pragma unroll
-    for (int r = 0; r < kR; ++r) acc[r] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int i = 0; i < kGPW; ++i) {
-        if (g0 + i >= G) break;  // wave-uniform
-        u32x4 xb[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-            xb[j] = *reinterpret_cast<const u32x4*>(sx + r16 * kRow + 2 * (128 * i + 32 * q + 8 * j));
-        f32x4 xs = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int j = 0; j < 4; ++j) xs = mfma16_bf16(aoff, xb[j], xs);
-#pragma unroll
-        for (int r = 0; r < kR; ++r) {
-            const uint32_t ws[4] = {w[i][r].x, w[i][r].y, w[i][r].z, w[i][r].w};
-            f32x4 d = xs;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) d = mfma16_bf16(unpack_w4_24(ws[j]), xb[j], d);
-            const uint32_t s01 = sc[i][r].x, s23 = sc[i][r].y;
-            acc[r].x = fmaf(__half2float(__ushort_as_half(static_cast<uint16_t>(s01))), d.x, acc[r].x);
-            acc[r].y = fmaf(__half2float(__ushort_as_half(static_cast<uint16_t>(s01 >> 16))), d.y, acc[r].y);
-            acc[r].z = fmaf(__half2float(__ushort_as_half(static_cast<uint16_t>(s23))), d.z, acc[r].z);
-            acc[r].w = fmaf(__half2float(__ushort_as_half(static_cast<uint16_t>(s23 >> 16))), d.w, acc[r].w);
-        }
-    }
-    // lane holds D[row 16 r + 4 q + e][token r16]; part[row][token] in the wave's strip
-    float* part = reinterpret_cast<float*>(sx);
-#pragma unroll
-    for (int r = 0; r < kR; ++r)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) part[(16 * r + 4 * q + e) * 16 + r16] = acc[r][e];
-    __syncthreads();
-    for (int i = threadIdx.x; i < T * m; i += kBlock) {
-        const int row = i / m, t = i - row * m;
-        const int64_t grow = tile * T + row;
-        if (grow >= n) continue;
-        float sum = 0.0f;
-#pragma unroll
-        for (int v = 0; v < kWaves; ++v) sum += reinterpret_cast<const float*>(strips[v])[row * 16 + t];
-        y[t * n + grow] = 0.125f * sum + (bias ? bias[grow] : 0.0f);
     }
 }
 
@@ -1091,11 +1109,11 @@ int launch_mfma_fold(int64_t gpw, int64_t tiles, hipStream_t s, const uint16_t* 
         return fail(TQ_EINVAL, "tq_mlp_w4g128_decode: %d rows of h at %lld groups per wave", rows, (long long)gpw);
     const dim3 grid(static_cast<unsigned>(tiles), 2u);
     if (gpw <= 1)
-        k_decode_tiled_mfma<kR, 1, true><<<grid, kBlock, 0, s>>>(h, rows, pt, st, nullptr, n, k, y);
+        k_decode_tiled_mfma_sx<kR, 1, true><<<grid, kBlock, 0, s>>>(h, rows, pt, st, nullptr, n, k, y);
     else if (gpw <= 2)
-        k_decode_tiled_mfma<kR, 2, true><<<grid, kBlock, 0, s>>>(h, rows, pt, st, nullptr, n, k, y);
+        k_decode_tiled_mfma_sx<kR, 2, true><<<grid, kBlock, 0, s>>>(h, rows, pt, st, nullptr, n, k, y);
     else
-        k_decode_tiled_mfma<kR, 4, true><<<grid, kBlock, 0, s>>>(h, rows, pt, st, nullptr, n, k, y);
+        k_decode_tiled_mfma_sx<kR, 4, true><<<grid, kBlock, 0, s>>>(h, rows, pt, st, nullptr, n, k, y);
     return check_launch("tq_mlp_w4g128_decode");
 }
 

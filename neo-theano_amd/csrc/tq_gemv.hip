@@ -47,7 +47,10 @@ struct CodeFp8 {
 // Chunk c covers k in [1024c, 1024c + 1024): lane l owns the 16 codes at
 // k = 1024c + 16l.  y = s[row] * sum(value(q) * x) + b.
 //
-// One 512-thread block per CU (persistent), 8 waves.  With kKS = 1 every wave
+// kWB waves per block, 8 / kWB blocks per CU (persistent): 4-wave blocks, two
+// per CU, at one token (each block stages x itself; 4.6 against 4.75 us at
+// 4096 x 4096), one 8-wave block per CU beyond (x of several tokens staged
+// twice per CU costs more than it gains).  With kKS = 1 every wave
 // owns a contiguous run of rows and all of K; with kKS = 2 the waves pair up:
 // both waves of a pair own the same run of rows, the first takes chunks
 // 0 .. kC0 - 1 and the second the rest, so each holds half of x in registers
@@ -56,11 +59,14 @@ struct CodeFp8 {
 // (unconditional: rows past its run re-read its last row and are not
 // stored), then the block stages x in LDS once (f32, K-contiguous per token)
 // and every lane copies its 16-value slices into registers; rows are then
-// consumed kRows at a time with the next group's loads issued before the
-// current group's arithmetic.  x crosses L2 once per block instead of once per
+// consumed kRows at a time.  The next group's loads go out once the current
+// group's have landed, before its arithmetic: one group in flight per wave.
+// With every wave's next rows requested at once (8 KB per wave, the whole
+// 16.8 MB weight of a 4096 x 4096 layer in flight) the same GEMV took 5.13
+// against 4.63 us.  x crosses L2 once per block instead of once per
 // wave.  A pair's two partial sums of a row meet in LDS after the row loop
 // and are added in a fixed order (first half + second half).
-constexpr int kBlockW8 = 512;
+constexpr int kBlockW8 = 512;  // the fused-activation GEMV: 8 waves, one block per CU
 constexpr int kWavesW8 = kBlockW8 / kWave;
 
 // LDS slot of x item j (4 values) of a token: item 4l + e of a 256-item chunk is
@@ -70,23 +76,24 @@ constexpr int kWavesW8 = kBlockW8 / kWave;
 __device__ __forceinline__ int xslot(int j) { return j ^ ((j >> 4) & 3); }
 constexpr int kMaxPairRows = 64;  // rows per wave pair that the LDS partial sums hold
 
-template <class Code, int kM, int kChunks, int kRows, int kKS>
-__global__ __launch_bounds__(kBlockW8) void k_gemv_w8(const float* __restrict__ x, int64_t x_stride,
+template <class Code, int kM, int kChunks, int kRows, int kKS, int kWB>
+__global__ __launch_bounds__(64 * kWB, 8 / kWB) void k_gemv_w8(const float* __restrict__ x, int64_t x_stride,
                                                       const typename Code::code_t* __restrict__ q,
                                                       const float* __restrict__ s,
                                                       const float* __restrict__ bias, int64_t n,
                                                       int64_t k, float* __restrict__ y,
                                                       int64_t y_stride, int64_t rows_per_wave) {
     static_assert(kKS == 1 || kKS == 2, "K split over one or two waves");
+    constexpr int kBlk = 64 * kWB;
     constexpr int kC0 = (kChunks + kKS - 1) / kKS;  // chunks of the first (or only) wave of a pair
     __shared__ f32x4 xs[kM][kChunks * 256];
-    __shared__ float part[kKS == 2 ? kWavesW8 : 1][kKS == 2 ? kMaxPairRows : 1][kM];
+    __shared__ float part[kKS == 2 ? kWB : 1][kKS == 2 ? kMaxPairRows : 1][kM];
     const int lane = threadIdx.x & (kWave - 1);
     const int wv = threadIdx.x >> 6;
     const int half = kKS == 2 ? (wv & 1) : 0;
     // chunks [cb, cb + nc) of every row; the second wave of a pair may have fewer
     const int cb = half * kC0, nc = half == 0 ? kC0 : kChunks - kC0;
-    const int64_t wave = uniform(static_cast<int64_t>(blockIdx.x) * (kWavesW8 / kKS) + wv / kKS);
+    const int64_t wave = uniform(static_cast<int64_t>(blockIdx.x) * (kWB / kKS) + wv / kKS);
     const int64_t row_begin = wave * rows_per_wave;
     const int64_t row_end = min(n, row_begin + rows_per_wave);
     const int64_t row_last = max(row_begin, row_end - 1);  // clamp target (valid when the run is empty too)
@@ -106,20 +113,20 @@ __global__ __launch_bounds__(kBlockW8) void k_gemv_w8(const float* __restrict__ 
     // the weight rows issued after it), then the first rows, then x -> LDS (zero
     // past K) and each lane's 16-value slices -> registers
     const int k4 = static_cast<int>(k >> 2);
-    constexpr int kXItems = kM * kChunks * 256, kXPer = (kXItems + kBlockW8 - 1) / kBlockW8;
+    constexpr int kXItems = kM * kChunks * 256, kXPer = (kXItems + kBlk - 1) / kBlk;
     f32x4 xv[kXPer];
 #pragma unroll
     for (int qi = 0; qi < kXPer; ++qi) {
-        const int i = threadIdx.x + qi * kBlockW8;
+        const int i = threadIdx.x + qi * kBlk;
         const int m = i / (kChunks * 256), j = i - m * (kChunks * 256);
         xv[qi] = i < kXItems && j < k4 ? *reinterpret_cast<const f32x4*>(x + m * x_stride + 4 * j)
                                        : f32x4{0.f, 0.f, 0.f, 0.f};
     }
-    i32x4 wq[kRows][kC0];
-    load_rows(row_begin, wq);
+    i32x4 wa[kRows][kC0], wb[kRows][kC0];
+    load_rows(row_begin, wa);
 #pragma unroll
     for (int qi = 0; qi < kXPer; ++qi) {
-        const int i = threadIdx.x + qi * kBlockW8;
+        const int i = threadIdx.x + qi * kBlk;
         const int m = i / (kChunks * 256), j = i - m * (kChunks * 256);
         if (i < kXItems) xs[m][xslot(j)] = xv[qi];
     }
@@ -139,13 +146,8 @@ __global__ __launch_bounds__(kBlockW8) void k_gemv_w8(const float* __restrict__ 
                 xr[m][c][4 * j + 3] = v.w;
             }
 
-    for (int64_t row0 = row_begin; row0 < row_end; row0 += kRows) {
-        i32x4 cur[kRows][kC0];
-#pragma unroll
-        for (int r = 0; r < kRows; ++r)
-#pragma unroll
-            for (int c = 0; c < kC0; ++c) cur[r][c] = wq[r][c];
-        if (row0 + kRows < row_end) load_rows(row0 + kRows, wq);
+    // the kRows rows at row0 from the registers `cur` (stores past the run skipped)
+    auto group = [&](int64_t row0, const i32x4 (&cur)[kRows][kC0]) {
 #pragma unroll
         for (int r = 0; r < kRows; ++r) {
             float acc[kM];
@@ -167,11 +169,17 @@ __global__ __launch_bounds__(kBlockW8) void k_gemv_w8(const float* __restrict__ 
             }
             const int64_t row = row0 + r;
             if constexpr (kKS == 1) {
-                const float sc = s[min(row, row_clamp)];
+                // scale and bias read at a wave-uniform address (scalar loads): a bias
+                // read under the lane-0 store condition became a vector load whose
+                // wait, hoisted ahead of the arithmetic, also waited for every
+                // weight load in flight
+                const int64_t rc = min(row, row_clamp);
+                const float sc = s[rc];
+                const float bb = bias ? bias[rc] : 0.0f;
 #pragma unroll
                 for (int m = 0; m < kM; ++m) {
                     const float v = wave_sum(acc[m]);
-                    if (lane == 0 && row < row_end) y[m * y_stride + row] = sc * v + (bias ? bias[row] : 0.0f);
+                    if (lane == 0 && row < row_end) y[m * y_stride + row] = sc * v + bb;
                 }
             } else {
 #pragma unroll
@@ -181,6 +189,28 @@ __global__ __launch_bounds__(kBlockW8) void k_gemv_w8(const float* __restrict__ 
                 }
             }
         }
+    };
+    // Row groups alternate between two register buffers, the next group's loads
+    // issued before the current group's arithmetic.  The arithmetic reads the
+    // buffers in place: a copy of a register whose load is in flight waits for
+    // that load, which would make every group wait for all of its loads.
+    for (int64_t row0 = row_begin;;) {
+        if (row0 + kRows >= row_end) {
+            group(row0, wa);
+            break;
+        }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the current group has landed
+        load_rows(row0 + kRows, wb);
+        group(row0, wa);
+        row0 += kRows;
+        if (row0 + kRows >= row_end) {
+            group(row0, wb);
+            break;
+        }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        load_rows(row0 + kRows, wa);
+        group(row0, wb);
+        row0 += kRows;
     }
     if constexpr (kKS == 2) {
         __syncthreads();
@@ -291,8 +321,8 @@ __global__ __launch_bounds__(kBlockW8) void k_gemv_a8(const float* __restrict__ 
         xv[qi] = i < kXItems && j < k4 ? *reinterpret_cast<const f32x4*>(x + m * x_stride + 4 * j)
                                        : f32x4{0.f, 0.f, 0.f, 0.f};
     }
-    i32x4 wq[kRows][kChunks];
-    load_rows(row_begin, wq);
+    i32x4 wa[kRows][kChunks], wb[kRows][kChunks];
+    load_rows(row_begin, wa);
 
     // x -> LDS (zero past K) and the NaN-ignoring absmax of each row over its K values
     float mx[kM];
@@ -348,13 +378,7 @@ __global__ __launch_bounds__(kBlockW8) void k_gemv_a8(const float* __restrict__ 
                 P::unpack(xs[m][xslot(c * 256 + 4 * lane + j)], &xr[m][c][j * P::kRegsPer4]);
     if (row_begin >= row_end) return;
 
-    for (int64_t row0 = row_begin; row0 < row_end; row0 += kRows) {
-        i32x4 cur[kRows][kChunks];
-#pragma unroll
-        for (int r = 0; r < kRows; ++r)
-#pragma unroll
-            for (int c = 0; c < kChunks; ++c) cur[r][c] = wq[r][c];
-        if (row0 + kRows < row_end) load_rows(row0 + kRows, wq);
+    auto group = [&](int64_t row0, const i32x4 (&cur)[kRows][kChunks]) {
 #pragma unroll
         for (int r = 0; r < kRows; ++r) {
             typename P::acc_t acc[kM];
@@ -365,23 +389,42 @@ __global__ __launch_bounds__(kBlockW8) void k_gemv_a8(const float* __restrict__ 
 #pragma unroll
                 for (int m = 0; m < kM; ++m) P::dot16(cur[r][c], xr[m][c], acc[m]);
             const int64_t row = row0 + r;
-            const float sc = s[min(row, row_clamp)];
+            const int64_t rc = min(row, row_clamp);
+            const float sc = s[rc];
+            const float bb = bias ? bias[rc] : 0.0f;  // wave-uniform, as in k_gemv_w8
 #pragma unroll
             for (int m = 0; m < kM; ++m) {
                 const float v = P::total(acc[m]);
-                if (lane == 0 && row < row_end) y[m * y_stride + row] = fmaf(v * sa[m], sc, bias ? bias[row] : 0.0f);
+                if (lane == 0 && row < row_end) y[m * y_stride + row] = fmaf(v * sa[m], sc, bb);
             }
         }
+    };
+    // two register buffers in turn, read in place (as in k_gemv_w8)
+    for (int64_t row0 = row_begin;;) {
+        if (row0 + kRows >= row_end) {
+            group(row0, wa);
+            break;
+        }
+        load_rows(row0 + kRows, wb);
+        group(row0, wa);
+        row0 += kRows;
+        if (row0 + kRows >= row_end) {
+            group(row0, wb);
+            break;
+        }
+        load_rows(row0 + kRows, wa);
+        group(row0, wb);
+        row0 += kRows;
     }
 }
 
-// Persistent grid: one block per CU (fewer if there are few rows), contiguous
-// row runs per wave (or wave pair: `runs_per_block` runs per block), a
-// multiple of kRows each.
+// Persistent grid: blocks_per_cu blocks per CU (fewer if there are few rows),
+// contiguous row runs per wave (or wave pair: `runs_per_block` runs per block),
+// a multiple of kRows each.
 template <int kRows>
 void grid_for_rows(int64_t n, int64_t* blocks, int64_t* rows_per_wave, int runs_per_block = kWavesW8,
-                   int64_t max_rows = INT64_MAX) {
-    const int64_t slots = static_cast<int64_t>(device_cu_count()) * runs_per_block;
+                   int64_t max_rows = INT64_MAX, int blocks_per_cu = 1) {
+    const int64_t slots = static_cast<int64_t>(device_cu_count()) * blocks_per_cu * runs_per_block;
     int64_t waves = (n + kRows - 1) / kRows;
     if (waves > slots) waves = slots;
     if ((n + waves - 1) / waves > max_rows) waves = (n + max_rows - 1) / max_rows;  // more blocks than CUs
@@ -392,8 +435,8 @@ void grid_for_rows(int64_t n, int64_t* blocks, int64_t* rows_per_wave, int runs_
     *blocks = (waves + runs_per_block - 1) / runs_per_block;
 }
 
-// Rows in flight per wave: two, unless the x slices held in registers (16 values
-// per token and chunk) would leave no room for two double-buffered groups of
+// Rows per group: two, unless the x slices held in registers (16 values per
+// token and chunk) would leave no room for two double-buffered groups of
 // weight rows (the compiler then spills): one at kM * kChunks > 4.
 constexpr int rows_in_flight(int x_regs) { return x_regs <= 64 ? 2 : 1; }
 
@@ -414,12 +457,15 @@ template <class Code, int kM, int kChunks>
 void launch_w8(const float* x, int64_t xs, const typename Code::code_t* q, const float* s, const float* b,
                int64_t n, int64_t k, float* y, int64_t ys, hipStream_t st) {
     constexpr int kKS = ks_for(kM, kChunks);
-    constexpr int kRows = rows_in_flight(kM * ((kChunks + kKS - 1) / kKS) * 16);
+    // one token: groups of one row (the next row requested once the current one
+    // has landed) in 4-wave blocks, two per CU
+    constexpr int kRows = kM == 1 ? 1 : rows_in_flight(kM * ((kChunks + kKS - 1) / kKS) * 16);
+    constexpr int kWB = kM == 1 ? 4 : 8;
     int64_t blocks, rpw;
     static_assert(kMaxPairRows % kRows == 0, "row runs are whole row groups");
-    grid_for_rows<kRows>(n, &blocks, &rpw, kWavesW8 / kKS, kKS == 2 ? kMaxPairRows : INT64_MAX);
-    k_gemv_w8<Code, kM, kChunks, kRows, kKS><<<static_cast<unsigned>(blocks), kBlockW8, 0, st>>>(x, xs, q, s, b, n,
-                                                                                               k, y, ys, rpw);
+    grid_for_rows<kRows>(n, &blocks, &rpw, kWB / kKS, kKS == 2 ? kMaxPairRows : INT64_MAX, 8 / kWB);
+    k_gemv_w8<Code, kM, kChunks, kRows, kKS, kWB><<<static_cast<unsigned>(blocks), 64 * kWB, 0, st>>>(
+        x, xs, q, s, b, n, k, y, ys, rpw);
 }
 
 template <class Code, int kM, int kChunks = 1>

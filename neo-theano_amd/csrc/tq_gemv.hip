@@ -66,9 +66,6 @@ struct CodeFp8 {
 // against 4.63 us.  x crosses L2 once per block instead of once per
 // wave.  A pair's two partial sums of a row meet in LDS after the row loop
 // and are added in a fixed order (first half + second half).
-constexpr int kBlockW8 = 512;  // the fused-activation GEMV: 8 waves, one block per CU
-constexpr int kWavesW8 = kBlockW8 / kWave;
-
 // LDS slot of x item j (4 values) of a token: item 4l + e of a 256-item chunk is
 // lane l's e-th 16-byte slice, and e is xor-ed with bits 2-3 of l, so that the
 // 64 lanes' reads of one e fall in distinct banks (lanes 64 bytes apart collide
@@ -283,17 +280,18 @@ struct A8<FmtFp8> {
     __device__ static float total(acc_t a) { return wave_sum(a); }
 };
 
-template <class Fmt, int kM, int kChunks, int kRows>
-__global__ __launch_bounds__(kBlockW8) void k_gemv_a8(const float* __restrict__ x, int64_t x_stride,
+template <class Fmt, int kM, int kChunks, int kRows, int kWB>
+__global__ __launch_bounds__(64 * kWB, 8 / kWB) void k_gemv_a8(const float* __restrict__ x, int64_t x_stride,
                                                       const typename Fmt::code_t* __restrict__ q,
                                                       const float* __restrict__ s, const float* __restrict__ bias,
                                                       int64_t n, int64_t k, float* __restrict__ y, int64_t y_stride,
                                                       int64_t rows_per_wave) {
     using P = A8<Fmt>;
+    constexpr int kBlk = 64 * kWB;
     __shared__ f32x4 xs[kM][kChunks * 256];
-    __shared__ float red[kWavesW8][kM];
+    __shared__ float red[kWB][kM];
     const int lane = threadIdx.x & (kWave - 1), wv = threadIdx.x >> 6;
-    const int64_t wave = uniform(static_cast<int64_t>(blockIdx.x) * kWavesW8 + wv);
+    const int64_t wave = uniform(static_cast<int64_t>(blockIdx.x) * kWB + wv);
     const int64_t row_begin = wave * rows_per_wave;
     const int64_t row_end = min(n, row_begin + rows_per_wave);
     const int64_t row_last = max(row_begin, row_end - 1);
@@ -312,11 +310,11 @@ __global__ __launch_bounds__(kBlockW8) void k_gemv_a8(const float* __restrict__ 
     // x first (vmcnt completes in order: the absmax and coding of x then wait for x
     // alone, not for the weight rows issued after it), then the first rows
     const int k4 = static_cast<int>(k >> 2);
-    constexpr int kXItems = kM * kChunks * 256, kXPer = (kXItems + kBlockW8 - 1) / kBlockW8;
+    constexpr int kXItems = kM * kChunks * 256, kXPer = (kXItems + kBlk - 1) / kBlk;
     f32x4 xv[kXPer];
 #pragma unroll
     for (int qi = 0; qi < kXPer; ++qi) {
-        const int i = threadIdx.x + qi * kBlockW8;
+        const int i = threadIdx.x + qi * kBlk;
         const int m = i / (kChunks * 256), j = i - m * (kChunks * 256);
         xv[qi] = i < kXItems && j < k4 ? *reinterpret_cast<const f32x4*>(x + m * x_stride + 4 * j)
                                        : f32x4{0.f, 0.f, 0.f, 0.f};
@@ -330,7 +328,7 @@ __global__ __launch_bounds__(kBlockW8) void k_gemv_a8(const float* __restrict__ 
     for (int m = 0; m < kM; ++m) mx[m] = -INFINITY;
 #pragma unroll
     for (int qi = 0; qi < kXPer; ++qi) {
-        const int i = threadIdx.x + qi * kBlockW8;
+        const int i = threadIdx.x + qi * kBlk;
         if (i >= kXItems) continue;
         const int m = i / (kChunks * 256), j = i - m * (kChunks * 256);
         const f32x4 v = xv[qi];
@@ -353,12 +351,12 @@ __global__ __launch_bounds__(kBlockW8) void k_gemv_a8(const float* __restrict__ 
     for (int m = 0; m < kM; ++m) {
         float r = red[0][m];
 #pragma unroll
-        for (int i = 1; i < kWavesW8; ++i) r = fmaxf(r, red[i][m]);
+        for (int i = 1; i < kWB; ++i) r = fmaxf(r, red[i][m]);
         sa[m] = row_scale<Fmt>(absmax_finish(r));
     }
     // the block codes each 4-value entry once (in place in LDS, slot by slot), then
     // every lane copies its 16-value slices into registers
-    for (int i = threadIdx.x; i < kM * kChunks * 256; i += kBlockW8) {
+    for (int i = threadIdx.x; i < kM * kChunks * 256; i += kBlk) {
         const int m = i / (kChunks * 256), j = i - m * (kChunks * 256);
         typename P::xreg_t e[P::kRegsPer4];
         float sm = sa[0];
@@ -399,12 +397,14 @@ __global__ __launch_bounds__(kBlockW8) void k_gemv_a8(const float* __restrict__ 
             }
         }
     };
-    // two register buffers in turn, read in place (as in k_gemv_w8)
+    // two register buffers in turn, read in place, the next group requested once
+    // the current one has landed (as in k_gemv_w8)
     for (int64_t row0 = row_begin;;) {
         if (row0 + kRows >= row_end) {
             group(row0, wa);
             break;
         }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         load_rows(row0 + kRows, wb);
         group(row0, wa);
         row0 += kRows;
@@ -412,6 +412,7 @@ __global__ __launch_bounds__(kBlockW8) void k_gemv_a8(const float* __restrict__ 
             group(row0, wb);
             break;
         }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         load_rows(row0 + kRows, wa);
         group(row0, wb);
         row0 += kRows;
@@ -422,8 +423,8 @@ __global__ __launch_bounds__(kBlockW8) void k_gemv_a8(const float* __restrict__ 
 // contiguous row runs per wave (or wave pair: `runs_per_block` runs per block),
 // a multiple of kRows each.
 template <int kRows>
-void grid_for_rows(int64_t n, int64_t* blocks, int64_t* rows_per_wave, int runs_per_block = kWavesW8,
-                   int64_t max_rows = INT64_MAX, int blocks_per_cu = 1) {
+void grid_for_rows(int64_t n, int64_t* blocks, int64_t* rows_per_wave, int runs_per_block, int64_t max_rows,
+                   int blocks_per_cu) {
     const int64_t slots = static_cast<int64_t>(device_cu_count()) * blocks_per_cu * runs_per_block;
     int64_t waves = (n + kRows - 1) / kRows;
     if (waves > slots) waves = slots;
@@ -480,11 +481,13 @@ void dispatch_w8(int chunks, const float* x, int64_t xs, const typename Code::co
 template <class Fmt, int kM, int kChunks>
 void launch_a8(const float* x, int64_t xs, const typename Fmt::code_t* q, const float* s, const float* b, int64_t n,
                int64_t k, float* y, int64_t ys, hipStream_t st) {
-    constexpr int kRows = rows_in_flight(kM * kChunks * 4 * A8<Fmt>::kRegsPer4);
+    // one token: one row per group in 4-wave blocks, two per CU (as the weight-only GEMV)
+    constexpr int kRows = kM == 1 ? 1 : rows_in_flight(kM * kChunks * 4 * A8<Fmt>::kRegsPer4);
+    constexpr int kWB = kM == 1 ? 4 : 8;
     int64_t blocks, rpw;
-    grid_for_rows<kRows>(n, &blocks, &rpw);
-    k_gemv_a8<Fmt, kM, kChunks, kRows><<<static_cast<unsigned>(blocks), kBlockW8, 0, st>>>(x, xs, q, s, b, n, k, y,
-                                                                                         ys, rpw);
+    grid_for_rows<kRows>(n, &blocks, &rpw, kWB, INT64_MAX, 8 / kWB);
+    k_gemv_a8<Fmt, kM, kChunks, kRows, kWB><<<static_cast<unsigned>(blocks), 64 * kWB, 0, st>>>(x, xs, q, s, b, n, k,
+                                                                                              y, ys, rpw);
 }
 
 template <class Fmt, int kM, int kChunks = 1>

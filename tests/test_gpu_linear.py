@@ -80,10 +80,14 @@ def test_gemv_w8_config2(tq, c2, m):
 
 # K % 16 != 0 and K > 8192 take the shape-general kernel (e.g. the reference's Linear(3, 2));
 # 2-4 tokens with K split over a wave pair: a second half with fewer chunks (K = 3088,
-# 3072), rows per pair past the LDS partials (N = 70000: more blocks than CUs)
+# 3072), rows per pair past the LDS partials (N = 70000: more blocks than CUs); runs of
+# several row groups per wave, in even and odd numbers, through the two alternating
+# register buffers (N = 14336 and 30000 at one token: 7 and 15 rows per wave; N = 9000 at
+# two tokens: 3 groups of 2 rows)
 @pytest.mark.parametrize("n,k,m", [(1000, 1024, 1), (17, 16, 2), (333, 3088, 3), (64, 8192, 4), (5, 2000, 16),
                                    (2, 3, 4), (50, 100, 3), (64, 9000, 2), (70000, 2048, 3), (4100, 3072, 4),
-                                   (515, 8192, 2)])
+                                   (515, 8192, 2), (14336, 4096, 1), (30000, 1024, 1), (9000, 1024, 2),
+                                   (8192, 2048, 1)])
 def test_gemv_w8_shapes_bias(tq, oracle, n, k, m):
     w = normal(50, (n, k), 0.02)
     x = normal(50, (m, k), 1.0, stream=1)
@@ -557,7 +561,8 @@ def test_gemm_w4g128_bf16_entry_points_agree(tq, oracle):
 
 
 # ------------------------------------------ decode W8A8 / FP8, fused activations
-@pytest.mark.parametrize("m,n,k", [(1, 4096, 4096), (3, 512, 1024), (16, 272, 8192), (5, 33, 48), (2, 4096, 128)])
+@pytest.mark.parametrize("m,n,k", [(1, 4096, 4096), (3, 512, 1024), (16, 272, 8192), (5, 33, 48), (2, 4096, 128),
+                                   (1, 14336, 4096), (1, 30000, 1024)])
 def test_gemv_w8a8_fused_equals_quantize_plus_gemm(tq, oracle, m, n, k):
     """One launch (activation codes computed in the GEMV) gives the two-step
     path's y bit for bit: same codes, exact int32 sums, same epilogue."""
@@ -582,7 +587,7 @@ def test_gemv_w8a8_fused_equals_quantize_plus_gemm(tq, oracle, m, n, k):
     assert_close(host(y1), oracle.linear_w8a8(rqa, rsa, rqw, rsw, b), RTOL, ATOL, "fused w8a8 vs oracle")
 
 
-@pytest.mark.parametrize("m,n,k", [(1, 4096, 4096), (4, 512, 1024), (16, 272, 8192), (3, 40, 64)])
+@pytest.mark.parametrize("m,n,k", [(1, 4096, 4096), (4, 512, 1024), (16, 272, 8192), (3, 40, 64), (1, 14336, 2048)])
 def test_gemv_fp8a8_fused_vs_oracle(tq, oracle, m, n, k):
     import torch
     from theano_quantize import _abi

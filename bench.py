@@ -49,7 +49,7 @@ def parse_args():
     p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--only", default=None,
                    help="run one workload: gemv_w4, gemv_w8, gemv_fp8, gemv_w4_m, w8a8_decode, w8a8, fp8, mha, storage, "
-                        "roundtrip, mlp, mlp_decode, copy")
+                        "roundtrip, mlp, mlp_mid, mlp_decode, copy")
     p.add_argument("--no-secondary", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=12.0, help="bound of the CPU baseline sample (0: skip)")
     p.add_argument("--eager", action="store_true", help="time eager launches instead of a HIP graph")
@@ -770,6 +770,48 @@ def main():
                                                            of_random_peak(tf, "bf16_mfma_TFLOPS_random_operands")}
         log(f"w4a16 linear M=512 N=14336 K=4096: {ms * 1e3:.1f} us  {tf:.0f} TFLOP/s")
         del mlp, wsl, yl
+
+    # --------------- mid-size M on the prefill kernels (C5 weights, M = 64, 128)
+    if not args.no_secondary and want("mlp_mid"):
+        d5, f5 = 4096, 14336
+        base = tq.QuantizedMLP.from_tensors(dt(normal_f32(4, (f5, d5), 0.02)), dt(normal_f32(4, (f5, d5), 0.02, 1)),
+                                            dt(normal_f32(4, (d5, f5), 0.02, 2)))
+        wbytes = 3 * f5 * d5 // 2 + 3 * f5 * d5 // 128 * 2
+        mats = [(base.gate, base.up, base.down)] + [tuple(tuple(t.clone() for t in w) for w in
+                                                          (base.gate, base.up, base.down))
+                                                    for _ in range(rotation(wbytes) - 1)]
+        res = {}
+        for mm in (64, 128):
+            x = bf16(normal_f32(4, (mm, d5), 1.0, stream=3))
+            nb = int(_abi.lib().tq_mlp_w4g128_workspace_bytes(mm, d5, f5))
+            ws = torch.empty((nb,), dtype=torch.uint8, device=dev)
+            y = torch.empty((mm, d5), dtype=torch.float32, device=dev)
+            nbl = int(_abi.lib().tq_gemm_w4g128_bf16_workspace_bytes(mm, d5))
+            wsl = torch.empty((nbl,), dtype=torch.uint8, device=dev)
+            yl = torch.empty((mm, f5), dtype=torch.float32, device=dev)
+
+            def launch_mid(i, mm=mm, x=x, ws=ws, nb=nb, y=y):
+                g, u, dn = mats[i % len(mats)]
+                _abi.call("tq_mlp_w4g128", ptr(x), mm, d5, f5, ptr(g[0]), ptr(g[1]), ptr(u[0]), ptr(u[1]),
+                          ptr(dn[0]), ptr(dn[1]), ptr(ws), nb, ptr(y), stream())
+
+            def launch_mid_lin(i, mm=mm, x=x, wsl=wsl, nbl=nbl, yl=yl):
+                g = mats[i % len(mats)][0]
+                _abi.call("tq_gemm_w4g128_bf16_ws", ptr(x), mm, ptr(g[0]), ptr(g[1]), None, f5, d5, ptr(wsl), nbl,
+                          ptr(yl), stream())
+
+            steps = max(10, args.steps // 5)
+            ms, mode = timer.run(launch_mid, steps, 3)
+            tf = 6.0 * mm * f5 * d5 / (ms * 1e-3) / 1e12
+            msl, model = timer.run(launch_mid_lin, steps, 3)
+            tfl = 2.0 * mm * f5 * d5 / (msl * 1e-3) / 1e12
+            res[f"m{mm}"] = {"ffn_us": round(ms * 1e3, 2), "ffn_timing": mode, "ffn_tokens/s": round(mm / (ms * 1e-3), 1),
+                             "ffn_TFLOP/s": round(tf, 1), "ffn_weights_GB/s": round(wbytes / (ms * 1e-3) / 1e9, 1),
+                             "linear_n14336_k4096_us": round(msl * 1e3, 2), "linear_timing": model,
+                             "linear_TFLOP/s": round(tfl, 1)}
+            log(f"prefill FFN M={mm}: {ms * 1e3:.1f} us; INT4 Linear M={mm}: {msl * 1e3:.1f} us")
+        secondary["prefill_mid_m"] = res
+        del base, mats
 
     # ------------------------------- decode FFN (C5 weights, M = 1, 2, 4, 8, 16)
     if not args.no_secondary and want("mlp_decode"):

@@ -10,11 +10,11 @@
 //           the weight unpack produces) and X[g][m] = -192 * sum of group g of
 //           row m, stored as three bf16 planes (hi, mid, lo) whose sum is the
 //           f32 value; zeroes y (the down launch adds two K halves into it).
-//   gate/up one block per 128 rows x 128 columns of h; h = SiLU(x Wg^T) * (x Wu^T)
+//   gate/up one block per 128 (or 64) rows x 128 columns of h; h = SiLU(x Wg^T) * (x Wu^T)
 //           is written as bf16 hi + lo planes (hi + lo keeps ~2^-17 of h) in
 //           the xp order, with the same -192 * group-sum planes for the down
 //           projection (a block's 128 columns are one of its groups).
-//   down    one block per 64 rows x 256 columns and half of K; the two halves
+//   down    one block per 64 rows x 256 (or 64) columns and half of K; the two halves
 //           are added into the zeroed y with float atomics (two addends onto
 //           zero: the sum does not depend on their order).
 //
@@ -457,6 +457,28 @@ using DnCfg = FfnCfg<kDnWM, kDnWN, kDnTM, kDnTN, 1, 2>;
 constexpr int kLnWM = 2, kLnWN = 4, kLnTM = 2, kLnTN = 2;
 using LinCfg = FfnCfg<kLnWM, kLnWN, kLnTM, kLnTN, 1, 1>;
 
+// Narrow tiles for mid-size M, where the tiles above leave most CUs idle or run
+// padding rows (at M = 64 the 128-row gate/up tiles are half padding and the
+// down projection has 32 blocks): gate/up 64 x 128 h (2 x 4 waves of 32 rows x
+// (32 gate + 32 up)), down 64 x 64 y (2 x 2 waves of 32 x 32 on the two planes,
+// K in two halves), Linear 64 x 128 y (2 x 4 waves of 32 x 32).
+using GuSCfg = FfnCfg<2, 4, 1, 1, 2, 1>;
+using DnSCfg = FfnCfg<2, 2, 1, 1, 1, 2>;
+using LinSCfg = FfnCfg<2, 4, 1, 1, 1, 1>;
+
+// Relative time of a launch: rounds of blocks over the CUs times the MFMA work of
+// one block (BM x BN x groups of K) times the time per unit of work of the tile
+// set, in thousandths of the wide tiles' (narrow tiles move more bytes per MFMA:
+// per block-round at D = 4096, F = N = 14336, gate/up 64-row tiles take 1.25x,
+// the 64 x 64 down tiles 1.4x and the 64 x 128 Linear tiles ~1.25x the wide
+// tiles' time per MFMA).  The tile set with the smaller figure runs; ties keep
+// the wide tiles.
+constexpr int64_t kWideCost = 1000, kNarrowGuCost = 1250, kNarrowDnCost = 1400, kNarrowLinCost = 1250;
+int64_t launch_cost(int64_t blocks, int64_t bm, int64_t bn, int64_t groups, int64_t per_unit) {
+    const int64_t cus = device_cu_count();
+    return (blocks + cus - 1) / cus * bm * bn * groups * per_unit;
+}
+
 struct FfnWorkspace {
     int64_t mpad, xp, xs, hh, hl, hs, bytes;  // byte offsets of the parts, total
 };
@@ -526,8 +548,17 @@ int tq_mlp_w4g128(const uint16_t* x_bf16, int64_t m, int64_t d, int64_t f, const
 
     const int64_t items = m * (d / 128);
     TQ_REQUIRE((items + 15) / 16 < (int64_t(1) << 31), "tq_mlp_w4g128: problem too large");
-    const int64_t gu_tiles = ((m + GuCfg::BM - 1) / GuCfg::BM) * (f / GuCfg::BN);
-    const int64_t dn_tiles = ((m + DnCfg::BM - 1) / DnCfg::BM) * (d / DnCfg::BN) * kDnSplit;
+    // wide or narrow tiles per launch, whichever leaves less work on the busiest CU
+    static_assert(GuCfg::BN == GuSCfg::BN && DnCfg::BM == DnSCfg::BM, "the tile sets share these sides");
+    const int64_t gu_tm = (m + GuCfg::BM - 1) / GuCfg::BM, gus_tm = (m + GuSCfg::BM - 1) / GuSCfg::BM;
+    const int64_t gu_tn = f / GuCfg::BN, dn_tm = (m + DnCfg::BM - 1) / DnCfg::BM;
+    const bool gu_narrow = launch_cost(gus_tm * gu_tn, GuSCfg::BM, GuSCfg::BN, d / 128, kNarrowGuCost) <
+                           launch_cost(gu_tm * gu_tn, GuCfg::BM, GuCfg::BN, d / 128, kWideCost);
+    const bool dn_narrow =
+        launch_cost(dn_tm * (d / DnSCfg::BN) * kDnSplit, DnSCfg::BM, DnSCfg::BN, f / 256, kNarrowDnCost) <
+        launch_cost(dn_tm * (d / DnCfg::BN) * kDnSplit, DnCfg::BM, DnCfg::BN, f / 256, kWideCost);
+    const int64_t gu_tiles_m = gu_narrow ? gus_tm : gu_tm, gu_tiles = gu_tiles_m * gu_tn;
+    const int64_t dn_tiles_n = d / (dn_narrow ? DnSCfg::BN : DnCfg::BN), dn_tiles = dn_tm * dn_tiles_n * kDnSplit;
     TQ_REQUIRE(gu_tiles < (int64_t(1) << 31) && dn_tiles < (int64_t(1) << 31), "tq_mlp_w4g128: problem too large");
 
     k_ffn_prep<<<static_cast<unsigned>((items + 15) / 16), 256, 0, st>>>(x_bf16, m, d, w.mpad, xp, xs, y, d);
@@ -545,12 +576,15 @@ int tq_mlp_w4g128(const uint16_t* x_bf16, int64_t m, int64_t d, int64_t f, const
     a.n = f;
     a.k = d;
     a.mpad = w.mpad;
-    a.tiles_m = static_cast<int>((m + GuCfg::BM - 1) / GuCfg::BM);
-    a.tiles_n = static_cast<int>(f / GuCfg::BN);
+    a.tiles_m = static_cast<int>(gu_tiles_m);
+    a.tiles_n = static_cast<int>(gu_tn);
     a.h_hi = hh;
     a.h_lo = hl;
     a.hs = hs;
-    k_ffn<kGuWM, kGuWN, kGuTM, kGuTN, 2, 1, 1><<<static_cast<unsigned>(gu_tiles), GuCfg::kThreads, 0, st>>>(a);
+    if (gu_narrow)
+        k_ffn<2, 4, 1, 1, 2, 1, 1><<<static_cast<unsigned>(gu_tiles), GuSCfg::kThreads, 0, st>>>(a);
+    else
+        k_ffn<kGuWM, kGuWN, kGuTM, kGuTN, 2, 1, 1><<<static_cast<unsigned>(gu_tiles), GuCfg::kThreads, 0, st>>>(a);
     rc = check_launch("tq_mlp_w4g128 (gate/up)");
     if (rc != TQ_OK) return rc;
 
@@ -564,10 +598,14 @@ int tq_mlp_w4g128(const uint16_t* x_bf16, int64_t m, int64_t d, int64_t f, const
     b.n = d;
     b.k = f;
     b.mpad = w.mpad;
-    b.tiles_m = static_cast<int>((m + DnCfg::BM - 1) / DnCfg::BM);
-    b.tiles_n = static_cast<int>(d / DnCfg::BN);
+    b.tiles_m = static_cast<int>(dn_tm);
+    b.tiles_n = static_cast<int>(dn_tiles_n);
     b.y = y;
-    k_ffn<kDnWM, kDnWN, kDnTM, kDnTN, 1, 2, kDnSplit><<<static_cast<unsigned>(dn_tiles), DnCfg::kThreads, 0, st>>>(b);
+    if (dn_narrow)
+        k_ffn<2, 2, 1, 1, 1, 2, kDnSplit><<<static_cast<unsigned>(dn_tiles), DnSCfg::kThreads, 0, st>>>(b);
+    else
+        k_ffn<kDnWM, kDnWN, kDnTM, kDnTN, 1, 2, kDnSplit>
+            <<<static_cast<unsigned>(dn_tiles), DnCfg::kThreads, 0, st>>>(b);
     return check_launch("tq_mlp_w4g128 (down)");
 }
 
@@ -589,9 +627,9 @@ int tq_gemm_w4g128_bf16_ws(const uint16_t* x_bf16, int64_t m, const uint8_t* pac
     TQ_REQUIRE(k == 0 || (workspace && workspace_bytes >= need),
                "tq_gemm_w4g128_bf16_ws: workspace of %lld bytes, %lld needed", (long long)workspace_bytes,
                (long long)need);
-    // the pipelined kernel: scale pairs as dwords (K % 256), 256-column tiles,
-    // 16-byte vectors; anything else runs the workspace-free entry point
-    const bool fast = k > 0 && k % 256 == 0 && n % LinCfg::BN == 0 && x_bf16 && packed && s_f16 && y &&
+    // the pipelined kernels: scale pairs as dwords (K % 256), 128- or 256-column
+    // tiles, 16-byte vectors; anything else runs the workspace-free entry point
+    const bool fast = k > 0 && k % 256 == 0 && n % LinSCfg::BN == 0 && x_bf16 && packed && s_f16 && y &&
                       aligned(x_bf16, 16) && aligned(packed, 16) && aligned(s_f16, 4) && aligned(y, 16) &&
                       (!bias || aligned(bias, 4)) && aligned(workspace, 256);
     if (!fast) return tq_gemm_w4g128_bf16(x_bf16, m, packed, s_f16, bias, n, k, y, stream);
@@ -599,11 +637,26 @@ int tq_gemm_w4g128_bf16_ws(const uint16_t* x_bf16, int64_t m, const uint8_t* pac
     const int64_t mpad = (m + 127) / 128 * 128;
     uint16_t* xp = static_cast<uint16_t*>(workspace);
     uint32_t* xs = reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(workspace) + align256(m * k * 2));
-    const int64_t tiles_m = (m + LinCfg::BM - 1) / LinCfg::BM, tiles_n = n / LinCfg::BN;
     // K halves are added into y when the doubled grid still fits one round on the CUs
     // and each half keeps at least 8 groups (two addends onto zero: the sum does not
-    // depend on their order)
-    const bool split = 2 * tiles_m * tiles_n <= device_cu_count() && k / 128 >= 16;
+    // depend on their order).  Wide or narrow tiles, whichever leaves less work on
+    // the busiest CU (wide ones need N % 256).
+    auto plan = [&](int64_t bm, int64_t bn, int64_t per_unit, int64_t* tm, int64_t* tn, bool* split) {
+        *tm = (m + bm - 1) / bm;
+        *tn = n / bn;
+        *split = 2 * *tm * *tn <= device_cu_count() && k / 128 >= 16;
+        return launch_cost(*tm * *tn * (*split ? 2 : 1), bm, bn, k / 128 / (*split ? 2 : 1), per_unit);
+    };
+    int64_t tiles_m, tiles_n, wtm, wtn;
+    bool split, wsplit;
+    const int64_t narrow_cost = plan(LinSCfg::BM, LinSCfg::BN, kNarrowLinCost, &tiles_m, &tiles_n, &split);
+    const bool narrow =
+        n % LinCfg::BN != 0 || narrow_cost < plan(LinCfg::BM, LinCfg::BN, kWideCost, &wtm, &wtn, &wsplit);
+    if (!narrow) {
+        tiles_m = wtm;
+        tiles_n = wtn;
+        split = wsplit;
+    }
     const int64_t items = m * (k / 128);
     TQ_REQUIRE((items + 15) / 16 < (int64_t(1) << 31) && tiles_m * tiles_n * 2 < (int64_t(1) << 31),
                "tq_gemm_w4g128_bf16_ws: problem too large");
@@ -624,12 +677,15 @@ int tq_gemm_w4g128_bf16_ws(const uint16_t* x_bf16, int64_t m, const uint8_t* pac
     a.tiles_n = static_cast<int>(tiles_n);
     a.y = y;
     a.bias = bias;
-    if (split)
-        k_ffn<kLnWM, kLnWN, kLnTM, kLnTN, 1, 1, 2>
-            <<<static_cast<unsigned>(tiles_m * tiles_n * 2), LinCfg::kThreads, 0, st>>>(a);
+    const unsigned blocks = static_cast<unsigned>(tiles_m * tiles_n * (split ? 2 : 1));
+    if (narrow && split)
+        k_ffn<2, 4, 1, 1, 1, 1, 2><<<blocks, LinSCfg::kThreads, 0, st>>>(a);
+    else if (narrow)
+        k_ffn<2, 4, 1, 1, 1, 1, 1><<<blocks, LinSCfg::kThreads, 0, st>>>(a);
+    else if (split)
+        k_ffn<kLnWM, kLnWN, kLnTM, kLnTN, 1, 1, 2><<<blocks, LinCfg::kThreads, 0, st>>>(a);
     else
-        k_ffn<kLnWM, kLnWN, kLnTM, kLnTN, 1, 1, 1>
-            <<<static_cast<unsigned>(tiles_m * tiles_n), LinCfg::kThreads, 0, st>>>(a);
+        k_ffn<kLnWM, kLnWN, kLnTM, kLnTN, 1, 1, 1><<<blocks, LinCfg::kThreads, 0, st>>>(a);
     return check_launch("tq_gemm_w4g128_bf16_ws");
 }
 

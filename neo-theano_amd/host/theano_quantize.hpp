@@ -343,13 +343,13 @@ class QuantizedLinear : public Module {
     // quantize x into the scratch and run the GEMM (its skinny kernel up to 16
     // tokens: faster than the fused GEMV from 3 tokens).  w4 runs the
     // tiled GEMV in passes of 16 tokens up to m = kTiledPassesMaxM (at N = 14336,
-    // K = 4096: 22 / 42 us at m = 32 / 64 against 40 / 50 us for the prefill GEMM,
-    // 85 against 53 us at m = 128), the prefill GEMM beyond, with `workspace`
+    // K = 4096: 19 us at m = 17-32 against 21-24 us for the prefill GEMM on its
+    // 64-row tiles, 37 against 25.5 us at m = 64), the prefill GEMM beyond, with `workspace`
     // (workspace_bytes(m) bytes) when given.
     Result<void> forward_device(const void* x, int64_t m, float* y, hipStream_t stream,
                                 int8_t* act_codes = nullptr, float* act_scales = nullptr,
                                 void* workspace = nullptr, size_t workspace_bytes = 0) const;
-    static constexpr int64_t kTiledPassesMaxM = 64;
+    static constexpr int64_t kTiledPassesMaxM = 32;
     static constexpr int64_t kFusedA8MaxM = 2;
     // device scratch for m tokens: the w4 prefill path and the fp8 GEMV on
     // fake-quantized activations (m <= kFusedA8MaxM); 0 otherwise
@@ -404,9 +404,10 @@ class QuantizedMLP : public Module {
     // decode shapes (D and F at most 16384; 1 <= m <= 8, or m <= kDecodeMaxM where
     // D <= kDecodeOnePassD, whose gate/up takes 16 tokens in one launch) run
     // tq_mlp_w4g128_decode on row-tiled copies of the weights, in passes of
-    // kDecodePassM tokens; others tq_mlp_w4g128 (at D = 4096, F = 14336: 35-60 us
-    // for 5-16 tokens and 74-108 us for 17-32, against 134-143 us)
-    static constexpr int64_t kDecodeMaxM = 32;
+    // kDecodePassM tokens; others tq_mlp_w4g128 (at D = 4096, F = 14336: 35-48 us
+    // for 5-16 tokens and 66-78 us for 17-24, 93 us at 32, against 85-88 us for
+    // the prefill FFN on its 64-row tiles)
+    static constexpr int64_t kDecodeMaxM = 28;
     static constexpr int64_t kDecodePassM = 16;
     static constexpr size_t kDecodeOnePassD = 4096;
     bool decode_path(int64_t m) const {

@@ -20,7 +20,7 @@ Modes (chosen from the QConfig):
 Decode shapes (M <= 16 tokens) run the dequant-GEMV kernels; in "w8a8" and
 "fp8" modes the GEMV quantizes the activation rows itself (the same codes and
 product as quantize + GEMM, one launch).  "w4" runs the tiled GEMV in passes of
-16 tokens up to M = 64, where it is faster than the prefill GEMM, whose 128-row
+16 tokens up to M = 32, where it is faster than the prefill GEMM, whose 64-row
 M tiles are mostly empty there.  Prefill shapes run the i8-MFMA W8A8 GEMM, the
 fp8-MFMA GEMM or the bf16-MFMA W4A16 GEMM.
 """
@@ -43,14 +43,15 @@ DECODE_MAX_M = 16
 FUSED_A8_MAX_M = 2
 TILED_MAX_M = 16  # tokens per launch of the INT4 GEMV on the row-tiled copy
 # INT4 Linear: the tiled GEMV in passes of TILED_MAX_M tokens up to this M (at N =
-# 14336, K = 4096: 22 / 42 us at M = 32 / 64 against 40 / 50 us for the prefill
-# GEMM, 85 against 53 us at M = 128)
-TILED_PASSES_MAX_M = 64
+# 14336, K = 4096: 19 us at M = 17-32 against 21-24 us for the prefill GEMM on
+# its 64-row tiles; 28.5 / 37 against 24.5 / 25.5 us at M = 48 / 64)
+TILED_PASSES_MAX_M = 32
 # QuantizedMLP runs the decode kernels for up to 8 tokens, and, where D <= 4096
-# (its gate/up then takes 16 tokens in one launch), up to 32 tokens in passes of
-# 16; the prefill FFN beyond.  At D = 4096, F = 14336: 35-60 us for 5-16 tokens
-# and 74-108 us for 17-32, against 134-143 us.
-DECODE_MLP_MAX_M = 32
+# (its gate/up then takes 16 tokens in one launch), up to 28 tokens in passes of
+# 16; the prefill FFN beyond.  At D = 4096, F = 14336: 48 us at 16 tokens and
+# 66-78 us for 17-24 (93 us at 32), against 85-88 us for the prefill FFN on its
+# 64-row tiles at 16-32 tokens.
+DECODE_MLP_MAX_M = 28
 DECODE_MLP_PASS_M = 16
 DECODE_MLP_ONE_PASS_D = 4096
 MLP_DOWN_TILE_ROWS = 32  # tile height of the FFN's decode copy of down
@@ -106,7 +107,7 @@ class QuantizedLinear(Module):
         self.tiled = None
         if tiled and mode == "w4" and self.in_features <= 16384:
             # row-tiled copy (a permutation of qweight) for the decode GEMV (passes
-            # of 16 tokens up to M = 64)
+            # of 16 tokens up to M = 32)
             self.tiled = repack_i4_g128_tiled(qweight, scales)
 
     @staticmethod

@@ -435,7 +435,7 @@ TEST_GPU(test_parity_quantized_linear_w4) {
     std::vector<uint8_t> p(n * k / 2);
     std::vector<uint16_t> s(n * k / 128);
     tqo_quantize_i4_g128(w32.data(), n, k, p.data(), s.data());
-    for (size_t m : {1u, 3u, 9u, 40u, 65u}) {  // tiled GEMV (1-16, 3 passes at 40), W4A16 GEMM (65)
+    for (size_t m : {1u, 3u, 9u, 32u, 40u}) {  // tiled GEMV (1-16, 2 passes at 32), W4A16 GEMM (40)
         const auto xv = randn(m * k, 1.0, 42 + m);
         const auto y = layer.forward(Tensor::from_slice(xv, {m, k})).to_vec_f64().unwrap();
         std::vector<uint16_t> xb(m * k);
@@ -447,19 +447,19 @@ TEST_GPU(test_parity_quantized_linear_w4) {
 }
 
 TEST_GPU(test_parity_quantized_linear_w4_prefill) {
-    // N % 256 == 0 and K % 256 == 0, M > 64: the pipelined kernels (K split in two
-    // for the small grid at M = 100), with bias
+    // N % 256 == 0 and K % 256 == 0, M > 32: the pipelined kernels (64-row tiles
+    // with K split in two for the small grids at M = 64 and 100), with bias
     const size_t n = 512, k = 2048;
     const auto wv = randn(n * k, 0.02, 71), bv = randn(n, 0.1, 72);
     const QuantizedLinear layer = QuantizedLinear::from_tensors(Tensor::from_slice(wv, {n, k}),
                                                                 Tensor::from_slice(bv, {n}), QConfig::default_int4())
                                       .unwrap();
-    ASSERT(layer.workspace_bytes(100) > 0 && layer.workspace_bytes(64) == 0);
+    ASSERT(layer.workspace_bytes(100) > 0 && layer.workspace_bytes(64) > 0 && layer.workspace_bytes(32) == 0);
     const auto w32 = f32(wv), b32 = f32(bv);
     std::vector<uint8_t> p(n * k / 2);
     std::vector<uint16_t> s(n * k / 128);
     tqo_quantize_i4_g128(w32.data(), n, k, p.data(), s.data());
-    for (size_t m : {100u, 300u}) {
+    for (size_t m : {64u, 100u, 300u}) {
         const auto xv = randn(m * k, 1.0, 73 + m);
         const auto y = layer.forward(Tensor::from_slice(xv, {m, k})).to_vec_f64().unwrap();
         std::vector<uint16_t> xb(m * k);
@@ -535,8 +535,8 @@ TEST_GPU(test_parity_quantized_linear_fp8) {
 
 TEST_GPU(test_parity_quantized_mlp) {
     // M = 1, 2, 4, 5, 9, 16 run the decode kernels (M = 4: one K-split down launch;
-    // M >= 5: one gate/up launch, D <= 4096), M = 17, 32 two passes of them, M = 33
-    // the prefill FFN
+    // M >= 5: one gate/up launch, D <= 4096), M = 17, 28 two passes of them, M = 29
+    // and 33 the prefill FFN
     const size_t d = 256, f = 384;
     const auto gv = randn(f * d, 0.02, 61), uv = randn(f * d, 0.02, 62), dv = randn(d * f, 0.02, 63);
     const QuantizedMLP mlp = QuantizedMLP::from_tensors(Tensor::from_slice(gv, {f, d}), Tensor::from_slice(uv, {f, d}),
@@ -548,8 +548,8 @@ TEST_GPU(test_parity_quantized_mlp) {
     tqo_quantize_i4_g128(g32.data(), f, d, pg.data(), sg.data());
     tqo_quantize_i4_g128(u32.data(), f, d, pu.data(), su.data());
     tqo_quantize_i4_g128(d32.data(), d, f, pd.data(), sd.data());
-    for (size_t m : {1, 2, 4, 5, 9, 16, 17, 32, 33}) {
-        ASSERT(mlp.decode_path(static_cast<int64_t>(m)) == (m <= 32));
+    for (size_t m : {1, 2, 4, 5, 9, 16, 17, 28, 29, 33}) {
+        ASSERT(mlp.decode_path(static_cast<int64_t>(m)) == (m <= 28));
         const auto xv = randn(m * d, 1.0, 64 + m);
         const auto y = mlp.forward(Tensor::from_slice(xv, {m, d})).to_vec_f64().unwrap();
         std::vector<uint16_t> xb(m * d);
@@ -557,7 +557,7 @@ TEST_GPU(test_parity_quantized_mlp) {
         std::vector<double> ref(m * d);
         tqo_mlp_w4g128(xb.data(), m, d, f, pg.data(), sg.data(), pu.data(), su.data(), pd.data(), sd.data(),
                        ref.data());
-        assert_close(y, ref, m <= 32 ? "mlp decode" : "mlp prefill");
+        assert_close(y, ref, m <= 28 ? "mlp decode" : "mlp prefill");
     }
 }
 

@@ -185,10 +185,11 @@ def test_gemv_w4g128_tiled_shapes(tq, oracle, n, k, m, t):
     assert_close(host(y), oracle.linear_w4g128_bf16(xb, rp, rs, b), RTOL, ATOL, f"tiled {n}x{k} M={m} T={t}")
 
 
-# QuantizedLinear "w4" up to M = 64 runs the tiled GEMV in passes of 16 tokens
-# (17, 40, 64 below)
+# QuantizedLinear "w4" up to M = 32 runs the tiled GEMV in passes of 16 tokens
+# (17 and 32 below; 40 and 64 take the prefill GEMM)
 @pytest.mark.parametrize("n,k,m", [(100, 128, 1), (7, 2176, 2), (256, 14336, 1), (48, 16384, 3), (9, 4096, 16),
-                                   (33, 16512, 2), (100, 1024, 17), (9, 4096, 40), (300, 2048, 64)])
+                                   (33, 16512, 2), (100, 1024, 17), (256, 2048, 32), (9, 4096, 40),
+                                   (300, 2048, 64)])
 def test_gemv_w4g128_shapes_bias(tq, oracle, n, k, m):
     w = normal(51, (n, k), 0.02)
     xb = to_bf16_bits(normal(51, (m, k), 1.0, stream=1))
@@ -324,13 +325,15 @@ def test_misaligned_inputs_take_the_general_kernels(tq, oracle):
 
 
 # ----------------------------------------------------------------- W4A16
-# (17, 256, 512), (300, 512, 768), (64, 1024, 4096), (129, 768, 2048) run the
-# pipelined kernels (K split in two where the grid is small); the rest the
-# 16x16x32 / shape-general kernels.  The layer has no tiled copy, so that every
-# M takes the prefill GEMM.
+# (17, 256, 512), (300, 512, 768), (64, 1024, 4096), (129, 768, 2048) and
+# (64, 384, 1024) run the pipelined kernels on 64 x 128 tiles (K split in two
+# where the grid is small; N = 384 has no 256-column tiling); (512, 16384, 256)
+# on 128 x 256 tiles (as many rounds of work per CU either way: the wide tiles
+# win the tie); the rest the 16x16x32 / shape-general kernels.  The layer has
+# no tiled copy, so that every M takes the prefill GEMM.
 @pytest.mark.parametrize("m,n,k", [(17, 256, 512), (130, 64, 4096), (300, 128, 1024), (33, 16, 128),
                                    (40, 200, 1024), (20, 7, 256), (300, 512, 768), (64, 1024, 4096),
-                                   (129, 768, 2048)])
+                                   (129, 768, 2048), (64, 384, 1024), (512, 16384, 256)])
 def test_gemm_w4g128_bf16_shapes(tq, oracle, m, n, k):
     w = normal(55, (n, k), 0.02)
     xb = to_bf16_bits(normal(55, (m, k), 1.0, stream=1))
@@ -394,6 +397,25 @@ def test_mlp_config5_all_rows(tq, oracle):
     assert_close(y, ref, RTOL, ATOL, "mlp config 5 (all rows)")
 
 
+@pytest.mark.parametrize("m", [64, 200])
+def test_mlp_mid_m_config5_weights(tq, oracle, m):
+    """Mid-size M on the prefill kernels at the config-5 weights: M = 64 runs
+    gate/up on 64-row tiles and down on 64 x 64 tiles; M = 200 keeps gate/up on
+    128-row tiles (a tie in rounds x work) and runs down on 64 x 64 tiles.  All
+    rows against the f64 composition, sampled rows against the oracle."""
+    d, f = 4096, 14336
+    wg = normal(4, (f, d), 0.02)
+    wu = normal(4, (f, d), 0.02, stream=1)
+    wd = normal(4, (d, f), 0.02, stream=2)
+    xb = to_bf16_bits(normal(4, (m, d), 1.0, stream=4))
+    mlp = _prefill_only(tq, tq.QuantizedMLP.from_tensors(dev_tensor(wg), dev_tensor(wu), dev_tensor(wd)))
+    y = host(mlp(bf16_dev(xb)))
+    args = [a for t in (mlp.gate, mlp.up, mlp.down) for a in (host(t[0]), host(t[1]).view(np.uint16))]
+    rows = np.array([0, 63, m - 1])
+    assert_close(y[rows], oracle.mlp_w4g128(xb[rows], *args), RTOL, ATOL, f"mlp M={m} vs oracle")
+    assert_close(y, mlp_f64(xb, *args, oracle), RTOL, ATOL, f"mlp M={m} (all rows)")
+
+
 def _mlp_case(tq, m, d, f, seed=57):
     wg = normal(seed, (f, d), 0.02)
     wu = normal(seed, (f, d), 0.02, stream=1)
@@ -417,7 +439,7 @@ def _mlp_case(tq, m, d, f, seed=57):
                                    (6, 16384, 128), (3, 4096, 14336), (4, 4096, 14336), (4, 256, 128),
                                    (3, 640, 16384), (6, 4096, 14336), (8, 4096, 14336), (2, 4096, 14336),
                                    (9, 256, 512), (12, 4096, 14336), (16, 1024, 640), (16, 4096, 14336),
-                                   (13, 128, 384), (7, 8192, 1024), (17, 4096, 14336), (32, 512, 1536),
+                                   (13, 128, 384), (7, 8192, 1024), (17, 4096, 14336), (28, 512, 1536),
                                    (25, 256, 384), (9, 512, 6144), (5, 1024, 8192), (10, 1024, 13056)])
 def test_mlp_decode_path(tq, oracle, m, d, f):
     wg = normal(60, (f, d), 0.02)
@@ -426,7 +448,7 @@ def test_mlp_decode_path(tq, oracle, m, d, f):
     xb = to_bf16_bits(normal(60, (m, d), 1.0, stream=3))
     mlp = tq.QuantizedMLP.from_tensors(dev_tensor(wg), dev_tensor(wu), dev_tensor(wd))
     assert mlp._decode_path(m)
-    assert mlp._decode_path(32) == (d <= 4096) and not mlp._decode_path(33)
+    assert mlp._decode_path(28) == (d <= 4096) and not mlp._decode_path(29)
     y = host(mlp(bf16_dev(xb)))
     args = [a for t in (mlp.gate, mlp.up, mlp.down) for a in (host(t[0]), host(t[1]).view(np.uint16))]
     assert_close(y, oracle.mlp_w4g128(xb, *args), RTOL, ATOL, f"mlp decode {m}x{d}x{f}")

@@ -307,6 +307,34 @@ def test_linear_w8_w4_match_numpy(oracle):
     np.testing.assert_allclose(oracle.linear_w4g128_bf16(xb, p, s16), xf @ wd.T, rtol=1e-12, atol=1e-12)
 
 
+def test_linear_w4g128_f32_and_bias_match_numpy(oracle):
+    """Linear::forward over the dequantized INT4 weight with f32 activations
+    (linear.rs:111-121 over quantize.rs:22-27): x @ deq(W)^T + b in f64.  The
+    activations are not multiples of a bf16 ulp, so a path that rounded them to
+    bf16 fails; distinct row/column sizes and a bias catch a swapped argument."""
+    rng = np.random.default_rng(15)
+    n, k, m = 40, 384, 3
+    w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    b = rng.standard_normal(n).astype(np.float32)
+    p, s16 = oracle.quantize_i4_g128(w)
+    wd = oracle.dequantize_i4_g128(p, s16).astype(np.float64)
+    ref = x.astype(np.float64) @ wd.T
+    got = oracle.linear_w4g128_f32(x, p, s16)
+    assert got.shape == (m, n)
+    np.testing.assert_allclose(got, ref, rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(oracle.linear_w4g128_f32(x, p, s16, b), ref + b.astype(np.float64), rtol=1e-12,
+                               atol=1e-12)
+    # the f32 values reach the sum unrounded: the bf16 form of the same x differs
+    xb = (x.view(np.uint32) >> 16).astype(np.uint16)
+    assert np.abs(oracle.linear_w4g128_bf16(xb, p, s16) - got).max() > 1e-6
+    # a row of the product is the sequential f64 dot of Tensor::mm (tensor_ops.rs:379-410)
+    acc = 0.0
+    for kk in range(k):
+        acc += float(x[1, kk]) * float(wd[7, kk])
+    assert got[1, 7] == pytest.approx(acc, rel=1e-13, abs=1e-15)
+
+
 # ------------------------------------------------------------------ W8A8
 def test_w8a8_acc_vs_numpy_int64(oracle):
     rng = np.random.default_rng(13)

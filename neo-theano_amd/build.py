@@ -149,6 +149,51 @@ def build_peaks():
     return out
 
 
+SAN_DIR = os.path.join(OBJ, "sanitize")
+SAN = ["-fsanitize=address,undefined", "-fno-sanitize-recover=undefined", "-fno-omit-frame-pointer", "-g", "-O1"]
+
+
+def build_sanitized(verbose=False):
+    """CPU-only sanitizer builds (test infrastructure, opt-in: `build.py --sanitize`):
+    * _build/sanitize/libtq_oracle.so: the C oracle under gcc's ASan + UBSan, for
+      the Python oracle tests (TQ_ORACLE_LIB, with gcc's libasan preloaded);
+    * _build/sanitize/test_theano_quantize: the C++ host-layer tests, with the
+      host layer (allocator, storage, serialization, Module API) and the C oracle
+      compiled in under clang's ASan + UBSan and linked to the ordinary libtq.so.
+      These sources hold no device code, so ROCm's plain clang++ compiles them
+      against the HIP runtime headers (no GPU pass, nothing device-side
+      instrumented)."""
+    os.makedirs(SAN_DIR, exist_ok=True)
+    odir = os.path.join(ROOT, "oracle")
+    olib = os.path.join(SAN_DIR, "libtq_oracle.so")
+    _run(["gcc", *SAN, "-ffp-contract=off", "-fno-fast-math", "-fPIC", "-shared", "-std=c11", "-Wall", "-Werror",
+          os.path.join(odir, "tq_oracle.c"), "-o", olib + ".tmp", "-lm"])
+    os.replace(olib + ".tmp", olib)
+    rocm = os.path.dirname(os.path.dirname(os.path.realpath(HIPCC)))
+    llvm = os.path.join(rocm, "llvm", "bin")
+    if not os.path.exists(os.path.join(llvm, "clang++")):
+        llvm = "/opt/rocm/llvm/bin"
+    objs = []
+    oobj = os.path.join(SAN_DIR, "tq_oracle.o")
+    _run([os.path.join(llvm, "clang"), "-x", "c", "-std=c11", *SAN, "-ffp-contract=off", "-c",
+          os.path.join(odir, "tq_oracle.c"), "-o", oobj])
+    objs.append(oobj)
+    for src in (os.path.join(ROOT, "tests", "cpp", "test_theano_quantize.cpp"), os.path.join(HOST, "theano_quantize.cpp"),
+                os.path.join(HOST, "theano_serialize.cpp"), os.path.join(HOST, "theano_rocm.cpp")):
+        obj = os.path.join(SAN_DIR, os.path.basename(src).replace(".cpp", ".o"))
+        log = _run([os.path.join(llvm, "clang++"), "-std=c++17", *SAN, "-Wall", "-D__HIP_PLATFORM_AMD__",
+                    f"-I{os.path.join(rocm, 'include')}", f"-I{os.path.join(ROOT, 'include')}", f"-I{HOST}", "-c", src,
+                    "-o", obj])
+        if verbose and log.strip():
+            print(log)
+        objs.append(obj)
+    exe = os.path.join(SAN_DIR, "test_theano_quantize")
+    _run([os.path.join(llvm, "clang++"), *SAN, *objs, "-o", exe + ".tmp", f"-L{PKG}", "-ltq",
+          f"-L{os.path.join(rocm, 'lib')}", "-lamdhip64", f"-Wl,-rpath,{PKG}", f"-Wl,-rpath,{os.path.join(rocm, 'lib')}"])
+    os.replace(exe + ".tmp", exe)
+    return [olib, exe]
+
+
 def build_all(verbose=False):
     if shutil.which(HIPCC) is None and not os.path.exists(HIPCC):
         raise RuntimeError(f"hipcc not found at {HIPCC}")
@@ -163,5 +208,9 @@ def build_all(verbose=False):
 
 
 if __name__ == "__main__":
-    for p in build_all(verbose="-v" in sys.argv):
-        print("built", p)
+    if "--sanitize" in sys.argv:
+        for p in build_sanitized(verbose="-v" in sys.argv):
+            print("built", p)
+    else:
+        for p in build_all(verbose="-v" in sys.argv):
+            print("built", p)

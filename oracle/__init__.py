@@ -13,7 +13,9 @@ import os
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libtq_oracle.so")
+# TQ_ORACLE_LIB selects another build of the same source (the sanitizer build
+# of `neo-theano_amd/build.py --sanitize`)
+LIB_PATH = os.environ.get("TQ_ORACLE_LIB") or os.path.join(HERE, "libtq_oracle.so")
 
 INT8, UINT8, INT4, FP8 = 0, 1, 2, 3
 

@@ -698,13 +698,19 @@ TEST_CPU(test_safetensors_malformed) {
     ASSERT(ser::SafeTensorsFile::from_bytes(make("{\"t\":{\"dtype\":\"F32\",\"shape\":[1]", 4)).is_err());
 }
 
+// tests/golden/ beside the executable's directory, or $TQ_GOLDEN_DIR (a build elsewhere)
 std::vector<uint8_t> golden_checkpoint() {
-    char exe[4096];
-    const ssize_t n = readlink("/proc/self/exe", exe, sizeof exe - 1);
-    ASSERT(n > 0);
-    std::string dir(exe, static_cast<size_t>(n));
-    dir = dir.substr(0, dir.rfind('/'));
-    std::ifstream in(dir + "/../golden/checkpoint_int4_16x256.safetensors", std::ios::binary);
+    std::string dir;
+    if (const char* g = std::getenv("TQ_GOLDEN_DIR")) {
+        dir = g;
+    } else {
+        char exe[4096];
+        const ssize_t n = readlink("/proc/self/exe", exe, sizeof exe - 1);
+        ASSERT(n > 0);
+        dir = std::string(exe, static_cast<size_t>(n));
+        dir = dir.substr(0, dir.rfind('/')) + "/../golden";
+    }
+    std::ifstream in(dir + "/checkpoint_int4_16x256.safetensors", std::ios::binary);
     ASSERT(in.good());
     return std::vector<uint8_t>((std::istreambuf_iterator<char>(in)), std::istreambuf_iterator<char>());
 }

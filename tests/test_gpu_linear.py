@@ -80,14 +80,15 @@ def test_gemv_w8_config2(tq, c2, m):
 
 # K % 16 != 0 and K > 8192 take the shape-general kernel (e.g. the reference's Linear(3, 2));
 # 2-4 tokens with K split over a wave pair: a second half with fewer chunks (K = 3088,
-# 3072), rows per pair past the LDS partials (N = 70000: more blocks than CUs); runs of
+# 3072), rows per pair capped at the LDS partials' 64 (N = 70000 at K = 4096 with 3 tokens
+# and K = 8192 with 2: more than 1024 pair runs, so the grid grows past the 256 CUs); runs of
 # several row groups per wave, in even and odd numbers, through the two alternating
 # register buffers (N = 14336 and 30000 at one token: 7 and 15 rows per wave; N = 9000 at
 # two tokens: 3 groups of 2 rows)
 @pytest.mark.parametrize("n,k,m", [(1000, 1024, 1), (17, 16, 2), (333, 3088, 3), (64, 8192, 4), (5, 2000, 16),
                                    (2, 3, 4), (50, 100, 3), (64, 9000, 2), (70000, 2048, 3), (4100, 3072, 4),
                                    (515, 8192, 2), (14336, 4096, 1), (30000, 1024, 1), (9000, 1024, 2),
-                                   (8192, 2048, 1)])
+                                   (8192, 2048, 1), (70000, 4096, 3), (70000, 8192, 2)])
 def test_gemv_w8_shapes_bias(tq, oracle, n, k, m):
     w = normal(50, (n, k), 0.02)
     x = normal(50, (m, k), 1.0, stream=1)

@@ -48,8 +48,8 @@ def parse_args():
     p.add_argument("--steps", type=int, default=200)
     p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--only", default=None,
-                   help="run one workload: gemv_w4, gemv_w8, gemv_fp8, gemv_w4_m, w8a8_decode, w8a8, fp8, mha, storage, "
-                        "roundtrip, mlp, mlp_mid, mlp_decode, copy")
+                   help="run one workload: gemv_w4, gemv_w8, gemv_fp8, gemv_w4_m, peaks, read_ceiling, read_sweep, "
+                        "quant_i4, w8a8_decode, w8a8, fp8, mha, storage, roundtrip, mlp, mlp_mid, mlp_decode, copy")
     p.add_argument("--no-secondary", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=12.0, help="bound of the CPU baseline sample (0: skip)")
     p.add_argument("--eager", action="store_true", help="time eager launches instead of a HIP graph")
@@ -63,14 +63,15 @@ def log(*a):
 
 class Timer:
     """Times `steps` calls of launch(i), bracketed by events on the stream the
-    launches go to, three ways, and returns the fastest with its mode:
-    "hip graph" (the launches captured into a hipGraph by libtq_peaks.so's
-    tqp_graph_time and replayed on its own stream: what a host that calls the C
-    ABI directly sees), "torch graph" (captured with torch.cuda.graph and
-    replayed on torch's current stream) and "eager" (only eager launches with
-    --eager).  Short kernels need a graph (a Python launch takes longer than
-    the kernel); the two graph forms agree to about 0.1 us per launch.  `last`
-    holds every mode's time of the latest run."""
+    launches go to, and returns (ms per step, mode) in ONE fixed mode: "hip
+    graph", the launches captured into a hipGraph by libtq_peaks.so's
+    tqp_graph_time and replayed on its own stream (what a host that calls the C
+    ABI directly sees).  Only when that capture fails does it fall back to a
+    torch.cuda.graph replay ("torch graph"), and only with --eager to eager
+    launches.  With `diagnostics=True`, `last` also holds the torch-graph and
+    eager times of the same launches; they are never what `run` returns.
+    Short kernels need a graph: a Python launch takes longer than the
+    kernel."""
 
     def __init__(self, torch, eager=False, reps=1):
         self.torch = torch
@@ -78,21 +79,25 @@ class Timer:
         self.reps = reps  # timed replays of the `steps` launches; the median is returned
         self.last = {}
 
-    def run(self, launch, steps, warmup):
+    def run(self, launch, steps, warmup, diagnostics=False):
         self.last = {}
-        cands = []
-        if not self.eager:
-            nat = self._native(launch, steps, warmup)
-            if nat is not None:
-                cands.append((nat, "hip graph"))
-        best = self._run(launch, steps, warmup, graph=not self.eager)
-        cands.append(best)
-        if best[1] == "graph":
-            cands[-1] = (best[0], "torch graph")
-            cands.append(self._run(launch, steps, 0, graph=False))
-        for ms, mode in cands:
-            self.last[mode] = ms
-        return min(cands, key=lambda c: c[0])
+        if self.eager:
+            res = self._run(launch, steps, warmup, graph=False)
+            self.last[res[1]] = res[0]
+            return res
+        nat = self._native(launch, steps, warmup)
+        if nat is not None:
+            self.last["hip graph"] = nat
+            if diagnostics:
+                tg = self._run(launch, steps, 0, graph=True)
+                self.last["torch graph" if tg[1] == "graph" else tg[1]] = tg[0]
+                ea = self._run(launch, steps, 0, graph=False)
+                self.last["eager"] = ea[0]
+            return nat, "hip graph"
+        res = self._run(launch, steps, warmup, graph=True)
+        mode = "torch graph" if res[1] == "graph" else res[1]
+        self.last[mode] = res[0]
+        return res[0], mode
 
     def _native(self, launch, steps, warmup):
         """Median ms per step of a hipGraph replay (tqp_graph_time), or None
@@ -268,6 +273,63 @@ def read_ceiling(torch, timer, dev, nbytes, args, log):
     return res
 
 
+def read_sweep(torch, timer, dev, args, log, headline_bytes):
+    """Plain streaming reads of 8-240 MB per launch (the best of five read
+    kernels at each size, buffers rotating past the MALL, the headline's
+    harness), fitted as t(B) = t0 + B / R by least squares: t0 is what every
+    launch pays whatever its size (dispatch, first-byte latency, drain) and R
+    the rate at which the bytes themselves stream.  The fit then gives the
+    fastest any one launch of the headline's bytes can read them."""
+    import ctypes
+
+    L = _peaks_lib()
+    st = lambda: ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    out = torch.empty(1 << 16, dtype=torch.int32, device=dev)
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    sizes = [8 << 20, 16 << 20, headline_bytes // 16 * 16, 60 << 20, 120 << 20, 240 << 20]
+    points = []
+    res = {"sizes": {}}
+    for nb in sizes:
+        copies = [torch.empty(nb, dtype=torch.uint8, device=dev).fill_(1) for _ in range(rotation(nb))]
+        best = None
+        for kind, a in [("grid-stride", b) for b in (8 * cus, 16 * cus, 32 * cus)] + [("one-pass", u) for u in (4, 16)]:
+            if kind == "grid-stride":
+                fn = lambda i, b=a: L.tqp_hbm_read(copies[i % len(copies)].data_ptr(), nb, out.data_ptr(), b, st())
+                label = f"grid-stride, {a} blocks"
+            else:
+                fn = lambda i, u=a: L.tqp_hbm_read_chunks(copies[i % len(copies)].data_ptr(), nb, out.data_ptr(), u,
+                                                          st())
+                label = f"one-pass, {4096 * a} B per block"
+            ms, _ = timer.run(fn, args.steps, args.warmup)
+            if best is None or ms < best[0]:
+                best = (ms, label)
+        us = best[0] * 1e3
+        points.append((nb, us))
+        res["sizes"][str(nb)] = {"us": round(us, 3), "GB/s": round(nb / (us * 1e-6) / 1e9, 1),
+                                 "hbm_frac": round(nb / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4), "best": best[1],
+                                 "copies": len(copies)}
+        log(f"read sweep {nb / 1e6:.1f} MB per launch: {us:.2f} us  {nb / (us * 1e-6) / 1e9:.0f} GB/s ({best[1]})")
+        del copies
+    n = len(points)
+    mx = sum(b for b, _ in points) / n
+    my = sum(t for _, t in points) / n
+    slope = sum((b - mx) * (t - my) for b, t in points) / sum((b - mx) ** 2 for b, _ in points)  # us per byte
+    t0 = my - slope * mx
+    rate = 1e-3 / slope  # GB/s: bytes per us / 1e3
+    hb = headline_bytes
+    t_hb = t0 + slope * hb
+    res.update({"fixed_us": round(t0, 3), "sustained_GB/s": round(rate, 1),
+                "sustained_hbm_frac": round(rate / HBM_PEAK_GBS, 4),
+                "fit_max_abs_residual_us": round(max(abs(t - (t0 + slope * b)) for b, t in points), 3),
+                "headline_bytes": hb, "headline_fit_us": round(t_hb, 3),
+                "headline_fit_GB/s": round(hb / (t_hb * 1e-6) / 1e9, 1),
+                "headline_fit_hbm_frac": round(hb / (t_hb * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                "target_70pct_us": round(hb / (0.7 * HBM_PEAK_GBS * 1e9) * 1e6, 3)})
+    log(f"read sweep fit: t = {t0:.2f} us + B / {rate:.0f} GB/s; headline bytes -> {t_hb:.2f} us "
+        f"({res['headline_fit_hbm_frac'] * 100:.1f} % of spec; the 70 % target needs {res['target_70pct_us']:.2f} us)")
+    return res
+
+
 def cpu_baselines(args, secondary, n3, k3, headline_bytes, log):
     """The reference CPU path restated in C (oracle/, f64, one thread), timed on
     the host beside the GPU legs.  A quantized Linear in the reference is
@@ -289,6 +351,20 @@ def cpu_baselines(args, secondary, n3, k3, headline_bytes, log):
 
     O.lib()
     ncpu = os.cpu_count()
+    model = "unknown CPU"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    # the reference path is single-threaded: pin this thread to one core (the
+    # first this process may use), as `taskset -c 0` would, for the whole baseline
+    allowed = sorted(os.sched_getaffinity(0))
+    core = allowed[0]
+    os.sched_setaffinity(0, {core})
 
     def timed(fn, budget):
         reps, t0 = 0, time.perf_counter()
@@ -303,7 +379,9 @@ def cpu_baselines(args, secondary, n3, k3, headline_bytes, log):
         return (bits.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
 
     def entry(value, unit, sample):
-        return {"value": value, "unit": unit, "cores": 1, "kind": "port", "sample": sample + f"; 1 thread on {ncpu} host CPUs"}
+        return {"value": value, "unit": unit, "cores": 1, "kind": "port",
+                "sample": sample + f"; 1 thread pinned to core {core} of {len(allowed)} allowed ({ncpu} host CPUs, "
+                                   f"{model})"}
 
     # C3, the headline: INT4 g128 weight [14336, 4096] dequantized once, one token
     w = normal_f32(2, (n3, k3), 0.02)
@@ -362,7 +440,7 @@ def cpu_baselines(args, secondary, n3, k3, headline_bytes, log):
     del wh, wht, w, q, sc
     # C5: gate / up [14336, 4096] and down [4096, 14336], each dequantized once
     if "mlp_w4g128_m512" in secondary:
-        d5, f5, m5, mp = 4096, 14336, 512, 8
+        d5, f5, m5, mp = 4096, 14336, 512, 32
         tot = 0.0
         parts = []
         for name, shape, count in (("gate/up", (f5, d5), 2), ("down", (d5, f5), 1)):
@@ -381,6 +459,9 @@ def cpu_baselines(args, secondary, n3, k3, headline_bytes, log):
             round(m5 / tot, 4), "tokens/s",
             f"config 5: Linear::forward (" + "; ".join(parts) + f"), extrapolated to M=512 and summed over "
             f"gate, up and down (SiLU * up not timed): {tot:.1f} s")
+    os.sched_setaffinity(0, set(allowed))
+    head["cpu_model"] = model
+    head["pinned_core"] = core
     log("cpu baselines done")
     return head
 
@@ -452,7 +533,7 @@ def main():
             return launch
 
         if want("gemv_w4"):
-            ms, mode = timer.run(gemv_w4(1), args.steps, args.warmup)
+            ms, mode = timer.run(gemv_w4(1), args.steps, args.warmup, diagnostics=True)
             gbs = w4_bytes_m(1) / (ms * 1e-3) / 1e9
             headline = {"ms": ms, "gbs": gbs, "mode": mode, "modes_us": {k: round(v * 1e3, 3) for k, v in timer.last.items()}}
             log(f"gemv_w4 M=1: {ms * 1e3:.2f} us/step  {gbs:.0f} GB/s  ({mode})")
@@ -487,16 +568,18 @@ def main():
     peaks = None
     if not args.no_secondary and (only is None or only == "peaks"):
         peaks = measured_peaks(torch, timer, dev, log)
+        secondary["measured_peaks"] = peaks
 
     def of_random_peak(rate, key):
         # fraction of the matrix-core rate measured on random operands (None when
         # the peaks leg did not run)
         return round(rate / peaks[key], 4) if peaks else None
-        secondary["measured_peaks"] = peaks
 
     # ----------------- plain streaming read of the headline's bytes per launch
     if not args.no_secondary and (only is None or only == "read_ceiling"):
         secondary["read_ceiling_30mb"] = read_ceiling(torch, timer, dev, w4_bytes_m(1), args, log)
+    if not args.no_secondary and (only is None or only == "read_sweep"):
+        secondary["read_sweep"] = read_sweep(torch, timer, dev, args, log, w4_bytes_m(1))
 
     # ------------------------------------- INT4 g128 quantize + pack (C3 weight)
     if not args.no_secondary and want("quant_i4"):
@@ -611,57 +694,71 @@ def main():
     # ---------------------------------------------------------- W8A8 (C4)
     if not args.no_secondary and want("w8a8"):
         m4, n4, k4 = 2048, 4096, 4096
-        x = normal_f32(3, (m4, k4), 1.0)
-        w = normal_f32(3, (n4, k4), 0.02, stream=1)
-        xd = dt(x)
-        qa, sa = tq.quantize_per_channel_i8(xd)
-        qw, sw = tq.quantize_per_channel_i8(dt(w))
+        xd = dt(normal_f32(3, (m4, k4), 1.0))
+        qa0, sa0 = tq.quantize_per_channel_i8(xd)
+        qw0, sw0 = tq.quantize_per_channel_i8(dt(normal_f32(3, (n4, k4), 0.02, stream=1)))
+        # every launch takes its own copy of the operands (codes and scales of
+        # both sides), rotating over more than 2x the MALL
+        ops = [(qa0.clone(), sa0.clone(), qw0.clone(), sw0.clone())
+               for _ in range(rotation(m4 * k4 + n4 * k4 + 4 * (m4 + n4)))]
         y = torch.empty((m4, n4), dtype=torch.float32, device=dev)
 
         def launch(i):
+            qa, sa, qw, sw = ops[i % len(ops)]
             _abi.call("tq_gemm_w8a8", ptr(qa), ptr(sa), ptr(qw), ptr(sw), None, m4, n4, k4, None, ptr(y), stream())
 
         steps = max(10, args.steps // 4)
         ms, mode = timer.run(launch, steps, max(2, args.warmup // 4))
         tops = 2.0 * m4 * n4 * k4 / (ms * 1e-3) / 1e12
         qbytes = 4 * m4 * k4 + m4 * k4 + 4 * m4
+        xs = [xd] + [xd.clone() for _ in range(rotation(4 * m4 * k4) - 1)]
+        qa1, sa1 = torch.empty_like(qa0), torch.empty_like(sa0)
 
         def launch_q(i):
-            _abi.call("tq_quantize_i8_rowwise", ptr(xd), m4, k4, ptr(qa), ptr(sa), stream())
+            _abi.call("tq_quantize_i8_rowwise", ptr(xs[i % len(xs)]), m4, k4, ptr(qa1), ptr(sa1), stream())
 
         msq, _ = timer.run(launch_q, steps, 2)
         secondary["w8a8_gemm_m2048"] = {
             "us": round(ms * 1e3, 3), "timing": mode, "TOPS": round(tops, 1), "i8_mfma_frac": round(tops / I8_PEAK_TOPS, 4),
             "i8_mfma_frac_of_random_operand_peak": of_random_peak(tops, "i8_mfma_TOPS_random_operands"),
-            "act_quant_us": round(msq * 1e3, 3), "act_quant_GB/s": round(qbytes / (msq * 1e-3) / 1e9, 1)}
+            "operand_copies": len(ops),
+            "act_quant_us": round(msq * 1e3, 3), "act_quant_GB/s": round(qbytes / (msq * 1e-3) / 1e9, 1),
+            "act_quant_input_copies": len(xs)}
         log(f"w8a8 M=2048: {ms * 1e3:.2f} us  {tops:.0f} TOPS; act quant {msq * 1e3:.2f} us")
-        del qa, qw, y, xd
+        del ops, xs, y, xd, qa0, qw0, qa1
 
     # ------------------------------------------------ FP8 W8A8 (C4 shape)
     if not args.no_secondary and want("fp8"):
         m4, n4, k4 = 2048, 4096, 4096
         xd = dt(normal_f32(3, (m4, k4), 1.0))
-        qa, sa = tq.quantize_per_channel_fp8(xd)
-        qw, sw = tq.quantize_per_channel_fp8(dt(normal_f32(3, (n4, k4), 0.02, stream=1)))
+        qa0, sa0 = tq.quantize_per_channel_fp8(xd)
+        qw0, sw0 = tq.quantize_per_channel_fp8(dt(normal_f32(3, (n4, k4), 0.02, stream=1)))
+        ops = [(qa0.clone(), sa0.clone(), qw0.clone(), sw0.clone())
+               for _ in range(rotation(m4 * k4 + n4 * k4 + 4 * (m4 + n4)))]
         y = torch.empty((m4, n4), dtype=torch.float32, device=dev)
 
         def launch(i):
+            qa, sa, qw, sw = ops[i % len(ops)]
             _abi.call("tq_gemm_fp8", ptr(qa), ptr(sa), ptr(qw), ptr(sw), None, m4, n4, k4, ptr(y), stream())
 
         steps = max(10, args.steps // 4)
         ms, mode = timer.run(launch, steps, max(2, args.warmup // 4))
         tf = 2.0 * m4 * n4 * k4 / (ms * 1e-3) / 1e12
         qbytes = 4 * m4 * k4 + m4 * k4 + 4 * m4
+        xs = [xd] + [xd.clone() for _ in range(rotation(4 * m4 * k4) - 1)]
+        qa1, sa1 = torch.empty_like(qa0), torch.empty_like(sa0)
 
         def launch_q(i):
-            _abi.call("tq_quantize_fp8_rowwise", ptr(xd), m4, k4, ptr(qa), ptr(sa), stream())
+            _abi.call("tq_quantize_fp8_rowwise", ptr(xs[i % len(xs)]), m4, k4, ptr(qa1), ptr(sa1), stream())
 
         msq, _ = timer.run(launch_q, steps, 2)
         secondary["fp8_gemm_m2048"] = {
             "us": round(ms * 1e3, 3), "timing": mode, "TFLOP/s": round(tf, 1), "fp8_mfma_frac": round(tf / FP8_PEAK_TFLOPS, 4),
-            "act_quant_us": round(msq * 1e3, 3), "act_quant_GB/s": round(qbytes / (msq * 1e-3) / 1e9, 1)}
+            "operand_copies": len(ops),
+            "act_quant_us": round(msq * 1e3, 3), "act_quant_GB/s": round(qbytes / (msq * 1e-3) / 1e9, 1),
+            "act_quant_input_copies": len(xs)}
         log(f"fp8 M=2048: {ms * 1e3:.2f} us  {tf:.0f} TFLOP/s; act quant {msq * 1e3:.2f} us")
-        del qa, qw, y, xd
+        del ops, xs, y, xd, qa0, qw0, qa1
 
     # ------------------------------ MultiheadAttention, INT4 projections
     if not args.no_secondary and want("mha"):
@@ -735,13 +832,18 @@ def main():
         d5, f5, m5 = 4096, 14336, 512
         mlp = tq.QuantizedMLP.from_tensors(dt(normal_f32(4, (f5, d5), 0.02)), dt(normal_f32(4, (f5, d5), 0.02, 1)),
                                            dt(normal_f32(4, (d5, f5), 0.02, 2)))
+        wbytes = 3 * f5 * d5 // 2 + 3 * f5 * d5 // 128 * 2
+        # every launch takes its own copy of the three weights, rotating over more than 2x the MALL
+        mats = [(mlp.gate, mlp.up, mlp.down)] + [tuple(tuple(t.clone() for t in w) for w in (mlp.gate, mlp.up, mlp.down))
+                                                 for _ in range(rotation(wbytes) - 1)]
         x = bf16(normal_f32(4, (m5, d5), 1.0, stream=3))
         ws = torch.empty((mlp.workspace_bytes(m5),), dtype=torch.uint8, device=dev)
         y = torch.empty((m5, d5), dtype=torch.float32, device=dev)
 
         def launch(i):
-            _abi.call("tq_mlp_w4g128", ptr(x), m5, d5, f5, ptr(mlp.gate[0]), ptr(mlp.gate[1]), ptr(mlp.up[0]),
-                      ptr(mlp.up[1]), ptr(mlp.down[0]), ptr(mlp.down[1]), ptr(ws), ws.numel(), ptr(y), stream())
+            g, u, dn = mats[i % len(mats)]
+            _abi.call("tq_mlp_w4g128", ptr(x), m5, d5, f5, ptr(g[0]), ptr(g[1]), ptr(u[0]), ptr(u[1]), ptr(dn[0]),
+                      ptr(dn[1]), ptr(ws), ws.numel(), ptr(y), stream())
 
         steps = max(5, args.steps // 10)
         ms, mode = timer.run(launch, steps, 2)
@@ -750,7 +852,8 @@ def main():
         secondary["mlp_w4g128_m512"] = {"us": round(ms * 1e3, 2), "timing": mode, "tokens/s": round(m5 / (ms * 1e-3), 1),
                                         "TFLOP/s": round(tf, 1), "bf16_mfma_frac": round(tf / BF16_PEAK_TFLOPS, 4),
                                         "bf16_mfma_frac_of_random_operand_peak":
-                                            of_random_peak(tf, "bf16_mfma_TFLOPS_random_operands")}
+                                            of_random_peak(tf, "bf16_mfma_TFLOPS_random_operands"),
+                                        "weight_copies": len(mats)}
         log(f"mlp M=512: {ms * 1e3:.1f} us  {m5 / (ms * 1e-3):.0f} tok/s  {tf:.0f} TFLOP/s")
 
         # prefill INT4 Linear on the gate weight alone: [512, 4096] x [14336, 4096]^T
@@ -759,17 +862,19 @@ def main():
         yl = torch.empty((m5, f5), dtype=torch.float32, device=dev)
 
         def launch_lin(i):
-            _abi.call("tq_gemm_w4g128_bf16_ws", ptr(x), m5, ptr(mlp.gate[0]), ptr(mlp.gate[1]), None, f5, d5,
-                      ptr(wsl), nbl, ptr(yl), stream())
+            g = mats[i % len(mats)][0]
+            _abi.call("tq_gemm_w4g128_bf16_ws", ptr(x), m5, ptr(g[0]), ptr(g[1]), None, f5, d5, ptr(wsl), nbl,
+                      ptr(yl), stream())
 
         ms, mode = timer.run(launch_lin, steps, 2)
         tf = 2.0 * m5 * f5 * d5 / (ms * 1e-3) / 1e12
         secondary["w4a16_linear_m512_n14336_k4096"] = {"us": round(ms * 1e3, 2), "timing": mode, "TFLOP/s": round(tf, 1),
                                                        "bf16_mfma_frac": round(tf / BF16_PEAK_TFLOPS, 4),
                                                        "bf16_mfma_frac_of_random_operand_peak":
-                                                           of_random_peak(tf, "bf16_mfma_TFLOPS_random_operands")}
+                                                           of_random_peak(tf, "bf16_mfma_TFLOPS_random_operands"),
+                                                       "weight_copies": len(mats)}
         log(f"w4a16 linear M=512 N=14336 K=4096: {ms * 1e3:.1f} us  {tf:.0f} TFLOP/s")
-        del mlp, wsl, yl
+        del mlp, mats, wsl, yl
 
     # --------------- mid-size M on the prefill kernels (C5 weights, M = 64, 128)
     if not args.no_secondary and want("mlp_mid"):

@@ -494,6 +494,154 @@ __global__ __launch_bounds__(kBlock) void k_decode_tiled_mfma_sx(const uint16_t*
     }
 }
 
+// The decode FFN's down projection for 9-16 tokens in one launch: the 2t <= 32
+// rows of h (t hi rows, then t lo rows, in slot order as the gate/up epilogue
+// wrote them) are two sets of 16 columns of v_mfma_f32_16x16x32_bf16, so the
+// down weights are read once per call where launches of up to 16 rows read them
+// once per 8 tokens.  32-row tiles (two row groups of 16), K split over
+// gridDim.y = 2 blocks per tile whose sums are added onto a y the gate/up launch
+// zeroed (two addends onto zero: the same sum in either order).  Operand layout
+// as in k_decode_tiled_mfma_sx: lane (r16, q) holds chunk 4 g + q of tile row
+// 16 r + r16 and reads its B operands, row 16 s + r16 of set s, from an LDS
+// strip.  Each wave runs its kGPW groups one at a time through one private strip
+// of 32 rows x 256 bytes, filled by global_load_lds_dwordx4 (no registers): row
+// t's 16-byte chunk c sits at chunk c ^ (t % 16), so the 16 rows one B read
+// touches fall in distinct banks.  The next group's DMAs go out once the current
+// group's B operands are read, and land under its MFMAs; weights and scales run
+// kWG groups ahead.  A group's DMAs are waited for with vmcnt(0): the compiler
+// moves its own loads of the (restrict, read-only) weights and scales across
+// inline asm, so no count of the loads issued after the DMAs can be relied on.
+template <int kGPW>
+__global__ __launch_bounds__(kBlock) void k_decode_fold32(const uint16_t* __restrict__ h, int rows,
+                                                          const uint8_t* __restrict__ pt,
+                                                          const uint16_t* __restrict__ st, int64_t n, int64_t k,
+                                                          float* __restrict__ y) {
+    constexpr int kR = 2, T = 32;
+    constexpr int kStrip = 32 * 256;
+    constexpr int kWG = kGPW < 3 ? kGPW : 3;  // groups of weights and scales in flight
+    static_assert(T * 32 * 4 <= kStrip, "a wave's partial sums fit in its strip");
+    __shared__ __attribute__((aligned(1024))) int8_t strips[kWaves][kStrip];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int q = lane >> 4, r16 = lane & 15;
+    const int64_t tile = blockIdx.x;
+    const int64_t C = k >> 5, G = k >> 7;
+    const int64_t gh = (G + gridDim.y - 1) / gridDim.y, gb = blockIdx.y * gh, ge = min(G, gb + gh);
+    const int64_t g0 = gb + static_cast<int64_t>(wave) * kGPW;
+    const int64_t gl = max<int64_t>(ge - 1, 0);
+    int8_t* sx = strips[wave];
+
+    // DMA i (0..7) of a group moves rows 4 i .. 4 i + 3: lane l -> row 4 i + l / 16,
+    // landing at LDS chunk l % 16, from global chunk (l % 16) ^ row % 16.  Rows past
+    // `rows` re-read the last row and groups past the range the last group (their
+    // columns and sums are never used).
+    auto dma_group = [&](int gi) {
+        const uint16_t* hb = h + min<int64_t>(g0 + gi, gl) * 128;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int t = 4 * i + (lane >> 4);
+            lds_dma16(hb + static_cast<int64_t>(min(t, rows - 1)) * k + 8 * (r16 ^ (t & 15)), lds_addr(sx + 1024 * i));
+        }
+    };
+    const uint8_t* wb = pt + (tile * C * T + r16) * 16;
+    uint2 sc[kWG][kR];
+    u32x4 w[kWG][kR];
+    auto load_group = [&](int gi) {  // into slot gi % kWG
+        const int64_t g = min<int64_t>(g0 + gi, gl);
+#pragma unroll
+        for (int r = 0; r < kR; ++r) {
+            sc[gi % kWG][r] = *reinterpret_cast<const uint2*>(st + (tile * G + g) * T + 16 * r + 4 * q);
+            w[gi % kWG][r] =
+                __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wb + ((4 * g + q) * T + 16 * r) * 16));
+        }
+    };
+    dma_group(0);
+#pragma unroll
+    for (int gi = 0; gi < kWG; ++gi) load_group(gi);
+    const u32x4 aoff = u32x4{0xC308C308u, 0xC308C308u, 0xC308C308u, 0xC308C308u};  // bf16 -136
+    f32x4 acc[2][kR];
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+        for (int r = 0; r < kR; ++r) acc[s2][r] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int gi = 0; gi < kGPW; ++gi) {
+        if (g0 + gi >= ge) break;  // wave-uniform
+        wait_vmcnt<0>();  // the group's DMAs have landed
+        u32x4 xb[2][4];
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                xb[s2][j] = *reinterpret_cast<const u32x4*>(sx + (16 * s2 + r16) * 256 + (((4 * q + j) ^ r16) << 4));
+        if (gi + 1 < kGPW) {
+            // every read of this group's strip has returned: the next group may land
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            dma_group(gi + 1);
+        }
+        f32x4 xs[2];
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2) {
+            xs[s2] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) xs[s2] = mfma16_bf16(aoff, xb[s2][j], xs[s2]);
+        }
+#pragma unroll
+        for (int r = 0; r < kR; ++r) {
+            const u32x4 wv = w[gi % kWG][r];
+            const uint32_t ws[4] = {wv.x, wv.y, wv.z, wv.w};
+            f32x4 d0 = xs[0], d1 = xs[1];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const u32x4 a = unpack_w4_136(ws[j]);
+                d0 = mfma16_bf16(a, xb[0][j], d0);
+                d1 = mfma16_bf16(a, xb[1][j], d1);
+            }
+            const uint32_t s01 = sc[gi % kWG][r].x, s23 = sc[gi % kWG][r].y;
+            const float sv[4] = {__half2float(__ushort_as_half(static_cast<uint16_t>(s01))),
+                                 __half2float(__ushort_as_half(static_cast<uint16_t>(s01 >> 16))),
+                                 __half2float(__ushort_as_half(static_cast<uint16_t>(s23))),
+                                 __half2float(__ushort_as_half(static_cast<uint16_t>(s23 >> 16)))};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                acc[0][r][e] = fmaf(sv[e], d0[e], acc[0][r][e]);
+                acc[1][r][e] = fmaf(sv[e], d1[e], acc[1][r][e]);
+            }
+        }
+        // this group's weights and scales are consumed: their slot takes group gi + kWG
+        if (gi + kWG < kGPW) load_group(gi + kWG);
+    }
+    // no DMA into the strip is still in flight (a wave past its range issued some),
+    // and every read of it has returned: its partial sums go there,
+    // part[row][column], lane holding D[row 16 r + 4 q + e][column 16 s + r16]
+    asm volatile("s_waitcnt vmcnt(0)\n\ts_waitcnt lgkmcnt(0)" ::: "memory");
+    float* part = reinterpret_cast<float*>(sx);
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+        for (int r = 0; r < kR; ++r)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) part[(16 * r + 4 * q + e) * 32 + 16 * s2 + r16] = acc[s2][r][e];
+    __syncthreads();
+    auto wsum = [&](int row, int c) {
+        float sum = 0.0f;
+#pragma unroll
+        for (int v = 0; v < kWaves; ++v) sum += reinterpret_cast<const float*>(strips[v])[row * 32 + c];
+        return sum;
+    };
+    const int tt = rows >> 1;
+    for (int i = threadIdx.x; i < T * tt; i += kBlock) {
+        const int row = i / tt, t = i - row * tt;
+        const int64_t grow = tile * T + row;
+        if (grow >= n) continue;
+        const float v = wsum(row, t) + wsum(row, tt + t);
+        if (gridDim.y == 1)
+            y[t * n + grow] = v;
+        else
+            atomicAdd(&y[t * n + grow], v);
+    }
+}
+
 // Decode kernel for 1..kM tokens (kM * kR <= 16), T = 16 kR rows per tile.
 //
 // Lane l (i = l % 16, kg = l / 16) loads, per step, the 16 bytes of row
@@ -565,16 +713,16 @@ __device__ __forceinline__ void plain_epilogue(const WSum& wsum, int m, int T, i
     }
 }
 
-// kEpiGateUp for m <= 16 tokens of a 64-row gate/up tile (n = 2f stacked rows).
+// kEpiGateUp for m <= 16 tokens of a 64-row gate/up tile (n = 2f stacked rows),
+// run by the threads whose index in the tile's thread range is i (a range starts
+// at a multiple of 64 threads).
 template <class WSum>
-__device__ __forceinline__ void gate_up_epilogue(const WSum& wsum, int m, int64_t tile, int64_t n, uint16_t* hout,
-                                                 float* xsum, int tok0, int mtot, int rows_group, float* yz,
-                                                 int64_t yz_n) {
+__device__ __forceinline__ void gate_up_h(const WSum& wsum, int m, int64_t tile, int64_t n, uint16_t* hout,
+                                          float* xsum, int tok0, int mtot, int rows_group, int i) {
     const int64_t f = n >> 1;  // h columns: the stacked weight has 2f rows, f % 32 == 0
     const int lane = threadIdx.x & 63;
     // thread i < 32 m: token i / 32, column 32 tile + i % 32, so that the 32
     // columns of a token are one half of a wave (two whole DPP rows)
-    const int i = threadIdx.x;
     if (i < m * 32) {
         const int j = i >> 5, r = i & 31;
         const int64_t hc = tile * 32 + r;
@@ -600,10 +748,21 @@ __device__ __forceinline__ void gate_up_epilogue(const WSum& wsum, int m, int64_
             xsum[rl * (f >> 5) + tile] = tl;
         }
     }
-    // the output a K-split down projection accumulates into
+}
+
+// The output a K-split down projection accumulates into, zeroed by the grid.
+__device__ __forceinline__ void zero_grid(float* yz, int64_t yz_n) {
     for (int64_t q = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; q < yz_n;
          q += static_cast<int64_t>(gridDim.x) * kBlock)
         yz[q] = 0.0f;
+}
+
+template <class WSum>
+__device__ __forceinline__ void gate_up_epilogue(const WSum& wsum, int m, int64_t tile, int64_t n, uint16_t* hout,
+                                                 float* xsum, int tok0, int mtot, int rows_group, float* yz,
+                                                 int64_t yz_n) {
+    gate_up_h(wsum, m, tile, n, hout, xsum, tok0, mtot, rows_group, static_cast<int>(threadIdx.x));
+    zero_grid(yz, yz_n);
 }
 
 template <int kR, int kM, int kGPW, int kWinD, int kEpi>
@@ -827,9 +986,14 @@ __device__ __forceinline__ f32x16 mfma32_bf16(u32x4 a, u32x4 b, f32x16 c) {
 // otherwise.  A lane of the result holds D[8 (q / 4) + 4 kg + q % 4][l % 32],
 // q = 0..15: 16 rows (four runs of four) of row group c % kR for token c / kR.
 // x staging (slot order, DPP group sums), group scales, the refill window and
-// the epilogues are those of k_decode_diag; no K split.  Each wave's partial
-// sums go to its own x strips once its loop is done (no other wave reads them).
-template <int kR, int kM, int kGPW, int kWinD, int kEpi>
+// the epilogues are those of k_decode_diag; no K split.  A block takes kTPB
+// consecutive tiles with one staging of x: the weight window runs on from one
+// tile into the next, each tile keeps its own sums, and both go to the wave's x
+// strips once its loop is done (no other wave reads them), so the epilogue of
+// tile tt runs on threads [512 tt, 512 tt + 32 m).  With 448 tiles (F = 14336),
+// kTPB = 2 makes 224 blocks, one round on 256 CUs, where one tile per block ran
+// 1.75 rounds and staged every token's x once per tile.
+template <int kR, int kM, int kGPW, int kWinD, int kEpi, int kTPB = 1>
 __global__ __launch_bounds__(kBlock) void k_decode_diag32(const uint16_t* __restrict__ x, int m,
                                                           const uint8_t* __restrict__ pt,
                                                           const uint16_t* __restrict__ st,
@@ -839,22 +1003,26 @@ __global__ __launch_bounds__(kBlock) void k_decode_diag32(const uint16_t* __rest
                                                           int rows_group, float* __restrict__ yz, int64_t yz_n) {
     static_assert(kR == 2 && kEpi == kEpiGateUp, "gate/up tiles: 64 rows, two row groups of 32");
     static_assert(kM * kR <= 32, "columns are (token, row group) pairs");
+    static_assert(kTPB == 1 || kTPB == 2, "one or two tiles per block");
     constexpr int T = 32 * kR;
     constexpr int kS = 2 / kR;             // chunks per step
     constexpr int kSPG = 4 / kS;           // steps per group
     constexpr int kCPW = 4 * kGPW;         // chunks per wave
-    constexpr int kSteps = kCPW / kS;      // weight loads per lane
+    constexpr int kSteps = kCPW / kS;      // weight loads per lane and tile
+    constexpr int kStepsB = kSteps * kTPB;  // ... over the block's tiles
     constexpr int kStrip = kCPW * 64;      // bytes of one token's slice (bf16)
     constexpr int kStripP = kStrip + 16;   // padded, as in k_decode_diag
     constexpr int kItems = kM * kCPW * 8;  // 4-element items of the slices
     constexpr int kIPL = (kItems + kWave - 1) / kWave;
-    constexpr int kW = kWinD < kSteps ? kWinD : kSteps;
-    static_assert(T * 4 <= kStripP, "a wave's partial sums fit in its x strips");
+    constexpr int kW = kWinD < kStepsB ? kWinD : kStepsB;
+    static_assert(kTPB * T * 4 <= kStripP, "a wave's partial sums of its tiles fit in its x strips");
+    static_assert(kTPB * 512 <= kBlock && kM * 32 <= 512, "a tile's epilogue takes 32 m of its 512 threads");
     __shared__ __attribute__((aligned(16))) uint8_t xs[kWaves][kM][kStripP];
     __shared__ __attribute__((aligned(16))) uint8_t zs[kStrip];  // zeros, written by every wave
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int64_t tile = blockIdx.x;
+    const int64_t tiles = (n + T - 1) / T;
+    const int64_t tile0 = static_cast<int64_t>(blockIdx.x) * kTPB;
     const int64_t C = k >> 5, G = k >> 7;
     const int64_t g0 = static_cast<int64_t>(wave) * kGPW, c0 = 4 * g0;
     const int l32 = lane & 31, kg = lane >> 5;
@@ -873,19 +1041,28 @@ __global__ __launch_bounds__(kBlock) void k_decode_diag32(const uint16_t* __rest
         const int64_t kx = min<int64_t>(c0 * 32 + 4 * r, k - 4);
         xv[q] = j < m ? *reinterpret_cast<const uint2*>(x + j * k + kx) : make_uint2(0u, 0u);
     }
+    // the first tile's scales now; a second tile's are loaded when its loop starts
     uint2 sc[kGPW][4];
+    auto load_scales = [&](int64_t t) {
 #pragma unroll
-    for (int g = 0; g < kGPW; ++g)
+        for (int g = 0; g < kGPW; ++g)
 #pragma unroll
-        for (int r4 = 0; r4 < 4; ++r4)
-            sc[g][r4] = *reinterpret_cast<const uint2*>(st + (tile * G + min<int64_t>(g0 + g, G - 1)) * T + rbase +
-                                                        8 * r4);
-    const uint8_t* wb = pt + (tile * C * T + 32 * rg + l32) * 16;
+            for (int r4 = 0; r4 < 4; ++r4)
+                sc[g][r4] = *reinterpret_cast<const uint2*>(st + (t * G + min<int64_t>(g0 + g, G - 1)) * T + rbase +
+                                                            8 * r4);
+    };
+    load_scales(tile0);
+    // step i of the block: tile tile0 + i / kSteps (clamped to the last tile),
+    // chunk c0 + (i % kSteps) kS + cs
+    auto wload = [&](int i) {
+        const int64_t t = min<int64_t>(tile0 + i / kSteps, tiles - 1);
+        const uint8_t* wb = pt + (t * C * T + 32 * rg + l32) * 16;
+        return __builtin_nontemporal_load(
+            reinterpret_cast<const u32x4*>(wb + min<int64_t>(c0 + (i % kSteps) * kS + cs, 4 * G - 1) * T * 16));
+    };
     u32x4 w[kW];
 #pragma unroll
-    for (int i = 0; i < kW; ++i)
-        w[i] = __builtin_nontemporal_load(
-            reinterpret_cast<const u32x4*>(wb + min<int64_t>(c0 + i * kS + cs, 4 * G - 1) * T * 16));
+    for (int i = 0; i < kW; ++i) w[i] = wload(i);
 
     for (int b = lane * 16; b < kStrip; b += kWave * 16) *reinterpret_cast<u32x4*>(&zs[b]) = u32x4{0u, 0u, 0u, 0u};
     // stage: lanes 2b, 2b+1 hold an 8-block's (x0..x3) and (x4..x7); the even lane
@@ -923,60 +1100,71 @@ __global__ __launch_bounds__(kBlock) void k_decode_diag32(const uint16_t* __rest
     const bool diag = rgc == rg && tok < kM;
     const uint8_t* bsrc = diag ? &xs[wave][tok][cs * 64] : &zs[0];
 
-    f32x16 tot = f32x16{};
+    f32x16 tot[kTPB];
 #pragma unroll
-    for (int g = 0; g < kGPW; ++g) {
-        const bool live = g0 + g < G;
-        f32x16 a0 = f32x16{}, a1 = f32x16{};
+    for (int tt = 0; tt < kTPB; ++tt) {
+        if (tt > 0) load_scales(min<int64_t>(tile0 + tt, tiles - 1));
+        tot[tt] = f32x16{};
 #pragma unroll
-        for (int ss = 0; ss < kSPG; ++ss) {
-            const int i = kSPG * g + ss;  // step
-            const int slot = i % kW;
-            const uint32_t ws[4] = {w[slot].x, w[slot].y, w[slot].z, w[slot].w};
+        for (int g = 0; g < kGPW; ++g) {
+            const bool live = g0 + g < G;
+            f32x16 a0 = f32x16{}, a1 = f32x16{};
 #pragma unroll
-            for (int d = 0; d < 4; ++d) {
-                const u32x4 b = *reinterpret_cast<const u32x4*>(bsrc + (i * kS * 4 + d) * 16);
-                if (d & 1)
-                    a1 = mfma32_bf16(unpack_w4_136(ws[d]), b, a1);
-                else
-                    a0 = mfma32_bf16(unpack_w4_136(ws[d]), b, a0);
+            for (int ss = 0; ss < kSPG; ++ss) {
+                const int li = kSPG * g + ss;     // step of the tile
+                const int i = kSteps * tt + li;   // step of the block
+                const int slot = i % kW;
+                const uint32_t ws[4] = {w[slot].x, w[slot].y, w[slot].z, w[slot].w};
+#pragma unroll
+                for (int d = 0; d < 4; ++d) {
+                    const u32x4 b = *reinterpret_cast<const u32x4*>(bsrc + (li * kS * 4 + d) * 16);
+                    if (d & 1)
+                        a1 = mfma32_bf16(unpack_w4_136(ws[d]), b, a1);
+                    else
+                        a0 = mfma32_bf16(unpack_w4_136(ws[d]), b, a0);
+                }
+                if (i + kW < kStepsB) {
+                    w[slot] = wload(i + kW);
+                    __builtin_amdgcn_sched_barrier(0);  // the refill is issued here, not after the group
+                }
             }
-            if (i + kW < kSteps) {
-                w[slot] = __builtin_nontemporal_load(
-                    reinterpret_cast<const u32x4*>(wb + min<int64_t>(c0 + (i + kW) * kS + cs, 4 * G - 1) * T * 16));
-                __builtin_amdgcn_sched_barrier(0);  // the refill is issued here, not after the group
-            }
-        }
 #pragma unroll
-        for (int r4 = 0; r4 < 4; ++r4) {
-            const uint32_t s01 = live ? sc[g][r4].x : 0u, s23 = live ? sc[g][r4].y : 0u;
-            const float sv[4] = {__half2float(__ushort_as_half(static_cast<uint16_t>(s01))),
-                                 __half2float(__ushort_as_half(static_cast<uint16_t>(s01 >> 16))),
-                                 __half2float(__ushort_as_half(static_cast<uint16_t>(s23))),
-                                 __half2float(__ushort_as_half(static_cast<uint16_t>(s23 >> 16)))};
+            for (int r4 = 0; r4 < 4; ++r4) {
+                const uint32_t s01 = live ? sc[g][r4].x : 0u, s23 = live ? sc[g][r4].y : 0u;
+                const float sv[4] = {__half2float(__ushort_as_half(static_cast<uint16_t>(s01))),
+                                     __half2float(__ushort_as_half(static_cast<uint16_t>(s01 >> 16))),
+                                     __half2float(__ushort_as_half(static_cast<uint16_t>(s23))),
+                                     __half2float(__ushort_as_half(static_cast<uint16_t>(s23 >> 16)))};
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int q = 4 * r4 + e;
-                tot[q] = fmaf(sv[e], (a0[q] + a1[q]) - corr[g], tot[q]);
+                for (int e = 0; e < 4; ++e) {
+                    const int q = 4 * r4 + e;
+                    tot[tt][q] = fmaf(sv[e], (a0[q] + a1[q]) - corr[g], tot[tt][q]);
+                }
             }
         }
     }
-    // this wave's strips are dead: its partial sums, [token][tile row] f32, go there
+    // this wave's strips are dead: its partial sums, [tile][token][tile row] f32, go there
     float* part = reinterpret_cast<float*>(&xs[wave][0][0]);
     if (tok < kM) {
 #pragma unroll
-        for (int r4 = 0; r4 < 4; ++r4)
-            *reinterpret_cast<f32x4*>(&part[tok * T + rbase + 8 * r4]) =
-                f32x4{tot[4 * r4], tot[4 * r4 + 1], tot[4 * r4 + 2], tot[4 * r4 + 3]};
+        for (int tt = 0; tt < kTPB; ++tt)
+#pragma unroll
+            for (int r4 = 0; r4 < 4; ++r4)
+                *reinterpret_cast<f32x4*>(&part[(tt * kM + tok) * T + rbase + 8 * r4]) =
+                    f32x4{tot[tt][4 * r4], tot[tt][4 * r4 + 1], tot[tt][4 * r4 + 2], tot[tt][4 * r4 + 3]};
     }
     __syncthreads();
+    const int tt = kTPB == 1 ? 0 : static_cast<int>(threadIdx.x >> 9);  // wave-uniform
     auto wsum = [&](int j, int r) {
         float s = 0.0f;
 #pragma unroll
-        for (int v = 0; v < kWaves; ++v) s += reinterpret_cast<const float*>(&xs[v][0][0])[j * T + r];
+        for (int v = 0; v < kWaves; ++v) s += reinterpret_cast<const float*>(&xs[v][0][0])[(tt * kM + j) * T + r];
         return s;
     };
-    gate_up_epilogue(wsum, m, tile, n, hout, xsum, tok0, mtot, rows_group, yz, yz_n);
+    if (tile0 + tt < tiles)
+        gate_up_h(wsum, m, tile0 + tt, n, hout, xsum, tok0, mtot, rows_group,
+                  static_cast<int>(threadIdx.x) - 512 * tt);
+    zero_grid(yz, yz_n);
 }
 
 // kR in {1, 2, 4}; kM in {1, 2, 4} (3 tokens run as 4 with a zero token); groups per
@@ -1059,15 +1247,25 @@ int launch_diag32(int64_t gpw, int64_t tiles, hipStream_t s, const DiagArgs& a) 
         return fail(TQ_EINVAL, "tq_gemv_w4g128_tiled: %d tokens at %lld groups per wave", a.m, (long long)gpw);
     if (kEpi == kEpiGateUp && (!a.xsum || !aligned(a.xsum, 4)))
         return fail(TQ_EINVAL, "tq_mlp_w4g128_decode: no place for the block sums of h");
-    const unsigned grid = static_cast<unsigned>(tiles);
-#define TQ_DIAG32(G)                                                                                          \
-    k_decode_diag32<kR, kM, G, 3, kEpi><<<grid, kBlock, 0, s>>>(a.x, a.m, a.pt, a.st, a.b, a.n, a.k, a.y, a.hout, \
-                                                                a.xsum, a.tok0, a.mtot, a.rows_group, a.yz,     \
-                                                                a.yz_n)
-    if (gpw <= 1)
-        TQ_DIAG32(1);
-    else
-        TQ_DIAG32(2);
+    // two tiles per block where one per block would take more than one round (and
+    // their sums fit the strips: 2 groups per wave)
+    const bool two = gpw == 2 && tiles > device_cu_count();
+    const unsigned grid = static_cast<unsigned>(two ? (tiles + 1) / 2 : tiles);
+#define TQ_DIAG32(G, P)                                                                                        \
+    k_decode_diag32<kR, kM, G, 3, kEpi, P><<<grid, kBlock, 0, s>>>(a.x, a.m, a.pt, a.st, a.b, a.n, a.k, a.y,       \
+                                                                   a.hout, a.xsum, a.tok0, a.mtot, a.rows_group, \
+                                                                   a.yz, a.yz_n)
+    if (gpw <= 1) {
+        TQ_DIAG32(1, 1);
+    } else if (!two) {
+        TQ_DIAG32(2, 1);
+    } else if constexpr (kM == 16) {
+        TQ_DIAG32(2, 2);
+    } else {
+        // the 8-token form of two tiles spills (128 VGPRs); 5-8 tokens run on the
+        // 16-token one, whose extra B columns are zeros
+        return launch_diag32<kR, 16, kEpi>(gpw, tiles, s, a);
+    }
 #undef TQ_DIAG32
     return check_launch("tq_gemv_w4g128_tiled");
 }
@@ -1114,6 +1312,25 @@ int launch_mfma_fold(int64_t gpw, int64_t tiles, hipStream_t s, const uint16_t* 
         k_decode_tiled_mfma_sx<kR, 2, true><<<grid, kBlock, 0, s>>>(h, rows, pt, st, nullptr, n, k, y);
     else
         k_decode_tiled_mfma_sx<kR, 4, true><<<grid, kBlock, 0, s>>>(h, rows, pt, st, nullptr, n, k, y);
+    return check_launch("tq_mlp_w4g128_decode");
+}
+
+// The decode FFN's down projection for 9-16 tokens in one launch (2t <= 32 rows
+// of h, 32-row tiles, K split in two onto a zeroed y); gpw is the groups per
+// wave of one K half.
+int launch_fold32(int64_t gpw, int64_t tiles, hipStream_t s, const uint16_t* h, int rows, const uint8_t* pt,
+                  const uint16_t* st, int64_t n, int64_t k, float* y) {
+    if (gpw > 4 || rows > 32 || rows % 2 != 0)
+        return fail(TQ_EINVAL, "tq_mlp_w4g128_decode: %d rows of h at %lld groups per wave", rows, (long long)gpw);
+    const dim3 grid(static_cast<unsigned>(tiles), 2u);
+    if (gpw <= 1)
+        k_decode_fold32<1><<<grid, kBlock, 0, s>>>(h, rows, pt, st, n, k, y);
+    else if (gpw <= 2)
+        k_decode_fold32<2><<<grid, kBlock, 0, s>>>(h, rows, pt, st, n, k, y);
+    else if (gpw <= 3)
+        k_decode_fold32<3><<<grid, kBlock, 0, s>>>(h, rows, pt, st, n, k, y);
+    else
+        k_decode_fold32<4><<<grid, kBlock, 0, s>>>(h, rows, pt, st, n, k, y);
     return check_launch("tq_mlp_w4g128_decode");
 }
 
@@ -1373,7 +1590,10 @@ int mlp_decode(const char* fn, const uint16_t* x_bf16, int64_t m, int64_t d, int
     // their 2t <= 16 rows as the columns of the MFMA kernel (x read from L2, no
     // LDS strips to fit), K split in two as for quads.
     const bool octets = kr == 2 && mi >= 5;
-    const int group = octets ? 8 : (block ? 4 : 2);  // tokens per MlpRows group
+    // 9-16 tokens on 32-row down tiles: all 2m rows of h in one down launch
+    // (k_decode_fold32), the down weights read once
+    const bool one_down = octets && mi >= 9;
+    const int group = one_down ? 16 : (octets ? 8 : (block ? 4 : 2));  // tokens per MlpRows group
     const int64_t gu_tiles = (f + 31) / 32, gu_gpw = ((d >> 7) + kWaves - 1) / kWaves;
     // 5-16 tokens: one launch of the 32x32 kernel where its x strips fit the LDS
     const bool gu32 = diag32_fits(mi, gu_gpw);
@@ -1402,6 +1622,7 @@ int mlp_decode(const char* fn, const uint16_t* x_bf16, int64_t m, int64_t d, int
     }
     const int64_t dn_tiles = (d + down_tile_rows - 1) / down_tile_rows, dn_gpw = ((f >> 7) + kWaves - 1) / kWaves;
     const int64_t gpw2 = (((f >> 7) + 1) / 2 + kWaves - 1) / kWaves;  // of a K half
+    if (one_down) return launch_fold32(gpw2, dn_tiles, st, h, 2 * mi, down_t, down_s_t, d, f, y);
     if (octets) {
         for (int c = 0; 8 * c < mi; ++c) {
             const int t = mi - 8 * c < 8 ? mi - 8 * c : 8;

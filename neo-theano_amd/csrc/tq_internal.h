@@ -98,6 +98,16 @@ __device__ __forceinline__ void lds_dma16(const void* g, uint32_t la) {
 __device__ __forceinline__ void lds_dma4(const void* g, uint32_t la) {
     asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, off" ::"s"(la), "v"(g) : "memory", "m0");
 }
+// Waits until at most N vector memory operations of the wave are outstanding (the
+// completion of LDS DMAs, which the compiler does not track).  A count N > 0 is
+// only safe when every load it counts is issued by inline asm too: the compiler
+// moves its own loads of restrict read-only memory across inline asm, memory
+// clobber or not.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt counts 0..63");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
 #pragma clang diagnostic pop
 
 // Lane permutes within rows of 16 lanes through DPP, a VALU operand modifier

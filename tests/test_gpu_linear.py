@@ -434,14 +434,18 @@ def _mlp_case(tq, m, d, f, seed=57):
 # (including F = 128 where the second block has no groups); one to eight groups
 # per wave, F not a multiple of 64, the Llama shape.  At 5-16 tokens the down
 # launch stages h through LDS by runs of 1, 2 or 4 groups per wave (the last in
-# two phases, F = 13056 leaving a phase half live).
+# two phases, F = 13056 leaving a phase half live); at 9-16 tokens one launch
+# takes all 2m rows of h through per-group LDS strips (1, 2, 3 and 4 groups per
+# wave: F = 640, 6144, 8320, 14336).  Gate/up tiles past the CU count run two per
+# block (D = 2560-4096 with F = 8320-16384).
 @pytest.mark.parametrize("m,d,f", [(1, 128, 128), (2, 256, 384), (3, 512, 1024), (4, 1024, 640), (5, 256, 512),
                                    (7, 384, 1152), (8, 2048, 256), (1, 4096, 14336), (2, 14336, 4096),
                                    (6, 16384, 128), (3, 4096, 14336), (4, 4096, 14336), (4, 256, 128),
                                    (3, 640, 16384), (6, 4096, 14336), (8, 4096, 14336), (2, 4096, 14336),
                                    (9, 256, 512), (12, 4096, 14336), (16, 1024, 640), (16, 4096, 14336),
                                    (13, 128, 384), (7, 8192, 1024), (17, 4096, 14336), (28, 512, 1536),
-                                   (25, 256, 384), (9, 512, 6144), (5, 1024, 8192), (10, 1024, 13056)])
+                                   (25, 256, 384), (9, 512, 6144), (5, 1024, 8192), (10, 1024, 13056),
+                                   (7, 3072, 9216), (11, 2560, 8320), (16, 4096, 16384)])
 def test_mlp_decode_path(tq, oracle, m, d, f):
     wg = normal(60, (f, d), 0.02)
     wu = normal(60, (f, d), 0.02, stream=1)

@@ -90,6 +90,28 @@ def test_quantize_i8_rowwise_special_rows(tq, oracle):
     assert np.array_equal(rq[0].astype(np.int64), expect)
 
 
+# Codes only with 1025-4096 elements per row and at most 8 rows per CU runs a wave
+# per row: K a multiple of 16 but not of 256 (masked lanes) and K = 2048, 4096 (no
+# masks), with ties, NaN, inf, all-NaN and subnormal rows, up to 2048 rows.
+@pytest.mark.parametrize("rows,k", [(9, 1040), (9, 2064), (9, 4096), (2048, 1296), (1999, 2048)])
+def test_quantize_rowwise_codes_only_wave_rows(tq, oracle, rows, k):
+    base = [np.zeros(k, np.float32), tie_row(k), -tie_row(k)]
+    nanrow = weights(26, (k,), 1.0)
+    nanrow[::7] = np.nan
+    infrow = weights(27, (k,), 1.0)
+    infrow[k - 1] = -np.inf
+    allnan = np.full(k, np.nan, np.float32)
+    tiny = (weights(28, (k,), 1.0) * 1e-38).astype(np.float32)
+    special = np.stack(base + [nanrow, infrow, allnan, tiny])
+    w = np.concatenate([special, weights(29, (rows - len(special) if rows > len(special) else 2, k), 1.0)])
+    q, s = tq.quantize_per_channel_i8(dev_tensor(w))
+    rq, rs = oracle.quantize_i8_rowwise(w)
+    assert ieee_equal(host(s), rs) and np.array_equal(host(q), rq)
+    q8, s8 = tq.quantize_per_channel_fp8(dev_tensor(w))
+    rq8, rs8 = oracle.quantize_fp8_rowwise(w)
+    assert ieee_equal(host(s8), rs8) and np.array_equal(host(q8), rq8)
+
+
 def test_unaligned_and_offset_views(tq, oracle):
     import torch
 

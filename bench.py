@@ -185,6 +185,7 @@ def _peaks_lib():
     L.tqp_hbm_read_chunks.argtypes = [vp, i64, vp, i32, vp]
     L.tqp_hbm_read_waves.argtypes = [vp, i64, vp, i32, i32, vp]
     L.tqp_gemv_w4_skeleton.argtypes = [vp, vp, vp, i64, i64, vp, vp]
+    L.tqp_gemm_w8a8_phases.argtypes = [vp, vp, vp, vp, i32, i32, i32, vp, vp, vp]
     for fn in (L.tqp_mfma_i8, L.tqp_mfma_bf16, L.tqp_mfma_i8_random, L.tqp_mfma_bf16_random):
         fn.argtypes = [i32, i32, vp, vp]
     return L
@@ -466,6 +467,47 @@ def cpu_baselines(args, secondary, n3, k3, headline_bytes, log):
     return head
 
 
+def w8a8_phases(torch, np, ops, y, m, n, k, log, launches=5):
+    """Per-wave phases of single launches of the W8A8 GEMM kernel (the library's
+    kernel instantiated with real-time stamps in libtq_peaks.so): each timed
+    launch follows five untimed back-to-back launches and a synchronization, so
+    it runs warm but alone, unlike the back-to-back launches of the timed leg.
+    Microseconds from the first wave's start, percentiles (0, 50, 100) over the
+    1024 waves, medians over the launches.  The caller adds `mfma_floor_us`, the GEMM's MFMA time at the
+    measured random-operand i8 rate of one block per CU, when the peaks leg
+    ran."""
+    import ctypes
+
+    L = _peaks_lib()
+    st = lambda: ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    waves = (m // 128) * (n // 256) * 4
+    ts = torch.zeros(waves * 6, dtype=torch.int64, device=y.device)
+    runs = []
+    for r in range(launches):
+        for i in range(5):
+            qa, sa, qw, sw = ops[(r * 6 + i) % len(ops)]
+            L.tqp_gemm_w8a8_phases(qa.data_ptr(), sa.data_ptr(), qw.data_ptr(), sw.data_ptr(), m, n, k, y.data_ptr(),
+                                   ts.data_ptr(), st())
+        qa, sa, qw, sw = ops[(r * 6 + 5) % len(ops)]
+        torch.cuda.synchronize()
+        rc = L.tqp_gemm_w8a8_phases(qa.data_ptr(), sa.data_ptr(), qw.data_ptr(), sw.data_ptr(), m, n, k, y.data_ptr(),
+                                     ts.data_ptr(), st())
+        torch.cuda.synchronize()
+        if rc != 0:
+            raise RuntimeError(f"tqp_gemm_w8a8_phases: hipError {rc}")
+        a = ts.view(waves, 6).cpu().numpy().astype(np.int64)
+        rel = (a[:, :4] - a[:, 0].min()) * 0.01  # 100 MHz ticks -> us
+        runs.append({"span": rel[:, 3].max(), "start": rel[:, 0], "first_stage": rel[:, 1] - rel[:, 0],
+                     "k_loop": rel[:, 2] - rel[:, 1], "epilogue": rel[:, 3] - rel[:, 2]})
+    med = lambda v: round(float(np.median(v)), 2)
+    out = {"launches": launches, "span_us": med([r["span"] for r in runs])}
+    for key in ("start", "first_stage", "k_loop", "epilogue"):
+        out[key + "_us_p0_p50_p100"] = [med([np.percentile(r[key], p) for r in runs]) for p in (0, 50, 100)]
+    log(f"w8a8 one launch: span {out['span_us']} us; K loop {out['k_loop_us_p0_p50_p100']} us; "
+        f"epilogue {out['epilogue_us_p0_p50_p100']} us")
+    return out
+
+
 def rotation(bytes_per_copy):
     return max(2, math.ceil(2 * MALL_BYTES / bytes_per_copy) + 1)
 
@@ -725,6 +767,11 @@ def main():
             "act_quant_us": round(msq * 1e3, 3), "act_quant_GB/s": round(qbytes / (msq * 1e-3) / 1e9, 1),
             "act_quant_input_copies": len(xs)}
         log(f"w8a8 M=2048: {ms * 1e3:.2f} us  {tops:.0f} TOPS; act quant {msq * 1e3:.2f} us")
+        ph = w8a8_phases(torch, np, ops, y, m4, n4, k4, log)
+        if peaks:
+            ph["mfma_floor_us"] = round(2.0 * m4 * n4 * k4 / (peaks["i8_mfma_TOPS_random_operands_1_block_per_cu"]
+                                                          * 1e12) * 1e6, 2)
+        secondary["w8a8_gemm_m2048"]["phases_one_launch"] = ph
         del ops, xs, y, xd, qa0, qw0, qa1
 
     # ------------------------------------------------ FP8 W8A8 (C4 shape)

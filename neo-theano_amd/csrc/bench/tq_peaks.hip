@@ -21,9 +21,15 @@
 //    data does: they draw more power and the part holds a lower clock.
 //  * tqp_graph_time: captures a caller's launches into a hipGraph and times its
 //    replays with events on the capture stream.
+//  * tqp_gemm_w8a8_phases: one launch of the library's W8A8 GEMM kernel
+//    (tq_gemm_dma.h, the same source as libtq.so's) instantiated with per-wave
+//    real-time stamps: start, first stage landed, end of the K loop, end of the
+//    epilogue.
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+
+#include "../tq_gemm_dma.h"
 
 namespace {
 
@@ -370,6 +376,22 @@ int tqp_mfma_i8_random(int blocks, int iters, int32_t* out, hipStream_t stream) 
 
 int tqp_mfma_bf16_random(int blocks, int iters, float* out, hipStream_t stream) {
     k_mfma_bf16_random<<<blocks, 256, 0, stream>>>(iters, 1, out);
+    return static_cast<int>(hipGetLastError());
+}
+
+// One launch of k_gemm_w8a8_dma<true> at M x N x K (M % 128 == 0, N % 256 == 0,
+// K % 128 == 0; the library's dispatch runs this kernel at those shapes): qa [M,
+// K] and qw [N, K] int8 codes, sa [M] and sw [N] scales, y f32 [M, N]; ts
+// receives 6 words per wave, (M / 128) (N / 256) 4 waves: the real-time clock
+// (100 MHz) at the wave's start, once the first stage has landed, after the K
+// loop and after the epilogue's stores, then the wave's HW_ID register and 0.
+int tqp_gemm_w8a8_phases(const int8_t* qa, const float* sa, const int8_t* qw, const float* sw, int m, int n, int k,
+                         float* y, uint64_t* ts, hipStream_t stream) {
+    if (m <= 0 || n <= 0 || k <= 0 || m % 128 != 0 || n % 256 != 0 || k % 128 != 0 || !ts)
+        return static_cast<int>(hipErrorInvalidValue);
+    const int tm = m / 128, tn = n / 256;
+    tq::k_gemm_w8a8_dma<true><<<tm * tn, 256, 0, stream>>>(qa, sa, qw, sw, nullptr, m, n, k, nullptr, y, tm, tn,
+                                                           ts);
     return static_cast<int>(hipGetLastError());
 }
 

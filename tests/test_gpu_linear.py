@@ -485,6 +485,33 @@ def test_mlp_decode_down_tile_heights(tq, oracle, tile_rows, m, d, f):
     assert_close(host(y), oracle.mlp_w4g128(xb, *args), RTOL, ATOL, f"mlp decode {tile_rows}-row down, {m}x{d}x{f}")
 
 
+# The decode FFN takes x rows 8-byte aligned (the gate/up kernels load x in 8-byte
+# pieces): the same result as from a 16-byte aligned copy, at 5-16 tokens (one
+# and two gate/up tiles per block) and with the one-launch down projection.
+@pytest.mark.parametrize("m,d,f", [(6, 4096, 14336), (12, 4096, 14336), (16, 1024, 640), (9, 512, 6144)])
+def test_mlp_decode_x_8_byte_aligned(tq, oracle, m, d, f):
+    import torch
+    from theano_quantize import _abi
+    from theano_quantize._tensor import ptr, stream
+
+    print(f"decode FFN, x 8-byte aligned: M={m} D={d} F={f}", flush=True)
+    mlp, xb = _mlp_case(tq, m, d, f, seed=64)
+    gu_t, gu_st, dn_t, dn_st, t = mlp.decode
+    nb = int(_abi.lib().tq_mlp_w4g128_decode_workspace_bytes(m, d, f))
+    ws = torch.empty((nb,), dtype=torch.uint8, device="cuda")
+    buf = torch.zeros(m * d + 4, dtype=torch.bfloat16, device="cuda")
+    x = buf[4:].view(m, d)
+    x.copy_(bf16_dev(xb))
+    assert x.data_ptr() % 16 == 8
+    args = [a for w in (mlp.gate, mlp.up, mlp.down) for a in (host(w[0]), host(w[1]).view(np.uint16))]
+    ref = oracle.mlp_w4g128(xb, *args)
+    for xin in (x, bf16_dev(xb)):
+        y = torch.full((m, d), float("nan"), dtype=torch.float32, device="cuda")
+        _abi.call("tq_mlp_w4g128_decode", ptr(xin), m, d, f, ptr(gu_t), ptr(gu_st), ptr(dn_t), ptr(dn_st), t,
+                  ptr(ws), nb, ptr(y), stream())
+        assert_close(host(y), ref, RTOL, ATOL, f"mlp decode {m}x{d}x{f}, x at {xin.data_ptr() % 16} mod 16")
+
+
 def test_mlp_decode_and_prefill_agree_and_reuse_workspace(tq, oracle):
     """Both paths meet the tolerance on the same weights; one decode workspace
     serves calls of decreasing M; a short one is rejected."""

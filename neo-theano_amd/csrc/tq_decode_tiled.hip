@@ -503,24 +503,79 @@ __global__ __launch_bounds__(kBlock) void k_decode_tiled_mfma_sx(const uint16_t*
 // zeroed (two addends onto zero: the same sum in either order).  Operand layout
 // as in k_decode_tiled_mfma_sx: lane (r16, q) holds chunk 4 g + q of tile row
 // 16 r + r16 and reads its B operands, row 16 s + r16 of set s, from an LDS
-// strip.  Each wave runs its kGPW groups one at a time through one private strip
-// of 32 rows x 256 bytes, filled by global_load_lds_dwordx4 (no registers): row
-// t's 16-byte chunk c sits at chunk c ^ (t % 16), so the 16 rows one B read
-// touches fall in distinct banks.  The next group's DMAs go out once the current
-// group's B operands are read, and land under its MFMAs; weights and scales run
-// kWG groups ahead.  A group's DMAs are waited for with vmcnt(0): the compiler
-// moves its own loads of the (restrict, read-only) weights and scales across
-// inline asm, so no count of the loads issued after the DMAs can be relied on.
+// strip of 32 rows x 256 bytes filled by global_load_lds_dwordx4: row t's
+// 16-byte chunk c sits at chunk c ^ (t % 16), so the 16 rows one B read touches
+// fall in distinct banks.
+//
+// Blocks of 8 waves (256 VGPRs per lane): each wave owns two strips and runs its
+// kGPW groups with group g's rows in strip g % 2, so a group's DMAs go out two
+// groups ahead (once the group that used the strip has read its B operands), and
+// its weights and scales kFoldWin groups ahead.  Every load of the loop is inline
+// asm (the DMAs, and the weight and scale loads into registers), so the compiler
+// adds no waits there: it counts only its own loads, and a wait of its own for a
+// weight would also hold the wave until the DMAs issued after that weight had
+// landed.  Before group g the wave waits until g's DMAs, weights and scales have
+// landed, counting the loads issued after them (fold_after); the wait names the
+// group's weight and scale registers as operands, so no use of them can be
+// scheduled ahead of it.
+constexpr int kFoldWaves = 8;
+constexpr int kFoldWin = 2;  // groups of weights and scales in flight
+constexpr int kFoldLPG = 4;  // load instructions per group: 2 row groups x (scales, weights)
+
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// Loads issued after the later of group gi's DMAs (8 instructions) and its
+// weight and scale loads (kFoldLPG), up to the wait of group gi, in the
+// kernel's issue order: DMA(0), DMA(1), LG(0 .. win-1), then for each group g
+// before gi: DMA(g + 2), LG(g + win).
 template <int kGPW>
-__global__ __launch_bounds__(kBlock) void k_decode_fold32(const uint16_t* __restrict__ h, int rows,
-                                                          const uint8_t* __restrict__ pt,
-                                                          const uint16_t* __restrict__ st, int64_t n, int64_t k,
-                                                          float* __restrict__ y) {
+constexpr int fold_after(int gi) {
+    constexpr int win = kFoldWin < kGPW ? kFoldWin : kGPW;
+    int pos = 0, last = 0;
+    auto dma = [&](int g) {
+        if (g >= kGPW) return;
+        pos += 8;
+        if (g == gi && pos > last) last = pos;
+    };
+    auto lg = [&](int g) {
+        if (g >= kGPW) return;
+        pos += kFoldLPG;
+        if (g == gi && pos > last) last = pos;
+    };
+    dma(0);
+    dma(1);
+    for (int g = 0; g < win; ++g) lg(g);
+    for (int g = 0; g < gi; ++g) {
+        dma(g + 2);
+        lg(g + win);
+    }
+    return pos - last;
+}
+
+__device__ __forceinline__ void asm_load16(u32x4& d, const void* p) {
+    asm volatile("global_load_dwordx4 %0, %1, off nt" : "=v"(d) : "v"(p) : "memory");
+}
+__device__ __forceinline__ void asm_load8(u32x2& d, const void* p) {
+    asm volatile("global_load_dwordx2 %0, %1, off" : "=v"(d) : "v"(p) : "memory");
+}
+template <int N>
+__device__ __forceinline__ void fold_wait(u32x4& w0, u32x4& w1, u32x2& s0, u32x2& s1) {
+    static_assert(N >= 0 && N < 64, "vmcnt counts 0..63");
+    asm volatile("s_waitcnt vmcnt(%4)" : "+v"(w0), "+v"(w1), "+v"(s0), "+v"(s1) : "n"(N) : "memory");
+}
+
+template <int kGPW>
+__global__ __launch_bounds__(kFoldWaves * 64) void k_decode_fold32(const uint16_t* __restrict__ h, int rows,
+                                                                   const uint8_t* __restrict__ pt,
+                                                                   const uint16_t* __restrict__ st, int64_t n,
+                                                                   int64_t k, float* __restrict__ y) {
+    static_assert(kGPW >= 1 && kGPW <= 8, "1..8 groups per wave");
     constexpr int kR = 2, T = 32;
     constexpr int kStrip = 32 * 256;
-    constexpr int kWG = kGPW < 3 ? kGPW : 3;  // groups of weights and scales in flight
+    constexpr int kWin = kFoldWin < kGPW ? kFoldWin : kGPW;
     static_assert(T * 32 * 4 <= kStrip, "a wave's partial sums fit in its strip");
-    __shared__ __attribute__((aligned(1024))) int8_t strips[kWaves][kStrip];
+    static_assert(fold_after<kGPW>(0) < 64, "vmcnt counts 0..63");
+    __shared__ __attribute__((aligned(1024))) int8_t strips[kFoldWaves][2][kStrip];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int q = lane >> 4, r16 = lane & 15;
@@ -529,14 +584,14 @@ __global__ __launch_bounds__(kBlock) void k_decode_fold32(const uint16_t* __rest
     const int64_t gh = (G + gridDim.y - 1) / gridDim.y, gb = blockIdx.y * gh, ge = min(G, gb + gh);
     const int64_t g0 = gb + static_cast<int64_t>(wave) * kGPW;
     const int64_t gl = max<int64_t>(ge - 1, 0);
-    int8_t* sx = strips[wave];
 
-    // DMA i (0..7) of a group moves rows 4 i .. 4 i + 3: lane l -> row 4 i + l / 16,
-    // landing at LDS chunk l % 16, from global chunk (l % 16) ^ row % 16.  Rows past
-    // `rows` re-read the last row and groups past the range the last group (their
-    // columns and sums are never used).
+    // DMA i (0..7) of group gi moves rows 4 i .. 4 i + 3 into strip gi % 2: lane l
+    // -> row 4 i + l / 16, landing at LDS chunk l % 16, from global chunk
+    // (l % 16) ^ row % 16.  Rows past `rows` re-read the last row and groups past
+    // the range the last group (their columns and sums are never used).
     auto dma_group = [&](int gi) {
         const uint16_t* hb = h + min<int64_t>(g0 + gi, gl) * 128;
+        int8_t* sx = strips[wave][gi & 1];
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             const int t = 4 * i + (lane >> 4);
@@ -544,20 +599,20 @@ __global__ __launch_bounds__(kBlock) void k_decode_fold32(const uint16_t* __rest
         }
     };
     const uint8_t* wb = pt + (tile * C * T + r16) * 16;
-    uint2 sc[kWG][kR];
-    u32x4 w[kWG][kR];
-    auto load_group = [&](int gi) {  // into slot gi % kWG
+    u32x2 sc[kWin][kR];
+    u32x4 w[kWin][kR];
+    auto load_group = [&](int gi) {  // into slot gi % kWin
         const int64_t g = min<int64_t>(g0 + gi, gl);
 #pragma unroll
         for (int r = 0; r < kR; ++r) {
-            sc[gi % kWG][r] = *reinterpret_cast<const uint2*>(st + (tile * G + g) * T + 16 * r + 4 * q);
-            w[gi % kWG][r] =
-                __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wb + ((4 * g + q) * T + 16 * r) * 16));
+            asm_load8(sc[gi % kWin][r], st + (tile * G + g) * T + 16 * r + 4 * q);
+            asm_load16(w[gi % kWin][r], wb + ((4 * g + q) * T + 16 * r) * 16);
         }
     };
     dma_group(0);
+    if (kGPW > 1) dma_group(1);
 #pragma unroll
-    for (int gi = 0; gi < kWG; ++gi) load_group(gi);
+    for (int gi = 0; gi < kWin; ++gi) load_group(gi);
     const u32x4 aoff = u32x4{0xC308C308u, 0xC308C308u, 0xC308C308u, 0xC308C308u};  // bf16 -136
     f32x4 acc[2][kR];
 #pragma unroll
@@ -567,17 +622,33 @@ __global__ __launch_bounds__(kBlock) void k_decode_fold32(const uint16_t* __rest
 #pragma unroll
     for (int gi = 0; gi < kGPW; ++gi) {
         if (g0 + gi >= ge) break;  // wave-uniform
-        wait_vmcnt<0>();  // the group's DMAs have landed
+        const int sl = gi % kWin;
+        switch (gi) {
+#define TQ_FOLD_WAIT(G)                                                                        \
+    case G:                                                                                    \
+        if constexpr (G < kGPW) fold_wait<fold_after<kGPW>(G)>(w[sl][0], w[sl][1], sc[sl][0], sc[sl][1]); \
+        break;
+            TQ_FOLD_WAIT(0)
+            TQ_FOLD_WAIT(1)
+            TQ_FOLD_WAIT(2)
+            TQ_FOLD_WAIT(3)
+            TQ_FOLD_WAIT(4)
+            TQ_FOLD_WAIT(5)
+            TQ_FOLD_WAIT(6)
+            TQ_FOLD_WAIT(7)
+#undef TQ_FOLD_WAIT
+        }
+        const int8_t* sx = strips[wave][gi & 1];
         u32x4 xb[2][4];
 #pragma unroll
         for (int s2 = 0; s2 < 2; ++s2)
 #pragma unroll
             for (int j = 0; j < 4; ++j)
                 xb[s2][j] = *reinterpret_cast<const u32x4*>(sx + (16 * s2 + r16) * 256 + (((4 * q + j) ^ r16) << 4));
-        if (gi + 1 < kGPW) {
-            // every read of this group's strip has returned: the next group may land
+        if (gi + 2 < kGPW) {
+            // every read of this strip has returned: group gi + 2 may land in it
             asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-            dma_group(gi + 1);
+            dma_group(gi + 2);
         }
         f32x4 xs[2];
 #pragma unroll
@@ -588,7 +659,7 @@ __global__ __launch_bounds__(kBlock) void k_decode_fold32(const uint16_t* __rest
         }
 #pragma unroll
         for (int r = 0; r < kR; ++r) {
-            const u32x4 wv = w[gi % kWG][r];
+            const u32x4 wv = w[sl][r];
             const uint32_t ws[4] = {wv.x, wv.y, wv.z, wv.w};
             f32x4 d0 = xs[0], d1 = xs[1];
 #pragma unroll
@@ -597,7 +668,7 @@ __global__ __launch_bounds__(kBlock) void k_decode_fold32(const uint16_t* __rest
                 d0 = mfma16_bf16(a, xb[0][j], d0);
                 d1 = mfma16_bf16(a, xb[1][j], d1);
             }
-            const uint32_t s01 = sc[gi % kWG][r].x, s23 = sc[gi % kWG][r].y;
+            const uint32_t s01 = sc[sl][r].x, s23 = sc[sl][r].y;
             const float sv[4] = {__half2float(__ushort_as_half(static_cast<uint16_t>(s01))),
                                  __half2float(__ushort_as_half(static_cast<uint16_t>(s01 >> 16))),
                                  __half2float(__ushort_as_half(static_cast<uint16_t>(s23))),
@@ -608,14 +679,14 @@ __global__ __launch_bounds__(kBlock) void k_decode_fold32(const uint16_t* __rest
                 acc[1][r][e] = fmaf(sv[e], d1[e], acc[1][r][e]);
             }
         }
-        // this group's weights and scales are consumed: their slot takes group gi + kWG
-        if (gi + kWG < kGPW) load_group(gi + kWG);
+        // this group's weights and scales are consumed: their slot takes group gi + kWin
+        if (gi + kWin < kGPW) load_group(gi + kWin);
     }
-    // no DMA into the strip is still in flight (a wave past its range issued some),
-    // and every read of it has returned: its partial sums go there,
+    // no DMA into the strips is still in flight (a wave past its range issued some),
+    // and every read of them has returned: the partial sums go to strip 0,
     // part[row][column], lane holding D[row 16 r + 4 q + e][column 16 s + r16]
     asm volatile("s_waitcnt vmcnt(0)\n\ts_waitcnt lgkmcnt(0)" ::: "memory");
-    float* part = reinterpret_cast<float*>(sx);
+    float* part = reinterpret_cast<float*>(strips[wave][0]);
 #pragma unroll
     for (int s2 = 0; s2 < 2; ++s2)
 #pragma unroll
@@ -626,11 +697,11 @@ __global__ __launch_bounds__(kBlock) void k_decode_fold32(const uint16_t* __rest
     auto wsum = [&](int row, int c) {
         float sum = 0.0f;
 #pragma unroll
-        for (int v = 0; v < kWaves; ++v) sum += reinterpret_cast<const float*>(strips[v])[row * 32 + c];
+        for (int v = 0; v < kFoldWaves; ++v) sum += reinterpret_cast<const float*>(strips[v][0])[row * 32 + c];
         return sum;
     };
     const int tt = rows >> 1;
-    for (int i = threadIdx.x; i < T * tt; i += kBlock) {
+    for (int i = threadIdx.x; i < T * tt; i += kFoldWaves * 64) {
         const int row = i / tt, t = i - row * tt;
         const int64_t grow = tile * T + row;
         if (grow >= n) continue;
@@ -964,201 +1035,163 @@ __global__ __launch_bounds__(kBlock) void k_decode_diag(const uint16_t* __restri
     }
 }
 
-__device__ __forceinline__ f32x16 mfma32_bf16(u32x4 a, u32x4 b, f32x16 c) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
-                                                   0, 0, 0);
-}
-
-// The diagonal kernel on v_mfma_f32_32x32x16_bf16, for the FFN's gate/up at 5-16
-// tokens: T = 32 kR rows per tile (kR = 2: 32 gate rows, then 32 up rows); the
-// MFMA's two k-groups (lanes 0-31, 32-63) are kR row groups of 32 rows times
-// 2 / kR chunks, and its 32 columns hold the (token, row group) pairs c = j kR +
-// row group, so a 64-row tile takes 16 tokens in one pass (the 16x16x32 form
-// stops at 4 and would read the weights once per 4 tokens).  A 32x32x16 MFMA
-// keeps the pipe twice as long per weight byte as a 16x16x32 one, so the plain
-// GEMV at 5-16 tokens stays on k_decode_tiled_mfma (measured faster: 8.8 against
-// 9.9 us at 5 tokens, 14336 x 4096).
+// The FFN's gate/up at 5-16 tokens on v_mfma_f32_16x16x32_bf16: the MFMA's 16
+// columns are the 16 token slots (tokens past m are zero rows of x), so every
+// MFMA column carries a token.  A block of 16 waves takes kTPB consecutive
+// 64-row tiles (gate rows 0-31, up rows 32-63 of each) with one staging of x;
+// its waves split K into runs of kGPW groups.  Lane (r16, q) holds, per
+// (tile, group) step and row block rb, the 16 bytes of chunk 4 g + q of tile row
+// 16 rb + r16; dword d is the A operand of MFMA d of that row block (row r16,
+// k-group q).  Its B operand for MFMA d is token r16's 8-block 4 (4 g + q) + d of
+// the wave's x slice in slot order (the unpack's order), read from the wave's LDS
+// strip and shared by the 4 row blocks; the output lane holds D[tile row 16 rb +
+// 4 q + e][token r16].  The accumulators restart per step; the step's f16 row
+// scales and 136 * sum(x) of the group are applied as tot += s * (acc - 136 X_g).
 //
-// Lane l (kg = l / 32) loads, per step, the 16 bytes of tile row 32 (kg % kR) +
-// l % 32 at chunk kS step + kg / kR (kS = 2 / kR chunks per step) and feeds each
-// of their 4 dwords to one MFMA as A row l % 32 of k-group kg.  B lane (kg, c)
-// holds token c / kR's 8 values of that k-slice when c % kR == kg % kR, zeros
-// otherwise.  A lane of the result holds D[8 (q / 4) + 4 kg + q % 4][l % 32],
-// q = 0..15: 16 rows (four runs of four) of row group c % kR for token c / kR.
-// x staging (slot order, DPP group sums), group scales, the refill window and
-// the epilogues are those of k_decode_diag; no K split.  A block takes kTPB
-// consecutive tiles with one staging of x: the weight window runs on from one
-// tile into the next, each tile keeps its own sums, and both go to the wave's x
-// strips once its loop is done (no other wave reads them), so the epilogue of
-// tile tt runs on threads [512 tt, 512 tt + 32 m).  With 448 tiles (F = 14336),
-// kTPB = 2 makes 224 blocks, one round on 256 CUs, where one tile per block ran
-// 1.75 rounds and staged every token's x once per tile.
-template <int kR, int kM, int kGPW, int kWinD, int kEpi, int kTPB = 1>
-__global__ __launch_bounds__(kBlock) void k_decode_diag32(const uint16_t* __restrict__ x, int m,
-                                                          const uint8_t* __restrict__ pt,
-                                                          const uint16_t* __restrict__ st,
-                                                          const float* __restrict__ bias, int64_t n, int64_t k,
-                                                          float* __restrict__ y, uint16_t* __restrict__ hout,
-                                                          float* __restrict__ xsum, int tok0, int mtot,
-                                                          int rows_group, float* __restrict__ yz, int64_t yz_n) {
-    static_assert(kR == 2 && kEpi == kEpiGateUp, "gate/up tiles: 64 rows, two row groups of 32");
-    static_assert(kM * kR <= 32, "columns are (token, row group) pairs");
+// x staging: each lane loads 16-byte 8-blocks of its tokens' slices (tokens past
+// m read as zeros), puts each in slot order with four byte permutes and writes it
+// to the token's strip (padded by 16 bytes, so the 16 rows of one B read fall in
+// distinct banks); the block's group sums come from v_dot2 against (1, 1) and a
+// DPP row sum (a group is 16 consecutive 8-blocks, one 16-lane row) and reach the
+// lanes of their token through LDS.  Weights and scales run kGuWin steps ahead
+// of the arithmetic.  The waves' partial sums meet in LDS in a fixed order (over
+// the wave's dead strips), and the epilogue of tile tt runs on threads [512 tt,
+// 512 tt + 32 m).  With 448 tiles (F = 14336) two tiles per block make 224
+// blocks, one round on 256 CUs.
+constexpr int kGuWin = 2;  // (tile, group) steps of weights and scales in flight
+
+template <int kGPW, int kTPB>
+__global__ __launch_bounds__(kBlock) void k_decode_gu16(const uint16_t* __restrict__ x, int m,
+                                                        const uint8_t* __restrict__ pt,
+                                                        const uint16_t* __restrict__ st, int64_t n, int64_t k,
+                                                        uint16_t* __restrict__ hout, float* __restrict__ xsum,
+                                                        int tok0, int mtot, int rows_group, float* __restrict__ yz,
+                                                        int64_t yz_n) {
     static_assert(kTPB == 1 || kTPB == 2, "one or two tiles per block");
-    constexpr int T = 32 * kR;
-    constexpr int kS = 2 / kR;             // chunks per step
-    constexpr int kSPG = 4 / kS;           // steps per group
-    constexpr int kCPW = 4 * kGPW;         // chunks per wave
-    constexpr int kSteps = kCPW / kS;      // weight loads per lane and tile
-    constexpr int kStepsB = kSteps * kTPB;  // ... over the block's tiles
-    constexpr int kStrip = kCPW * 64;      // bytes of one token's slice (bf16)
-    constexpr int kStripP = kStrip + 16;   // padded, as in k_decode_diag
-    constexpr int kItems = kM * kCPW * 8;  // 4-element items of the slices
-    constexpr int kIPL = (kItems + kWave - 1) / kWave;
-    constexpr int kW = kWinD < kStepsB ? kWinD : kStepsB;
-    static_assert(kTPB * T * 4 <= kStripP, "a wave's partial sums of its tiles fit in its x strips");
+    constexpr int kM = 16, T = 64, kRB = T / 16;
+    constexpr int kCPW = 4 * kGPW;      // chunks per wave
+    constexpr int kStrip = kCPW * 64;   // bytes of one token's slice (bf16)
+    constexpr int kStripP = kStrip + 16;
+    constexpr int kBPT = 4 * kCPW;      // 8-blocks of a token's slice
+    constexpr int kItems = kM * kBPT;
+    static_assert(kItems % kWave == 0 && kBPT % 16 == 0, "whole loads; a group is one 16-lane row");
+    constexpr int kIPL = kItems / kWave;
+    constexpr int kSteps = kTPB * kGPW;  // (tile, group) steps of the block
+    constexpr int kWin = kGuWin < kSteps ? kGuWin : kSteps;
+    // a wave's region: its token strips (strip j at j kStripP), later its partial sums
+    constexpr int kRegion = kM * kStripP > kTPB * kM * T * 4 ? kM * kStripP : kTPB * kM * T * 4;
     static_assert(kTPB * 512 <= kBlock && kM * 32 <= 512, "a tile's epilogue takes 32 m of its 512 threads");
-    __shared__ __attribute__((aligned(16))) uint8_t xs[kWaves][kM][kStripP];
-    __shared__ __attribute__((aligned(16))) uint8_t zs[kStrip];  // zeros, written by every wave
+    __shared__ __attribute__((aligned(16))) uint8_t xs[kWaves][kRegion];
+    __shared__ float csum[kWaves][kM][kGPW];  // sums of the wave's groups, per token
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int r16 = lane & 15, q = lane >> 4;
     const int64_t tiles = (n + T - 1) / T;
     const int64_t tile0 = static_cast<int64_t>(blockIdx.x) * kTPB;
     const int64_t C = k >> 5, G = k >> 7;
     const int64_t g0 = static_cast<int64_t>(wave) * kGPW, c0 = 4 * g0;
-    const int l32 = lane & 31, kg = lane >> 5;
-    const int rg = kg % kR, cs = kg / kR;  // this lane's row group and chunk slot (loads)
-    const int tok = l32 / kR;              // token of this lane's output column
-    const int rgc = l32 % kR;              // row group of this lane's output column
-    const int rbase = 32 * rgc + 4 * kg;   // its output rows: rbase + 8 r4 + e, r4, e = 0..3
 
-    // x items: item it -> token it / (8 kCPW), elements 4 (it % (8 kCPW)) .. + 3 of
-    // the wave's slice (clamped past K; zero past m)
-    uint2 xv[kIPL];
+    // x items: item it -> token it / kBPT, elements 8 (it % kBPT) .. + 7 of the
+    // wave's slice (clamped past K; zero past m)
+    u32x4 xv[kIPL];
 #pragma unroll
-    for (int q = 0; q < kIPL; ++q) {
-        const int it = min(lane + kWave * q, kItems - 1);
-        const int j = it / (kCPW * 8), r = it - j * (kCPW * 8);
-        const int64_t kx = min<int64_t>(c0 * 32 + 4 * r, k - 4);
-        xv[q] = j < m ? *reinterpret_cast<const uint2*>(x + j * k + kx) : make_uint2(0u, 0u);
+    for (int i = 0; i < kIPL; ++i) {
+        const int it = lane + kWave * i;
+        const int j = it / kBPT, b = it - j * kBPT;
+        const int64_t kx = min<int64_t>(c0 * 32 + 8 * b, k - 8);
+        xv[i] = j < m ? *reinterpret_cast<const u32x4*>(x + j * k + kx) : u32x4{0u, 0u, 0u, 0u};
     }
-    // the first tile's scales now; a second tile's are loaded when its loop starts
-    uint2 sc[kGPW][4];
-    auto load_scales = [&](int64_t t) {
+    // step s: tile tile0 + s / kGPW (clamped to the last tile), group g0 + s % kGPW
+    // (clamped to the last group; past K the scale is zero below)
+    uint2 sc[kWin][kRB];
+    u32x4 w[kWin][kRB];
+    auto load_step = [&](int s) {  // into slot s % kWin
+        const int64_t t = min<int64_t>(tile0 + s / kGPW, tiles - 1), g = min<int64_t>(g0 + s % kGPW, G - 1);
 #pragma unroll
-        for (int g = 0; g < kGPW; ++g)
-#pragma unroll
-            for (int r4 = 0; r4 < 4; ++r4)
-                sc[g][r4] = *reinterpret_cast<const uint2*>(st + (t * G + min<int64_t>(g0 + g, G - 1)) * T + rbase +
-                                                            8 * r4);
+        for (int rb = 0; rb < kRB; ++rb) {
+            sc[s % kWin][rb] = *reinterpret_cast<const uint2*>(st + (t * G + g) * T + 16 * rb + 4 * q);
+            w[s % kWin][rb] = __builtin_nontemporal_load(
+                reinterpret_cast<const u32x4*>(pt + ((t * C + 4 * g + q) * T + 16 * rb + r16) * 16));
+        }
     };
-    load_scales(tile0);
-    // step i of the block: tile tile0 + i / kSteps (clamped to the last tile),
-    // chunk c0 + (i % kSteps) kS + cs
-    auto wload = [&](int i) {
-        const int64_t t = min<int64_t>(tile0 + i / kSteps, tiles - 1);
-        const uint8_t* wb = pt + (t * C * T + 32 * rg + l32) * 16;
-        return __builtin_nontemporal_load(
-            reinterpret_cast<const u32x4*>(wb + min<int64_t>(c0 + (i % kSteps) * kS + cs, 4 * G - 1) * T * 16));
-    };
-    u32x4 w[kW];
 #pragma unroll
-    for (int i = 0; i < kW; ++i) w[i] = wload(i);
+    for (int s = 0; s < kWin; ++s) load_step(s);
 
-    for (int b = lane * 16; b < kStrip; b += kWave * 16) *reinterpret_cast<u32x4*>(&zs[b]) = u32x4{0u, 0u, 0u, 0u};
-    // stage: lanes 2b, 2b+1 hold an 8-block's (x0..x3) and (x4..x7); the even lane
-    // writes slots (x0,x4)(x1,x5), the odd lane (x2,x6)(x3,x7)
-    float gsum[kIPL];
+    // stage: a lane's 8-block (x0..x7) goes to its strip as (x0,x4)(x1,x5)(x2,x6)(x3,x7)
+    const uint32_t ones = 0x3F803F80u;  // bf16 (1, 1)
 #pragma unroll
-    for (int q = 0; q < kIPL; ++q) {
-        const int it = lane + kWave * q;
-        const int itc = min(it, kItems - 1);
-        const int j = itc / (kCPW * 8), r = itc - j * (kCPW * 8);
-        const uint2 v = xv[q];
-        const uint2 p = make_uint2(dpp_u32<kDppXor1>(v.x), dpp_u32<kDppXor1>(v.y));
-        const bool odd = r & 1;
-        const uint32_t hi = odd ? v.y : p.x, lo = odd ? p.y : v.x;
-        if (it < kItems)
-            *reinterpret_cast<uint2*>(&xs[wave][j][(r >> 1) * 16 + (odd ? 8 : 0)]) =
-                make_uint2(__builtin_amdgcn_perm(hi, lo, 0x05040100u), __builtin_amdgcn_perm(hi, lo, 0x07060302u));
-        // a group is 32 consecutive items (half the wave): the sums of its two rows
-        gsum[q] = lane_group_sum<16>(bf16_lo(v.x) + bf16_hi(v.x) + bf16_lo(v.y) + bf16_hi(v.y));
+    for (int i = 0; i < kIPL; ++i) {
+        const int it = lane + kWave * i;
+        const int j = it / kBPT, b = it - j * kBPT;
+        const u32x4 v = xv[i];
+        *reinterpret_cast<u32x4*>(&xs[wave][j * kStripP + b * 16]) =
+            u32x4{__builtin_amdgcn_perm(v.z, v.x, 0x05040100u), __builtin_amdgcn_perm(v.z, v.x, 0x07060302u),
+                  __builtin_amdgcn_perm(v.w, v.y, 0x05040100u), __builtin_amdgcn_perm(v.w, v.y, 0x07060302u)};
+        float s = dot2_bf16(v.x, ones, 0.0f);
+        s = dot2_bf16(v.y, ones, s);
+        s = dot2_bf16(v.z, ones, s);
+        s = dot2_bf16(v.w, ones, s);
+        s = lane_group_sum<16>(s);
+        if (r16 == 0) csum[wave][j][b >> 4] = s;
     }
+    // the strips and sums are private to the wave: its LDS accesses complete in order
     float corr[kGPW];
 #pragma unroll
-    for (int g = 0; g < kGPW; ++g) {
-        float c = 0.0f;
-#pragma unroll
-        for (int j = 0; j < kM; ++j) {
-            const int it = j * kCPW * 8 + 32 * g;  // first item of (token j, group g)
-            const int src = __float_as_int(gsum[it / kWave]);
-            const float v = __int_as_float(__builtin_amdgcn_readlane(src, it % kWave)) +
-                            __int_as_float(__builtin_amdgcn_readlane(src, it % kWave + 16));
-            c = tok == j ? v : c;
-        }
-        corr[g] = 136.0f * c;
-    }
-    const bool diag = rgc == rg && tok < kM;
-    const uint8_t* bsrc = diag ? &xs[wave][tok][cs * 64] : &zs[0];
+    for (int g = 0; g < kGPW; ++g) corr[g] = 136.0f * csum[wave][r16][g];
+    const uint8_t* bsrc = &xs[wave][r16 * kStripP];
 
-    f32x16 tot[kTPB];
+    f32x4 tot[kTPB][kRB];
 #pragma unroll
-    for (int tt = 0; tt < kTPB; ++tt) {
-        if (tt > 0) load_scales(min<int64_t>(tile0 + tt, tiles - 1));
-        tot[tt] = f32x16{};
+    for (int tt = 0; tt < kTPB; ++tt)
 #pragma unroll
-        for (int g = 0; g < kGPW; ++g) {
-            const bool live = g0 + g < G;
-            f32x16 a0 = f32x16{}, a1 = f32x16{};
+        for (int rb = 0; rb < kRB; ++rb) tot[tt][rb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int ss = 0; ss < kSPG; ++ss) {
-                const int li = kSPG * g + ss;     // step of the tile
-                const int i = kSteps * tt + li;   // step of the block
-                const int slot = i % kW;
-                const uint32_t ws[4] = {w[slot].x, w[slot].y, w[slot].z, w[slot].w};
+    for (int s = 0; s < kSteps; ++s) {
+        const int tt = s / kGPW, g = s % kGPW;
+        const bool live = g0 + g < G;
+        u32x4 bx[4];
 #pragma unroll
-                for (int d = 0; d < 4; ++d) {
-                    const u32x4 b = *reinterpret_cast<const u32x4*>(bsrc + (li * kS * 4 + d) * 16);
-                    if (d & 1)
-                        a1 = mfma32_bf16(unpack_w4_136(ws[d]), b, a1);
-                    else
-                        a0 = mfma32_bf16(unpack_w4_136(ws[d]), b, a0);
-                }
-                if (i + kW < kStepsB) {
-                    w[slot] = wload(i + kW);
-                    __builtin_amdgcn_sched_barrier(0);  // the refill is issued here, not after the group
-                }
+        for (int d = 0; d < 4; ++d) bx[d] = *reinterpret_cast<const u32x4*>(bsrc + (16 * g + 4 * q + d) * 16);
+        f32x4 acc[kRB];
+#pragma unroll
+        for (int rb = 0; rb < kRB; ++rb) acc[rb] = f32x4{0.f, 0.f, 0.f, 0.f};
+        const int slot = s % kWin;
+#pragma unroll
+        for (int d = 0; d < 4; ++d)
+#pragma unroll
+            for (int rb = 0; rb < kRB; ++rb) {
+                const u32x4 wv = w[slot][rb];
+                const uint32_t wd = d == 0 ? wv.x : (d == 1 ? wv.y : (d == 2 ? wv.z : wv.w));
+                acc[rb] = mfma16_bf16(unpack_w4_136(wd), bx[d], acc[rb]);
             }
 #pragma unroll
-            for (int r4 = 0; r4 < 4; ++r4) {
-                const uint32_t s01 = live ? sc[g][r4].x : 0u, s23 = live ? sc[g][r4].y : 0u;
-                const float sv[4] = {__half2float(__ushort_as_half(static_cast<uint16_t>(s01))),
-                                     __half2float(__ushort_as_half(static_cast<uint16_t>(s01 >> 16))),
-                                     __half2float(__ushort_as_half(static_cast<uint16_t>(s23))),
-                                     __half2float(__ushort_as_half(static_cast<uint16_t>(s23 >> 16)))};
+        for (int rb = 0; rb < kRB; ++rb) {
+            const uint32_t s01 = live ? sc[slot][rb].x : 0u, s23 = live ? sc[slot][rb].y : 0u;
+            const float sv[4] = {__half2float(__ushort_as_half(static_cast<uint16_t>(s01))),
+                                 __half2float(__ushort_as_half(static_cast<uint16_t>(s01 >> 16))),
+                                 __half2float(__ushort_as_half(static_cast<uint16_t>(s23))),
+                                 __half2float(__ushort_as_half(static_cast<uint16_t>(s23 >> 16)))};
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const int q = 4 * r4 + e;
-                    tot[tt][q] = fmaf(sv[e], (a0[q] + a1[q]) - corr[g], tot[tt][q]);
-                }
-            }
+            for (int e = 0; e < 4; ++e) tot[tt][rb][e] = fmaf(sv[e], acc[rb][e] - corr[g], tot[tt][rb][e]);
+        }
+        if (s + kWin < kSteps) {
+            load_step(s + kWin);
+            __builtin_amdgcn_sched_barrier(0);  // the refill is issued here, not at its use
         }
     }
     // this wave's strips are dead: its partial sums, [tile][token][tile row] f32, go there
-    float* part = reinterpret_cast<float*>(&xs[wave][0][0]);
-    if (tok < kM) {
+    float* part = reinterpret_cast<float*>(&xs[wave][0]);
 #pragma unroll
-        for (int tt = 0; tt < kTPB; ++tt)
+    for (int tt = 0; tt < kTPB; ++tt)
 #pragma unroll
-            for (int r4 = 0; r4 < 4; ++r4)
-                *reinterpret_cast<f32x4*>(&part[(tt * kM + tok) * T + rbase + 8 * r4]) =
-                    f32x4{tot[tt][4 * r4], tot[tt][4 * r4 + 1], tot[tt][4 * r4 + 2], tot[tt][4 * r4 + 3]};
-    }
+        for (int rb = 0; rb < kRB; ++rb)
+            *reinterpret_cast<f32x4*>(&part[(tt * kM + r16) * T + 16 * rb + 4 * q]) = tot[tt][rb];
     __syncthreads();
     const int tt = kTPB == 1 ? 0 : static_cast<int>(threadIdx.x >> 9);  // wave-uniform
     auto wsum = [&](int j, int r) {
         float s = 0.0f;
 #pragma unroll
-        for (int v = 0; v < kWaves; ++v) s += reinterpret_cast<const float*>(&xs[v][0][0])[(tt * kM + j) * T + r];
+        for (int v = 0; v < kWaves; ++v) s += reinterpret_cast<const float*>(&xs[v][0])[(tt * kM + j) * T + r];
         return s;
     };
     if (tile0 + tt < tiles)
@@ -1236,44 +1269,34 @@ int launch_diag_m(int64_t gpw, int64_t tiles, hipStream_t s, const DiagArgs& a) 
     return launch_diag<kR, 4, kEpi>(gpw, tiles, s, a);
 }
 
-// The 32x32 gate/up kernel for 5-16 tokens (rounded up to 8 or 16), at most 2
-// groups per wave (D <= 4096 over 16 waves; with more, x, its sums and the
-// scales held per lane would spill).
-constexpr bool diag32_fits(int64_t m, int64_t gpw) { return m >= 5 && m <= 16 && gpw <= 2; }
+// The 16x16x32 gate/up kernel for 5-16 tokens, at most 2 groups per wave (D <=
+// 4096 over 16 waves; with more, the 16 tokens' x strips outgrow the LDS).
+constexpr bool gu16_fits(int64_t m, int64_t gpw) { return m >= 5 && m <= 16 && gpw <= 2; }
 
-template <int kR, int kM, int kEpi>
-int launch_diag32(int64_t gpw, int64_t tiles, hipStream_t s, const DiagArgs& a) {
-    if (a.ksplit != 1 || !diag32_fits(a.m, gpw))
-        return fail(TQ_EINVAL, "tq_gemv_w4g128_tiled: %d tokens at %lld groups per wave", a.m, (long long)gpw);
-    if (kEpi == kEpiGateUp && (!a.xsum || !aligned(a.xsum, 4)))
+int launch_gu16(int64_t gpw, int64_t tiles, hipStream_t s, const DiagArgs& a) {
+    if (a.ksplit != 1 || !gu16_fits(a.m, gpw))
+        return fail(TQ_EINVAL, "tq_mlp_w4g128_decode: %d tokens at %lld groups per wave", a.m, (long long)gpw);
+    if (!a.xsum || !aligned(a.xsum, 4))
         return fail(TQ_EINVAL, "tq_mlp_w4g128_decode: no place for the block sums of h");
-    // two tiles per block where one per block would take more than one round (and
-    // their sums fit the strips: 2 groups per wave)
-    const bool two = gpw == 2 && tiles > device_cu_count();
+    // two tiles per block where one per block would take more than one round
+    const bool two = tiles > device_cu_count();
     const unsigned grid = static_cast<unsigned>(two ? (tiles + 1) / 2 : tiles);
-#define TQ_DIAG32(G, P)                                                                                        \
-    k_decode_diag32<kR, kM, G, 3, kEpi, P><<<grid, kBlock, 0, s>>>(a.x, a.m, a.pt, a.st, a.b, a.n, a.k, a.y,       \
-                                                                   a.hout, a.xsum, a.tok0, a.mtot, a.rows_group, \
-                                                                   a.yz, a.yz_n)
+#define TQ_GU16(G, P)                                                                                             \
+    k_decode_gu16<G, P><<<grid, kBlock, 0, s>>>(a.x, a.m, a.pt, a.st, a.n, a.k, a.hout, a.xsum, a.tok0, a.mtot, \
+                                                a.rows_group, a.yz, a.yz_n)
     if (gpw <= 1) {
-        TQ_DIAG32(1, 1);
-    } else if (!two) {
-        TQ_DIAG32(2, 1);
-    } else if constexpr (kM == 16) {
-        TQ_DIAG32(2, 2);
+        if (two)
+            TQ_GU16(1, 2);
+        else
+            TQ_GU16(1, 1);
     } else {
-        // the 8-token form of two tiles spills (128 VGPRs); 5-8 tokens run on the
-        // 16-token one, whose extra B columns are zeros
-        return launch_diag32<kR, 16, kEpi>(gpw, tiles, s, a);
+        if (two)
+            TQ_GU16(2, 2);
+        else
+            TQ_GU16(2, 1);
     }
-#undef TQ_DIAG32
-    return check_launch("tq_gemv_w4g128_tiled");
-}
-
-template <int kR, int kEpi>
-int launch_diag32_m(int64_t gpw, int64_t tiles, hipStream_t s, const DiagArgs& a) {
-    if (a.m <= 8) return launch_diag32<kR, 8, kEpi>(gpw, tiles, s, a);
-    return launch_diag32<kR, 16, kEpi>(gpw, tiles, s, a);
+#undef TQ_GU16
+    return check_launch("tq_mlp_w4g128_decode");
 }
 
 template <int kEpi>
@@ -1317,20 +1340,25 @@ int launch_mfma_fold(int64_t gpw, int64_t tiles, hipStream_t s, const uint16_t* 
 
 // The decode FFN's down projection for 9-16 tokens in one launch (2t <= 32 rows
 // of h, 32-row tiles, K split in two onto a zeroed y); gpw is the groups per
-// wave of one K half.
+// wave of one K half over the kernel's 8 waves.
 int launch_fold32(int64_t gpw, int64_t tiles, hipStream_t s, const uint16_t* h, int rows, const uint8_t* pt,
                   const uint16_t* st, int64_t n, int64_t k, float* y) {
-    if (gpw > 4 || rows > 32 || rows % 2 != 0)
+    if (gpw < 1 || gpw > 8 || rows > 32 || rows % 2 != 0)
         return fail(TQ_EINVAL, "tq_mlp_w4g128_decode: %d rows of h at %lld groups per wave", rows, (long long)gpw);
     const dim3 grid(static_cast<unsigned>(tiles), 2u);
-    if (gpw <= 1)
-        k_decode_fold32<1><<<grid, kBlock, 0, s>>>(h, rows, pt, st, n, k, y);
-    else if (gpw <= 2)
-        k_decode_fold32<2><<<grid, kBlock, 0, s>>>(h, rows, pt, st, n, k, y);
-    else if (gpw <= 3)
-        k_decode_fold32<3><<<grid, kBlock, 0, s>>>(h, rows, pt, st, n, k, y);
-    else
-        k_decode_fold32<4><<<grid, kBlock, 0, s>>>(h, rows, pt, st, n, k, y);
+    constexpr unsigned kThreads = kFoldWaves * 64;
+#define TQ_FOLD(G) k_decode_fold32<G><<<grid, kThreads, 0, s>>>(h, rows, pt, st, n, k, y)
+    switch (gpw) {
+        case 1: TQ_FOLD(1); break;
+        case 2: TQ_FOLD(2); break;
+        case 3: TQ_FOLD(3); break;
+        case 4: TQ_FOLD(4); break;
+        case 5: TQ_FOLD(5); break;
+        case 6: TQ_FOLD(6); break;
+        case 7: TQ_FOLD(7); break;
+        default: TQ_FOLD(8); break;
+    }
+#undef TQ_FOLD
     return check_launch("tq_mlp_w4g128_decode");
 }
 
@@ -1595,9 +1623,9 @@ int mlp_decode(const char* fn, const uint16_t* x_bf16, int64_t m, int64_t d, int
     const bool one_down = octets && mi >= 9;
     const int group = one_down ? 16 : (octets ? 8 : (block ? 4 : 2));  // tokens per MlpRows group
     const int64_t gu_tiles = (f + 31) / 32, gu_gpw = ((d >> 7) + kWaves - 1) / kWaves;
-    // 5-16 tokens: one launch of the 32x32 kernel where its x strips fit the LDS
-    const bool gu32 = diag32_fits(mi, gu_gpw);
-    if (gu32) {
+    // 5-16 tokens: one launch of the 16x16x32 kernel where its x strips fit the LDS
+    const bool gu16 = gu16_fits(mi, gu_gpw);
+    if (gu16) {
         DiagArgs a{x_bf16, mi, gate_up_t, gate_up_s_t, nullptr, 2 * f, d, nullptr, h, 0, mi};
         a.rows_group = group;
         a.xsum = hsum;
@@ -1605,10 +1633,10 @@ int mlp_decode(const char* fn, const uint16_t* x_bf16, int64_t m, int64_t d, int
             a.yz = y;
             a.yz_n = m * d;
         }
-        const int rc = launch_diag32_m<2, kEpiGateUp>(gu_gpw, gu_tiles, st, a);
+        const int rc = launch_gu16(gu_gpw, gu_tiles, st, a);
         if (rc != TQ_OK) return rc;
     }
-    for (int j0 = 0; j0 < mi && !gu32; j0 += 4) {
+    for (int j0 = 0; j0 < mi && !gu16; j0 += 4) {
         const int mm = mi - j0 < 4 ? mi - j0 : 4;
         DiagArgs a{x_bf16 + j0 * d, mm, gate_up_t, gate_up_s_t, nullptr, 2 * f, d, nullptr, h, j0, mi};
         a.rows_group = group;
@@ -1622,7 +1650,10 @@ int mlp_decode(const char* fn, const uint16_t* x_bf16, int64_t m, int64_t d, int
     }
     const int64_t dn_tiles = (d + down_tile_rows - 1) / down_tile_rows, dn_gpw = ((f >> 7) + kWaves - 1) / kWaves;
     const int64_t gpw2 = (((f >> 7) + 1) / 2 + kWaves - 1) / kWaves;  // of a K half
-    if (one_down) return launch_fold32(gpw2, dn_tiles, st, h, 2 * mi, down_t, down_s_t, d, f, y);
+    if (one_down) {
+        const int64_t gpw8 = (((f >> 7) + 1) / 2 + kFoldWaves - 1) / kFoldWaves;  // of a K half, 8 waves
+        return launch_fold32(gpw8, dn_tiles, st, h, 2 * mi, down_t, down_s_t, d, f, y);
+    }
     if (octets) {
         for (int c = 0; 8 * c < mi; ++c) {
             const int t = mi - 8 * c < 8 ? mi - 8 * c : 8;

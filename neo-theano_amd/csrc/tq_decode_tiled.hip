@@ -41,8 +41,7 @@
 //    staging, no barrier before the arithmetic) and consumes its loads in
 //    order; the runs meet in LDS (details at the kernel).
 //    k_decode_tiled_mfma_sx is the same with each wave's x fetched as whole
-//    token rows into a private LDS strip (runs of up to 2 groups, and the decode
-//    FFN's down projection in two phases of 2 groups).
+//    token rows into a private LDS strip (runs of up to 2 groups).
 #include <mutex>
 
 #include "tq_internal.h"
@@ -347,25 +346,15 @@ __global__ __launch_bounds__(kBlock) void k_decode_tiled_mfma(const uint16_t* __
 // i * 4 / kGP + l / (16 kGP), elements 8 (l % (16 kGP)) .. + 7 of the phase's
 // slice), writes them to a private LDS strip in the slot order of the weight
 // unpack (token rows padded by 16 bytes, so the 16 tokens' B reads of one MFMA
-// hit distinct banks) and reads the B operands back from it.  Runs of 4 groups
-// (the FFN's down projection, K = F split in two) go in two phases through a
-// strip of two groups: the x of both phases is loaded up front and the second
-// phase overwrites the strip after the first has read it (the strip is private
-// to the wave, whose LDS accesses complete in order).  The wave's partial sums
-// go into its own strip once its loop is done.
-// kFold: the decode FFN's down projection on h as kEpiGateUp wrote it (each
-// 8-block in the slot order of unpack_w4_136, which then unpacks the weights as
-// 136 + q, with -136 as the constant operand and no factor), m = 2t rows of t
-// tokens (hi rows, then lo rows) whose two halves are added per token, and K
-// split over gridDim.y blocks per tile added into a zeroed y (two addends onto
-// zero: the same sum in either order).
-template <int kR, int kGPW, bool kFold = false>
+// hit distinct banks) and reads the B operands back from it.  The wave's
+// partial sums go into its own strip once its loop is done.
+template <int kR, int kGPW>
 __global__ __launch_bounds__(kBlock) void k_decode_tiled_mfma_sx(const uint16_t* __restrict__ x, int m,
                                                                  const uint8_t* __restrict__ pt,
                                                                  const uint16_t* __restrict__ st,
                                                                  const float* __restrict__ bias, int64_t n,
                                                                  int64_t k, float* __restrict__ y) {
-    static_assert(kGPW == 1 || kGPW == 2 || kGPW == 4, "runs of 1, 2 or 4 groups per wave");
+    static_assert(kGPW == 1 || kGPW == 2, "runs of 1 or 2 groups per wave");
     constexpr int kGP = kGPW < 2 ? kGPW : 2;  // groups per phase
     constexpr int kP = kGPW / kGP;             // phases
     constexpr int T = 16 * kR;
@@ -419,9 +408,8 @@ __global__ __launch_bounds__(kBlock) void k_decode_tiled_mfma_sx(const uint16_t*
     }
     uint8_t* sx = strips[wave];
 
-    // bf16 -136 (kFold) or -192: minus the offset of the unpacked weights
-    const u32x4 aoff = kFold ? u32x4{0xC308C308u, 0xC308C308u, 0xC308C308u, 0xC308C308u}
-                             : u32x4{0xC340C340u, 0xC340C340u, 0xC340C340u, 0xC340C340u};
+    // bf16 -192: minus the offset of the unpacked weights
+    const u32x4 aoff = u32x4{0xC340C340u, 0xC340C340u, 0xC340C340u, 0xC340C340u};
     f32x4 acc[kR];
 #pragma unroll
     for (int r = 0; r < kR; ++r) acc[r] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -431,7 +419,7 @@ __global__ __launch_bounds__(kBlock) void k_decode_tiled_mfma_sx(const uint16_t*
 #pragma unroll
         for (int i = 0; i < kNI; ++i) {
             const int t = i * kTPI + lane / kLPT;
-            *reinterpret_cast<u32x4*>(sx + t * kRow + 2 * e0) = kFold ? xl[p][i] : pair_slots(xl[p][i]);
+            *reinterpret_cast<u32x4*>(sx + t * kRow + 2 * e0) = pair_slots(xl[p][i]);
         }
 #pragma unroll
         for (int ii = 0; ii < kGP; ++ii) {
@@ -450,7 +438,7 @@ __global__ __launch_bounds__(kBlock) void k_decode_tiled_mfma_sx(const uint16_t*
                 f32x4 d = xs;
 #pragma unroll
                 for (int j = 0; j < 4; ++j)
-                    d = mfma16_bf16(kFold ? unpack_w4_136(ws[j]) : unpack_w4_24(ws[j]), xb[j], d);
+                    d = mfma16_bf16(unpack_w4_24(ws[j]), xb[j], d);
                 const uint32_t s01 = sc[i][r].x, s23 = sc[i][r].y;
                 acc[r].x = fmaf(__half2float(__ushort_as_half(static_cast<uint16_t>(s01))), d.x, acc[r].x);
                 acc[r].y = fmaf(__half2float(__ushort_as_half(static_cast<uint16_t>(s01 >> 16))), d.y, acc[r].y);
@@ -472,25 +460,11 @@ __global__ __launch_bounds__(kBlock) void k_decode_tiled_mfma_sx(const uint16_t*
         for (int v = 0; v < kWaves; ++v) sum += reinterpret_cast<const float*>(strips[v])[row * 16 + t];
         return sum;
     };
-    if constexpr (kFold) {
-        const int tt = m >> 1;
-        for (int i = threadIdx.x; i < T * tt; i += kBlock) {
-            const int row = i / tt, t = i - row * tt;
-            const int64_t grow = tile * T + row;
-            if (grow >= n) continue;
-            const float v = (wsum(row, t) + wsum(row, tt + t)) + (bias && blockIdx.y == 0 ? bias[grow] : 0.0f);
-            if (gridDim.y == 1)
-                y[t * n + grow] = v;
-            else
-                atomicAdd(&y[t * n + grow], v);
-        }
-    } else {
-        for (int i = threadIdx.x; i < T * m; i += kBlock) {
-            const int row = i / m, t = i - row * m;
-            const int64_t grow = tile * T + row;
-            if (grow >= n) continue;
-            y[t * n + grow] = 0.125f * wsum(row, t) + (bias ? bias[grow] : 0.0f);
-        }
+    for (int i = threadIdx.x; i < T * m; i += kBlock) {
+        const int row = i / m, t = i - row * m;
+        const int64_t grow = tile * T + row;
+        if (grow >= n) continue;
+        y[t * n + grow] = 0.125f * wsum(row, t) + (bias ? bias[grow] : 0.0f);
     }
 }
 
@@ -524,17 +498,17 @@ constexpr int kFoldLPG = 4;  // load instructions per group: 2 row groups x (sca
 
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
-// Loads issued after the later of group gi's DMAs (8 instructions) and its
-// weight and scale loads (kFoldLPG), up to the wait of group gi, in the
+// Loads issued after the later of group gi's DMAs (4 instructions per set) and
+// its weight and scale loads (kFoldLPG), up to the wait of group gi, in the
 // kernel's issue order: DMA(0), DMA(1), LG(0 .. win-1), then for each group g
 // before gi: DMA(g + 2), LG(g + win).
-template <int kGPW>
+template <int kGPW, int kSets>
 constexpr int fold_after(int gi) {
     constexpr int win = kFoldWin < kGPW ? kFoldWin : kGPW;
     int pos = 0, last = 0;
     auto dma = [&](int g) {
         if (g >= kGPW) return;
-        pos += 8;
+        pos += 4 * kSets;
         if (g == gi && pos > last) last = pos;
     };
     auto lg = [&](int g) {
@@ -564,17 +538,19 @@ __device__ __forceinline__ void fold_wait(u32x4& w0, u32x4& w1, u32x2& s0, u32x2
     asm volatile("s_waitcnt vmcnt(%4)" : "+v"(w0), "+v"(w1), "+v"(s0), "+v"(s1) : "n"(N) : "memory");
 }
 
-template <int kGPW>
+template <int kGPW, int kSets>
 __global__ __launch_bounds__(kFoldWaves * 64) void k_decode_fold32(const uint16_t* __restrict__ h, int rows,
                                                                    const uint8_t* __restrict__ pt,
                                                                    const uint16_t* __restrict__ st, int64_t n,
                                                                    int64_t k, float* __restrict__ y) {
     static_assert(kGPW >= 1 && kGPW <= 8, "1..8 groups per wave");
+    static_assert(kSets == 1 || kSets == 2, "one or two sets of 16 rows of h");
     constexpr int kR = 2, T = 32;
-    constexpr int kStrip = 32 * 256;
+    constexpr int kHR = 16 * kSets;  // rows of h (MFMA columns)
+    constexpr int kStrip = kHR * 256;
     constexpr int kWin = kFoldWin < kGPW ? kFoldWin : kGPW;
-    static_assert(T * 32 * 4 <= kStrip, "a wave's partial sums fit in its strip");
-    static_assert(fold_after<kGPW>(0) < 64, "vmcnt counts 0..63");
+    static_assert(T * kHR * 4 <= kStrip, "a wave's partial sums fit in its strip");
+    static_assert(fold_after<kGPW, kSets>(0) < 64, "vmcnt counts 0..63");
     __shared__ __attribute__((aligned(1024))) int8_t strips[kFoldWaves][2][kStrip];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -585,7 +561,7 @@ __global__ __launch_bounds__(kFoldWaves * 64) void k_decode_fold32(const uint16_
     const int64_t g0 = gb + static_cast<int64_t>(wave) * kGPW;
     const int64_t gl = max<int64_t>(ge - 1, 0);
 
-    // DMA i (0..7) of group gi moves rows 4 i .. 4 i + 3 into strip gi % 2: lane l
+    // DMA i (0 .. 4 kSets - 1) of group gi moves rows 4 i .. 4 i + 3 into strip gi % 2: lane l
     // -> row 4 i + l / 16, landing at LDS chunk l % 16, from global chunk
     // (l % 16) ^ row % 16.  Rows past `rows` re-read the last row and groups past
     // the range the last group (their columns and sums are never used).
@@ -593,7 +569,7 @@ __global__ __launch_bounds__(kFoldWaves * 64) void k_decode_fold32(const uint16_
         const uint16_t* hb = h + min<int64_t>(g0 + gi, gl) * 128;
         int8_t* sx = strips[wave][gi & 1];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
+        for (int i = 0; i < 4 * kSets; ++i) {
             const int t = 4 * i + (lane >> 4);
             lds_dma16(hb + static_cast<int64_t>(min(t, rows - 1)) * k + 8 * (r16 ^ (t & 15)), lds_addr(sx + 1024 * i));
         }
@@ -614,9 +590,9 @@ __global__ __launch_bounds__(kFoldWaves * 64) void k_decode_fold32(const uint16_
 #pragma unroll
     for (int gi = 0; gi < kWin; ++gi) load_group(gi);
     const u32x4 aoff = u32x4{0xC308C308u, 0xC308C308u, 0xC308C308u, 0xC308C308u};  // bf16 -136
-    f32x4 acc[2][kR];
+    f32x4 acc[kSets][kR];
 #pragma unroll
-    for (int s2 = 0; s2 < 2; ++s2)
+    for (int s2 = 0; s2 < kSets; ++s2)
 #pragma unroll
         for (int r = 0; r < kR; ++r) acc[s2][r] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -626,7 +602,7 @@ __global__ __launch_bounds__(kFoldWaves * 64) void k_decode_fold32(const uint16_
         switch (gi) {
 #define TQ_FOLD_WAIT(G)                                                                        \
     case G:                                                                                    \
-        if constexpr (G < kGPW) fold_wait<fold_after<kGPW>(G)>(w[sl][0], w[sl][1], sc[sl][0], sc[sl][1]); \
+        if constexpr (G < kGPW) fold_wait<fold_after<kGPW, kSets>(G)>(w[sl][0], w[sl][1], sc[sl][0], sc[sl][1]); \
         break;
             TQ_FOLD_WAIT(0)
             TQ_FOLD_WAIT(1)
@@ -639,9 +615,9 @@ __global__ __launch_bounds__(kFoldWaves * 64) void k_decode_fold32(const uint16_
 #undef TQ_FOLD_WAIT
         }
         const int8_t* sx = strips[wave][gi & 1];
-        u32x4 xb[2][4];
+        u32x4 xb[kSets][4];
 #pragma unroll
-        for (int s2 = 0; s2 < 2; ++s2)
+        for (int s2 = 0; s2 < kSets; ++s2)
 #pragma unroll
             for (int j = 0; j < 4; ++j)
                 xb[s2][j] = *reinterpret_cast<const u32x4*>(sx + (16 * s2 + r16) * 256 + (((4 * q + j) ^ r16) << 4));
@@ -650,9 +626,9 @@ __global__ __launch_bounds__(kFoldWaves * 64) void k_decode_fold32(const uint16_
             asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
             dma_group(gi + 2);
         }
-        f32x4 xs[2];
+        f32x4 xs[kSets];
 #pragma unroll
-        for (int s2 = 0; s2 < 2; ++s2) {
+        for (int s2 = 0; s2 < kSets; ++s2) {
             xs[s2] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int j = 0; j < 4; ++j) xs[s2] = mfma16_bf16(aoff, xb[s2][j], xs[s2]);
@@ -661,12 +637,14 @@ __global__ __launch_bounds__(kFoldWaves * 64) void k_decode_fold32(const uint16_
         for (int r = 0; r < kR; ++r) {
             const u32x4 wv = w[sl][r];
             const uint32_t ws[4] = {wv.x, wv.y, wv.z, wv.w};
-            f32x4 d0 = xs[0], d1 = xs[1];
+            f32x4 d[kSets];
+#pragma unroll
+            for (int s2 = 0; s2 < kSets; ++s2) d[s2] = xs[s2];
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const u32x4 a = unpack_w4_136(ws[j]);
-                d0 = mfma16_bf16(a, xb[0][j], d0);
-                d1 = mfma16_bf16(a, xb[1][j], d1);
+#pragma unroll
+                for (int s2 = 0; s2 < kSets; ++s2) d[s2] = mfma16_bf16(a, xb[s2][j], d[s2]);
             }
             const uint32_t s01 = sc[sl][r].x, s23 = sc[sl][r].y;
             const float sv[4] = {__half2float(__ushort_as_half(static_cast<uint16_t>(s01))),
@@ -674,10 +652,9 @@ __global__ __launch_bounds__(kFoldWaves * 64) void k_decode_fold32(const uint16_
                                  __half2float(__ushort_as_half(static_cast<uint16_t>(s23))),
                                  __half2float(__ushort_as_half(static_cast<uint16_t>(s23 >> 16)))};
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                acc[0][r][e] = fmaf(sv[e], d0[e], acc[0][r][e]);
-                acc[1][r][e] = fmaf(sv[e], d1[e], acc[1][r][e]);
-            }
+            for (int e = 0; e < 4; ++e)
+#pragma unroll
+                for (int s2 = 0; s2 < kSets; ++s2) acc[s2][r][e] = fmaf(sv[e], d[s2][e], acc[s2][r][e]);
         }
         // this group's weights and scales are consumed: their slot takes group gi + kWin
         if (gi + kWin < kGPW) load_group(gi + kWin);
@@ -688,16 +665,16 @@ __global__ __launch_bounds__(kFoldWaves * 64) void k_decode_fold32(const uint16_
     asm volatile("s_waitcnt vmcnt(0)\n\ts_waitcnt lgkmcnt(0)" ::: "memory");
     float* part = reinterpret_cast<float*>(strips[wave][0]);
 #pragma unroll
-    for (int s2 = 0; s2 < 2; ++s2)
+    for (int s2 = 0; s2 < kSets; ++s2)
 #pragma unroll
         for (int r = 0; r < kR; ++r)
 #pragma unroll
-            for (int e = 0; e < 4; ++e) part[(16 * r + 4 * q + e) * 32 + 16 * s2 + r16] = acc[s2][r][e];
+            for (int e = 0; e < 4; ++e) part[(16 * r + 4 * q + e) * kHR + 16 * s2 + r16] = acc[s2][r][e];
     __syncthreads();
     auto wsum = [&](int row, int c) {
         float sum = 0.0f;
 #pragma unroll
-        for (int v = 0; v < kFoldWaves; ++v) sum += reinterpret_cast<const float*>(strips[v][0])[row * 32 + c];
+        for (int v = 0; v < kFoldWaves; ++v) sum += reinterpret_cast<const float*>(strips[v][0])[row * kHR + c];
         return sum;
     };
     const int tt = rows >> 1;
@@ -1320,34 +1297,14 @@ int launch_mfma(int64_t gpw, int64_t tiles, hipStream_t s, const uint16_t* x, in
     return check_launch("tq_gemv_w4g128_tiled");
 }
 
-// The decode FFN's down projection for up to 8 tokens per launch (2t <= 16 rows of
-// h): the MFMA kernel in fold mode, K split in two onto a zeroed y; gpw is the
-// groups per wave of one K half.
-template <int kR>
-int launch_mfma_fold(int64_t gpw, int64_t tiles, hipStream_t s, const uint16_t* h, int rows, const uint8_t* pt,
-                     const uint16_t* st, int64_t n, int64_t k, float* y) {
-    if (gpw > 4 || rows > 16 || rows % 2 != 0)
-        return fail(TQ_EINVAL, "tq_mlp_w4g128_decode: %d rows of h at %lld groups per wave", rows, (long long)gpw);
-    const dim3 grid(static_cast<unsigned>(tiles), 2u);
-    if (gpw <= 1)
-        k_decode_tiled_mfma_sx<kR, 1, true><<<grid, kBlock, 0, s>>>(h, rows, pt, st, nullptr, n, k, y);
-    else if (gpw <= 2)
-        k_decode_tiled_mfma_sx<kR, 2, true><<<grid, kBlock, 0, s>>>(h, rows, pt, st, nullptr, n, k, y);
-    else
-        k_decode_tiled_mfma_sx<kR, 4, true><<<grid, kBlock, 0, s>>>(h, rows, pt, st, nullptr, n, k, y);
-    return check_launch("tq_mlp_w4g128_decode");
-}
-
-// The decode FFN's down projection for 9-16 tokens in one launch (2t <= 32 rows
+// The decode FFN's down projection for 5-16 tokens in one launch (2t <= 32 rows
 // of h, 32-row tiles, K split in two onto a zeroed y); gpw is the groups per
 // wave of one K half over the kernel's 8 waves.
-int launch_fold32(int64_t gpw, int64_t tiles, hipStream_t s, const uint16_t* h, int rows, const uint8_t* pt,
-                  const uint16_t* st, int64_t n, int64_t k, float* y) {
-    if (gpw < 1 || gpw > 8 || rows > 32 || rows % 2 != 0)
-        return fail(TQ_EINVAL, "tq_mlp_w4g128_decode: %d rows of h at %lld groups per wave", rows, (long long)gpw);
-    const dim3 grid(static_cast<unsigned>(tiles), 2u);
+template <int kSets>
+void launch_fold32_sets(int64_t gpw, const dim3& grid, hipStream_t s, const uint16_t* h, int rows,
+                        const uint8_t* pt, const uint16_t* st, int64_t n, int64_t k, float* y) {
     constexpr unsigned kThreads = kFoldWaves * 64;
-#define TQ_FOLD(G) k_decode_fold32<G><<<grid, kThreads, 0, s>>>(h, rows, pt, st, n, k, y)
+#define TQ_FOLD(G) k_decode_fold32<G, kSets><<<grid, kThreads, 0, s>>>(h, rows, pt, st, n, k, y)
     switch (gpw) {
         case 1: TQ_FOLD(1); break;
         case 2: TQ_FOLD(2); break;
@@ -1359,6 +1316,17 @@ int launch_fold32(int64_t gpw, int64_t tiles, hipStream_t s, const uint16_t* h, 
         default: TQ_FOLD(8); break;
     }
 #undef TQ_FOLD
+}
+
+int launch_fold32(int64_t gpw, int64_t tiles, hipStream_t s, const uint16_t* h, int rows, const uint8_t* pt,
+                  const uint16_t* st, int64_t n, int64_t k, float* y) {
+    if (gpw < 1 || gpw > 8 || rows > 32 || rows % 2 != 0)
+        return fail(TQ_EINVAL, "tq_mlp_w4g128_decode: %d rows of h at %lld groups per wave", rows, (long long)gpw);
+    const dim3 grid(static_cast<unsigned>(tiles), 2u);
+    if (rows <= 16)
+        launch_fold32_sets<1>(gpw, grid, s, h, rows, pt, st, n, k, y);
+    else
+        launch_fold32_sets<2>(gpw, grid, s, h, rows, pt, st, n, k, y);
     return check_launch("tq_mlp_w4g128_decode");
 }
 
@@ -1614,14 +1582,11 @@ int mlp_decode(const char* fn, const uint16_t* x_bf16, int64_t m, int64_t d, int
     // 16-row down tiles and for 1-4 tokens on 32-row tiles, whose 128 tiles x 2 K
     // halves fill 256 CUs in one round at D = 4096.
     const bool block = (kr == 1 && (mi == 3 || mi == 4)) || kr == 2;
-    // Octets (5-16 tokens on 32-row down tiles): one down launch per eight tokens,
-    // their 2t <= 16 rows as the columns of the MFMA kernel (x read from L2, no
-    // LDS strips to fit), K split in two as for quads.
-    const bool octets = kr == 2 && mi >= 5;
-    // 9-16 tokens on 32-row down tiles: all 2m rows of h in one down launch
-    // (k_decode_fold32), the down weights read once
-    const bool one_down = octets && mi >= 9;
-    const int group = one_down ? 16 : (octets ? 8 : (block ? 4 : 2));  // tokens per MlpRows group
+    // 5-16 tokens on 32-row down tiles: all 2m <= 32 rows of h in one down launch
+    // (k_decode_fold32: one set of 16 MFMA columns up to 8 tokens, two beyond),
+    // the down weights read once
+    const bool one_down = kr == 2 && mi >= 5;
+    const int group = one_down ? 16 : (block ? 4 : 2);  // tokens per MlpRows group
     const int64_t gu_tiles = (f + 31) / 32, gu_gpw = ((d >> 7) + kWaves - 1) / kWaves;
     // 5-16 tokens: one launch of the 16x16x32 kernel where its x strips fit the LDS
     const bool gu16 = gu16_fits(mi, gu_gpw);
@@ -1653,15 +1618,6 @@ int mlp_decode(const char* fn, const uint16_t* x_bf16, int64_t m, int64_t d, int
     if (one_down) {
         const int64_t gpw8 = (((f >> 7) + 1) / 2 + kFoldWaves - 1) / kFoldWaves;  // of a K half, 8 waves
         return launch_fold32(gpw8, dn_tiles, st, h, 2 * mi, down_t, down_s_t, d, f, y);
-    }
-    if (octets) {
-        for (int c = 0; 8 * c < mi; ++c) {
-            const int t = mi - 8 * c < 8 ? mi - 8 * c : 8;
-            const int rc = launch_mfma_fold<2>(gpw2, dn_tiles, st, h + 16 * c * f, 2 * t, down_t, down_s_t, d, f,
-                                               y + 8 * c * d);
-            if (rc != TQ_OK) return rc;
-        }
-        return TQ_OK;
     }
     if (block) {
         for (int c = 0; 4 * c < mi; ++c) {

@@ -28,6 +28,14 @@
 // dimension is padded with zeros to 32, 64 or 128.  A running max of -inf
 // (every key so far masked) leaves the row untouched; a row masked everywhere
 // ends as 0/0 = NaN, as the reference's softmax gives.
+//
+// With D % 4 == 0 and 16-byte aligned K and V rows (k_attention_vec) a thread
+// loads K as 16-byte quads along d and V as four keys at one d (coalesced
+// along d across the wave), both stored to LDS as 8-byte runs, with offsets
+// fixed per thread and a uniform step per item, so whole tiles load without
+// clamps; it fits two waves per SIMD in 256 registers.  Other head dimensions
+// keep the per-element loads (k_attention, one wave per SIMD).  Both give the
+// same bits.
 #include <cmath>
 
 #include "tq_internal.h"
@@ -74,8 +82,9 @@ __device__ __forceinline__ void split8(const float* v, u32x4& hi, u32x4& lo) {
 
 __device__ __forceinline__ int vcol(int key) { return (key & ~12) | ((key & 4) << 1) | ((key & 8) >> 1); }
 
-template <int kDP>
-__global__ __launch_bounds__(kWaves * kWave) void k_attention(const float* __restrict__ q, int64_t ldq,
+// kVec: D % 4 == 0 and 16-byte aligned rows of K and V, loaded as whole quads.
+template <int kDP, bool kVec>
+__device__ __forceinline__ void attention_block(const float* __restrict__ q, int64_t ldq,
                                                               const float* __restrict__ k, int64_t ldk,
                                                               const float* __restrict__ v, int64_t ldv,
                                                               const float* __restrict__ mask, int64_t mask_batch,
@@ -115,29 +124,106 @@ __global__ __launch_bounds__(kWaves * kWave) void k_attention(const float* __res
         mask ? mask + ((mask_batch == 1 ? 0 : static_cast<int64_t>(b)) * S + min(qrow, S - 1)) * static_cast<int64_t>(S)
              : nullptr;
 
-    // tile loads: element e = tid + 256 i -> key e / kDP, d e % kDP (coalesced along d)
+    // tile loads.  Scalar: element e = tid + 256 i -> key e / kDP, d e % kDP
+    // (coalesced along d).  kVec: K item e -> key e / (kDP / 4), the quad of d
+    // from 4 (e % (kDP / 4)), one 16-byte load; V item e -> d = e % kDP and keys
+    // 4 (e / kDP) .. + 3, four loads coalesced along d across the wave, so that
+    // both land in LDS as 8-byte runs (K along d, the transposed V along keys).
+    // Rows past S and d past D read clamped addresses and are zeroed.
+    constexpr int kQuads = kElems / 4;  // K and V items per thread (kVec)
     float kreg[kElems], vreg[kElems];
+    // kVec: the element offsets of item 0 from its tile's first row (the host
+    // keeps a tile's offsets below 2^31) and whether its d is inside the head;
+    // item i has the same d and keys 256 i / (kDP / 4) (K) or 4 (256 i / kDP)
+    // (V) further on
+    constexpr int kKeyStepK = kWaves * kWave / (kDP / 4), kKeyStepV = 4 * (kWaves * kWave / kDP);
+    const int dq = 4 * (tid % (kDP / 4)), dv = tid % kDP;
+    const uint32_t koff = static_cast<uint32_t>((tid / (kDP / 4)) * ldk + col + min(dq, D - 4));
+    const uint32_t voff = static_cast<uint32_t>(4 * (tid / kDP) * ldv + col + min(dv, D - 1));
+    const bool kin = dq < D, vin = dv < D;
     auto load_tile = [&](int j0) {
+        if constexpr (kVec) {
+            if (j0 + kKT <= S) {  // a whole tile (uniform): no row clamps
 #pragma unroll
-        for (int i = 0; i < kElems; ++i) {
-            const int e = tid + i * kWaves * kWave, key = e / kDP, d = e % kDP;
-            const bool ok = j0 + key < S && d < D;
-            const int64_t row = base + (ok ? j0 + key : 0);
-            kreg[i] = ok ? k[row * ldk + col + d] : 0.f;
-            vreg[i] = ok ? v[row * ldv + col + d] : 0.f;
+                for (int i = 0; i < kQuads; ++i) {
+                    const float* kb = k + (base + j0 + i * kKeyStepK) * ldk;
+                    const float4 kv = *reinterpret_cast<const float4*>(kb + koff);
+                    kreg[4 * i] = kin ? kv.x : 0.f;
+                    kreg[4 * i + 1] = kin ? kv.y : 0.f;
+                    kreg[4 * i + 2] = kin ? kv.z : 0.f;
+                    kreg[4 * i + 3] = kin ? kv.w : 0.f;
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const float x = (v + (base + j0 + i * kKeyStepV + r) * ldv)[voff];
+                        vreg[4 * i + r] = vin ? x : 0.f;
+                    }
+                }
+                return;
+            }
+#pragma unroll
+            for (int i = 0; i < kQuads; ++i) {
+                const int e = tid + i * kWaves * kWave;
+                const int key = e / (kDP / 4), d = 4 * (e % (kDP / 4));
+                const bool ok = j0 + key < S && d < D;
+                const int64_t row = base + min(j0 + key, S - 1);
+                const float4 kv = *reinterpret_cast<const float4*>(k + row * ldk + col + min(d, D - 4));
+                kreg[4 * i] = ok ? kv.x : 0.f;
+                kreg[4 * i + 1] = ok ? kv.y : 0.f;
+                kreg[4 * i + 2] = ok ? kv.z : 0.f;
+                kreg[4 * i + 3] = ok ? kv.w : 0.f;
+                const int dv = e % kDP, k4 = 4 * (e / kDP);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const bool okv = j0 + k4 + r < S && dv < D;
+                    const float x = v[(base + min(j0 + k4 + r, S - 1)) * ldv + col + min(dv, D - 1)];
+                    vreg[4 * i + r] = okv ? x : 0.f;
+                }
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < kElems; ++i) {
+                const int e = tid + i * kWaves * kWave, key = e / kDP, d = e % kDP;
+                const bool ok = j0 + key < S && d < D;
+                const int64_t row = base + (ok ? j0 + key : 0);
+                kreg[i] = ok ? k[row * ldk + col + d] : 0.f;
+                vreg[i] = ok ? v[row * ldv + col + d] : 0.f;
+            }
         }
     };
     auto store_tile = [&](int buf) {
+        if constexpr (kVec) {
 #pragma unroll
-        for (int i = 0; i < kElems; ++i) {
-            const int e = tid + i * kWaves * kWave, key = e / kDP, d = e % kDP;
-            uint16_t hi, lo;
-            split(kreg[i], hi, lo);
-            ksh[buf][key * kKRow + d] = hi;
-            ksl[buf][key * kKRow + d] = lo;
-            split(vreg[i], hi, lo);
-            vsh[buf][d * kVRow + vcol(key)] = hi;
-            vsl[buf][d * kVRow + vcol(key)] = lo;
+            for (int i = 0; i < kQuads; ++i) {
+                const int e = tid + i * kWaves * kWave;
+                const int key = e / (kDP / 4), d = 4 * (e % (kDP / 4));
+                uint16_t h4[4], l4[4];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) split(kreg[4 * i + r], h4[r], l4[r]);
+                *reinterpret_cast<uint2*>(&ksh[buf][key * kKRow + d]) =
+                    make_uint2(h4[0] | static_cast<uint32_t>(h4[1]) << 16, h4[2] | static_cast<uint32_t>(h4[3]) << 16);
+                *reinterpret_cast<uint2*>(&ksl[buf][key * kKRow + d]) =
+                    make_uint2(l4[0] | static_cast<uint32_t>(l4[1]) << 16, l4[2] | static_cast<uint32_t>(l4[3]) << 16);
+                const int dv = e % kDP, k4 = 4 * (e / kDP);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) split(vreg[4 * i + r], h4[r], l4[r]);
+                // keys 4a .. 4a + 3 sit at 4 consecutive columns of the transposed tile
+                *reinterpret_cast<uint2*>(&vsh[buf][dv * kVRow + vcol(k4)]) =
+                    make_uint2(h4[0] | static_cast<uint32_t>(h4[1]) << 16, h4[2] | static_cast<uint32_t>(h4[3]) << 16);
+                *reinterpret_cast<uint2*>(&vsl[buf][dv * kVRow + vcol(k4)]) =
+                    make_uint2(l4[0] | static_cast<uint32_t>(l4[1]) << 16, l4[2] | static_cast<uint32_t>(l4[3]) << 16);
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < kElems; ++i) {
+                const int e = tid + i * kWaves * kWave, key = e / kDP, d = e % kDP;
+                uint16_t hi, lo;
+                split(kreg[i], hi, lo);
+                ksh[buf][key * kKRow + d] = hi;
+                ksl[buf][key * kKRow + d] = lo;
+                split(vreg[i], hi, lo);
+                vsh[buf][d * kVRow + vcol(key)] = hi;
+                vsl[buf][d * kVRow + vcol(key)] = lo;
+            }
         }
     };
 
@@ -176,7 +262,8 @@ __global__ __launch_bounds__(kWaves * kWave) void k_attention(const float* __res
         for (int r = 0; r < 16; ++r) {
             const int key = j0 + 8 * (r >> 2) + 4 * g + (r & 3);
             float sc = st[r] * scale2;
-            if (mrow) sc = fmaf(mrow[min(key, S - 1)], kLog2e, sc);  // clamped: no divergent branch
+            // `mask` (a kernel argument) is uniform: no divergent branch; the index is clamped
+            if (mask) sc = fmaf(mrow[min(key, S - 1)], kLog2e, sc);
             sc = key < S ? sc : -INFINITY;
             p[r] = sc;
             mt = fmaxf(mt, sc);
@@ -200,9 +287,11 @@ __global__ __launch_bounds__(kWaves * kWave) void k_attention(const float* __res
         split8(p, ph[0], pl[0]);
         split8(p + 8, ph[1], pl[1]);
         // O^T[d][q] += sum_key V[key][d] P[q][key]
+        // alpha is 1 in every lane once the running maxima settle: the rescale is skipped
+        const bool rescale = __ballot(alpha != 1.0f) != 0;
 #pragma unroll
         for (int c = 0; c < kBlocks; ++c) {
-            ot[c] *= alpha;
+            if (rescale) ot[c] *= alpha;
             const uint16_t* vh = &vsh[buf][(32 * c + lr) * kVRow + 8 * g];
             const uint16_t* vl = &vsl[buf][(32 * c + lr) * kVRow + 8 * g];
 #pragma unroll
@@ -234,6 +323,26 @@ __global__ __launch_bounds__(kWaves * kWave) void k_attention(const float* __res
     }
 }
 
+// Two waves per SIMD where the quad loads leave the registers for them (256 per
+// lane); the scalar form keeps one (its element loads need more).
+template <int kDP>
+__global__ __launch_bounds__(kWaves * kWave) __attribute__((amdgpu_waves_per_eu(2))) void k_attention_vec(
+    const float* __restrict__ q, int64_t ldq, const float* __restrict__ k, int64_t ldk, const float* __restrict__ v,
+    int64_t ldv, const float* __restrict__ mask, int64_t mask_batch, int S, int D, float scale, float* __restrict__ o,
+    int64_t ldo) {
+    attention_block<kDP, true>(q, ldq, k, ldk, v, ldv, mask, mask_batch, S, D, scale, o, ldo);
+}
+
+template <int kDP>
+__global__ __launch_bounds__(kWaves * kWave) void k_attention(const float* __restrict__ q, int64_t ldq,
+                                                              const float* __restrict__ k, int64_t ldk,
+                                                              const float* __restrict__ v, int64_t ldv,
+                                                              const float* __restrict__ mask, int64_t mask_batch,
+                                                              int S, int D, float scale, float* __restrict__ o,
+                                                              int64_t ldo) {
+    attention_block<kDP, false>(q, ldq, k, ldk, v, ldv, mask, mask_batch, S, D, scale, o, ldo);
+}
+
 }  // namespace
 }  // namespace tq
 
@@ -260,14 +369,20 @@ extern "C" int tq_attention_f32(const float* q, int64_t ldq, const float* k, int
     const float scale = static_cast<float>(1.0 / std::sqrt(static_cast<double>(head_dim)));
     const float* mk = mask_batch ? mask : nullptr;
     const int S = static_cast<int>(seq), D = static_cast<int>(head_dim);
-    if (head_dim <= 32)
-        k_attention<32><<<grid, kWaves * kWave, 0, as_hip(stream)>>>(q, ldq, k, ldk, v, ldv, mk, mask_batch, S, D,
-                                                                      scale, out, ldo);
-    else if (head_dim <= 64)
-        k_attention<64><<<grid, kWaves * kWave, 0, as_hip(stream)>>>(q, ldq, k, ldk, v, ldv, mk, mask_batch, S, D,
-                                                                      scale, out, ldo);
-    else
-        k_attention<128><<<grid, kWaves * kWave, 0, as_hip(stream)>>>(q, ldq, k, ldk, v, ldv, mk, mask_batch, S, D,
-                                                                       scale, out, ldo);
+    // whole quads of d where every K and V row is 16-byte aligned
+    // (and element offsets within a key tile below 2^31)
+    const bool vec = head_dim % 4 == 0 && ldk % 4 == 0 && ldv % 4 == 0 && aligned(k, 16) && aligned(v, 16) &&
+                     kKT * std::max(ldk, ldv) + e < (int64_t(1) << 31);
+#define TQ_ATT(KERNEL, DP)                                                                                \
+    KERNEL<DP><<<grid, kWaves * kWave, 0, as_hip(stream)>>>(q, ldq, k, ldk, v, ldv, mk, mask_batch, S, D, scale, \
+                                                            out, ldo)
+    if (head_dim <= 32) {
+        if (vec) TQ_ATT(k_attention_vec, 32); else TQ_ATT(k_attention, 32);
+    } else if (head_dim <= 64) {
+        if (vec) TQ_ATT(k_attention_vec, 64); else TQ_ATT(k_attention, 64);
+    } else {
+        if (vec) TQ_ATT(k_attention_vec, 128); else TQ_ATT(k_attention, 128);
+    }
+#undef TQ_ATT
     return check_launch("tq_attention_f32");
 }

@@ -62,6 +62,35 @@ def test_attention_core_vs_oracle(tq, oracle, B, S, H, D):
         assert_close(got, ref, RTOL, ATOL, f"attention B={B} S={S} H={H} D={D}")
 
 
+@pytest.mark.parametrize("B,S,H,D", [(1, 77, 4, 128), (2, 40, 3, 64), (1, 33, 2, 32), (1, 64, 2, 12)])
+def test_attention_quad_and_element_loads_agree(tq, B, S, H, D):
+    """Row strides that are multiples of 4 floats take the quad-load kernel, a
+    stride of 3E + 1 the per-element one: the same q, k, v and mask give the
+    same bits (a partial last key tile included)."""
+    import torch
+    from theano_quantize import _abi
+    from theano_quantize._tensor import ptr, stream
+
+    E = H * D
+    qkv = normal(94, (B * S, 3 * E), 1.0)
+    rng = np.random.default_rng(S + D)
+    mask = np.where(rng.random((B, S, S)) < 0.25, -np.inf, rng.standard_normal((B, S, S))).astype(np.float32)
+    mask[:, :, 0] = 0.0
+    md = dev(mask)
+    outs = []
+    for pad in (0, 1):
+        buf = np.zeros((B * S, 3 * E + pad), np.float32)
+        buf[:, :3 * E] = qkv
+        d = dev(buf)
+        ld = 3 * E + pad
+        out = torch.empty((B * S, E), dtype=torch.float32, device="cuda")
+        _abi.call("tq_attention_f32", ptr(d), ld, ptr(d[:, E:]), ld, ptr(d[:, 2 * E:]), ld, ptr(md), B, B, S, H, D,
+                  ptr(out), E, stream())
+        outs.append(host(out))
+    assert np.isfinite(outs[0]).all()
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32)), f"B={B} S={S} H={H} D={D}"
+
+
 def test_attention_fully_masked_row_is_nan(tq, oracle):
     B, S, H, D = 1, 70, 2, 8
     qkv = normal(92, (B * S, 3 * H * D), 1.0)

@@ -34,8 +34,10 @@
 // along d across the wave), both stored to LDS as 8-byte runs, with offsets
 // fixed per thread and a uniform step per item, so whole tiles load without
 // clamps; it fits two waves per SIMD in 256 registers.  Other head dimensions
-// keep the per-element loads (k_attention, one wave per SIMD).  Both give the
-// same bits.
+// keep the per-element loads (k_attention, one wave per SIMD).  At head dim 128
+// a launch with a block per CU or more takes 8-wave blocks (256 queries, each
+// key tile loaded and split once for all of them).  All forms give the same
+// bits.
 #include <cmath>
 
 #include "tq_internal.h"
@@ -45,9 +47,8 @@ namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
-constexpr int kWaves = 4;
+constexpr int kWaves = 4;           // waves per block (8 in the wide form)
 constexpr int kQW = 32;              // query rows per wave
-constexpr int kQB = kWaves * kQW;    // per block
 constexpr int kKT = 32;              // keys per tile
 constexpr int kMaxD = 128;
 
@@ -83,7 +84,8 @@ __device__ __forceinline__ void split8(const float* v, u32x4& hi, u32x4& lo) {
 __device__ __forceinline__ int vcol(int key) { return (key & ~12) | ((key & 4) << 1) | ((key & 8) >> 1); }
 
 // kVec: D % 4 == 0 and 16-byte aligned rows of K and V, loaded as whole quads.
-template <int kDP, bool kVec>
+// kW waves per block share each key tile (kW x 32 queries).
+template <int kDP, bool kVec, int kW>
 __device__ __forceinline__ void attention_block(const float* __restrict__ q, int64_t ldq,
                                                               const float* __restrict__ k, int64_t ldk,
                                                               const float* __restrict__ v, int64_t ldv,
@@ -94,12 +96,13 @@ __device__ __forceinline__ void attention_block(const float* __restrict__ q, int
     constexpr int kKRow = kDP + 8;     // K plane row (bf16), padded
     constexpr int kVRow = kKT + 8;     // transposed V plane row (bf16), padded
     constexpr int kBlocks = kDP / 32;  // 32-wide d blocks of O^T
-    constexpr int kElems = kKT * kDP / (kWaves * kWave);  // tile elements per thread (K and V each)
+    constexpr int kElems = kKT * kDP / (kW * kWave);  // tile elements per thread (K and V each)
+    static_assert(!kVec || kElems % 4 == 0, "whole quads per thread");
     __shared__ __attribute__((aligned(16))) uint16_t ksh[2][kKT * kKRow], ksl[2][kKT * kKRow];
     __shared__ __attribute__((aligned(16))) uint16_t vsh[2][kDP * kVRow], vsl[2][kDP * kVRow];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 5, lr = lane & 31;
     const int h = blockIdx.y, b = blockIdx.z;
-    const int qrow = blockIdx.x * kQB + wave * kQW + lr;  // this lane's query row
+    const int qrow = blockIdx.x * (kW * kQW) + wave * kQW + lr;  // this lane's query row
     const int64_t base = static_cast<int64_t>(b) * S;
     const int col = h * D;
     constexpr float kLog2e = 1.4426950408889634f;
@@ -136,7 +139,7 @@ __device__ __forceinline__ void attention_block(const float* __restrict__ q, int
     // keeps a tile's offsets below 2^31) and whether its d is inside the head;
     // item i has the same d and keys 256 i / (kDP / 4) (K) or 4 (256 i / kDP)
     // (V) further on
-    constexpr int kKeyStepK = kWaves * kWave / (kDP / 4), kKeyStepV = 4 * (kWaves * kWave / kDP);
+    constexpr int kKeyStepK = kW * kWave / (kDP / 4), kKeyStepV = 4 * (kW * kWave / kDP);
     const int dq = 4 * (tid % (kDP / 4)), dv = tid % kDP;
     const uint32_t koff = static_cast<uint32_t>((tid / (kDP / 4)) * ldk + col + min(dq, D - 4));
     const uint32_t voff = static_cast<uint32_t>(4 * (tid / kDP) * ldv + col + min(dv, D - 1));
@@ -162,7 +165,7 @@ __device__ __forceinline__ void attention_block(const float* __restrict__ q, int
             }
 #pragma unroll
             for (int i = 0; i < kQuads; ++i) {
-                const int e = tid + i * kWaves * kWave;
+                const int e = tid + i * kW * kWave;
                 const int key = e / (kDP / 4), d = 4 * (e % (kDP / 4));
                 const bool ok = j0 + key < S && d < D;
                 const int64_t row = base + min(j0 + key, S - 1);
@@ -182,7 +185,7 @@ __device__ __forceinline__ void attention_block(const float* __restrict__ q, int
         } else {
 #pragma unroll
             for (int i = 0; i < kElems; ++i) {
-                const int e = tid + i * kWaves * kWave, key = e / kDP, d = e % kDP;
+                const int e = tid + i * kW * kWave, key = e / kDP, d = e % kDP;
                 const bool ok = j0 + key < S && d < D;
                 const int64_t row = base + (ok ? j0 + key : 0);
                 kreg[i] = ok ? k[row * ldk + col + d] : 0.f;
@@ -194,7 +197,7 @@ __device__ __forceinline__ void attention_block(const float* __restrict__ q, int
         if constexpr (kVec) {
 #pragma unroll
             for (int i = 0; i < kQuads; ++i) {
-                const int e = tid + i * kWaves * kWave;
+                const int e = tid + i * kW * kWave;
                 const int key = e / (kDP / 4), d = 4 * (e % (kDP / 4));
                 uint16_t h4[4], l4[4];
 #pragma unroll
@@ -215,7 +218,7 @@ __device__ __forceinline__ void attention_block(const float* __restrict__ q, int
         } else {
 #pragma unroll
             for (int i = 0; i < kElems; ++i) {
-                const int e = tid + i * kWaves * kWave, key = e / kDP, d = e % kDP;
+                const int e = tid + i * kW * kWave, key = e / kDP, d = e % kDP;
                 uint16_t hi, lo;
                 split(kreg[i], hi, lo);
                 ksh[buf][key * kKRow + d] = hi;
@@ -324,13 +327,15 @@ __device__ __forceinline__ void attention_block(const float* __restrict__ q, int
 }
 
 // Two waves per SIMD where the quad loads leave the registers for them (256 per
-// lane); the scalar form keeps one (its element loads need more).
-template <int kDP>
-__global__ __launch_bounds__(kWaves * kWave) __attribute__((amdgpu_waves_per_eu(2))) void k_attention_vec(
+// lane); the scalar form keeps one (its element loads need more).  kW = 8: the
+// wide form, 256 queries per block, each key tile loaded and split once for
+// twice as many queries.
+template <int kDP, int kW>
+__global__ __launch_bounds__(kW * kWave) __attribute__((amdgpu_waves_per_eu(2))) void k_attention_vec(
     const float* __restrict__ q, int64_t ldq, const float* __restrict__ k, int64_t ldk, const float* __restrict__ v,
     int64_t ldv, const float* __restrict__ mask, int64_t mask_batch, int S, int D, float scale, float* __restrict__ o,
     int64_t ldo) {
-    attention_block<kDP, true>(q, ldq, k, ldk, v, ldv, mask, mask_batch, S, D, scale, o, ldo);
+    attention_block<kDP, true, kW>(q, ldq, k, ldk, v, ldv, mask, mask_batch, S, D, scale, o, ldo);
 }
 
 template <int kDP>
@@ -340,7 +345,7 @@ __global__ __launch_bounds__(kWaves * kWave) void k_attention(const float* __res
                                                               const float* __restrict__ mask, int64_t mask_batch,
                                                               int S, int D, float scale, float* __restrict__ o,
                                                               int64_t ldo) {
-    attention_block<kDP, false>(q, ldq, k, ldk, v, ldv, mask, mask_batch, S, D, scale, o, ldo);
+    attention_block<kDP, false, kWaves>(q, ldq, k, ldk, v, ldv, mask, mask_batch, S, D, scale, o, ldo);
 }
 
 }  // namespace
@@ -364,8 +369,6 @@ extern "C" int tq_attention_f32(const float* q, int64_t ldq, const float* k, int
     TQ_REQUIRE(seq < (int64_t(1) << 30) && heads < 65536 && batch < 65536, "tq_attention_f32: problem too large");
     TQ_REQUIRE(aligned(q, 4) && aligned(k, 4) && aligned(v, 4) && aligned(out, 4) && (!mask || aligned(mask, 4)),
                "tq_attention_f32: misaligned pointer");
-    const dim3 grid(static_cast<unsigned>((seq + kQB - 1) / kQB), static_cast<unsigned>(heads),
-                    static_cast<unsigned>(batch));
     const float scale = static_cast<float>(1.0 / std::sqrt(static_cast<double>(head_dim)));
     const float* mk = mask_batch ? mask : nullptr;
     const int S = static_cast<int>(seq), D = static_cast<int>(head_dim);
@@ -373,15 +376,23 @@ extern "C" int tq_attention_f32(const float* q, int64_t ldq, const float* k, int
     // (and element offsets within a key tile below 2^31)
     const bool vec = head_dim % 4 == 0 && ldk % 4 == 0 && ldv % 4 == 0 && aligned(k, 16) && aligned(v, 16) &&
                      kKT * std::max(ldk, ldv) + e < (int64_t(1) << 31);
-#define TQ_ATT(KERNEL, DP)                                                                                \
-    KERNEL<DP><<<grid, kWaves * kWave, 0, as_hip(stream)>>>(q, ldq, k, ldk, v, ldv, mk, mask_batch, S, D, scale, \
-                                                            out, ldo)
+    // head dim 128: 8-wave blocks where they still give every CU a block (measured
+    // at S = 2048, H = 32: 310-315 against 343 us eager)
+    const int64_t wide_blocks = (seq + 8 * kQW - 1) / (8 * kQW) * heads * batch;
+    const int waves = vec && head_dim > 64 && wide_blocks >= device_cu_count() ? 8 : kWaves;
+    const dim3 grid(static_cast<unsigned>((seq + waves * kQW - 1) / (waves * kQW)), static_cast<unsigned>(heads),
+                    static_cast<unsigned>(batch));
+#define TQ_ATT(KERNEL, ...)                                                                                     \
+    KERNEL<__VA_ARGS__><<<grid, waves * kWave, 0, as_hip(stream)>>>(q, ldq, k, ldk, v, ldv, mk, mask_batch, S, D, \
+                                                                    scale, out, ldo)
     if (head_dim <= 32) {
-        if (vec) TQ_ATT(k_attention_vec, 32); else TQ_ATT(k_attention, 32);
+        if (vec) TQ_ATT(k_attention_vec, 32, kWaves); else TQ_ATT(k_attention, 32);
     } else if (head_dim <= 64) {
-        if (vec) TQ_ATT(k_attention_vec, 64); else TQ_ATT(k_attention, 64);
+        if (vec) TQ_ATT(k_attention_vec, 64, kWaves); else TQ_ATT(k_attention, 64);
+    } else if (vec) {
+        if (waves == 8) TQ_ATT(k_attention_vec, 128, 8); else TQ_ATT(k_attention_vec, 128, kWaves);
     } else {
-        if (vec) TQ_ATT(k_attention_vec, 128); else TQ_ATT(k_attention, 128);
+        TQ_ATT(k_attention, 128);
     }
 #undef TQ_ATT
     return check_launch("tq_attention_f32");

@@ -91,6 +91,34 @@ def test_attention_quad_and_element_loads_agree(tq, B, S, H, D):
     assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32)), f"B={B} S={S} H={H} D={D}"
 
 
+def test_attention_wide_blocks_agree(tq):
+    """At head dim 128 a launch with a block per CU or more runs 8-wave blocks
+    (256 queries); the same batches one at a time run 4-wave blocks.  Every
+    query row's arithmetic is the same in both: the same bits."""
+    import torch
+    from theano_quantize import _abi
+    from theano_quantize._tensor import ptr, stream
+
+    B, S, H, D = 4, 256, 64, 128  # 4 x 64 blocks of 256 queries
+    E = H * D
+    assert B * H * ((S + 255) // 256) >= torch.cuda.get_device_properties(0).multi_processor_count
+    d = dev(normal(95, (B * S, 3 * E), 1.0))
+    causal = dev(np.triu(np.full((1, S, S), -np.inf, np.float32), k=1))
+
+    def run(rows, nb):
+        out = torch.empty((nb * S, E), dtype=torch.float32, device="cuda")
+        x = d[rows]
+        _abi.call("tq_attention_f32", ptr(x), 3 * E, ptr(x[:, E:]), 3 * E, ptr(x[:, 2 * E:]), 3 * E, ptr(causal), 1,
+                  nb, S, H, D, ptr(out), E, stream())
+        return host(out)
+
+    wide = run(slice(0, B * S), B)
+    for b in range(B):
+        narrow = run(slice(b * S, (b + 1) * S), 1)
+        assert np.isfinite(narrow).all()
+        assert np.array_equal(wide[b * S:(b + 1) * S].view(np.uint32), narrow.view(np.uint32)), f"batch {b}"
+
+
 def test_attention_fully_masked_row_is_nan(tq, oracle):
     B, S, H, D = 1, 70, 2, 8
     qkv = normal(92, (B * S, 3 * H * D), 1.0)

@@ -1022,15 +1022,15 @@ __global__ __launch_bounds__(kBlock) void k_decode_diag(const uint16_t* __restri
 // k-group q).  Its B operand for MFMA d is token r16's 8-block 4 (4 g + q) + d of
 // the wave's x slice in slot order (the unpack's order), read from the wave's LDS
 // strip and shared by the 4 row blocks; the output lane holds D[tile row 16 rb +
-// 4 q + e][token r16].  The accumulators restart per step; the step's f16 row
-// scales and 136 * sum(x) of the group are applied as tot += s * (acc - 136 X_g).
+// 4 q + e][token r16].  The accumulators restart per step from -136 X_g (X_g the
+// token's sum over the group: four MFMAs of the step's B operands against bf16
+// -136, shared by the row blocks), and the step's f16 row scales are applied as
+// tot += s * acc.
 //
 // x staging: each lane loads 16-byte 8-blocks of its tokens' slices (tokens past
 // m read as zeros), puts each in slot order with four byte permutes and writes it
 // to the token's strip (padded by 16 bytes, so the 16 rows of one B read fall in
-// distinct banks); the block's group sums come from v_dot2 against (1, 1) and a
-// DPP row sum (a group is 16 consecutive 8-blocks, one 16-lane row) and reach the
-// lanes of their token through LDS.  Weights and scales run kGuWin steps ahead
+// distinct banks).  Weights and scales run kGuWin steps ahead
 // of the arithmetic.  The waves' partial sums meet in LDS in a fixed order (over
 // the wave's dead strips), and the epilogue of tile tt runs on threads [512 tt,
 // 512 tt + 32 m).  With 448 tiles (F = 14336) two tiles per block make 224
@@ -1059,7 +1059,6 @@ __global__ __launch_bounds__(kBlock) void k_decode_gu16(const uint16_t* __restri
     constexpr int kRegion = kM * kStripP > kTPB * kM * T * 4 ? kM * kStripP : kTPB * kM * T * 4;
     static_assert(kTPB * 512 <= kBlock && kM * 32 <= 512, "a tile's epilogue takes 32 m of its 512 threads");
     __shared__ __attribute__((aligned(16))) uint8_t xs[kWaves][kRegion];
-    __shared__ float csum[kWaves][kM][kGPW];  // sums of the wave's groups, per token
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int r16 = lane & 15, q = lane >> 4;
@@ -1095,7 +1094,6 @@ __global__ __launch_bounds__(kBlock) void k_decode_gu16(const uint16_t* __restri
     for (int s = 0; s < kWin; ++s) load_step(s);
 
     // stage: a lane's 8-block (x0..x7) goes to its strip as (x0,x4)(x1,x5)(x2,x6)(x3,x7)
-    const uint32_t ones = 0x3F803F80u;  // bf16 (1, 1)
 #pragma unroll
     for (int i = 0; i < kIPL; ++i) {
         const int it = lane + kWave * i;
@@ -1104,18 +1102,12 @@ __global__ __launch_bounds__(kBlock) void k_decode_gu16(const uint16_t* __restri
         *reinterpret_cast<u32x4*>(&xs[wave][j * kStripP + b * 16]) =
             u32x4{__builtin_amdgcn_perm(v.z, v.x, 0x05040100u), __builtin_amdgcn_perm(v.z, v.x, 0x07060302u),
                   __builtin_amdgcn_perm(v.w, v.y, 0x05040100u), __builtin_amdgcn_perm(v.w, v.y, 0x07060302u)};
-        float s = dot2_bf16(v.x, ones, 0.0f);
-        s = dot2_bf16(v.y, ones, s);
-        s = dot2_bf16(v.z, ones, s);
-        s = dot2_bf16(v.w, ones, s);
-        s = lane_group_sum<16>(s);
-        if (r16 == 0) csum[wave][j][b >> 4] = s;
     }
-    // the strips and sums are private to the wave: its LDS accesses complete in order
-    float corr[kGPW];
-#pragma unroll
-    for (int g = 0; g < kGPW; ++g) corr[g] = 136.0f * csum[wave][r16][g];
+    // the strips are private to the wave: its LDS accesses complete in order
     const uint8_t* bsrc = &xs[wave][r16 * kStripP];
+    // bf16 -136 in every A entry: the MFMAs over a group's B operands give -136 x
+    // (the token's sum over the group) in every row, the start of each row block's sums
+    const u32x4 aoff = u32x4{0xC308C308u, 0xC308C308u, 0xC308C308u, 0xC308C308u};
 
     f32x4 tot[kTPB][kRB];
 #pragma unroll
@@ -1129,9 +1121,12 @@ __global__ __launch_bounds__(kBlock) void k_decode_gu16(const uint16_t* __restri
         u32x4 bx[4];
 #pragma unroll
         for (int d = 0; d < 4; ++d) bx[d] = *reinterpret_cast<const u32x4*>(bsrc + (16 * g + 4 * q + d) * 16);
+        f32x4 xoff = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int d = 0; d < 4; ++d) xoff = mfma16_bf16(aoff, bx[d], xoff);
         f32x4 acc[kRB];
 #pragma unroll
-        for (int rb = 0; rb < kRB; ++rb) acc[rb] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int rb = 0; rb < kRB; ++rb) acc[rb] = xoff;
         const int slot = s % kWin;
 #pragma unroll
         for (int d = 0; d < 4; ++d)
@@ -1149,7 +1144,7 @@ __global__ __launch_bounds__(kBlock) void k_decode_gu16(const uint16_t* __restri
                                  __half2float(__ushort_as_half(static_cast<uint16_t>(s23))),
                                  __half2float(__ushort_as_half(static_cast<uint16_t>(s23 >> 16)))};
 #pragma unroll
-            for (int e = 0; e < 4; ++e) tot[tt][rb][e] = fmaf(sv[e], acc[rb][e] - corr[g], tot[tt][rb][e]);
+            for (int e = 0; e < 4; ++e) tot[tt][rb][e] = fmaf(sv[e], acc[rb][e], tot[tt][rb][e]);
         }
         if (s + kWin < kSteps) {
             load_step(s + kWin);

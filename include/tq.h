@@ -372,7 +372,9 @@ int tq_mlp_w4g128_decode_noalloc(const uint16_t* x_bf16, int64_t m, int64_t d, i
  * v = q + 2E).  mask: NULL (mask_batch = 0) or additive f32 [mask_batch, seq,
  * seq], mask_batch 1 (broadcast) or batch, shared by the heads.  out: [batch *
  * seq, ldo].  head_dim <= 128.  A row whose scores are all -inf gives NaN, as
- * the reference's softmax does.
+ * the reference's softmax does.  head_dim % 4 == 0 with k and v 16-byte aligned
+ * and ldk, ldv multiples of 4 takes the faster quad-load kernel; every form
+ * gives the same bits.
  * ------------------------------------------------------------------------ */
 int tq_attention_f32(const float* q, int64_t ldq, const float* k, int64_t ldk, const float* v,
                      int64_t ldv, const float* mask, int64_t mask_batch, int64_t batch, int64_t seq,

@@ -183,31 +183,27 @@ __device__ __forceinline__ int wave_sum(int v) { return wave_reduce(v, OpAdd{});
 // round_half_away_from_zero(a / s) for a >= 0 (or +inf), s > 0 finite normal,
 // exact with respect to the real quotient (the reference rounds the f64
 // quotient, which lies on the same side of every half-integer as the exact
-// one).  `inv_s` is any approximation of 1/s good to a few ulp; `cap` is an
-// integer-valued float <= 2^22: quotients above it come back as cap or cap+1,
-// which every caller clamps.  NaN `a` is the caller's business.
+// one).  `inv_s` is 1/s within 2 ulp; `cap` is an integer-valued float <= 256:
+// quotients above cap come back as cap or cap+1, which every caller clamps.
+// NaN `a` gives 0 (fmax(NaN, 0) = 0, and its NaN residual adds nothing).
 //
-// Why it is exact: n0 = floor(min(a*inv_s, cap) + 1/2) is within one of the
-// true n.  The residual r = fma(-n0, s, a) = a - n0*s is exact whenever
-// |a - n0*s| <= s (it is a multiple of ulp(s)/2 below 2^24 of them), so the
-// tests r >= s/2 and r < -s/2 against the exact half-way points are exact;
-// when |a - n0*s| > s the rounded r is still on the correct side.
+// Why it is exact: for q = a/s <= cap + 1/2, t = fma(a, inv_s, 1/2 - 2^-12) is
+// q + 1/2 - 2^-12 within q 2^-22 + 257 * 2^-24 < 2^-13, so n0 = floor(min(t,
+// cap)) is the rounded n = floor(q + 1/2) or n - 1, never n + 1.  The residual
+// r = fma(-n0, s, a) = a - n0*s is then exact (|r| < 1.5 s, a multiple of
+// ulp(s)/2 below 2^24 of them), and n = n0 + 1 exactly when r >= s/2.  Above
+// the cap, r > s/2 is rounded on the correct side.
 __device__ __forceinline__ float rhaz_div(float a, float s, float inv_s, float half_s,
                                           float cap) {
-    const float t = fminf(a * inv_s, cap);
-    float n = floorf(t + 0.5f);
+    const float n = floorf(fminf(fmaxf(fmaf(a, inv_s, 0.5f - 0x1p-12f), 0.0f), cap));
     const float r = fmaf(-n, s, a);
-    n = (r >= half_s) ? n + 1.0f : n;
-    n = (r < -half_s) ? n - 1.0f : n;
-    return n;
+    return (r >= half_s) ? n + 1.0f : n;
 }
 
-// Signed code for x given |x|'s rounded quotient n: NaN -> 0, sign from x,
-// clamp to [qmin, qmax].
+// Signed code for x given |x|'s rounded quotient n (rhaz_div: 0 for NaN x): sign
+// from x, clamp to [qmin, qmax].
 __device__ __forceinline__ int signed_code(float x, float n, int qmin, int qmax) {
-    n = (x == x) ? n : 0.0f;
-    int c = static_cast<int>(n);  // n is integral, 0 <= n <= cap + 1
-    c = (x < 0.0f) ? -c : c;
+    const int c = static_cast<int>(copysignf(n, x));  // n is integral, 0 <= n <= cap + 1
     return min(max(c, qmin), qmax);
 }
 

@@ -18,18 +18,17 @@ __device__ __forceinline__ int code_i8(float x, float s, float inv_s, float half
     return signed_code(x, n, -128, 127);
 }
 
-// INT8 code of x for its row's own scale s = f32(max(absmax/127, 1e-10)) (finite):
-// |x| / s <= 127 (1 + 2^-22), so the code stays in [-127, 127] before the clamp.
-// fmax(NaN, 0) = 0 sends NaN to code 0 without a separate test; the rounding is
-// rhaz_div's (candidate, exact residual, +-1).
+// INT8 code of x for its row's own scale s = f32(max(absmax/127, 1e-10)) (finite),
+// round half away from zero of |x| / s, exact: rhaz_div's one-sided rounding
+// without its cap, since q = |x| / s <= 127 (1 + 2^-23) gives n <= 127 (the code
+// is in [-127, 127], no clamp).  fmax(NaN, 0) = 0 sends NaN to code 0 (its
+// residual is NaN: no correction).
 __device__ __forceinline__ int code_i8_row(float x, float s, float inv_s, float half_s) {
     const float a = fabsf(x);
-    float n = floorf(fmaxf(a * inv_s, 0.0f) + 0.5f);
+    float n = floorf(fmaxf(fmaf(a, inv_s, 0.5f - 0x1p-12f), 0.0f));
     const float r = fmaf(-n, s, a);
     n = (r >= half_s) ? n + 1.0f : n;
-    n = (r < -half_s) ? n - 1.0f : n;
-    const int c = static_cast<int>(copysignf(n, x));
-    return min(max(c, -128), 127);
+    return static_cast<int>(copysignf(n, x));
 }
 
 __device__ __forceinline__ uint32_t pack4_i8(int a, int b, int c, int d) {

@@ -82,28 +82,24 @@ __global__ __launch_bounds__(kBlock) void k_quant_rows_vec(const float* __restri
 // 128-thread blocks of two waves; wave w takes rows w, w + (waves in the grid),
 // ...; lane l holds f32x4 items l + 64 i of the row, so every wave-wide load
 // reads 1 KB contiguously, and the row maximum is a wave reduction (no LDS, no
-// barrier).  At 2048 x 4096 (the W8A8 activations): 10.1 us against 10.8 us
-// for four waves per row in 256-thread blocks; the same loads and stores with
-// the coder replaced by a trivial fold take 8.1 us, a plain read of the 42 MB
-// 8.0 us.
-template <class Fmt, int kI, bool kFit>
+// barrier).  Serves K that is not 2048 or 4096 (those take k_quant_rows_split).
+template <class Fmt, int kI>
 __global__ __launch_bounds__(128) void k_quant_rows_wave(const float* __restrict__ w, int64_t rows, int64_t k,
                                                          typename Fmt::code_t* __restrict__ q,
                                                          float* __restrict__ s) {
     const int lane = threadIdx.x & 63;
-    const int k4 = kFit ? 64 * kI : static_cast<int>(k >> 2);  // kFit: K == 256 kI
+    const int k4 = static_cast<int>(k >> 2);
     const int64_t nw = static_cast<int64_t>(gridDim.x) * 2;
     for (int64_t row = static_cast<int64_t>(blockIdx.x) * 2 + (threadIdx.x >> 6); row < rows; row += nw) {
         const f32x4* src = reinterpret_cast<const f32x4*>(w + row * k);
         // every load is issued (lanes past the row re-read its last item, which
         // leaves the maximum unchanged): a load under a lane mask made the compiler
-        // wait for each one before the next (14.4 against 10.1 us at 2048 x 4096),
-        // and a clamped index costs every load its own address (11.8 us)
+        // wait for each one before the next (14.4 against 10.1 us at 2048 x 4096)
         f32x4 v[kI];
         float m = -INFINITY;
 #pragma unroll
         for (int i = 0; i < kI; ++i)
-            v[i] = __builtin_nontemporal_load(src + (kFit ? lane + 64 * i : min(lane + 64 * i, k4 - 1)));
+            v[i] = __builtin_nontemporal_load(src + min(lane + 64 * i, k4 - 1));
 #pragma unroll
         for (int i = 0; i < kI; ++i)
             m = fmaxf(m, fmaxf(fmaxf(fabsf(v[i].x), fabsf(v[i].y)), fmaxf(fabsf(v[i].z), fabsf(v[i].w))));
@@ -114,9 +110,46 @@ __global__ __launch_bounds__(128) void k_quant_rows_wave(const float* __restrict
 #pragma unroll
         for (int i = 0; i < kI; ++i) {
             const int idx = lane + 64 * i;
-            if (kFit || idx < k4) __builtin_nontemporal_store(coder.code4(v[i]), qd + idx);
+            if (idx < k4) __builtin_nontemporal_store(coder.code4(v[i]), qd + idx);
         }
     }
+}
+
+// ---- per-row quantize, one row per block of kW waves (codes only, K == 256 kI kW) ----
+// Wave v holds the v-th kW-th of the row (lane l: f32x4 items l + 64 i of it);
+// the wave maxima meet in LDS.  A row's coding starts only once its last bytes
+// are in, so the launch ends with the coding of the rows that land last: spread
+// over kW waves, that tail is 1/kW of a wave-per-row kernel's.  At 2048 x 4096
+// (the W8A8 activations): 8.7-8.8 us with 4 waves per row, 8.8-8.9 with 2, 9.4-9.5
+// with 8 and 9.2 with a wave per row; the same loads and stores with the coder
+// replaced by a trivial fold take 8.1 us, a plain read of the 42 MB 8.0 us.
+template <class Fmt, int kI, int kW>
+__global__ __launch_bounds__(64 * kW) void k_quant_rows_split(const float* __restrict__ w, int64_t k,
+                                                              typename Fmt::code_t* __restrict__ q,
+                                                              float* __restrict__ s) {
+    __shared__ float red[kW];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int64_t row = blockIdx.x;
+    const f32x4* src = reinterpret_cast<const f32x4*>(w + row * k) + wave * 64 * kI;
+    f32x4 v[kI];
+    float m = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < kI; ++i) v[i] = __builtin_nontemporal_load(src + lane + 64 * i);
+#pragma unroll
+    for (int i = 0; i < kI; ++i)
+        m = fmaxf(m, fmaxf(fmaxf(fabsf(v[i].x), fabsf(v[i].y)), fmaxf(fabsf(v[i].z), fabsf(v[i].w))));
+    m = wave_max(m);
+    if (lane == 0) red[wave] = m;
+    __syncthreads();
+    m = red[0];
+#pragma unroll
+    for (int j = 1; j < kW; ++j) m = fmaxf(m, red[j]);
+    const float sc = row_scale<Fmt>(absmax_finish(m));
+    if (threadIdx.x == 0) s[row] = sc;
+    const typename Fmt::Row coder(sc);
+    uint32_t* qd = reinterpret_cast<uint32_t*>(q + row * k) + wave * 64 * kI;
+#pragma unroll
+    for (int i = 0; i < kI; ++i) __builtin_nontemporal_store(coder.code4(v[i]), qd + lane + 64 * i);
 }
 
 // ---- per-row quantize, any K / alignment: two passes over the row ----
@@ -483,20 +516,21 @@ int launch_quant_rows(const float* w, int64_t rows, int64_t k, typename Fmt::cod
     const dim3 grid(static_cast<unsigned>(rows)), block(kBlock);
     const int64_t cus = device_cu_count();
     if (vec && !w_hat && k > 1024 && k <= 4096 && rows <= 8 * cus) {
-        // codes only, 1-4 K elements, at most 8 rows per CU: a wave per row (2048 x
-        // 4096: 10.2 against 10.8 us).  Past that the persistent blocks below stay
-        // ahead (4096 x 4096: 17.3 us, against 17.9 with two rows per wave and 20.3
-        // with one, 64 MB in flight at once).
+        // codes only, 1-4 K elements, at most 8 rows per CU: a row per 4-wave block
+        // at K = 2048 and 4096, a wave per row otherwise.  Past that the persistent
+        // blocks below stay ahead (4096 x 4096: 17.3 us, against 17.9 with two rows
+        // per wave and 20.3 with one, 64 MB in flight at once).
         const int64_t nb = (rows + 1) / 2;
         const unsigned g = static_cast<unsigned>(nb);
+        constexpr int kSplitW = 4;
         if (k == 2048)
-            k_quant_rows_wave<Fmt, 8, true><<<g, 128, 0, st>>>(w, rows, k, q, s);
+            k_quant_rows_split<Fmt, 8 / kSplitW, kSplitW><<<grid, 64 * kSplitW, 0, st>>>(w, k, q, s);
         else if (k == 4096)
-            k_quant_rows_wave<Fmt, 16, true><<<g, 128, 0, st>>>(w, rows, k, q, s);
+            k_quant_rows_split<Fmt, 16 / kSplitW, kSplitW><<<grid, 64 * kSplitW, 0, st>>>(w, k, q, s);
         else if (k < 2048)
-            k_quant_rows_wave<Fmt, 8, false><<<g, 128, 0, st>>>(w, rows, k, q, s);
+            k_quant_rows_wave<Fmt, 8><<<g, 128, 0, st>>>(w, rows, k, q, s);
         else
-            k_quant_rows_wave<Fmt, 16, false><<<g, 128, 0, st>>>(w, rows, k, q, s);
+            k_quant_rows_wave<Fmt, 16><<<g, 128, 0, st>>>(w, rows, k, q, s);
     } else if (vec) {
         const int64_t items = (k / 4 + kBlock - 1) / kBlock;
         // codes only: persistent, at most 8 blocks per CU, each taking every

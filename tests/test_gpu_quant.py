@@ -91,8 +91,9 @@ def test_quantize_i8_rowwise_special_rows(tq, oracle):
 
 
 # Codes only with 1025-4096 elements per row and at most 8 rows per CU runs a wave
-# per row: K a multiple of 16 but not of 256 (masked lanes) and K = 2048, 4096 (no
-# masks), with ties, NaN, inf, all-NaN and subnormal rows, up to 2048 rows.
+# per row (K a multiple of 16 but not of 256: masked lanes) or a row per 4-wave
+# block (K = 2048, 4096), with ties, NaN, inf, all-NaN and subnormal rows, up to
+# 2048 rows.
 @pytest.mark.parametrize("rows,k", [(9, 1040), (9, 2064), (9, 4096), (2048, 1296), (1999, 2048)])
 def test_quantize_rowwise_codes_only_wave_rows(tq, oracle, rows, k):
     base = [np.zeros(k, np.float32), tie_row(k), -tie_row(k)]

@@ -190,9 +190,11 @@ __device__ __forceinline__ int wave_sum(int v) { return wave_reduce(v, OpAdd{});
 // Why it is exact: for q = a/s <= cap + 1/2, t = fma(a, inv_s, 1/2 - 2^-12) is
 // q + 1/2 - 2^-12 within q 2^-22 + 257 * 2^-24 < 2^-13, so n0 = floor(min(t,
 // cap)) is the rounded n = floor(q + 1/2) or n - 1, never n + 1.  The residual
-// r = fma(-n0, s, a) = a - n0*s is then exact (|r| < 1.5 s, a multiple of
-// ulp(s)/2 below 2^24 of them), and n = n0 + 1 exactly when r >= s/2.  Above
-// the cap, r > s/2 is rounded on the correct side.
+// r = fma(-n0, s, a), a - n0*s rounded once, decides: for n0 = n it is exact
+// (|r| <= s/2 and, with a >= s/2, a multiple of ulp(s)/2; for a < s/2, n0 = 0
+// and r = a) and below s/2; for n0 = n - 1 the exact value lies in [s/2, 1.5 s)
+// and rounding keeps it >= s/2.  So n = n0 + 1 exactly when r >= s/2.  Above
+// the cap, r > s/2 likewise.
 __device__ __forceinline__ float rhaz_div(float a, float s, float inv_s, float half_s,
                                           float cap) {
     const float n = floorf(fminf(fmaxf(fmaf(a, inv_s, 0.5f - 0x1p-12f), 0.0f), cap));

@@ -42,6 +42,7 @@ __device__ __forceinline__ float block_max(float v, float* red) {
 // loads issued before the current row's reduction).  The
 // block reduction alternates between two LDS slots, so a wave that runs ahead
 // into the next row never overwrites a maximum another wave has still to read.
+// Serves K other than 2048 and 4096, which take k_quant_rows_split.
 template <class Fmt, int kItems>
 __global__ __launch_bounds__(kBlock) void k_quant_rows_vec(const float* __restrict__ w, int64_t rows, int64_t k,
                                                            typename Fmt::code_t* __restrict__ q,
@@ -115,18 +116,19 @@ __global__ __launch_bounds__(128) void k_quant_rows_wave(const float* __restrict
     }
 }
 
-// ---- per-row quantize, one row per block of kW waves (codes only, K == 256 kI kW) ----
+// ---- per-row quantize, one row per block of kW waves (K == 256 kI kW) ----
 // Wave v holds the v-th kW-th of the row (lane l: f32x4 items l + 64 i of it);
-// the wave maxima meet in LDS.  A row's coding starts only once its last bytes
-// are in, so the launch ends with the coding of the rows that land last: spread
-// over kW waves, that tail is 1/kW of a wave-per-row kernel's.  At 2048 x 4096
-// (the W8A8 activations): 8.7-8.8 us with 4 waves per row, 8.8-8.9 with 2, 9.4-9.5
-// with 8 and 9.2 with a wave per row; the same loads and stores with the coder
+// the wave maxima meet in LDS; codes, and the dequantized copy when w_hat is
+// given.  A row's coding starts only once its last bytes are in, so the launch
+// ends with the coding of the rows that land last: spread over kW waves, that
+// tail is 1/kW of a wave-per-row kernel's.  At 2048 x 4096 (the W8A8
+// activations): 8.7-8.8 us with 4 waves per row, 8.8-8.9 with 2, 9.4-9.5 with 8
+// and 9.2 with a wave per row; the same loads and stores with the coder
 // replaced by a trivial fold take 8.1 us, a plain read of the 42 MB 8.0 us.
 template <class Fmt, int kI, int kW>
 __global__ __launch_bounds__(64 * kW) void k_quant_rows_split(const float* __restrict__ w, int64_t k,
                                                               typename Fmt::code_t* __restrict__ q,
-                                                              float* __restrict__ s) {
+                                                              float* __restrict__ s, float* __restrict__ w_hat) {
     __shared__ float red[kW];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int64_t row = blockIdx.x;
@@ -149,7 +151,13 @@ __global__ __launch_bounds__(64 * kW) void k_quant_rows_split(const float* __res
     const typename Fmt::Row coder(sc);
     uint32_t* qd = reinterpret_cast<uint32_t*>(q + row * k) + wave * 64 * kI;
 #pragma unroll
-    for (int i = 0; i < kI; ++i) __builtin_nontemporal_store(coder.code4(v[i]), qd + lane + 64 * i);
+    for (int i = 0; i < kI; ++i) {
+        const uint32_t c = coder.code4(v[i]);
+        __builtin_nontemporal_store(c, qd + lane + 64 * i);
+        if (w_hat)
+            __builtin_nontemporal_store(Fmt::value4(c, sc),
+                                        reinterpret_cast<f32x4*>(w_hat + row * k) + wave * 64 * kI + lane + 64 * i);
+    }
 }
 
 // ---- per-row quantize, any K / alignment: two passes over the row ----
@@ -515,19 +523,22 @@ int launch_quant_rows(const float* w, int64_t rows, int64_t k, typename Fmt::cod
                      (!q || aligned(q, 4)) && (!w_hat || aligned(w_hat, 16));
     const dim3 grid(static_cast<unsigned>(rows)), block(kBlock);
     const int64_t cus = device_cu_count();
-    if (vec && !w_hat && k > 1024 && k <= 4096 && rows <= 8 * cus) {
-        // codes only, 1-4 K elements, at most 8 rows per CU: a row per 4-wave block
-        // at K = 2048 and 4096, a wave per row otherwise.  Past that the persistent
-        // blocks below stay ahead (4096 x 4096: 17.3 us, against 17.9 with two rows
-        // per wave and 20.3 with one, 64 MB in flight at once).
-        const int64_t nb = (rows + 1) / 2;
-        const unsigned g = static_cast<unsigned>(nb);
+    if (vec && q && (k == 2048 || k == 4096)) {
+        // a row per 4-wave block, with or without the dequantized copy: W8A8
+        // activations 2048 x 4096 8.8 us; 4096 x 4096 codes 15.7 us and round trip
+        // 26.1 us, against 16.3 / 26.8 us for the persistent and per-row blocks below
         constexpr int kSplitW = 4;
         if (k == 2048)
-            k_quant_rows_split<Fmt, 8 / kSplitW, kSplitW><<<grid, 64 * kSplitW, 0, st>>>(w, k, q, s);
-        else if (k == 4096)
-            k_quant_rows_split<Fmt, 16 / kSplitW, kSplitW><<<grid, 64 * kSplitW, 0, st>>>(w, k, q, s);
-        else if (k < 2048)
+            k_quant_rows_split<Fmt, 8 / kSplitW, kSplitW><<<grid, 64 * kSplitW, 0, st>>>(w, k, q, s, w_hat);
+        else
+            k_quant_rows_split<Fmt, 16 / kSplitW, kSplitW><<<grid, 64 * kSplitW, 0, st>>>(w, k, q, s, w_hat);
+    } else if (vec && !w_hat && k > 1024 && k <= 4096 && rows <= 8 * cus) {
+        // codes only, other K of 1-4 K elements, at most 8 rows per CU: a wave per
+        // row.  Past that the persistent blocks below stay ahead (4096 x 4096: 17.3
+        // us, against 17.9 with two rows per wave and 20.3 with one, 64 MB in flight
+        // at once).
+        const unsigned g = static_cast<unsigned>((rows + 1) / 2);
+        if (k < 2048)
             k_quant_rows_wave<Fmt, 8><<<g, 128, 0, st>>>(w, rows, k, q, s);
         else
             k_quant_rows_wave<Fmt, 16><<<g, 128, 0, st>>>(w, rows, k, q, s);

@@ -81,7 +81,7 @@ def test_quantize_fp8_rowwise_shapes(tq, oracle, rows, k):
     assert np.array_equal(host(q2), rq) and np.array_equal(host(s2), rs)
 
 
-@pytest.mark.parametrize("k", [64, 30])
+@pytest.mark.parametrize("k", [64, 30, 2048, 4096])
 def test_quantize_fp8_special_rows(tq, oracle, k):
     w = normal(72, (7, k), 1.0)
     w[6] *= 1e-38  # subnormal inputs

@@ -64,8 +64,9 @@ def test_quantize_i8_rowwise_ragged(tq, oracle, shape):
     assert ieee_equal(host(d), oracle.dequantize_i8_rowwise(rq, rs))
 
 
-def test_quantize_i8_rowwise_special_rows(tq, oracle):
-    k = 512
+# K = 2048 and 4096 run the 4-wave-per-row kernel with the dequantized copy
+@pytest.mark.parametrize("k", [512, 2048, 4096])
+def test_quantize_i8_rowwise_special_rows(tq, oracle, k):
     rows = [np.zeros(k, np.float32), tie_row(k), -tie_row(k), weights(21, (k,), 1.0)]
     nanrow = weights(22, (k,), 1.0)
     nanrow[::7] = np.nan

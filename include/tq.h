@@ -220,14 +220,15 @@ int tq_gemv_fp8(const float* x, int64_t m, const uint8_t* q, const float* s,
  * with exact int32 dot products: the same y as tq_quantize_i8_rowwise +
  * tq_gemm_w8a8, bit for bit, in one launch.  Requires K % 16 == 0, K <= 8192,
  * x and qw 16-byte aligned (TQ_EINVAL otherwise: run the two-step path).  At
- * 4096 x 4096 faster than the two-step path for M <= 2 (5.4 / 7.0 against 9.8 /
- * 10.2 us), slower from M = 3 (12.0 against 10.6 us; 52.3 against 12.5 at 16). */
+ * 4096 x 4096 faster than the two-step path for M <= 2 (5.1 against 9.2-9.5 us
+ * at M = 1), slower from M = 3 (13.3 against 9.7-9.9 us at 4; 49.4 against 11.3
+ * at 16). */
 int tq_gemv_w8a8(const float* x, int64_t m, const int8_t* qw, const float* sw,
                  const float* bias, int64_t n, int64_t k, float* y, tq_stream_t stream);
 /* The FP8 counterpart (tq_quantize_fp8_rowwise + tq_gemm_fp8 in one launch;
  * f32 accumulation, so equal to the GEMM within the float tolerance).  Faster
- * than the two-step path at 4096 x 4096 for M <= 2 (6.2 / 6.9 against 9.3 /
- * 9.5 us), slower from M = 3 (12.9 against 10.0 us; 54.0 against 11.3 at 16). */
+ * than the two-step path at 4096 x 4096 for M <= 2 (5.5-5.6 against 9.3-9.5 us
+ * at M = 1), slower from M = 3 (12.9 against 10.0 us; 54.0 against 11.3 at 16). */
 int tq_gemv_fp8a8(const float* x, int64_t m, const uint8_t* qw, const float* sw,
                   const float* bias, int64_t n, int64_t k, float* y, tq_stream_t stream);
 

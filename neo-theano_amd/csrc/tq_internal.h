@@ -90,13 +90,16 @@ __device__ __forceinline__ uint32_t lds_addr(const int8_t* l) {
 // waits.  M0 is listed as clobbered so that the compiler never assumes a value
 // of its own survives the statement (clang warns that M0 is reserved, i.e. not
 // saved for the statement, which is the intent: nothing is to be preserved).
+// An LDS DMA reads M0 one wait state after a scalar write of it (the gap the
+// compiler itself leaves between the two on gfx950), hence the s_nop 0: the
+// hazard recognizer does not look inside inline asm.
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
 __device__ __forceinline__ void lds_dma16(const void* g, uint32_t la) {
-    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(la), "v"(g) : "memory", "m0");
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(la), "v"(g) : "memory", "m0");
 }
 __device__ __forceinline__ void lds_dma4(const void* g, uint32_t la) {
-    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, off" ::"s"(la), "v"(g) : "memory", "m0");
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, off" ::"s"(la), "v"(g) : "memory", "m0");
 }
 // Waits until at most N vector memory operations of the wave are outstanding (the
 // completion of LDS DMAs, which the compiler does not track).  A count N > 0 is

@@ -661,8 +661,15 @@ __global__ __launch_bounds__(kFoldWaves * 64) void k_decode_fold32(const uint16_
     }
     // no DMA into the strips is still in flight (a wave past its range issued some),
     // and every read of them has returned: the partial sums go to strip 0,
-    // part[row][column], lane holding D[row 16 r + 4 q + e][column 16 s + r16]
-    asm volatile("s_waitcnt vmcnt(0)\n\ts_waitcnt lgkmcnt(0)" ::: "memory");
+    // part[row][column], lane holding D[row 16 r + 4 q + e][column 16 s + r16].
+    // A wave that left the loop early still has weight and scale loads in flight
+    // into registers that are dead on that path: the compiler would be free to
+    // place other values there before the wait, and the landing loads would
+    // overwrite them.  Every slot is an operand of the final wait, so all of them
+    // stay allocated until it.
+#pragma unroll
+    for (int s2 = 0; s2 < kWin; ++s2) fold_wait<0>(w[s2][0], w[s2][1], sc[s2][0], sc[s2][1]);
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     float* part = reinterpret_cast<float*>(strips[wave][0]);
 #pragma unroll
     for (int s2 = 0; s2 < kSets; ++s2)

@@ -493,7 +493,7 @@ __global__ __launch_bounds__(kBlock) void k_decode_tiled_mfma_sx(const uint16_t*
 // group's weight and scale registers as operands, so no use of them can be
 // scheduled ahead of it.
 constexpr int kFoldWaves = 8;
-constexpr int kFoldWin = 2;  // groups of weights and scales in flight
+constexpr int kFoldWin = 4;  // groups of weights and scales in flight (2 and 3: ~0.3 us slower at 8 tokens)
 constexpr int kFoldLPG = 4;  // load instructions per group: 2 row groups x (scales, weights)
 
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
